@@ -1,0 +1,390 @@
+#!/usr/bin/env python3
+"""W4G64 linear benchmark on one MI355X: decode GEMV HBM GB/s and prefill GEMM
+TFLOP/s, each as a fraction of the MI355X peak.
+
+Decode workload (the `value` line): one step = the seven Qwen2-1.5B linear
+shapes (q/k/v/o, gate/up/down) at activation rows 1, 4 and 16, fp16
+activations, symmetric RTN W4G64 weights -- 21 linear calls.  Weights are
+replicated into distinct device copies (~800 MB in total) and every call of a
+step reads a different copy, so the 256 MB Infinity Cache and the L2s cannot
+serve a repeat: the figure is HBM throughput.  Each step is captured once as a
+HIP graph; the timed region replays K step graphs back to back between two
+device synchronizations.  value = algorithmic bytes of the step / step time.
+
+The roofline object is for the kernel that does the decode work
+(gemv_kernel<f16,1>, all 21 calls): its duration per call is measured live
+with HIP events that hipExtLaunchKernelGGL records at the kernel's own start
+and end (the same figure rocprofv3 --kernel-trace reports), on the stream the
+kernel runs on; achieved = algorithmic bytes / summed kernel durations.
+
+Algorithmic bytes per call (M rows, N out, K in):
+    N*K/2 + 2*N*K/64 + N*K/128 + 2*M*K + 2*M*N
+(packed codes, fp16 scales, packed zeros, fp16 activations, fp16 outputs).
+
+The prefill GEMM (gate/up 8960x1536 and down 1536x8960 at rows 128/512/2048,
+bf16) is reported in the "gemm" object with its own roofline (MFMA bound).
+
+Parity against the CPU oracle is checked for every timed case before any
+timing, as the reference's harness does (scripts/autotune_phase_e_triton_v6.py:96-113).
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import platform
+import statistics
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+REPO_ROOT = Path(__file__).resolve().parent
+PACKAGE_ROOT = REPO_ROOT / "qwen2-int4-systems_amd"
+for _path in (REPO_ROOT, PACKAGE_ROOT):
+    if str(_path) not in sys.path:
+        sys.path.insert(0, str(_path))
+
+METRIC = "W4G64 GEMV HBM GB/s (M=1) + GEMM TFLOP/s (M=2048), % of MI355X peak"
+HBM_PEAK_GBS = 8000.0
+MFMA_PEAK_TFLOPS = 2500.0  # dense fp16/bf16
+DECODE_ROWS = (1, 4, 16)
+PREFILL_ROWS = (128, 512, 2048)
+PREFILL_SHAPES = ("gate_proj", "down_proj")
+COPIES = 32  # distinct weight copies per shape (32 x 25.2 MB = 806 MB)
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def algorithmic_bytes(m: int, n: int, k: int, act_bytes: int = 2) -> int:
+    return n * k // 2 + 2 * n * (k // 64) + n * (k // 64) // 2 + act_bytes * m * k + act_bytes * m * n
+
+
+class Hip:
+    """The few HIP runtime calls the harness needs (events, sync)."""
+
+    def __init__(self) -> None:
+        self.lib = ctypes.CDLL("libamdhip64.so")
+        self.lib.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.lib.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+        self.lib.hipEventSynchronize.argtypes = [ctypes.c_void_p]
+        self.lib.hipEventDestroy.argtypes = [ctypes.c_void_p]
+
+    def event(self) -> ctypes.c_void_p:
+        ev = ctypes.c_void_p()
+        if self.lib.hipEventCreate(ctypes.byref(ev)) != 0:
+            raise RuntimeError("hipEventCreate failed")
+        return ev
+
+    def elapsed_ms(self, start, stop) -> float:
+        self.lib.hipEventSynchronize(stop)
+        ms = ctypes.c_float()
+        if self.lib.hipEventElapsedTime(ctypes.byref(ms), start, stop) != 0:
+            raise RuntimeError("hipEventElapsedTime failed")
+        return float(ms.value)
+
+
+def to_device(arr: np.ndarray, dtype: str, torch):
+    arr = np.ascontiguousarray(arr)
+    if dtype == "bf16":
+        return torch.from_numpy(arr.view(np.int16)).view(torch.bfloat16).cuda()
+    return torch.from_numpy(arr).cuda()
+
+
+def check_parity(out, ref32: np.ndarray, label: str) -> float:
+    got = out.float().cpu().numpy()
+    rel = float(np.abs(got - ref32).max() / max(float(np.abs(ref32).max()), 1e-30))
+    if not np.isfinite(got).all() or rel > 1e-2:
+        raise SystemExit(f"parity failed for {label}: normwise relative error {rel:.3e}")
+    return rel
+
+
+def timed_call(lib, hip, x, w, y, workspace, stream, events):
+    from qwen_int4_hip import _lib
+
+    q, s, z = w
+    rows, k = x.shape
+    n = y.shape[1]
+    code = {"torch.float16": _lib.DTYPE_F16, "torch.bfloat16": _lib.DTYPE_BF16}[str(x.dtype)]
+    _lib.check(lib.w4g64_linear_timed(
+        ctypes.c_void_p(x.data_ptr()), code, ctypes.c_void_p(q.data_ptr()), ctypes.c_void_p(s.data_ptr()),
+        ctypes.c_void_p(z.data_ptr()), None, _lib.DTYPE_NONE, ctypes.c_void_p(y.data_ptr()), rows, n, k,
+        None if workspace is None else ctypes.c_void_p(workspace.data_ptr()),
+        0 if workspace is None else workspace.numel(), stream, events[0], events[1]))
+
+
+def kernel_durations(cases, reps, hip, torch):
+    """Per-case kernel durations (ms) from start/stop events recorded by the
+    kernel launch itself; calls rotate over the weight copies."""
+    from qwen_int4_hip import _lib
+    from qwen_int4_hip.kernels import _workspace
+
+    lib = _lib.load()
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    pairs = [(hip.event(), hip.event()) for _ in range(len(cases) * reps)]
+    outputs = []
+    i = 0
+    for rep in range(reps):
+        for case in cases:
+            x, copies, n = case["x"], case["copies"], case["n"]
+            w = copies[(case["copy0"] + rep * 3) % len(copies)]
+            y = torch.empty((x.shape[0], n), dtype=x.dtype, device="cuda")
+            ws_bytes = lib.w4g64_linear_workspace_bytes(x.shape[0], n, x.shape[1],
+                                                        _lib.DTYPE_F16 if x.dtype == torch.float16 else _lib.DTYPE_BF16)
+            ws = _workspace(torch.device("cuda"), ws_bytes)
+            timed_call(lib, hip, x, w, y, ws, stream, pairs[i])
+            outputs.append(y)
+            i += 1
+    torch.cuda.synchronize()
+    durations = [[] for _ in cases]
+    i = 0
+    for rep in range(reps):
+        for c in range(len(cases)):
+            durations[c].append(hip.elapsed_ms(*pairs[i]))
+            i += 1
+    for a, b in pairs:
+        hip.lib.hipEventDestroy(a)
+        hip.lib.hipEventDestroy(b)
+    return durations
+
+
+def cpu_baseline(decode_cases_np, torch, budget_s: float = 12.0):
+    """The reference's torch path restated on CPU, timed on host cores over a
+    bounded sample of decode steps."""
+    from oracle import oracle as O
+
+    threads = max(1, min(16, os.cpu_count() or 1))
+    torch.set_num_threads(threads)
+    tensors = []
+    step_bytes = 0
+    for case in decode_cases_np:
+        q, s, z = (torch.from_numpy(a) for a in case["w"])
+        tensors.append((torch.from_numpy(case["x"]), q, s, z, case["n"], case["k"]))
+        step_bytes += case["bytes"]
+    def one_step():
+        for x, q, s, z, n, k in tensors:
+            O.reference_linear_torch(x, q, s, z, None, out_features=n, in_features=k)
+    one_step()  # warm-up
+    times = []
+    start = time.perf_counter()
+    while len(times) < 30 and (time.perf_counter() - start) < budget_s:
+        t0 = time.perf_counter()
+        one_step()
+        times.append(time.perf_counter() - t0)
+    step_s = statistics.median(times)
+    cpu_model = platform.processor() or "unknown"
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "value": step_bytes / step_s / 1e9,
+        "unit": "GB/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"{len(times)} decode steps (21 calls each: 7 shapes x rows 1/4/16, fp16) of the torch CPU "
+                   f"restatement of the reference's torch backend; median {step_s * 1e3:.1f} ms/step; "
+                   f"host {cpu_model}, os.cpu_count()={os.cpu_count()}"),
+    }
+
+
+def main() -> int:
+    parser = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=512)
+    parser.add_argument("--warmup", type=int, default=64)
+    parser.add_argument("--kernel-reps", type=int, default=32, help="event-timed calls per case")
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--no-gemm", action="store_true")
+    parser.add_argument("--report", type=str, default="", help="write the detailed JSON report here")
+    args = parser.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported by this build "
+              "(the W4G64 path has no multi-GPU component).", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from oracle import oracle as O
+    from qwen_int4_hip import hip_available, linear_canonical_w4g64_hip, linear_kernel_name
+
+    if not hip_available():
+        raise SystemExit("bench.py needs a ROCm GPU and the built HIP library")
+    hip = Hip()
+    props = torch.cuda.get_device_properties(0)
+    log(f"device: {props.name} CUs={props.multi_processor_count}")
+
+    # ---------------- decode workload ----------------
+    shapes = O.QWEN2_SHAPES
+    weights_np = {name: O.symmetric_weights(n, k, O.BASE_SEED + n + k) for name, (n, k) in shapes.items()}
+    copies = {}
+    for name, (q, s, z) in weights_np.items():
+        base = (torch.from_numpy(q).cuda(), torch.from_numpy(s).cuda(), torch.from_numpy(z).cuda())
+        copies[name] = [tuple(t.clone() for t in base) for _ in range(COPIES)]
+    distinct_mb = sum(sum(t.numel() * t.element_size() for t in c[0]) for c in copies.values()) * COPIES / 1e6
+    cases = []
+    for r_index, rows in enumerate(DECODE_ROWS):
+        for s_index, (name, (n, k)) in enumerate(shapes.items()):
+            x_np = O.activations(rows, k, seed=O.BASE_SEED + 1000 * rows + s_index, dtype="fp16")
+            cases.append({"name": name, "rows": rows, "n": n, "k": k, "x_np": x_np, "x": to_device(x_np, "fp16", torch),
+                          "copies": copies[name], "copy0": r_index, "bytes": algorithmic_bytes(rows, n, k)})
+    step_bytes = sum(c["bytes"] for c in cases)
+
+    # parity before timing
+    worst = 0.0
+    for c in cases:
+        q, s, z = weights_np[c["name"]]
+        ref = O.reference_linear(c["x_np"], q, s, z, None, out_features=c["n"], in_features=c["k"], x_dtype="fp16")
+        out = linear_canonical_w4g64_hip(c["x"], *c["copies"][0])
+        worst = max(worst, check_parity(out, ref.astype(np.float32), f"{c['name']} rows={c['rows']}"))
+    log(f"decode parity ok: worst normwise relative error {worst:.2e}")
+
+    # HIP graphs: graph p runs the 21 calls of a step on copies (3p + rows_index) % COPIES
+    side = torch.cuda.Stream()
+    phases = COPIES
+    graphs = []
+    with torch.cuda.stream(side):
+        for c in cases:  # warm up on the capture stream (creates its workspace outside capture)
+            linear_canonical_w4g64_hip(c["x"], *c["copies"][0])
+        torch.cuda.synchronize()
+        for p in range(phases):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=side):
+                for c in cases:
+                    linear_canonical_w4g64_hip(c["x"], *c["copies"][(3 * p + c["copy0"]) % COPIES])
+            graphs.append(g)
+    torch.cuda.synchronize()
+    for i in range(args.warmup):
+        graphs[i % phases].replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        graphs[i % phases].replay()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = wall * 1e3 / args.steps
+    value = step_bytes / (ms_per_step * 1e-3) / 1e9
+    log(f"decode: {ms_per_step * 1e3:.1f} us/step, {value:.1f} GB/s whole-step ({step_bytes / 1e6:.1f} MB/step)")
+
+    # live per-kernel durations (events recorded by the kernel launch itself)
+    durations = kernel_durations(cases, args.kernel_reps, hip, torch)
+    per_case = []
+    kernel_ms_total = 0.0
+    for c, d in zip(cases, durations):
+        mean_ms = statistics.fmean(d)
+        kernel_ms_total += mean_ms
+        per_case.append({
+            "name": c["name"], "rows": c["rows"], "n": c["n"], "k": c["k"], "bytes": c["bytes"],
+            "kernel": linear_kernel_name(c["rows"], c["n"], c["k"], torch.float16),
+            "kernel_us_mean": mean_ms * 1e3, "kernel_us_median": statistics.median(d) * 1e3,
+            "GBps": c["bytes"] / (mean_ms * 1e-3) / 1e9,
+        })
+    achieved = step_bytes / (kernel_ms_total * 1e-3) / 1e9
+    m1_mlp = [p for p in per_case if p["rows"] == 1 and p["name"] in ("gate_proj", "up_proj", "down_proj")]
+    m1_mlp_gbs = sum(p["bytes"] for p in m1_mlp) / (sum(p["kernel_us_mean"] for p in m1_mlp) * 1e-6) / 1e9
+    for p in per_case:
+        log(f"  {p['name']:9s} rows={p['rows']:2d}  {p['kernel_us_mean']:7.2f} us  {p['GBps']:8.1f} GB/s")
+    log(f"decode kernel: {achieved:.1f} GB/s over all calls; M=1 MLP shapes {m1_mlp_gbs:.1f} GB/s")
+
+    result = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic",
+        "config": {
+            "workload": ("decode step: 7 Qwen2-1.5B W4G64 linear shapes (q/k/v/o 1536x1536 & 256x1536, gate/up "
+                         "8960x1536, down 1536x8960) x activation rows {1,4,16}, fp16 N(0,1) activations, symmetric "
+                         "RTN weights N(0,0.02); 21 calls per step as one HIP graph"),
+            "weight_copies": COPIES,
+            "distinct_weight_MB": round(distinct_mb, 1),
+            "bytes_per_step": step_bytes,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "gemv_kernel<f16,1>",
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "m1_mlp_GBps": round(m1_mlp_gbs, 2),
+            "m1_mlp_frac": round(m1_mlp_gbs / HBM_PEAK_GBS, 4),
+        },
+    }
+
+    # ---------------- prefill GEMM ----------------
+    if not args.no_gemm:
+        gemm_cases = []
+        for name in PREFILL_SHAPES:
+            n, k = shapes[name]
+            for rows in PREFILL_ROWS:
+                x_np = O.activations(rows, k, seed=O.BASE_SEED + 7 * rows + n, dtype="bf16")
+                gemm_cases.append({"name": name, "rows": rows, "n": n, "k": k, "x_np": x_np,
+                                   "x": to_device(x_np, "bf16", torch), "copies": copies[name][:4], "copy0": 0})
+        for c in gemm_cases:
+            if c["rows"] != 2048:
+                continue
+            q, s, z = weights_np[c["name"]]
+            ref = O.reference_linear(c["x_np"], q, s, z, None, out_features=c["n"], in_features=c["k"],
+                                     x_dtype="bf16")
+            out = linear_canonical_w4g64_hip(c["x"], *c["copies"][0])
+            check_parity(out, O.bf16_bits_to_f32(ref), f"gemm {c['name']} rows={c['rows']}")
+        log("gemm parity ok")
+        gd = kernel_durations(gemm_cases, 8, hip, torch)
+        gemm_rows = []
+        flops_2048 = 0.0
+        ms_2048 = 0.0
+        for c, d in zip(gemm_cases, gd):
+            mean_ms = statistics.fmean(d)
+            flops = 2.0 * c["rows"] * c["n"] * c["k"]
+            tflops = flops / (mean_ms * 1e-3) / 1e12
+            gemm_rows.append({"name": c["name"], "rows": c["rows"], "n": c["n"], "k": c["k"],
+                              "kernel_us_mean": mean_ms * 1e3, "TFLOPs": tflops})
+            log(f"  gemm {c['name']:9s} rows={c['rows']:4d}  {mean_ms * 1e3:8.2f} us  {tflops:7.1f} TFLOP/s")
+            if c["rows"] == 2048:
+                flops_2048 += flops
+                ms_2048 += mean_ms
+        tf = flops_2048 / (ms_2048 * 1e-3) / 1e12
+        result["gemm"] = {
+            "metric": "W4G64 GEMM TFLOP/s at M=2048 (gate/up 8960x1536 and down 1536x8960, bf16)",
+            "value": round(tf, 2),
+            "unit": "TFLOP/s",
+            "dtype": "bf16",
+            "roofline": {"bound": "mfma", "kernel": "gemm_kernel<bf16>", "achieved": round(tf, 2),
+                         "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(tf / MFMA_PEAK_TFLOPS, 4),
+                         "traffic": None},
+            "per_shape": gemm_rows,
+        }
+
+    if not args.no_cpu_baseline:
+        decode_np = [{"x": c["x_np"], "w": weights_np[c["name"]], "n": c["n"], "k": c["k"], "bytes": c["bytes"]}
+                     for c in cases]
+        result["cpu_baseline"] = cpu_baseline(decode_np, torch)
+        log(f"cpu baseline: {result['cpu_baseline']['value']:.3f} GB/s on {result['cpu_baseline']['cores']} threads")
+    result["decode_per_shape"] = per_case
+    if args.report:
+        Path(args.report).parent.mkdir(parents=True, exist_ok=True)
+        Path(args.report).write_text(json.dumps(result, indent=2) + "\n")
+    line = {k: v for k, v in result.items() if k != "decode_per_shape"}
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,111 @@
+/*
+ * w4g64.h -- C ABI of the MI355X (gfx950) W4G64 INT4 linear backend.
+ *
+ * Every entry point takes plain device pointers, sizes and a HIP stream
+ * (passed as `void*`, NULL = the default stream) and returns an int status.
+ * Nothing here allocates device memory, synchronizes the stream or keeps
+ * hidden global state besides the per-thread error string.  Arguments are
+ * validated on the host before any launch; on a non-zero status nothing was
+ * launched (except W4G64_STATUS_HIP_ERROR, which reports a failed launch).
+ *
+ * Packed contract (the reference checkpoint layout, unchanged):
+ *   qweight  uint8 [out*in/2]  row-major [out, in/2]; byte n*(in/2)+k/2 holds
+ *            k even in the low nibble, k odd in the high nibble; signed
+ *            two's-complement INT4 codes.
+ *   scales   fp16  [out, in/64]
+ *   zeros    uint8 [(out*(in/64)+1)/2]  signed INT4 zero points, element
+ *            n*(in/64)+g, same nibble order.
+ *   dequant  W[n,k] = (code[n,k] - zero[n,k/64]) * scale[n,k/64]
+ * Reference: src/qwen_int4/quantization.py:17-84, :221-258 and
+ * src/qwen_int4/backends.py:73-98.
+ */
+#ifndef QWEN_INT4_HIP_W4G64_H
+#define QWEN_INT4_HIP_W4G64_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes.  The Python layer maps them onto the reference's exception
+ * types: INVALID_VALUE -> ValueError, INVALID_DTYPE -> TypeError,
+ * UNSUPPORTED/HIP_ERROR -> RuntimeError. */
+#define W4G64_STATUS_OK 0
+#define W4G64_STATUS_INVALID_VALUE 1
+#define W4G64_STATUS_INVALID_DTYPE 2
+#define W4G64_STATUS_WORKSPACE 3
+#define W4G64_STATUS_UNSUPPORTED 4
+#define W4G64_STATUS_HIP_ERROR 5
+
+/* Element type codes for activations, outputs and bias. */
+#define W4G64_DTYPE_NONE 0
+#define W4G64_DTYPE_F16 1
+#define W4G64_DTYPE_BF16 2
+#define W4G64_DTYPE_F32 3
+
+/* Version of this ABI (bumped on any signature or contract change). */
+int w4g64_abi_version(void);
+
+/* Message of the last failed call on this host thread ("" if none). */
+const char* w4g64_last_error(void);
+
+/* Decode `elements` signed INT4 values (canonical nibble order) from
+ * `packed_bytes` bytes into int8.  `elements` may be odd (truncates the last
+ * byte) and must be in [0, 2*packed_bytes].
+ * Replaces: unpack_canonical_signed_int4_triton
+ *           (src/qwen_int4/triton_kernels.py:119-146). */
+int w4g64_unpack_canonical_int4(const uint8_t* packed, int64_t packed_bytes, int8_t* out,
+                                int64_t elements, void* stream);
+
+/* Dequantize a canonical W4G64 weight to fp32 [out_features, in_features],
+ * bit-exact with the closed form above.
+ * Replaces: dequantize_canonical_w4g64_triton
+ *           (src/qwen_int4/triton_kernels.py:149-203). */
+int w4g64_dequantize_canonical(const uint8_t* qweight, const uint16_t* scales, const uint8_t* zeros,
+                               float* out, int64_t out_features, int64_t in_features, void* stream);
+
+/* Bytes of workspace w4g64_linear needs for this problem (0 = none).
+ * Layout: a fixed 64 KiB area of per-column-block arrival counters, then the
+ * fp32 split-K partial sums.  The counter area must be zero before the first
+ * call and every call leaves it zero, so a caller allocates and clears one
+ * workspace once (sized for its largest problem) and reuses it for every
+ * shape.  Calls sharing a workspace must be ordered on one stream. */
+int64_t w4g64_linear_workspace_bytes(int64_t rows, int64_t out_features, int64_t in_features,
+                                     int x_dtype);
+
+/* y[rows, out] = x[rows, in] @ dequant(W)^T (+ bias), fp32 accumulation,
+ * stored in x's dtype.  x: fp16/bf16/fp32 contiguous row-major; bias: NONE,
+ * fp16, bf16 or fp32 [out]; y: same dtype as x.  rows >= 1; in % 64 == 0.
+ * rows <= 16 runs the decode GEMV, larger rows the MFMA GEMM.
+ * Pointers must be 16-byte aligned (scales and bias: element aligned).
+ * Replaces: linear_canonical_w4g64_triton (src/qwen_int4/triton_kernels.py:206-268)
+ *           and the kernel it launches (:66-116). */
+int w4g64_linear(const void* x, int x_dtype, const uint8_t* qweight, const uint16_t* scales,
+                 const uint8_t* zeros, const void* bias, int bias_dtype, void* y, int64_t rows,
+                 int64_t out_features, int64_t in_features, void* workspace, int64_t workspace_bytes,
+                 void* stream);
+
+/* w4g64_linear that also records two hipEvent_t (passed as void*, either may
+ * be NULL) at the start and at the end of the kernel itself, so
+ * hipEventElapsedTime gives the kernel's own duration -- the figure a
+ * profiler reports -- even when the host enqueues slower than the GPU runs.
+ * For benchmarking; not usable inside stream capture.
+ * No counterpart in the reference (its harness times with CUDA events around
+ * the call, scripts/autotune_phase_e_triton_v6.py:44-56). */
+int w4g64_linear_timed(const void* x, int x_dtype, const uint8_t* qweight, const uint16_t* scales,
+                       const uint8_t* zeros, const void* bias, int bias_dtype, void* y, int64_t rows,
+                       int64_t out_features, int64_t in_features, void* workspace, int64_t workspace_bytes,
+                       void* stream, void* start_event, void* stop_event);
+
+/* Name of the kernel w4g64_linear launches for this problem (for profiles
+ * and reports); never NULL. */
+const char* w4g64_linear_kernel_name(int64_t rows, int64_t out_features, int64_t in_features,
+                                     int x_dtype);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QWEN_INT4_HIP_W4G64_H */

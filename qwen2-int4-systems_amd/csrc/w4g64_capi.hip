@@ -1,0 +1,155 @@
+// C ABI of the W4G64 backend (declared in include/w4g64.h).
+//
+// Host-side validation mirrors the fail-closed checks of the reference's
+// GPU wrappers (src/qwen_int4/triton_kernels.py:128-139, :163-189,
+// :224-256) for what a C caller can get wrong: null pointers, dtypes,
+// dimensions, alignment and workspace size.  Tensor-level checks that need
+// framework metadata (device, contiguity, shapes) live in the Python layer.
+// Nothing is launched when a check fails.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "../../include/w4g64.h"
+#include "w4g64_device.h"
+#include "w4g64_internal.h"
+
+namespace {
+
+thread_local char g_error[512] = "";
+
+int fail(int status, const char* fmt, ...) {
+    va_list args;
+    va_start(args, fmt);
+    vsnprintf(g_error, sizeof(g_error), fmt, args);
+    va_end(args);
+    return status;
+}
+
+int ok() {
+    g_error[0] = '\0';
+    return W4G64_STATUS_OK;
+}
+
+bool aligned(const void* p, uintptr_t bytes) { return (((uintptr_t)p) & (bytes - 1)) == 0; }
+
+int element_bytes(int dtype) { return dtype == W4G64_DTYPE_F32 ? 4 : 2; }
+
+int hip_status(hipError_t err, const char* what) {
+    if (err != hipSuccess) return fail(W4G64_STATUS_HIP_ERROR, "%s launch failed: %s", what, hipGetErrorString(err));
+    return ok();
+}
+
+}  // namespace
+
+extern "C" {
+
+int w4g64_abi_version(void) { return 1; }
+
+const char* w4g64_last_error(void) { return g_error; }
+
+int w4g64_unpack_canonical_int4(const uint8_t* packed, int64_t packed_bytes, int8_t* out, int64_t elements,
+                                void* stream) {
+    if (packed_bytes < 0) return fail(W4G64_STATUS_INVALID_VALUE, "packed byte count must be non-negative");
+    if (elements < 0 || elements > 2 * packed_bytes)
+        return fail(W4G64_STATUS_INVALID_VALUE, "elements must be in [0, %lld], got %lld", (long long)(2 * packed_bytes),
+                    (long long)elements);
+    if (elements == 0) return ok();
+    if (!packed || !out) return fail(W4G64_STATUS_INVALID_VALUE, "packed and out must be non-null device pointers");
+    return hip_status(w4g64::launch_unpack(packed, out, elements, (hipStream_t)stream), "unpack");
+}
+
+int w4g64_dequantize_canonical(const uint8_t* qweight, const uint16_t* scales, const uint8_t* zeros, float* out,
+                               int64_t out_features, int64_t in_features, void* stream) {
+    if (out_features <= 0) return fail(W4G64_STATUS_INVALID_VALUE, "out_features must be a positive integer");
+    if (in_features <= 0 || in_features % 64)
+        return fail(W4G64_STATUS_INVALID_VALUE,
+                    "canonical W4G64 dequantization requires in_features divisible by 64, got %lld",
+                    (long long)in_features);
+    if (!qweight || !scales || !zeros || !out)
+        return fail(W4G64_STATUS_INVALID_VALUE, "qweight, scales, zeros and out must be non-null device pointers");
+    if (!aligned(qweight, 4)) return fail(W4G64_STATUS_INVALID_VALUE, "qweight must be 4-byte aligned");
+    if (!aligned(out, 16)) return fail(W4G64_STATUS_INVALID_VALUE, "out must be 16-byte aligned");
+    if (!aligned(scales, 2)) return fail(W4G64_STATUS_INVALID_VALUE, "scales must be 2-byte aligned");
+    return hip_status(w4g64::launch_dequant(qweight, scales, zeros, out, out_features, in_features,
+                                            (hipStream_t)stream),
+                      "dequantize");
+}
+
+int64_t w4g64_linear_workspace_bytes(int64_t rows, int64_t out_features, int64_t in_features, int x_dtype) {
+    if (rows <= 0 || out_features <= 0 || in_features <= 0 || in_features % 64) return 0;
+    if (x_dtype != W4G64_DTYPE_F16 && x_dtype != W4G64_DTYPE_BF16 && x_dtype != W4G64_DTYPE_F32) return 0;
+    if (rows > w4g64::kGemvMaxRows) return 0;
+    return w4g64::plan_gemv(rows, out_features, in_features, x_dtype).workspace_bytes;
+}
+
+const char* w4g64_linear_kernel_name(int64_t rows, int64_t out_features, int64_t in_features, int x_dtype) {
+    if (rows <= 0 || out_features <= 0 || in_features <= 0 || in_features % 64) return "none";
+    if (x_dtype != W4G64_DTYPE_F16 && x_dtype != W4G64_DTYPE_BF16 && x_dtype != W4G64_DTYPE_F32) return "none";
+    if (rows <= w4g64::kGemvMaxRows)
+        return w4g64::gemv_kernel_name(w4g64::plan_gemv(rows, out_features, in_features, x_dtype), x_dtype);
+    return w4g64::gemm_kernel_name(rows, out_features, in_features, x_dtype);
+}
+
+static int linear_impl(const void* x, int x_dtype, const uint8_t* qweight, const uint16_t* scales,
+                       const uint8_t* zeros, const void* bias, int bias_dtype, void* y, int64_t rows,
+                       int64_t out_features, int64_t in_features, void* workspace, int64_t workspace_bytes, void* stream, void* start_event, void* stop_event) {
+    if (x_dtype != W4G64_DTYPE_F16 && x_dtype != W4G64_DTYPE_BF16 && x_dtype != W4G64_DTYPE_F32)
+        return fail(W4G64_STATUS_INVALID_DTYPE, "activations must have dtype float16, bfloat16, or float32");
+    if (bias_dtype != W4G64_DTYPE_NONE && bias_dtype != W4G64_DTYPE_F16 && bias_dtype != W4G64_DTYPE_BF16 &&
+        bias_dtype != W4G64_DTYPE_F32)
+        return fail(W4G64_STATUS_INVALID_DTYPE, "bias must have dtype float16, bfloat16, or float32");
+    if ((bias_dtype == W4G64_DTYPE_NONE) != (bias == nullptr))
+        return fail(W4G64_STATUS_INVALID_VALUE, "bias pointer and bias dtype disagree");
+    if (rows <= 0 || in_features <= 0 || in_features % 64)
+        return fail(W4G64_STATUS_INVALID_VALUE,
+                    "activations require a positive W4G64-compatible feature dimension (rows=%lld, in_features=%lld)",
+                    (long long)rows, (long long)in_features);
+    if (out_features <= 0) return fail(W4G64_STATUS_INVALID_VALUE, "out_features must be a positive integer");
+    if (out_features > (1ll << 30) || in_features > (1ll << 30) || rows > (1ll << 30) ||
+        rows * in_features > (1ll << 40) || rows * out_features > (1ll << 40))
+        return fail(W4G64_STATUS_UNSUPPORTED, "problem size exceeds the supported index range");
+    if (!x || !qweight || !scales || !zeros || !y)
+        return fail(W4G64_STATUS_INVALID_VALUE, "x, qweight, scales, zeros and y must be non-null device pointers");
+    if (!aligned(x, 16) || !aligned(qweight, 16))
+        return fail(W4G64_STATUS_INVALID_VALUE, "x and qweight must be 16-byte aligned");
+    if (!aligned(y, (uintptr_t)element_bytes(x_dtype)) || !aligned(scales, 2))
+        return fail(W4G64_STATUS_INVALID_VALUE, "y and scales must be element aligned");
+    if (bias && !aligned(bias, (uintptr_t)element_bytes(bias_dtype)))
+        return fail(W4G64_STATUS_INVALID_VALUE, "bias must be element aligned");
+
+    w4g64::LinearProblem p{x, x_dtype, qweight, scales, zeros, bias, bias_dtype, y, rows, out_features, in_features};
+    hipStream_t s = (hipStream_t)stream;
+    if (rows <= w4g64::kGemvMaxRows) {
+        if (out_features > w4g64::kGemvMaxColumnBlocks * 64)
+            return fail(W4G64_STATUS_UNSUPPORTED, "decode path supports at most %lld output features",
+                        (long long)(w4g64::kGemvMaxColumnBlocks * 64));
+        const w4g64::GemvPlan plan = w4g64::plan_gemv(rows, out_features, in_features, x_dtype);
+        if (plan.workspace_bytes > 0) {
+            if (!workspace || workspace_bytes < plan.workspace_bytes)
+                return fail(W4G64_STATUS_WORKSPACE, "workspace of %lld bytes required, got %lld",
+                            (long long)plan.workspace_bytes, (long long)(workspace ? workspace_bytes : 0));
+            if (!aligned(workspace, 16)) return fail(W4G64_STATUS_WORKSPACE, "workspace must be 16-byte aligned");
+        }
+        return hip_status(w4g64::launch_gemv(p, plan, workspace, s, (hipEvent_t)start_event, (hipEvent_t)stop_event),
+                          "gemv");
+    }
+    return hip_status(w4g64::launch_gemm(p, s, (hipEvent_t)start_event, (hipEvent_t)stop_event), "gemm");
+}
+
+int w4g64_linear(const void* x, int x_dtype, const uint8_t* qweight, const uint16_t* scales, const uint8_t* zeros,
+                 const void* bias, int bias_dtype, void* y, int64_t rows, int64_t out_features, int64_t in_features,
+                 void* workspace, int64_t workspace_bytes, void* stream) {
+    return linear_impl(x, x_dtype, qweight, scales, zeros, bias, bias_dtype, y, rows, out_features, in_features,
+                       workspace, workspace_bytes, stream, nullptr, nullptr);
+}
+
+int w4g64_linear_timed(const void* x, int x_dtype, const uint8_t* qweight, const uint16_t* scales,
+                       const uint8_t* zeros, const void* bias, int bias_dtype, void* y, int64_t rows,
+                       int64_t out_features, int64_t in_features, void* workspace, int64_t workspace_bytes,
+                       void* stream, void* start_event, void* stop_event) {
+    return linear_impl(x, x_dtype, qweight, scales, zeros, bias, bias_dtype, y, rows, out_features, in_features,
+                       workspace, workspace_bytes, stream, start_event, stop_event);
+}
+
+}  // extern "C"

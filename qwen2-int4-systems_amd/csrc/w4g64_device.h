@@ -1,0 +1,135 @@
+// Device-side helpers shared by the W4G64 kernels (gfx950 only).
+//
+// Nibble decode.  A packed dword holds 8 consecutive K values; byte b holds
+// k = 2b (low nibble) and k = 2b+1 (high nibble).  XOR with 0x8 maps every
+// signed nibble s in [-8, 7] to n' = s + 8 in [0, 15].  OR-ing n' into the
+// mantissa of a power of two builds an exact small float:
+//   fp16 0x6400 | n'         = 1024 + n'   (n' in mantissa bits 0-3)
+//   fp16 0x5400 | (n' << 4)  =   64 + n'   (n' in mantissa bits 4-7)
+//   bf16 0x4300 | n'         =  128 + n'
+// Masks 0x000F000F / 0x00F000F0 on the dword and on the dword >> 8 give the
+// pairs (k0,k4), (k1,k5), (k2,k6), (k3,k7), so an 8-value MFMA operand is
+// ordered [k0 k4 k1 k5 k2 k6 k3 k7]; activations are staged in the same
+// order, which leaves every dot product unchanged.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace w4g64 {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+typedef float float16v __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+enum XKind : int { kF16 = 1, kBF16 = 2, kF32 = 3 };
+
+// Slot order of the 8 values in an MFMA operand: slot p holds k = kSlotK[p].
+// (Used by host-side documentation/tests; kernels permute with v_perm.)
+
+__device__ __forceinline__ uint32_t nib_pair(uint32_t w, uint32_t mask, uint32_t magic) {
+    return ((w ^ 0x88888888u) & mask) | magic;
+}
+
+// Exact signed (code - zero) as fp16, slot order [k0 k4 k1 k5 k2 k6 k3 k7].
+// c_lo = 1032 + zero, c_hi = 72 + zero (both exact in fp16).
+__device__ __forceinline__ half8 dequant8_f16_int(uint32_t w, half2v c_lo, half2v c_hi) {
+    half2v h0 = __builtin_bit_cast(half2v, nib_pair(w, 0x000F000Fu, 0x64006400u)) - c_lo;
+    half2v h1 = __builtin_bit_cast(half2v, nib_pair(w, 0x00F000F0u, 0x54005400u)) - c_hi;
+    half2v h2 = __builtin_bit_cast(half2v, nib_pair(w >> 8, 0x000F000Fu, 0x64006400u)) - c_lo;
+    half2v h3 = __builtin_bit_cast(half2v, nib_pair(w >> 8, 0x00F000F0u, 0x54005400u)) - c_hi;
+    half8 r = {h0[0], h0[1], h1[0], h1[1], h2[0], h2[1], h3[0], h3[1]};
+    return r;
+}
+
+// bf16 values 128 + n' (exact), slot order [k0 k4 k1 k5 k2 k6 k3 k7].
+// The caller subtracts (136 + zero) * sum(x) from the fp32 dot product.
+__device__ __forceinline__ bf16x8 dequant8_bf16_biased(uint32_t w) {
+    u32x4 v;
+    v[0] = nib_pair(w, 0x000F000Fu, 0x43004300u);
+    v[1] = nib_pair(w >> 4, 0x000F000Fu, 0x43004300u);
+    v[2] = nib_pair(w >> 8, 0x000F000Fu, 0x43004300u);
+    v[3] = nib_pair(w >> 12, 0x000F000Fu, 0x43004300u);
+    return __builtin_bit_cast(bf16x8, v);
+}
+
+// Signed INT4 nibble e of a packed byte array (canonical order).
+__device__ __forceinline__ int nibble_at(const uint8_t* p, int64_t e) {
+    int b = p[e >> 1];
+    int n = (e & 1) ? (b >> 4) : (b & 0xF);
+    return n - ((n & 8) << 1);
+}
+
+// Permute 8 consecutive 16-bit values (as 4 dwords) into slot order.
+__device__ __forceinline__ u32x4 permute_slots(u32x4 d) {
+    u32x4 o;
+    o[0] = __builtin_amdgcn_perm(d[2], d[0], 0x05040100u);  // (x0, x4)
+    o[1] = __builtin_amdgcn_perm(d[2], d[0], 0x07060302u);  // (x1, x5)
+    o[2] = __builtin_amdgcn_perm(d[3], d[1], 0x05040100u);  // (x2, x6)
+    o[3] = __builtin_amdgcn_perm(d[3], d[1], 0x07060302u);  // (x3, x7)
+    return o;
+}
+
+__device__ __forceinline__ float bf16_bits_to_float(uint32_t b) {
+    return __builtin_bit_cast(float, b << 16);
+}
+
+__device__ __forceinline__ float half_bits_to_float(uint16_t h) {
+    return (float)__builtin_bit_cast(_Float16, h);
+}
+
+// Round-to-nearest-even conversions used for outputs.
+__device__ __forceinline__ uint16_t float_to_half_bits(float f) {
+    return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+__device__ __forceinline__ uint16_t float_to_bf16_bits(float f) {
+    return __builtin_bit_cast(uint16_t, (__bf16)f);
+}
+
+// Exact three-way split of an fp32 value into bf16 parts (hi + mid + lo == x
+// for every normal x whose parts stay normal), by truncation.
+__device__ __forceinline__ void split3_bf16(float x, uint16_t& hi, uint16_t& mid, uint16_t& lo) {
+    uint32_t xb = __builtin_bit_cast(uint32_t, x);
+    uint32_t hb = xb & 0xFFFF0000u;
+    float r1 = x - __builtin_bit_cast(float, hb);
+    uint32_t r1b = __builtin_bit_cast(uint32_t, r1);
+    uint32_t mb = r1b & 0xFFFF0000u;
+    float r2 = r1 - __builtin_bit_cast(float, mb);
+    hi = (uint16_t)(hb >> 16);
+    mid = (uint16_t)(mb >> 16);
+    lo = (uint16_t)(__builtin_bit_cast(uint32_t, r2) >> 16);
+}
+
+// Two-way split for the GEMM (16 significant bits; the bf16 weight tile
+// carries 8): hi by truncation, lo rounded.
+__device__ __forceinline__ void split2_bf16(float x, uint16_t& hi, uint16_t& lo) {
+    uint32_t xb = __builtin_bit_cast(uint32_t, x);
+    uint32_t hb = xb & 0xFFFF0000u;
+    float r1 = x - __builtin_bit_cast(float, hb);
+    hi = (uint16_t)(hb >> 16);
+    lo = float_to_bf16_bits(r1);
+}
+
+__device__ __forceinline__ float load_bias(const void* bias, int kind, int64_t n) {
+    if (kind == kF16) return half_bits_to_float(((const uint16_t*)bias)[n]);
+    if (kind == kBF16) return bf16_bits_to_float(((const uint16_t*)bias)[n]);
+    if (kind == kF32) return ((const float*)bias)[n];
+    return 0.0f;
+}
+
+template <int XK>
+__device__ __forceinline__ void store_out(void* y, int64_t idx, float v) {
+    if constexpr (XK == kF16) {
+        ((uint16_t*)y)[idx] = float_to_half_bits(v);
+    } else if constexpr (XK == kBF16) {
+        ((uint16_t*)y)[idx] = float_to_bf16_bits(v);
+    } else {
+        ((float*)y)[idx] = v;
+    }
+}
+
+}  // namespace w4g64

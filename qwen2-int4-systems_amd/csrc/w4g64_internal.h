@@ -1,0 +1,71 @@
+// Internal launch interface between the C ABI (w4g64_capi.hip) and the
+// kernel translation units.  Host code only; arguments are already validated.
+#pragma once
+
+#include <hip/hip_ext.h>
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace w4g64 {
+
+struct LinearProblem {
+    const void* x;
+    int x_kind;  // XKind
+    const uint8_t* qweight;
+    const uint16_t* scales;
+    const uint8_t* zeros;
+    const void* bias;
+    int bias_kind;  // 0 none, else XKind
+    void* y;
+    int64_t rows;
+    int64_t out_features;
+    int64_t in_features;
+};
+
+// Decode GEMV (rows <= kGemvMaxRows).
+constexpr int kGemvMaxRows = 16;
+// Workspace layout of every split-K GEMV call: a fixed counter area (one
+// 32-bit arrival counter per 64-column block, zero between calls) followed by
+// the fp32 partial sums.  The counter area has the same offset and size for
+// every shape, so calls with different shapes can share one workspace without
+// their partial sums ever landing on another shape's counters.
+constexpr int64_t kGemvCounterBytes = 64 * 1024;
+constexpr int64_t kGemvMaxColumnBlocks = kGemvCounterBytes / 4;  // 1,048,576 output features
+struct GemvPlan {
+    int n_blocks;          // column blocks of 64 output features
+    int splits;            // K splits across workgroups
+    int groups_per_split;  // 64-wide K groups per split
+    int tiles;             // 16-row MFMA A tiles (fp32 input uses 3 bf16 parts per row)
+    int64_t lds_bytes;     // dynamic LDS per workgroup
+    int64_t workspace_bytes;
+    int64_t counter_bytes;
+};
+GemvPlan plan_gemv(int64_t rows, int64_t out_features, int64_t in_features, int x_kind);
+hipError_t launch_gemv(const LinearProblem& p, const GemvPlan& plan, void* workspace, hipStream_t stream,
+                       hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
+const char* gemv_kernel_name(const GemvPlan& plan, int x_kind);
+
+// Prefill GEMM (rows > kGemvMaxRows).
+hipError_t launch_gemm(const LinearProblem& p, hipStream_t stream, hipEvent_t start = nullptr,
+                       hipEvent_t stop = nullptr);
+const char* gemm_kernel_name(int64_t rows, int64_t out_features, int64_t in_features, int x_kind);
+
+// Launch a kernel; with events, hipExtLaunchKernelGGL records them at the
+// kernel's own start and end (what a profiler reports as its duration).
+template <typename F, typename... Args>
+hipError_t launch_kernel(F kernel, dim3 grid, dim3 block, size_t lds, hipStream_t stream, hipEvent_t start,
+                         hipEvent_t stop, Args... args) {
+    if (start || stop) {
+        hipExtLaunchKernelGGL(kernel, grid, block, (uint32_t)lds, stream, start, stop, 0, args...);
+    } else {
+        hipLaunchKernelGGL(kernel, grid, block, lds, stream, args...);
+    }
+    return hipGetLastError();
+}
+
+// Primitives.
+hipError_t launch_unpack(const uint8_t* packed, int8_t* out, int64_t elements, hipStream_t stream);
+hipError_t launch_dequant(const uint8_t* qweight, const uint16_t* scales, const uint8_t* zeros, float* out,
+                          int64_t out_features, int64_t in_features, hipStream_t stream);
+
+}  // namespace w4g64

@@ -1,0 +1,78 @@
+"""ctypes binding of ``libw4g64_hip.so`` (C ABI declared in include/w4g64.h).
+
+The library is loaded from the package directory only.  If it is missing the
+HIP backend is unavailable and every entry point raises -- there is no other
+implementation to fall back to.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+LIBRARY_PATH = Path(__file__).resolve().parent / "libw4g64_hip.so"
+
+STATUS_OK = 0
+STATUS_INVALID_VALUE = 1
+STATUS_INVALID_DTYPE = 2
+STATUS_WORKSPACE = 3
+STATUS_UNSUPPORTED = 4
+STATUS_HIP_ERROR = 5
+
+DTYPE_NONE = 0
+DTYPE_F16 = 1
+DTYPE_BF16 = 2
+DTYPE_F32 = 3
+
+# (name, restype, argtypes) for every symbol include/w4g64.h declares.
+_p, _i64, _int = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+SIGNATURES = {
+    "w4g64_abi_version": (_int, []),
+    "w4g64_last_error": (ctypes.c_char_p, []),
+    "w4g64_unpack_canonical_int4": (_int, [_p, _i64, _p, _i64, _p]),
+    "w4g64_dequantize_canonical": (_int, [_p, _p, _p, _p, _i64, _i64, _p]),
+    "w4g64_linear_workspace_bytes": (_i64, [_i64, _i64, _i64, _int]),
+    "w4g64_linear": (_int, [_p, _int, _p, _p, _p, _p, _int, _p, _i64, _i64, _i64, _p, _i64, _p]),
+    "w4g64_linear_timed": (_int, [_p, _int, _p, _p, _p, _p, _int, _p, _i64, _i64, _i64, _p, _i64, _p, _p, _p]),
+    "w4g64_linear_kernel_name": (ctypes.c_char_p, [_i64, _i64, _i64, _int]),
+}
+
+_lock = threading.Lock()
+_library: ctypes.CDLL | None = None
+
+
+def library_built() -> bool:
+    return LIBRARY_PATH.exists()
+
+
+def load() -> ctypes.CDLL:
+    """Load (once) and return the library; raises RuntimeError if not built."""
+    global _library
+    if _library is not None:
+        return _library
+    with _lock:
+        if _library is None:
+            if not LIBRARY_PATH.exists():
+                raise RuntimeError(
+                    f"HIP W4G64 library is not built ({LIBRARY_PATH}); run __graft_entry__.build()"
+                )
+            lib = ctypes.CDLL(str(LIBRARY_PATH))
+            for name, (restype, argtypes) in SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype = restype
+                fn.argtypes = argtypes
+            _library = lib
+    return _library
+
+
+def check(status: int) -> None:
+    """Raise the reference's exception type for a non-zero C status."""
+    if status == STATUS_OK:
+        return
+    message = (load().w4g64_last_error() or b"").decode("utf-8", "replace")
+    if status == STATUS_INVALID_DTYPE:
+        raise TypeError(message)
+    if status in (STATUS_INVALID_VALUE, STATUS_WORKSPACE):
+        raise ValueError(message)
+    raise RuntimeError(message)

@@ -1,0 +1,178 @@
+"""CPU-side checks of the C ABI library and the host-side contract.
+
+No GPU compute happens here: the library is loaded and every symbol the
+header declares is resolved; the C layer's argument validation (which runs
+before any launch) is exercised with null/misaligned pointers; the Python
+layer's fail-closed validation mirrors the reference's rejection tests
+(tests/test_backends.py:140-270, tests/test_triton_unpack.py:49-56, :75-90,
+:122-130) on CPU tensors.
+"""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from qwen_int4_hip import _lib
+from qwen_int4_hip.backends import SUPPORTED_BACKENDS, validate_canonical_w4g64_inputs
+from qwen_int4_hip.linear import QuantLinear
+from qwen_int4_hip.quantization import PackingFormat
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "w4g64.h"
+
+pytestmark = pytest.mark.skipif(not _lib.library_built(), reason="HIP library not built (run __graft_entry__.build())")
+
+
+def _declared_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(w4g64_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    declared = _declared_functions()
+    assert declared, "no declarations parsed from include/w4g64.h"
+    for name in declared:
+        assert hasattr(lib, name), f"{name} declared in w4g64.h but not exported"
+    assert set(declared) == set(_lib.SIGNATURES), "ctypes signatures out of sync with the header"
+    assert lib.w4g64_abi_version() == 1
+
+
+def test_c_layer_rejects_before_launch():
+    lib = _lib.load()
+    null = None
+    buf = ctypes.create_string_buffer(64)
+    p = ctypes.c_void_p(ctypes.addressof(buf))
+    # bad activation dtype
+    assert lib.w4g64_linear(p, 9, p, p, p, null, 0, p, 1, 64, 64, null, 0, null) == _lib.STATUS_INVALID_DTYPE
+    assert b"dtype" in lib.w4g64_last_error()
+    # in_features not a multiple of 64
+    assert lib.w4g64_linear(p, 1, p, p, p, null, 0, p, 1, 64, 96, null, 0, null) == _lib.STATUS_INVALID_VALUE
+    assert b"W4G64" in lib.w4g64_last_error()
+    # null pointers
+    assert lib.w4g64_linear(null, 1, p, p, p, null, 0, p, 1, 64, 64, null, 0, null) == _lib.STATUS_INVALID_VALUE
+    # bias pointer without a bias dtype
+    assert lib.w4g64_linear(p, 1, p, p, p, p, 0, p, 1, 64, 64, null, 0, null) == _lib.STATUS_INVALID_VALUE
+    # misaligned activations
+    odd = ctypes.c_void_p(ctypes.addressof(buf) | 1)
+    assert lib.w4g64_linear(odd, 1, p, p, p, null, 0, p, 1, 64, 64, null, 0, null) == _lib.STATUS_INVALID_VALUE
+    assert b"aligned" in lib.w4g64_last_error()
+    # unpack element range
+    assert lib.w4g64_unpack_canonical_int4(p, 4, p, 9, null) == _lib.STATUS_INVALID_VALUE
+    assert b"elements" in lib.w4g64_last_error()
+    assert lib.w4g64_unpack_canonical_int4(p, 4, p, 0, null) == _lib.STATUS_OK
+    # dequant K not divisible by 64
+    assert lib.w4g64_dequantize_canonical(p, p, p, p, 1, 96, null) == _lib.STATUS_INVALID_VALUE
+    assert b"divisible" in lib.w4g64_last_error()
+
+
+def test_workspace_and_kernel_plan_queries():
+    lib = _lib.load()
+    # decode shapes that split K need a workspace; the GEMM path needs none
+    assert lib.w4g64_linear_workspace_bytes(1, 1536, 8960, _lib.DTYPE_F16) > 0
+    assert lib.w4g64_linear_workspace_bytes(2048, 8960, 1536, _lib.DTYPE_BF16) == 0
+    assert lib.w4g64_linear_workspace_bytes(1, 1536, 100, _lib.DTYPE_F16) == 0
+    assert lib.w4g64_linear_kernel_name(1, 8960, 1536, _lib.DTYPE_F16).startswith(b"gemv_kernel<f16")
+    assert lib.w4g64_linear_kernel_name(2048, 8960, 1536, _lib.DTYPE_BF16).startswith(b"gemm_kernel<bf16")
+    assert lib.w4g64_linear_kernel_name(1, 8960, 1536, 7) == b"none"
+
+
+def test_status_mapping_uses_reference_exception_types():
+    lib = _lib.load()
+    lib.w4g64_linear(None, 9, None, None, None, None, 0, None, 1, 64, 64, None, 0, None)
+    with pytest.raises(TypeError, match="dtype"):
+        _lib.check(_lib.STATUS_INVALID_DTYPE)
+    with pytest.raises(ValueError):
+        _lib.check(_lib.STATUS_INVALID_VALUE)
+    with pytest.raises(RuntimeError):
+        _lib.check(_lib.STATUS_HIP_ERROR)
+
+
+# ---- Python layer: fail-closed contract checks (CPU tensors suffice) -------
+
+def _tensors(out_features=6, in_features=128):
+    groups = in_features // 64
+    return (
+        torch.zeros(out_features * in_features // 2, 1, dtype=torch.uint8),
+        torch.ones(out_features, groups, dtype=torch.float16),
+        torch.zeros((out_features * groups + 1) // 2, 1, dtype=torch.uint8),
+    )
+
+
+def _validate(x, q, s, z, b=None, **over):
+    args = dict(out_features=6, in_features=128, group_size=64, packing=PackingFormat.CANONICAL)
+    args.update(over)
+    return validate_canonical_w4g64_inputs(x, q, s, z, b, **args)
+
+
+@pytest.mark.parametrize(
+    ("override", "error", "message"),
+    [
+        ({"group_size": 128}, ValueError, "W4G64"),
+        ({"packing": PackingFormat.LEGACY_SIGNED_ADD}, ValueError, "canonical INT4 packing"),
+        ({"in_features": 64}, ValueError, "activation feature dimension"),
+    ],
+)
+def test_rejects_incompatible_mapping(override, error, message):
+    q, s, z = _tensors()
+    with pytest.raises(error, match=message):
+        _validate(torch.ones(1, 128, dtype=torch.bfloat16), q, s, z, **override)
+
+
+@pytest.mark.parametrize("target", ["qweight", "scales", "zeros", "bias"])
+def test_rejects_inconsistent_tensor_shapes(target):
+    q, s, z = _tensors()
+    tensors = {"qweight": q, "scales": s, "zeros": z, "bias": torch.zeros(6, dtype=torch.bfloat16)}
+    tensors[target] = tensors[target][:-1]
+    with pytest.raises(ValueError, match=target):
+        _validate(torch.ones(1, 128, dtype=torch.bfloat16), tensors["qweight"], tensors["scales"],
+                  tensors["zeros"], tensors["bias"])
+
+
+@pytest.mark.parametrize(
+    ("mutation", "error", "message"),
+    [
+        ("qweight_dtype", TypeError, "uint8"),
+        ("zeros_dtype", TypeError, "uint8"),
+        ("scales_dtype", TypeError, "FP16"),
+        ("nonfinite_scale", ValueError, "finite"),
+        ("nonpositive_scale", ValueError, "positive"),
+        ("activation_dtype", TypeError, "FP16, BF16, or FP32"),
+    ],
+)
+def test_rejects_malformed_metadata(mutation, error, message):
+    q, s, z = _tensors()
+    x = torch.ones(1, 128, dtype=torch.bfloat16)
+    if mutation == "qweight_dtype":
+        q = q.to(torch.int8)
+    elif mutation == "zeros_dtype":
+        z = z.to(torch.int8)
+    elif mutation == "scales_dtype":
+        s = s.to(torch.float32)
+    elif mutation == "nonfinite_scale":
+        s[0, 0] = float("nan")
+    elif mutation == "nonpositive_scale":
+        s[0, 0] = 0
+    elif mutation == "activation_dtype":
+        x = x.to(torch.float64)
+    with pytest.raises(error, match=message):
+        _validate(x, q, s, z)
+
+
+def test_unknown_backend_is_rejected_and_registry_is_explicit():
+    # tests/test_backends.py:140-143
+    layer = QuantLinear(8, 4, group_size=4)
+    with pytest.raises(ValueError):
+        layer.set_backend("environment-variable-magic")
+    assert SUPPORTED_BACKENDS == ("hip",)
+    assert layer.qweight.shape == (16, 1) and layer.scales.shape == (4, 2) and layer.zeros.shape == (4, 1)
+    assert QuantLinear(128, 6, group_size=64, bias=True).bias.dtype == torch.bfloat16
+
+
+@pytest.mark.skipif(torch.cuda.is_available(), reason="checks the no-GPU failure mode")
+def test_hip_backend_fails_loudly_without_gpu():
+    layer = QuantLinear(128, 64, group_size=64, packing=PackingFormat.CANONICAL)
+    with pytest.raises(RuntimeError, match="HIP backend requires"):
+        layer(torch.zeros(1, 128, dtype=torch.float16))
