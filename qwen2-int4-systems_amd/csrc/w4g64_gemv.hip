@@ -5,36 +5,49 @@
 // (src/qwen_int4/backends.py:73-98) with the group scale applied once per
 // 64-wide group in fp32.
 //
-// Mapping (one workgroup = 4 waves = 64 output features x one K split):
-//   * each wave owns 16 consecutive output features n (MFMA B columns);
-//     lane (n = lane % 16, q = lane / 16) loads 8 packed bytes per group
-//     (q selects the 16-value quarter of the 64-value group), so a wave
-//     instruction fetches 16 rows x 32 contiguous bytes;
-//   * v_mfma_f32_16x16x32_{f16,bf16}: A = activations (16 rows, zero padded),
-//     B = exact small-integer weights, two MFMAs per group;
-//   * fp16 activations: B = (code - zero) built exactly with the 1024+n'
-//     magic and one v_pk_add_f16 per pair; group scale applied to the MFMA
-//     result in fp32;
-//   * bf16 activations: B = 128 + n' (exact in bf16); the per-group result is
-//     corrected by -(136 + zero) * sum_k x[m,k] before scaling;
-//   * fp32 activations: each row is split exactly into three bf16 parts
-//     (hi + mid + lo == x) that occupy three "virtual" A rows; the bf16 path
-//     runs on them and the parts are summed in fp32.
-//   * all weight loads of the wave's K range are issued before any math so
-//     the whole split is in flight at once (HBM latency hiding by MLP).
-//   * K splits across workgroups write fp32 partials to the workspace; the
-//     last workgroup to arrive for a 64-column block (per-block atomic
-//     counter) sums them in split order -- deterministic -- adds the bias,
-//     converts and stores, then resets the counter to zero.
+// MFMA mapping (v_mfma_f32_16x16x32_{f16,bf16}, two per 64-wide group):
+//   * B columns j = (row r, segment s), r < 16/SW, s < SW: a wave covers
+//     16/SW output features over the workgroup's K range, which is cut into SW
+//     segments taking the range's groups round robin (segment s takes groups
+//     g0 + s, g0 + s + SW, ...).  Lane (j = lane % 16, q = lane / 16) loads
+//     8 packed bytes per group (the 16-value quarter q of the group), so one
+//     wave load instruction reads SW consecutive groups of each of its rows.
+//   * A rows i = (virtual activation row m, segment s), i = m * SW + s.  Only
+//     the block diagonal of D (segment of row i == segment of column j) is
+//     used: at M <= 16 the matrix core has far more throughput than the HBM
+//     stream needs, so the off-diagonal products are free, and they let one
+//     wave own as little as one output feature -- enough workgroups to fill
+//     the chip without reducing across workgroups.
+//   * fp16 activations: B = (code - zero) exact, built with the 1024+n' magic
+//     and one v_pk_add_f16 per pair; the group scale multiplies the MFMA
+//     result in fp32.
+//   * bf16 activations: B = 128 + n' (exact in bf16); the group result is
+//     corrected by -(136 + zero) * sum_{k in g} x[m,k] before scaling.
+//   * fp32 activations: every row is split exactly into three bf16 parts
+//     (hi + mid + lo == x) that form three virtual rows; the bf16 path runs
+//     on them and the parts are summed in fp32.
+//   * every weight, scale and zero load of the lane is issued before the
+//     activations are staged, so the workgroup's whole weight slice is in
+//     flight at once.
+//   * optional K split across workgroups (only for many rows x few output
+//     features): partial sums go through device-coherent (sc1) stores; the
+//     last workgroup to arrive for a column block, known from a per-block
+//     atomic counter, adds them in split order (deterministic), adds the
+//     bias, stores the output and re-zeroes the counter.
+#include <stdio.h>
+
 #include "w4g64_device.h"
 #include "w4g64_internal.h"
 
 namespace w4g64 {
 namespace {
 
-constexpr int kWaves = 4;
-constexpr int kBlockCols = kWaves * 16;       // output features per workgroup
-constexpr int kMaxGroupsPerSplit = 12;        // 768 K values per split
+constexpr int kWaves = 4;          // compute waves; one more wave stages the activations
+constexpr int kThreads = (kWaves + 1) * 64;
+constexpr int kMaxSteps = 16;      // group steps per lane in one workgroup
+constexpr int kStepBuckets[] = {2, 3, 6, 9, 12, 16};
+
+typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
 
 struct GemvArgs {
     const void* x;
@@ -44,22 +57,24 @@ struct GemvArgs {
     const void* bias;
     int bias_kind;
     void* y;
-    int M;      // activation rows
-    int N;      // out_features
-    int K;      // in_features
-    int G;      // K / 64
-    int gps;    // groups per split
-    int splits;
-    int mv;     // virtual A rows (M, or 3M for fp32 input)
+    int M;       // activation rows
+    int N;       // out_features
+    int K;       // in_features
+    int G;       // K / 64
+    int gps;     // groups per K split
+    int splits;  // K splits across workgroups
+    int mv;      // virtual A rows (M, or 3M for fp32 input)
     float* partials;     // [splits][M][N]
-    unsigned* counters;  // [n_blocks]
+    unsigned* counters;  // [column blocks]
 };
 
-template <int XK, int TILES>
-__global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
+template <int XK, int SW, int STEPS, int TILES>
+__global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     __shared__ int s_last;
     constexpr int kParts = (XK == kF32) ? 3 : 1;
+    constexpr int R = 16 / SW;              // output features per wave
+    constexpr int kBlockCols = kWaves * R;  // output features per workgroup
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -67,156 +82,162 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     const int nb = blockIdx.x;
     const int split = blockIdx.y;
     const int g0 = split * a.gps;
-    const int cnt = min(a.gps, a.G - g0);
-    const int kbase = g0 * 64;
-    const int row_stride = a.gps * 64 + 8;    // 16-bit elements, +16 B pad per row
-    uint16_t* xs = (uint16_t*)smem;           // [mv][row_stride], slot-permuted
-    float* sx = (float*)(smem + (size_t)a.mv * row_stride * 2);  // [gps][mv] group sums
+    const int cnt = min(a.gps, a.G - g0);  // groups in this workgroup's K range
+    const int row_stride = a.gps * 64 + 8;  // 16-bit elements per staged row (+16 B pad)
+    uint16_t* xs = (uint16_t*)smem;         // [mv][row_stride], slot order
+    float* sx = (float*)(smem + (size_t)a.mv * row_stride * 2);  // [mv][gps] group sums (bf16/fp32)
 
-    // ---- weights of this lane: issue every load of the split up front ----
-    const int n = nb * kBlockCols + wave * 16 + (lane & 15);
+    // ---- this lane's column: output feature n, segment sj ----
+    const int j = lane & 15;
     const int q = lane >> 4;
+    const int rj = j / SW;
+    const int sj = j % SW;
+    const int n = nb * kBlockCols + wave * R + rj;
     const bool nvalid = n < a.N;
-    u32x2 wq[kMaxGroupsPerSplit];
-    float sc[kMaxGroupsPerSplit];
-    int zr[kMaxGroupsPerSplit];
-    // Branch-free: out-of-range rows/groups read row 0 / group 0 of the
-    // split (always valid) and are zeroed afterwards, so every load of the
-    // split is issued back to back.
     const int nrow = nvalid ? n : 0;
-    const uint8_t* wrow = a.qweight + (int64_t)nrow * (a.K / 2) + (int64_t)g0 * 32 + 8 * q;
-    const int64_t sbase = (int64_t)nrow * a.G + g0;
-#pragma unroll
-    for (int j = 0; j < kMaxGroupsPerSplit; ++j) {
-        const int jj = j < cnt ? j : 0;
-        wq[j] = __builtin_nontemporal_load((const u32x2*)(wrow + 32 * jj));
-    }
-#pragma unroll
-    for (int j = 0; j < kMaxGroupsPerSplit; ++j) {
-        const int jj = j < cnt ? j : 0;
-        sc[j] = half_bits_to_float(a.scales[sbase + jj]);
-        zr[j] = nibble_at(a.zeros, sbase + jj);
-    }
-    if (!nvalid) {
-#pragma unroll
-        for (int j = 0; j < kMaxGroupsPerSplit; ++j) {
-            wq[j] = u32x2{0u, 0u};
-            sc[j] = 0.0f;
-            zr[j] = 0;
-        }
-    }
+    u32x2 wq[STEPS];
+    float sc[STEPS];
+    int zr[STEPS];
+    const uint8_t* wrow = a.qweight + (int64_t)nrow * (a.K / 2) + 8 * q;
+    const int64_t sbase = (int64_t)nrow * a.G;
 
-    // ---- stage this split's activations in LDS (slot order) ----
-    const int items_per_row = cnt * 8;  // 8 values per item
-    for (int it = tid; it < a.M * items_per_row; it += 256) {
-        const int m = it / items_per_row;
-        const int c = it - m * items_per_row;
-        if constexpr (XK != kF32) {
-            const u32x4 v = *(const u32x4*)((const uint16_t*)a.x + (int64_t)m * a.K + kbase + 8 * c);
-            *(u32x4*)(xs + m * row_stride + 8 * c) = permute_slots(v);
-        } else {
-            const float* src = (const float*)a.x + (int64_t)m * a.K + kbase + 8 * c;
-            const float4v f0 = *(const float4v*)src;
-            const float4v f1 = *(const float4v*)(src + 4);
-            uint16_t hi[8], mid[8], lo[8];
+    if (wave < kWaves) {
+        // ---- compute waves: issue every weight / scale / zero load, step by step ----
+        // Unconditional loads (steps past the K range re-read group g0 and get a
+        // zero scale), interleaved so that step t is complete once the lane's
+        // first 3 (t + 1) loads have returned.
 #pragma unroll
-            for (int j = 0; j < 8; ++j) split3_bf16(j < 4 ? f0[j] : f1[j - 4], hi[j], mid[j], lo[j]);
-            u32x4 ph, pm, pl;
+        for (int t = 0; t < STEPS; ++t) {
+            const int gl = sj + SW * t;
+            const int g = gl < cnt ? g0 + gl : g0;
+            wq[t] = __builtin_nontemporal_load((const u32x2*)(wrow + (int64_t)g * 32));
+            sc[t] = half_bits_to_float(a.scales[sbase + g]);
+            zr[t] = nibble_at(a.zeros, sbase + g);
+        }
+    } else {
+        // ---- staging wave: this workgroup's activations into LDS (slot order) ----
+        const int kbase = g0 * 64;
+        const int items_per_row = cnt * 8;  // 8 values per item
+        for (int it = lane; it < a.M * items_per_row; it += 64) {
+            const int m = it / items_per_row;
+            const int c = it - m * items_per_row;
+            if constexpr (XK != kF32) {
+                const u32x4 v = *(const u32x4*)((const uint16_t*)a.x + (int64_t)m * a.K + kbase + 8 * c);
+                *(u32x4*)(xs + m * row_stride + 8 * c) = permute_slots(v);
+            } else {
+                const float* src = (const float*)a.x + (int64_t)m * a.K + kbase + 8 * c;
+                const float4v f0 = *(const float4v*)src;
+                const float4v f1 = *(const float4v*)(src + 4);
+                uint16_t hi[8], mid[8], lo[8];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                ph[j] = (uint32_t)hi[2 * j] | ((uint32_t)hi[2 * j + 1] << 16);
-                pm[j] = (uint32_t)mid[2 * j] | ((uint32_t)mid[2 * j + 1] << 16);
-                pl[j] = (uint32_t)lo[2 * j] | ((uint32_t)lo[2 * j + 1] << 16);
+                for (int e = 0; e < 8; ++e) split3_bf16(e < 4 ? f0[e] : f1[e - 4], hi[e], mid[e], lo[e]);
+                u32x4 ph, pm, pl;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    ph[e] = (uint32_t)hi[2 * e] | ((uint32_t)hi[2 * e + 1] << 16);
+                    pm[e] = (uint32_t)mid[2 * e] | ((uint32_t)mid[2 * e + 1] << 16);
+                    pl[e] = (uint32_t)lo[2 * e] | ((uint32_t)lo[2 * e + 1] << 16);
+                }
+                *(u32x4*)(xs + m * row_stride + 8 * c) = permute_slots(ph);
+                *(u32x4*)(xs + (a.M + m) * row_stride + 8 * c) = permute_slots(pm);
+                *(u32x4*)(xs + (2 * a.M + m) * row_stride + 8 * c) = permute_slots(pl);
             }
-            *(u32x4*)(xs + m * row_stride + 8 * c) = permute_slots(ph);
-            *(u32x4*)(xs + (a.M + m) * row_stride + 8 * c) = permute_slots(pm);
-            *(u32x4*)(xs + (2 * a.M + m) * row_stride + 8 * c) = permute_slots(pl);
+        }
+        if constexpr (XK != kF16) {
+            // group sums of every staged row (this wave's own LDS writes are ordered before its reads)
+            for (int idx = lane; idx < cnt * a.mv; idx += 64) {
+                const int r = idx / cnt;
+                const int gl = idx - r * cnt;
+                const uint16_t* src = xs + r * row_stride + 64 * gl;
+                float s = 0.0f;
+                for (int k = 0; k < 64; ++k) s += bf16_bits_to_float(src[k]);
+                sx[r * a.gps + gl] = s;
+            }
         }
     }
     __syncthreads();
-    if constexpr (XK != kF16) {
-        for (int idx = tid; idx < cnt * a.mv; idx += 256) {
-            const int j = idx / a.mv;
-            const int r = idx - j * a.mv;
-            const uint16_t* src = xs + r * row_stride + 64 * j;
-            float s = 0.0f;
-            for (int k = 0; k < 64; ++k) s += bf16_bits_to_float(src[k]);
-            sx[j * a.mv + r] = s;
-        }
-        __syncthreads();
-    }
 
-    // ---- MFMA over the split ----
+    // ---- MFMA over the group steps (compute waves) ----
     float4v acc[TILES];
 #pragma unroll
-    for (int t = 0; t < TILES; ++t) acc[t] = float4v{0.f, 0.f, 0.f, 0.f};
+    for (int tt = 0; tt < TILES; ++tt) acc[tt] = float4v{0.f, 0.f, 0.f, 0.f};
 
+    if (wave < kWaves) {
 #pragma unroll
-    for (int j = 0; j < kMaxGroupsPerSplit; ++j) {
-        if (j < cnt) {
-            if constexpr (XK == kF16) {
-                const _Float16 zl = (_Float16)(1032 + zr[j]);
-                const _Float16 zh = (_Float16)(72 + zr[j]);
-                const half8 b0 = dequant8_f16_int(wq[j][0], half2v{zl, zl}, half2v{zh, zh});
-                const half8 b1 = dequant8_f16_int(wq[j][1], half2v{zl, zl}, half2v{zh, zh});
+    for (int t = 0; t < STEPS; ++t) {
+        {
+            const float scale = (nvalid && sj + SW * t < cnt) ? sc[t] : 0.0f;  // zero: no contribution
 #pragma unroll
-                for (int t = 0; t < TILES; ++t) {
-                    const int row = 16 * t + (lane & 15);
-                    half8 a0 = {}, a1 = {};
-                    if (row < a.mv) {
-                        const uint16_t* src = xs + row * row_stride + 64 * j + 16 * q;
-                        a0 = *(const half8*)src;
-                        a1 = *(const half8*)(src + 8);
-                    }
-                    float4v d = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, b0, float4v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                    d = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b1, d, 0, 0, 0);
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) acc[t][r] = fmaf(sc[j], d[r], acc[t][r]);
+            for (int tt = 0; tt < TILES; ++tt) {
+                // A operand of this lane: A row il = virtual row m, segment sa.
+                const int il = 16 * tt + (lane & 15);
+                const int m = il / SW;
+                const int ga = il % SW + SW * t;  // the A row's group, local to this K range
+                u16x8 a0 = {}, a1 = {};
+                if (m < a.mv && ga < cnt) {
+                    const uint16_t* src = xs + m * row_stride + 64 * ga + 16 * q;
+                    a0 = *(const u16x8*)src;
+                    a1 = *(const u16x8*)(src + 8);
                 }
-            } else {
-                const bf16x8 b0 = dequant8_bf16_biased(wq[j][0]);
-                const bf16x8 b1 = dequant8_bf16_biased(wq[j][1]);
-                const float corr = 136.0f + (float)zr[j];
-#pragma unroll
-                for (int t = 0; t < TILES; ++t) {
-                    const int row = 16 * t + (lane & 15);
-                    bf16x8 a0 = {}, a1 = {};
-                    if (row < a.mv) {
-                        const uint16_t* src = xs + row * row_stride + 64 * j + 16 * q;
-                        a0 = *(const bf16x8*)src;
-                        a1 = *(const bf16x8*)(src + 8);
-                    }
-                    float4v d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b0, float4v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b1, d, 0, 0, 0);
+                float4v d;
+                if constexpr (XK == kF16) {
+                    const _Float16 zl = (_Float16)(1032 + zr[t]);
+                    const _Float16 zh = (_Float16)(72 + zr[t]);
+                    const half8 b0 = dequant8_f16_int(wq[t][0], half2v{zl, zl}, half2v{zh, zh});
+                    const half8 b1 = dequant8_f16_int(wq[t][1], half2v{zl, zl}, half2v{zh, zh});
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a0), b0,
+                                                               float4v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a1), b1, d, 0, 0, 0);
+                } else {
+                    const bf16x8 b0 = dequant8_bf16_biased(wq[t][0]);
+                    const bf16x8 b1 = dequant8_bf16_biased(wq[t][1]);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a0), b0,
+                                                                float4v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a1), b1, d, 0, 0, 0);
+                    // D rows i = 16 tt + 4 q + r.  The rows kept later share this
+                    // lane's segment, so their group is this lane's group gl.
+                    const float corr = 136.0f + (float)zr[t];
+                    const int gl = sj + SW * t;
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
-                        const int vr = 16 * t + 4 * q + r;
-                        const float s_x = vr < a.mv ? sx[j * a.mv + vr] : 0.0f;
-                        acc[t][r] = fmaf(sc[j], fmaf(-corr, s_x, d[r]), acc[t][r]);
+                        const int mi = (16 * tt + 4 * q + r) / SW;
+                        const float s_x = (mi < a.mv && gl < cnt) ? sx[mi * a.gps + gl] : 0.0f;
+                        d[r] = fmaf(-corr, s_x, d[r]);
                     }
                 }
+#pragma unroll
+                for (int r = 0; r < 4; ++r) acc[tt][r] = fmaf(scale, d[r], acc[tt][r]);
             }
         }
     }
+    }
 
-    // ---- epilogue: gather the 16 x 64 tile(s), fold fp32 parts ----
-    __syncthreads();  // xs / sx no longer read
-    float* red = (float*)smem;  // [16 * TILES][64]
+    // ---- epilogue: keep the block diagonal, sum segments and fp32 parts ----
+    __syncthreads();            // activations no longer read
+    float* red = (float*)smem;  // [mv][kBlockCols][SW]
+    if (wave < kWaves)
 #pragma unroll
-    for (int t = 0; t < TILES; ++t)
+    for (int tt = 0; tt < TILES; ++tt) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) red[(16 * t + 4 * q + r) * kBlockCols + wave * 16 + (lane & 15)] = acc[t][r];
+        for (int r = 0; r < 4; ++r) {
+            const int i = 16 * tt + 4 * q + r;
+            const int m = i / SW;
+            if (i % SW == sj && m < a.mv) red[(m * kBlockCols + wave * R + rj) * SW + sj] = acc[tt][r];
+        }
+    }
     __syncthreads();
 
     const int col0 = nb * kBlockCols;
-    for (int idx = tid; idx < a.M * kBlockCols; idx += 256) {
+    for (int idx = tid; idx < a.M * kBlockCols; idx += kThreads) {
         const int m = idx / kBlockCols;
         const int c = idx - m * kBlockCols;
         const int nn = col0 + c;
         if (nn >= a.N) continue;
         float v = 0.0f;
 #pragma unroll
-        for (int p = 0; p < kParts; ++p) v += red[(p * a.M + m) * kBlockCols + c];
+        for (int p = 0; p < kParts; ++p)
+#pragma unroll
+            for (int s = 0; s < SW; ++s) v += red[((p * a.M + m) * kBlockCols + c) * SW + s];
         if (a.splits == 1) {
             v += load_bias(a.bias, a.bias_kind, nn);
             store_out<XK>(a.y, (int64_t)m * a.N + nn, v);
@@ -227,17 +248,22 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     }
     if (a.splits == 1) return;
 
-    // ---- split-K: the last workgroup of this column block reduces ----
-    __threadfence();
+    // ---- K split across workgroups: the last arrival of the block reduces ----
+    // Partials travel through device-coherent (sc1) atomic stores and loads.
+    // The wait makes every partial store of this workgroup complete before the
+    // arrival is counted; the reducer loads only after its counter update
+    // returned.  No cache write-back or invalidation is needed.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (tid == 0) {
-        const unsigned prev = __hip_atomic_fetch_add(a.counters + nb, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        const unsigned prev = __hip_atomic_fetch_add(a.counters + nb, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         s_last = (prev == (unsigned)a.splits - 1u);
     }
     __syncthreads();
     if (!s_last) return;
-    __threadfence();
-    for (int idx = tid; idx < a.M * kBlockCols; idx += 256) {
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    for (int idx = tid; idx < a.M * kBlockCols; idx += kThreads) {
         const int m = idx / kBlockCols;
         const int c = idx - m * kBlockCols;
         const int nn = col0 + c;
@@ -252,57 +278,103 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     if (tid == 0) __hip_atomic_store(a.counters + nb, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+template <int XK, int SW, int STEPS, int TILES>
+hipError_t launch_typed(const GemvArgs& args, const GemvPlan& plan, hipStream_t stream, hipEvent_t start,
+                        hipEvent_t stop) {
+    return launch_kernel(gemv_kernel<XK, SW, STEPS, TILES>, dim3(plan.n_blocks, plan.splits), dim3(kThreads),
+                         (size_t)plan.lds_bytes, stream, start, stop, args);
+}
+
+template <int XK, int SW, int TILES>
+hipError_t launch_steps(const GemvArgs& args, const GemvPlan& plan, hipStream_t stream, hipEvent_t start,
+                        hipEvent_t stop) {
+    switch (plan.steps) {
+        case 2: return launch_typed<XK, SW, 2, TILES>(args, plan, stream, start, stop);
+        case 3: return launch_typed<XK, SW, 3, TILES>(args, plan, stream, start, stop);
+        case 6: return launch_typed<XK, SW, 6, TILES>(args, plan, stream, start, stop);
+        case 9: return launch_typed<XK, SW, 9, TILES>(args, plan, stream, start, stop);
+        case 12: return launch_typed<XK, SW, 12, TILES>(args, plan, stream, start, stop);
+        default: return launch_typed<XK, SW, 16, TILES>(args, plan, stream, start, stop);
+    }
+}
+
 template <int XK, int TILES>
-hipError_t launch_typed(const GemvArgs& args, const GemvPlan& plan, size_t lds, hipStream_t stream,
-                        hipEvent_t start, hipEvent_t stop) {
-    return launch_kernel(gemv_kernel<XK, TILES>, dim3(plan.n_blocks, plan.splits), dim3(256), lds, stream, start,
-                         stop, args);
+hipError_t launch_sw(const GemvArgs& args, const GemvPlan& plan, hipStream_t stream, hipEvent_t start,
+                     hipEvent_t stop) {
+    switch (plan.segments) {
+        case 16: return launch_steps<XK, 16, TILES>(args, plan, stream, start, stop);
+        case 8: return launch_steps<XK, 8, TILES>(args, plan, stream, start, stop);
+        case 4: return launch_steps<XK, 4, TILES>(args, plan, stream, start, stop);
+        case 2: return launch_steps<XK, 2, TILES>(args, plan, stream, start, stop);
+        default: return launch_steps<XK, 1, TILES>(args, plan, stream, start, stop);
+    }
 }
 
 }  // namespace
 
-GemvPlan plan_gemv(int64_t rows, int64_t out_features, int64_t in_features, int x_kind) {
+GemvPlan plan_gemv(int64_t rows, int64_t out_features, int64_t in_features, int x_kind, int force_segments,
+                   int force_splits) {
     GemvPlan plan{};
     const int64_t groups = in_features / 64;
     const int64_t parts = (x_kind == kF32) ? 3 : 1;
-    plan.tiles = (int)((rows * parts + 15) / 16);
-    plan.n_blocks = (int)((out_features + kBlockCols - 1) / kBlockCols);
-    // Aim for ~4 workgroups per CU (256 CUs) while keeping the split-K
-    // partial traffic (write + read, fp32) under 1/8 of the packed weight
-    // bytes: 2 * S * rows * N * 4 <= N * K / 16  =>  S <= K / (128 * rows).
-    int64_t target = (1024 + plan.n_blocks - 1) / plan.n_blocks;
-    int64_t traffic_cap = in_features / (128 * rows);
-    int64_t splits = target < traffic_cap ? target : traffic_cap;
-    if (splits < 1) splits = 1;
-    if (splits > groups) splits = groups;
-    int64_t gps = (groups + splits - 1) / splits;
-    if (gps > kMaxGroupsPerSplit) gps = kMaxGroupsPerSplit;
-    // Activation staging (virtual rows x split width, 16-bit) plus the group
-    // sums must fit a 60 KB dynamic-LDS budget (64 KB per workgroup).
     const int64_t mv = rows * parts;
-    auto lds_for = [&](int64_t g) {
-        int64_t bytes = mv * (g * 64 + 8) * 2 + g * mv * 4;
-        const int64_t red = (int64_t)16 * plan.tiles * kBlockCols * 4;
-        return bytes > red ? bytes : red;
+    // Segments: as many as fit the 16 MFMA rows (mv * SW <= 16), then fewer
+    // while that still leaves >= 1024 column blocks (more features per
+    // workgroup = more reuse of the staged activations).
+    int64_t sw = 1;
+    while (sw < 16 && mv * sw * 2 <= 16) sw *= 2;
+    auto blocks_for = [&](int64_t s) {
+        const int64_t cols = kWaves * (16 / s);
+        return (out_features + cols - 1) / cols;
     };
-    while (gps > 1 && lds_for(gps) > 60 * 1024) --gps;
+    while (sw > 1 && blocks_for(sw / 2) >= 1024) sw /= 2;
+    if (force_segments > 0) sw = force_segments;
+    plan.segments = (int)sw;
+    plan.tiles = (int)((mv * sw + 15) / 16);
+    plan.n_blocks = (int)blocks_for(sw);
+    // K splits: a lane holds at most kMaxSteps group steps; with few column
+    // blocks and many rows, split further so that >= 256 workgroups run.
+    int64_t splits = (groups + sw * kMaxSteps - 1) / (sw * kMaxSteps);
+    while (plan.n_blocks * splits < 256 && splits * 2 <= groups && groups / (splits * 2) >= sw) splits *= 2;
+    if (force_splits > 0) splits = force_splits;
+    int64_t gps = (groups + splits - 1) / splits;
+    // Staged activations (virtual rows x split width, 16-bit) plus the group
+    // sums must fit a 60 KB dynamic-LDS budget (64 KB per workgroup).
+    auto lds_for = [&](int64_t g) {
+        const int64_t stage = mv * (g * 64 + 8) * 2 + mv * g * 4;
+        const int64_t red = mv * kWaves * 16 * 4;
+        return stage > red ? stage : red;
+    };
+    while (lds_for(gps) > 60 * 1024 || (gps + sw - 1) / sw > kMaxSteps) {
+        ++splits;
+        gps = (groups + splits - 1) / splits;
+    }
     splits = (groups + gps - 1) / gps;
-    plan.lds_bytes = lds_for(gps);
     plan.splits = (int)splits;
-    plan.groups_per_split = (int)((groups + splits - 1) / splits);
+    plan.groups_per_split = (int)gps;
+    const int64_t need = (gps + sw - 1) / sw;
+    plan.steps = kMaxSteps;
+    for (int b : kStepBuckets)
+        if (b >= need) {
+            plan.steps = b;
+            break;
+        }
+    plan.lds_bytes = lds_for(gps);
     plan.counter_bytes = splits > 1 ? kGemvCounterBytes : 0;
     plan.workspace_bytes = splits > 1 ? plan.counter_bytes + splits * rows * out_features * 4 : 0;
     return plan;
 }
 
+GemvPlan plan_gemv(int64_t rows, int64_t out_features, int64_t in_features, int x_kind) {
+    return plan_gemv(rows, out_features, in_features, x_kind, 0, 0);
+}
+
 const char* gemv_kernel_name(const GemvPlan& plan, int x_kind) {
-    static const char* names[3][3] = {
-        {"gemv_kernel<f16,1>", "gemv_kernel<f16,2>", "gemv_kernel<f16,3>"},
-        {"gemv_kernel<bf16,1>", "gemv_kernel<bf16,2>", "gemv_kernel<bf16,3>"},
-        {"gemv_kernel<f32,1>", "gemv_kernel<f32,2>", "gemv_kernel<f32,3>"},
-    };
-    int t = plan.tiles < 1 ? 1 : (plan.tiles > 3 ? 3 : plan.tiles);
-    return names[x_kind - 1][t - 1];
+    static thread_local char name[64];
+    static const char* kinds[] = {"?", "f16", "bf16", "f32"};
+    snprintf(name, sizeof(name), "gemv_kernel<%s,%d,%d,%d>", kinds[x_kind & 3], plan.segments, plan.steps,
+             plan.tiles);
+    return name;
 }
 
 hipError_t launch_gemv(const LinearProblem& p, const GemvPlan& plan, void* workspace, hipStream_t stream,
@@ -324,16 +396,16 @@ hipError_t launch_gemv(const LinearProblem& p, const GemvPlan& plan, void* works
     args.mv = (int)(p.rows * (p.x_kind == kF32 ? 3 : 1));
     args.counters = (unsigned*)workspace;
     args.partials = workspace ? (float*)((char*)workspace + plan.counter_bytes) : nullptr;
-    const size_t lds = (size_t)plan.lds_bytes;
     switch (p.x_kind) {
         case kF16:
-            return launch_typed<kF16, 1>(args, plan, lds, stream, start, stop);
+            return launch_sw<kF16, 1>(args, plan, stream, start, stop);
         case kBF16:
-            return launch_typed<kBF16, 1>(args, plan, lds, stream, start, stop);
+            return launch_sw<kBF16, 1>(args, plan, stream, start, stop);
         default:
-            if (plan.tiles == 1) return launch_typed<kF32, 1>(args, plan, lds, stream, start, stop);
-            if (plan.tiles == 2) return launch_typed<kF32, 2>(args, plan, lds, stream, start, stop);
-            return launch_typed<kF32, 3>(args, plan, lds, stream, start, stop);
+            // more than 16 virtual rows only occurs with one segment per wave
+            if (plan.tiles == 1) return launch_sw<kF32, 1>(args, plan, stream, start, stop);
+            if (plan.tiles == 2) return launch_steps<kF32, 1, 2>(args, plan, stream, start, stop);
+            return launch_steps<kF32, 1, 3>(args, plan, stream, start, stop);
     }
 }
 

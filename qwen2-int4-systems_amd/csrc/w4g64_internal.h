@@ -32,7 +32,9 @@ constexpr int kGemvMaxRows = 16;
 constexpr int64_t kGemvCounterBytes = 64 * 1024;
 constexpr int64_t kGemvMaxColumnBlocks = kGemvCounterBytes / 4;  // 1,048,576 output features
 struct GemvPlan {
-    int n_blocks;          // column blocks of 64 output features
+    int segments;          // K segments per wave (16 / output features per wave)
+    int steps;             // group steps per lane (compile-time bucket >= groups_per_split / segments)
+    int n_blocks;          // column blocks (4 * 16 / segments output features each)
     int splits;            // K splits across workgroups
     int groups_per_split;  // 64-wide K groups per split
     int tiles;             // 16-row MFMA A tiles (fp32 input uses 3 bf16 parts per row)
@@ -41,6 +43,9 @@ struct GemvPlan {
     int64_t counter_bytes;
 };
 GemvPlan plan_gemv(int64_t rows, int64_t out_features, int64_t in_features, int x_kind);
+// Same, with the segment count and K split forced (> 0) -- for tuning sweeps.
+GemvPlan plan_gemv(int64_t rows, int64_t out_features, int64_t in_features, int x_kind, int force_segments,
+                   int force_splits);
 hipError_t launch_gemv(const LinearProblem& p, const GemvPlan& plan, void* workspace, hipStream_t stream,
                        hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
 const char* gemv_kernel_name(const GemvPlan& plan, int x_kind);
