@@ -366,7 +366,7 @@ def main() -> int:
             "value": round(tf, 2),
             "unit": "TFLOP/s",
             "dtype": "bf16",
-            "roofline": {"bound": "mfma", "kernel": "gemm_kernel<bf16>", "achieved": round(tf, 2),
+            "roofline": {"bound": "mfma", "kernel": "gemm2_kernel<bf16,256>", "achieved": round(tf, 2),
                          "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(tf / MFMA_PEAK_TFLOPS, 4),
                          "traffic": None},
             "per_shape": gemm_rows,

@@ -134,6 +134,8 @@ static int linear_impl(const void* x, int x_dtype, const uint8_t* qweight, const
         return hip_status(w4g64::launch_gemv(p, plan, workspace, s, (hipEvent_t)start_event, (hipEvent_t)stop_event),
                           "gemv");
     }
+    if (w4g64::gemm2_supported(p))
+        return hip_status(w4g64::launch_gemm2(p, s, (hipEvent_t)start_event, (hipEvent_t)stop_event), "gemm");
     return hip_status(w4g64::launch_gemm(p, s, (hipEvent_t)start_event, (hipEvent_t)stop_event), "gemm");
 }
 

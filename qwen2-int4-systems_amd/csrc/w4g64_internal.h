@@ -50,6 +50,11 @@ hipError_t launch_gemv(const LinearProblem& p, const GemvPlan& plan, void* works
                        hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
 const char* gemv_kernel_name(const GemvPlan& plan, int x_kind);
 
+// Prefill GEMM v2 (pipelined, fp16/bf16 activations).
+bool gemm2_supported(const LinearProblem& p);
+hipError_t launch_gemm2(const LinearProblem& p, hipStream_t stream, hipEvent_t start = nullptr,
+                        hipEvent_t stop = nullptr);
+
 // Prefill GEMM (rows > kGemvMaxRows).
 hipError_t launch_gemm(const LinearProblem& p, hipStream_t stream, hipEvent_t start = nullptr,
                        hipEvent_t stop = nullptr);

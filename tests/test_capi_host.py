@@ -76,7 +76,7 @@ def test_workspace_and_kernel_plan_queries():
     assert lib.w4g64_linear_workspace_bytes(2048, 8960, 1536, _lib.DTYPE_BF16) == 0
     assert lib.w4g64_linear_workspace_bytes(1, 1536, 100, _lib.DTYPE_F16) == 0
     assert lib.w4g64_linear_kernel_name(1, 8960, 1536, _lib.DTYPE_F16).startswith(b"gemv_kernel<f16")
-    assert lib.w4g64_linear_kernel_name(2048, 8960, 1536, _lib.DTYPE_BF16).startswith(b"gemm_kernel<bf16")
+    assert lib.w4g64_linear_kernel_name(2048, 8960, 1536, _lib.DTYPE_BF16).startswith(b"gemm2_kernel<bf16")
     assert lib.w4g64_linear_kernel_name(1, 8960, 1536, 7) == b"none"
 
 
