@@ -12,7 +12,7 @@ HIP graph; the timed region replays K step graphs back to back between two
 device synchronizations.  value = algorithmic bytes of the step / step time.
 
 The roofline object is for the kernel that does the decode work
-(gemv_kernel<f16,1>, all 21 calls): its duration per call is measured live
+(gemv_kernel<f16,...>, one instantiation per shape class; all 21 calls): its duration per call is measured live
 with HIP events that hipExtLaunchKernelGGL records at the kernel's own start
 and end (the same figure rocprofv3 --kernel-trace reports), on the stream the
 kernel runs on; achieved = algorithmic bytes / summed kernel durations.
@@ -317,7 +317,7 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "gemv_kernel<f16,1>",
+            "kernel": "gemv_kernel<f16,*> (all 21 calls of a step)",
             "achieved": round(achieved, 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
@@ -366,7 +366,7 @@ def main() -> int:
             "value": round(tf, 2),
             "unit": "TFLOP/s",
             "dtype": "bf16",
-            "roofline": {"bound": "mfma", "kernel": "gemm2_kernel<bf16,256>", "achieved": round(tf, 2),
+            "roofline": {"bound": "mfma", "kernel": "gemm2_kernel<bf16,128>", "achieved": round(tf, 2),
                          "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(tf / MFMA_PEAK_TFLOPS, 4),
                          "traffic": None},
             "per_shape": gemm_rows,

@@ -234,9 +234,9 @@ hipError_t launch_gemm(const LinearProblem& p, hipStream_t stream, hipEvent_t st
     }
 }
 
-const char* gemm_kernel_name(int64_t rows, int64_t, int64_t, int x_kind) {
-    if (x_kind == kF16) return rows > 128 ? "gemm2_kernel<f16,256>" : "gemm2_kernel<f16,128>";
-    if (x_kind == kBF16) return rows > 128 ? "gemm2_kernel<bf16,256>" : "gemm2_kernel<bf16,128>";
+const char* gemm_kernel_name(int64_t, int64_t, int64_t, int x_kind) {
+    if (x_kind == kF16) return "gemm2_kernel<f16,128>";
+    if (x_kind == kBF16) return "gemm2_kernel<bf16,128>";
     return "gemm_kernel<f32>";
 }
 

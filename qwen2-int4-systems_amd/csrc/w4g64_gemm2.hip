@@ -3,14 +3,19 @@
 // y[M, N] = x[M, K] @ W^T (+ bias), W[n,k] = (code - zero) * scale, fp32
 // accumulation in v_mfma_f32_32x32x16_{f16,bf16}.
 //
-// Workgroup = 4 waves, output tile BM x 256: wave w owns all BM rows of the
-// 64 output features [n0 + 64 w, n0 + 64 w + 64).  One K step = one 64-wide
-// quantization group.
+// Workgroup = 4 waves, output tile BM x 256 (BM = 128): wave w owns all BM
+// rows of the 64 output features [n0 + 64 w, n0 + 64 w + 64).  One K step =
+// one 64-wide quantization group.  Two workgroups share a CU (78 KB of LDS
+// and 256 registers per lane each), so the MFMA pipes stay busy while one of
+// them waits at its per-step barrier.
 //   * Every load is a gfx950 direct global->LDS load into a ring of S = 3
-//     stages, issued S-1 steps ahead: the activation tile (16-byte loads)
-//     and, per wave, its packed weight columns, scales and zero bytes.  Every 1 KB a wave instruction writes holds 8 tile rows; the 16 B
-//     chunks of a row are XOR-swizzled by (row & 7), which the fragment reads
-//     undo, so the 32 rows of a fragment read hit distinct banks.
+//     stages, issued up to S steps ahead (a stage is refilled as soon as
+//     every wave has finished reading it): the activation tile (16-byte loads)
+//     and, per wave, its packed weight columns, scales and zero bytes.
+//     Every 1 KB a wave instruction writes holds 8 tile rows; the 16 B
+//     chunks of a row are XOR-swizzled by a_swizzle(row), which the fragment
+//     reads undo: any 8 or 16 consecutive rows of one logical chunk land in
+//     distinct 16-byte bank groups, so fragment reads are conflict-free.
 //   * Weights (B): each wave reads back its own packed columns (16 B = 32
 //     consecutive K values per lane and column block) and dequantizes only
 //     its own columns:
@@ -22,12 +27,15 @@
 //     group, sub-step kk uses [32q + 8kk, 32q + 8kk + 8); A and B fragments
 //     use the same slots, so the contraction is unchanged.
 //   * Waits are explicit: every step issues the same number of vector memory
-//     operations (prefetches past the last step re-load the last step), so
-//     "this step's data has landed" is vmcnt <= (S - 2) * ops_per_step.  All
-//     loads are drained before the workgroup exits.
+//     operations, so "step s has landed" is a vmcnt bound known at compile
+//     time for each position in the loop (steps past the end are not issued;
+//     the waits near the end tighten accordingly).  All loads are drained
+//     before the workgroup exits.
 //   * Tiles are assigned so that the workgroups of one XCD (ids congruent
 //     mod 8) cover consecutive tiles of one row band: they share the
 //     activation band in their L2.
+#include <type_traits>
+
 #include "w4g64_device.h"
 #include "w4g64_internal.h"
 
@@ -36,6 +44,7 @@ namespace {
 
 constexpr int kStages = 3;
 constexpr int kBN = 256;  // 4 waves x 64 output features
+constexpr int kBM = 128;  // rows per tile: two workgroups fit one CU (LDS and registers)
 constexpr int kXcds = 8;
 
 struct Gemm2Args {
@@ -52,9 +61,48 @@ struct Gemm2Args {
     int G;
     int tiles_m;
     int tiles_n;
+    int vec_out;  // y is 16-byte aligned and N % 8 == 0: 16-byte output stores
 };
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// s_waitcnt with only the vector memory counter constrained (gfx9 encoding:
+// vmcnt bits [3:0] and [15:14], expcnt [6:4] and lgkmcnt [11:8] left at max).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+// Physical 16-byte chunk offset of tile row r (rows are 128 B = 8 chunks).
+// Row r's chunks start at bank group 8 (r & 1) (mod 16 groups of 4 banks);
+// the XOR term takes 8 distinct values over any 8 consecutive rows and over
+// the 8 rows of either parity among 16 consecutive rows.
+__device__ __forceinline__ int a_swizzle(int r) { return ((r >> 1) & 7) ^ ((r & 1) << 2); }
+
+// Scheduling shape of one sub-step: each of the MB A-fragment reads is paired
+// with two MFMAs, with up to V other VALU instructions after each MFMA, and
+// no instruction crosses the end of the sub-step.
+template <int MB, int V>
+__device__ __forceinline__ void sched_interleave() {
+#pragma unroll
+    for (int i = 0; i < MB; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        if constexpr (V > 0) __builtin_amdgcn_sched_group_barrier(0x002, V, 0);  // VALU
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        if constexpr (V > 0) __builtin_amdgcn_sched_group_barrier(0x002, V, 0);  // VALU
+    }
+    __builtin_amdgcn_sched_barrier(0);
+}
+__device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xF | (0x3 << 14) | (0x7 << 4)); }
+// Workgroup execution barrier without a memory fence (a fence would drain the
+// loads still in flight); the empty asm statements keep the compiler from
+// moving LDS accesses across it.
+__device__ __forceinline__ void block_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
 
 // Natural-order fp16 (code - zero) pairs of one packed dword:
 // pair b = (k = 2b, k = 2b + 1).  Byte b is replicated by v_perm; the mask
@@ -68,8 +116,16 @@ __device__ __forceinline__ uint32_t nib_pair_natural(uint32_t w, int b) {
     return ((rep ^ kSel) & kMask) | (kSel & ~kMask);
 }
 
+// Dequantized weights of one packed dword (8 consecutive K values of one
+// column) as 4 natural-order fp16 / bf16 pairs.
+//   fp16: (m - c) is exact in fp16 (m = magic value, c = magic offset + zero),
+//         then one fp16 multiply by the scale: RNE(d * scale).
+//   bf16: d * s = m * s - c * s, and both products fit in 22 bits, so one fp32
+//         FMA against the precomputed exact c * s yields d * s exactly;
+//         then RNE to bf16.
 template <int XK>
-__device__ __forceinline__ u32x4 dequant_natural(uint32_t w, uint32_t zc_bits, float s, uint32_t s2_bits) {
+__device__ __forceinline__ u32x4 dequant_natural(uint32_t w, uint32_t zc_bits, uint32_t s2_bits, float s,
+                                                 float cs_lo, float cs_hi) {
     u32x4 out;
     if constexpr (XK == kF16) {
         const half2v zc = __builtin_bit_cast(half2v, zc_bits);   // (1032 + z, 72 + z)
@@ -80,20 +136,18 @@ __device__ __forceinline__ u32x4 dequant_natural(uint32_t w, uint32_t zc_bits, f
             out[b] = __builtin_bit_cast(uint32_t, v);
         }
     } else {
-        const half2v zc = __builtin_bit_cast(half2v, zc_bits);
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
-            const half2v d = __builtin_bit_cast(half2v, nib_pair_natural(w, b)) - zc;  // exact ints
-            const float lo = (float)d[0] * s;  // exact in fp32
-            const float hi = (float)d[1] * s;
-            out[b] = (uint32_t)float_to_bf16_bits(lo) | ((uint32_t)float_to_bf16_bits(hi) << 16);
+            const half2v m = __builtin_bit_cast(half2v, nib_pair_natural(w, b));  // (1024 + n', 64 + n')
+            const float2v f = {__builtin_fmaf((float)m[0], s, -cs_lo), __builtin_fmaf((float)m[1], s, -cs_hi)};
+            out[b] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2v));  // one RNE pair conversion
         }
     }
     return out;
 }
 
 template <int XK, int BM>
-__global__ __launch_bounds__(256) void gemm2_kernel(Gemm2Args a) {
+__global__ __launch_bounds__(256, 2) void gemm2_kernel(Gemm2Args a) {
     constexpr int MB = BM / 32;                 // 32-row MFMA blocks per wave
     constexpr int kABytes = BM * 128;           // BM rows x 64 fp16/bf16 values
     constexpr int kWBytes = 4 * 2 * 1024;       // 4 waves x 2 column blocks x (32 columns x 32 B)
@@ -129,7 +183,7 @@ __global__ __launch_bounds__(256) void gemm2_kernel(Gemm2Args a) {
 #pragma unroll
     for (int d = 0; d < kDma; ++d) {
         const int r = 8 * (wave * kDma + d) + (lane >> 3);
-        const int chunk = (lane & 7) ^ (r & 7);
+        const int chunk = (lane & 7) ^ a_swizzle(r);
         int64_t m = m0 + r;
         m = m < a.M ? m : a.M - 1;  // rows past M load a valid row; their outputs are not stored
         a_src[d] = a.x + m * a.K + 8 * chunk;
@@ -149,9 +203,8 @@ __global__ __launch_bounds__(256) void gemm2_kernel(Gemm2Args a) {
     ncol = ncol < a.N ? ncol : a.N - 1;
     const int64_t s_row = ncol * a.G;
 
-    auto issue = [&](int g) {
-        const int gg = g < a.G ? g : a.G - 1;  // past the end: re-load the last step (uniform op count)
-        unsigned char* st = smem[g % kStages];
+    auto issue = [&](int gg) {  // callers pass gg < G only
+        unsigned char* st = smem[gg % kStages];
 #pragma unroll
         for (int d = 0; d < kDma; ++d)
             __builtin_amdgcn_global_load_lds((const void*)(a_src[d] + (int64_t)gg * 64),
@@ -172,85 +225,199 @@ __global__ __launch_bounds__(256) void gemm2_kernel(Gemm2Args a) {
 #pragma unroll
         for (int bj = 0; bj < 2; ++bj) acc[i][bj] = float16v{};
 
-#pragma unroll
-    for (int s = 0; s < kStages - 1; ++s) issue(s);
-
-    const int fr = lane & 31;
-    constexpr int kWait = kOpsPerStep * (kStages - 2);  // loads issued after this step's
-    static_assert(kWait < 64, "vmcnt is 6 bits");
-    constexpr int kWaitImm = (kWait & 0xF) | ((kWait >> 4) << 14) | (0x7 << 4) | (0xF << 8);
-
-    for (int g = 0; g < a.G; ++g) {
-        // This wave's loads for step g have landed (loads complete in order and
-        // kWait loads were issued after them); the barrier extends that to all
-        // waves and guarantees nobody still reads the stage refilled below
-        // (every wave consumed its LDS reads of step g-1 in that step's MFMAs).
-        // A bare s_barrier: __syncthreads() would add a release fence that
-        // drains the prefetches still in flight.
-        __builtin_amdgcn_s_waitcnt(kWaitImm);
-        __builtin_amdgcn_s_barrier();
-        issue(g + kStages - 1);
-
-        const unsigned char* st = smem[g % kStages];
-        // ---- dequantize this wave's B fragments ----
-        u32x4 bfrag[2][4];
-#pragma unroll
-        for (int bj = 0; bj < 2; ++bj) {
-            const u32x4 w = *(const u32x4*)(st + kABytes + 2048 * wave + 1024 * bj + 16 * lane);
-            const int c = 32 * bj + j;  // column within the wave
-            const uint16_t sbits = *(const uint16_t*)(st + kABytes + kWBytes + 256 * wave + 4 * c);
-            const int zb = st[kABytes + kWBytes + kSBytes + 256 * wave + 4 * c];
-            const int64_t e = (nw + c < a.N ? nw + c : a.N - 1) * a.G + g;
-            int zn = (e & 1) ? (zb >> 4) : (zb & 0xF);
-            zn -= (zn & 8) << 1;
-            const uint32_t zlo = 0x6408u + (uint32_t)zn;       // fp16 bits of 1032 + z
-            const uint32_t zhi = 0x5480u + 16u * (uint32_t)zn;  // fp16 bits of 72 + z
-            const uint32_t zc = (zlo & 0xFFFFu) | ((zhi & 0xFFFFu) << 16);
-            const float s = half_bits_to_float(sbits);
-            const uint32_t s2 = (uint32_t)sbits * 0x00010001u;
-#pragma unroll
-            for (int kk = 0; kk < 4; ++kk) bfrag[bj][kk] = dequant_natural<XK>(w[kk], zc, s, s2);
-        }
-        // ---- MFMA: A fragments from the swizzled stage ----
-#pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
-#pragma unroll
-            for (int bi = 0; bi < MB; ++bi) {
-                const int r = 32 * bi + fr;
-                const int chunk = (4 * q + kk) ^ (r & 7);
-                const u32x4 afr = *(const u32x4*)(st + r * 128 + chunk * 16);
-#pragma unroll
-                for (int bj = 0; bj < 2; ++bj) {
-                    if constexpr (XK == kF16) {
-                        acc[bi][bj] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-                            __builtin_bit_cast(half8, afr), __builtin_bit_cast(half8, bfrag[bj][kk]), acc[bi][bj],
-                            0, 0, 0);
-                    } else {
-                        acc[bi][bj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                            __builtin_bit_cast(bf16x8, afr), __builtin_bit_cast(bf16x8, bfrag[bj][kk]),
-                            acc[bi][bj], 0, 0, 0);
-                    }
-                }
-            }
-        }
-    }
-    __builtin_amdgcn_s_waitcnt(0);  // no DMA may still target this workgroup's LDS at exit
-
-    // ---- epilogue: 32x32 accumulator layout: column = lane % 32,
-    // row = 8 (r / 4) + 4 (lane / 32) + r % 4 ----
+    // parity of each of this lane's two dequant columns' zero element index at g = 0
+    int zpar[2];
 #pragma unroll
     for (int bj = 0; bj < 2; ++bj) {
         const int64_t n = nw + 32 * bj + j;
-        if (n >= a.N) continue;
-        const float b = load_bias(a.bias, a.bias_kind, n);
+        zpar[bj] = (int)(((n < a.N ? n : a.N - 1) * a.G) & 1);
+    }
+
+    // B fragments of step g, column block bj: this wave's packed columns,
+    // read back from the stage and dequantized in natural K order.
+    struct BRaw {
+        u32x4 w;
+        uint32_t sbits;
+        uint32_t zb;
+    };
+    auto read_b = [&](int g, int bj) {
+        const unsigned char* st = smem[g % kStages];
+        const int c = 32 * bj + j;  // column within the wave
+        BRaw r;
+        r.w = *(const u32x4*)(st + kABytes + 2048 * wave + 1024 * bj + 16 * lane);
+        r.sbits = *(const uint16_t*)(st + kABytes + kWBytes + 256 * wave + 4 * c);
+        r.zb = st[kABytes + kWBytes + kSBytes + 256 * wave + 4 * c];
+        return r;
+    };
+    auto dequant_b = [&](int g, int bj, const BRaw& r, u32x4 (&bf)[2][4]) {
+        int zn = (int)(((zpar[bj] ^ g) & 1) ? (r.zb >> 4) : (r.zb & 0xF));
+        zn -= (zn & 8) << 1;
+        const uint32_t zlo = 0x6408u + (uint32_t)zn;       // fp16 bits of 1032 + z
+        const uint32_t zhi = 0x5480u + 16u * (uint32_t)zn;  // fp16 bits of 72 + z
+        const uint32_t zc = (zlo & 0xFFFFu) | ((zhi & 0xFFFFu) << 16);
+        const float s = half_bits_to_float((uint16_t)r.sbits);
+        const uint32_t s2 = (r.sbits & 0xFFFFu) * 0x00010001u;
+        const float cs_lo = (float)(1032 + zn) * s;  // exact: 11-bit by 11-bit product
+        const float cs_hi = (float)(72 + zn) * s;
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) bf[bj][kk] = dequant_natural<XK>(r.w[kk], zc, s2, s, cs_lo, cs_hi);
+    };
+    // A fragments of sub-step kk from the swizzled stage.
+    const int fr = lane & 31;
+    auto read_a = [&](const unsigned char* st, int kk, u32x4 (&af)[MB]) {
+#pragma unroll
+        for (int bi = 0; bi < MB; ++bi) {
+            const int r = 32 * bi + fr;
+            const int chunk = (4 * q + kk) ^ a_swizzle(r);
+            af[bi] = *(const u32x4*)(st + r * 128 + chunk * 16);
+        }
+    };
+    auto mma = [&](const u32x4 (&af)[MB], const u32x4 (&bf)[2][4], int kk) {
 #pragma unroll
         for (int bi = 0; bi < MB; ++bi) {
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int64_t m = m0 + 32 * bi + 8 * (r / 4) + 4 * q + (r % 4);
-                if (m < a.M) store_out<XK>(a.y, m * a.N + n, acc[bi][bj][r] + b);
+            for (int bj = 0; bj < 2; ++bj) {
+                if constexpr (XK == kF16) {
+                    acc[bi][bj] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                        __builtin_bit_cast(half8, af[bi]), __builtin_bit_cast(half8, bf[bj][kk]), acc[bi][bj], 0, 0, 0);
+                } else {
+                    acc[bi][bj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                        __builtin_bit_cast(bf16x8, af[bi]), __builtin_bit_cast(bf16x8, bf[bj][kk]), acc[bi][bj], 0,
+                        0, 0);
+                }
             }
         }
+    };
+
+    // ---- rotated software pipeline ----
+    // Step g, four sub-steps of 2 * MB MFMAs each:
+    //   kk = 0: read this wave's B data of step g + 1 and the A fragments of
+    //           kk = 1;
+    //   kk = 1, 2: read the A fragments of kk + 1; dequantize B of step g + 1
+    //           (column block kk - 1) between the MFMAs;
+    //   kk = 3: workgroup barrier (every wave has finished reading stage g and
+    //           all of step g + 1 has landed), refill stage g with step g + 3,
+    //           read the A fragments of step g + 1, kk = 0.
+    // "Step s has landed" for this wave = its vector memory counter is at most
+    // the number of operations issued after step s's (in-order completion).
+    // Steps g + 3 < G run the branch-free body; the last (up to) three steps
+    // the same body with the tighter waits and without refills.
+    const int G = a.G;
+    issue(0);
+    if (G > 1) issue(1);
+    if (G > 2) issue(2);
+    if (G > 2) wait_vmcnt<2 * kOpsPerStep>();
+    else if (G > 1) wait_vmcnt<kOpsPerStep>();
+    else wait_vmcnt<0>();
+    block_barrier();
+
+    u32x4 bcur[2][4];
+    {
+        const BRaw r0 = read_b(0, 0);
+        const BRaw r1 = read_b(0, 1);
+        dequant_b(0, 0, r0, bcur);
+        dequant_b(0, 1, r1, bcur);
+    }
+    u32x4 a0[MB], a1[MB];
+    read_a(smem[0], 0, a0);
+
+    auto step = [&](int g, auto tail_tag) {
+        constexpr bool kTail = decltype(tail_tag)::value;
+        const unsigned char* st = smem[g % kStages];
+        const int gn = (kTail && g + 1 >= G) ? g : g + 1;  // last step: re-read its own (valid) stage
+        // ---- kk = 0 ----
+        if constexpr (kTail) wait_vmcnt<0>();
+        else wait_vmcnt<kOpsPerStep>();  // this wave's loads of step g + 1
+        const BRaw r0 = read_b(gn, 0);
+        const BRaw r1 = read_b(gn, 1);
+        read_a(st, 1, a1);
+        mma(a0, bcur, 0);
+        sched_interleave<MB, 0>();
+        // ---- kk = 1 ----
+        u32x4 bnext[2][4];
+        read_a(st, 2, a0);
+        dequant_b(gn, 0, r0, bnext);
+        mma(a1, bcur, 1);
+        sched_interleave<MB, XK == kF16 ? 5 : 6>();
+        // ---- kk = 2 ----
+        read_a(st, 3, a1);
+        dequant_b(gn, 1, r1, bnext);
+        mma(a0, bcur, 2);
+        sched_interleave<MB, XK == kF16 ? 5 : 6>();
+        // ---- kk = 3 ----
+        if (!kTail || g + 1 < G) {
+            wait_lgkmcnt0();
+            block_barrier();
+            if (!kTail) issue(g + 3);
+        }
+        read_a(smem[(g + 1) % kStages], 0, a0);
+        mma(a1, bcur, 3);
+        sched_interleave<MB, 1>();
+#pragma unroll
+        for (int bj = 0; bj < 2; ++bj)
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) bcur[bj][kk] = bnext[bj][kk];
+    };
+    int g = 0;
+    for (; g + 3 < G; ++g) step(g, std::false_type{});
+    for (; g < G; ++g) step(g, std::true_type{});
+    wait_vmcnt<0>();  // no DMA may still target this workgroup's LDS at exit
+
+    // ---- epilogue ----
+    // 32x32 accumulator layout: column = lane % 32, row = 8 (r / 4) +
+    // 4 (lane / 32) + r % 4.  Each wave stages its 64 output columns through
+    // LDS, half of its rows at a time, and writes 8 consecutive outputs
+    // (16 B) per lane: 8 full 128-byte row segments per store instruction.
+    // Row stride 144 B: the two lane halves (rows 4 apart) write disjoint
+    // banks and the 16-byte reads stay aligned.
+    block_barrier();  // every wave has finished reading the pipeline stages
+    constexpr int kOutStride = 144;
+    constexpr int kHalfRows = BM / 2;
+    static_assert(4 * kHalfRows * kOutStride <= kStages * kStageBytes, "output staging exceeds LDS");
+    unsigned char* ost = &smem[0][0] + wave * kHalfRows * kOutStride;
+    float bias_v[2];
+#pragma unroll
+    for (int bj = 0; bj < 2; ++bj) {
+        const int64_t n = nw + 32 * bj + j;
+        bias_v[bj] = n < a.N ? load_bias(a.bias, a.bias_kind, n) : 0.0f;
+    }
+    uint16_t* y = (uint16_t*)a.y;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+        for (int bi = 0; bi < MB / 2; ++bi) {
+#pragma unroll
+            for (int bj = 0; bj < 2; ++bj) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int row = 32 * bi + 8 * (r / 4) + 4 * q + (r % 4);
+                    const float v = acc[h * (MB / 2) + bi][bj][r] + bias_v[bj];
+                    *(uint16_t*)(ost + row * kOutStride + 2 * (32 * bj + j)) =
+                        XK == kF16 ? float_to_half_bits(v) : float_to_bf16_bits(v);
+                }
+            }
+        }
+        // LDS accesses of one wave complete in order; the empty asm keeps the
+        // compiler from reordering the staging writes and reads.
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int i = 0; i < kHalfRows / 8; ++i) {
+            const int row = 8 * i + (lane >> 3);
+            const int c8 = lane & 7;
+            const u32x4 v = *(const u32x4*)(ost + row * kOutStride + 16 * c8);
+            const int64_t m = m0 + h * kHalfRows + row;
+            const int64_t n = nw + 8 * c8;
+            if (m < a.M) {
+                if (a.vec_out && n + 8 <= a.N) {
+                    *(u32x4*)(y + m * a.N + n) = v;
+                } else {
+#pragma unroll 1
+                    for (int e = 0; e < 8; ++e)
+                        if (n + e < a.N) y[m * a.N + n + e] = (uint16_t)(v[e >> 1] >> (16 * (e & 1)));
+                }
+            }
+        }
+        asm volatile("" ::: "memory");
     }
 }
 
@@ -273,17 +440,12 @@ hipError_t launch_gemm2(const LinearProblem& p, hipStream_t stream, hipEvent_t s
     args.N = (int)p.out_features;
     args.K = (int)p.in_features;
     args.G = (int)(p.in_features / 64);
-    const bool big = p.rows > 128;
-    const int bm = big ? 256 : 128;
-    args.tiles_m = (int)((p.rows + bm - 1) / bm);
+    args.tiles_m = (int)((p.rows + kBM - 1) / kBM);
     args.tiles_n = (int)((p.out_features + kBN - 1) / kBN);
+    args.vec_out = (((uintptr_t)p.y & 15) == 0) && (p.out_features % 8 == 0);
     dim3 grid((unsigned)(args.tiles_m * args.tiles_n));
-    if (p.x_kind == kF16) {
-        return big ? launch_kernel(gemm2_kernel<kF16, 256>, grid, dim3(256), 0, stream, start, stop, args)
-                   : launch_kernel(gemm2_kernel<kF16, 128>, grid, dim3(256), 0, stream, start, stop, args);
-    }
-    return big ? launch_kernel(gemm2_kernel<kBF16, 256>, grid, dim3(256), 0, stream, start, stop, args)
-               : launch_kernel(gemm2_kernel<kBF16, 128>, grid, dim3(256), 0, stream, start, stop, args);
+    if (p.x_kind == kF16) return launch_kernel(gemm2_kernel<kF16, kBM>, grid, dim3(256), 0, stream, start, stop, args);
+    return launch_kernel(gemm2_kernel<kBF16, kBM>, grid, dim3(256), 0, stream, start, stop, args);
 }
 
 }  // namespace w4g64
