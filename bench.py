@@ -26,6 +26,14 @@ bf16) is reported in the "gemm" object with its own roofline (MFMA bound).
 
 Parity against the CPU oracle is checked for every timed case before any
 timing, as the reference's harness does (scripts/autotune_phase_e_triton_v6.py:96-113).
+
+HBM traffic (roofline "traffic"): `--profile-pass` runs, untimed, a
+calibration kernel of exactly known traffic (the unpack kernel: reads P bytes,
+writes 2P bytes), three decode steps on rotating weight copies and the M=2048
+GEMMs, each group after a 1 GiB write that evicts the caches, for two `rocprofv3 --pmc` runs (FETCH_SIZE, then WRITE_SIZE);
+`--summarize-pmc FETCH_CSV WRITE_CSV` scales each counter by the calibration
+kernel's reading and writes the per-launch traffic to profiles/pmc_traffic.json,
+which later bench runs report.
 """
 
 from __future__ import annotations
@@ -196,6 +204,123 @@ def cpu_baseline(decode_cases_np, torch, budget_s: float = 12.0):
     }
 
 
+PMC_TRAFFIC_FILE = REPO_ROOT / "profiles" / "pmc_traffic.json"
+CALIBRATION_PACKED_BYTES = 128 << 20  # unpack kernel: reads this, writes twice this
+SCRUB_BYTES = 1 << 30  # written before each measured group: evicts the L2s and the 256 MB Infinity Cache
+
+
+def decode_cases(torch, O, copies_per_shape: int):
+    """The decode step's 21 calls: weights (numpy), device copies, activations."""
+    shapes = O.QWEN2_SHAPES
+    weights_np = {name: O.symmetric_weights(n, k, O.BASE_SEED + n + k) for name, (n, k) in shapes.items()}
+    copies = {}
+    for name, (q, s, z) in weights_np.items():
+        base = (torch.from_numpy(q).cuda(), torch.from_numpy(s).cuda(), torch.from_numpy(z).cuda())
+        copies[name] = [tuple(t.clone() for t in base) for _ in range(copies_per_shape)]
+    cases = []
+    for r_index, rows in enumerate(DECODE_ROWS):
+        for s_index, (name, (n, k)) in enumerate(shapes.items()):
+            x_np = O.activations(rows, k, seed=O.BASE_SEED + 1000 * rows + s_index, dtype="fp16")
+            cases.append({"name": name, "rows": rows, "n": n, "k": k, "x_np": x_np, "x": to_device(x_np, "fp16", torch),
+                          "copies": copies[name], "copy0": r_index, "bytes": algorithmic_bytes(rows, n, k)})
+    return weights_np, copies, cases
+
+
+def profile_pass() -> int:
+    """Untimed dispatch sequence for rocprofv3 --pmc (see the module docstring)."""
+    import torch
+
+    from oracle import oracle as O
+    from qwen_int4_hip import (hip_available, linear_canonical_w4g64_hip,
+                               unpack_canonical_signed_int4_hip)
+
+    if not hip_available():
+        raise SystemExit("bench.py needs a ROCm GPU and the built HIP library")
+    scrub = torch.empty(SCRUB_BYTES, dtype=torch.uint8, device="cuda")
+    packed = torch.randint(0, 256, (CALIBRATION_PACKED_BYTES,), dtype=torch.uint8, device="cuda")
+    _, copies, cases = decode_cases(torch, O, 8)
+    scrub.fill_(1)
+    unpack_canonical_signed_int4_hip(packed)
+    for step in range(3):
+        scrub.fill_(2 + step)
+        for c in cases:
+            linear_canonical_w4g64_hip(c["x"], *c["copies"][(3 * step + c["copy0"]) % 8])
+    for name in PREFILL_SHAPES:
+        n, k = O.QWEN2_SHAPES[name]
+        x = to_device(O.activations(2048, k, seed=O.BASE_SEED + 7 * 2048 + n, dtype="bf16"), "bf16", torch)
+        for rep in range(2):
+            scrub.fill_(7 + rep)
+            linear_canonical_w4g64_hip(x, *copies[name][rep])
+    torch.cuda.synchronize()
+    log(f"profile pass done: 1 calibration dispatch, {3 * len(cases)} decode dispatches, "
+        f"{2 * len(PREFILL_SHAPES)} GEMM dispatches")
+    return 0
+
+
+def _pmc_dispatches(csv_path: str, counter: str):
+    """[(dispatch id, kernel name, counter value in KiB)] in dispatch order."""
+    import csv
+
+    per = {}
+    with open(csv_path, newline="") as fh:
+        for row in csv.DictReader(fh):
+            if row["Counter_Name"] != counter:
+                continue
+            key = int(row["Dispatch_Id"])
+            name, total = per.get(key, (row["Kernel_Name"], 0.0))
+            per[key] = (name, total + float(row["Counter_Value"]))
+    return [(k, v[0], v[1]) for k, v in sorted(per.items())]
+
+
+def summarize_pmc(fetch_csv: str, write_csv: str, out_path: str) -> int:
+    from oracle import oracle as O
+
+    fetch = _pmc_dispatches(fetch_csv, "FETCH_SIZE")
+    write = _pmc_dispatches(write_csv, "WRITE_SIZE")
+
+    def split(rows):
+        cal = [v for _, name, v in rows if "unpack_kernel" in name]
+        dec = [v for _, name, v in rows if "gemv_kernel" in name]
+        gem = [v for _, name, v in rows if "gemm" in name]
+        if len(cal) != 1 or len(dec) % 21 or not dec:
+            raise SystemExit(f"unexpected dispatch sequence: {len(cal)} calibration, {len(dec)} decode dispatches")
+        return cal[0], dec, gem
+
+    f_cal, f_dec, f_gem = split(fetch)
+    w_cal, w_dec, w_gem = split(write)
+    f_scale = (CALIBRATION_PACKED_BYTES / 1024) / f_cal   # true KiB per counted KiB
+    w_scale = (2 * CALIBRATION_PACKED_BYTES / 1024) / w_cal
+    steps = len(f_dec) // 21
+    step_bytes = sum(algorithmic_bytes(r, n, k) for r in DECODE_ROWS for (n, k) in O.QWEN2_SHAPES.values())
+    fetch_step = sum(f_dec) * f_scale * 1024 / steps
+    write_step = sum(w_dec) * w_scale * 1024 / steps
+    summary = {
+        "calibration": {"kernel": "unpack_kernel", "reads_bytes": CALIBRATION_PACKED_BYTES,
+                        "writes_bytes": 2 * CALIBRATION_PACKED_BYTES, "FETCH_SIZE_KiB": f_cal, "WRITE_SIZE_KiB": w_cal,
+                        "fetch_scale": f_scale, "write_scale": w_scale},
+        "decode": {"kernel": "gemv_kernel<f16,*>", "steps": steps, "launches_per_step": 21,
+                   "algorithmic_bytes_per_launch": step_bytes / 21,
+                   "fetch_bytes_per_launch": fetch_step / 21, "write_bytes_per_launch": write_step / 21,
+                   "traffic_bytes_per_launch": (fetch_step + write_step) / 21,
+                   "traffic_over_algorithmic": (fetch_step + write_step) / step_bytes},
+    }
+    if f_gem and len(f_gem) == len(w_gem):
+        per_call = [(a * f_scale + b * w_scale) * 1024 for a, b in zip(f_gem, w_gem)]
+        summary["gemm_2048"] = {"kernel": "gemm2_kernel<bf16,128>", "launches": len(per_call),
+                                "traffic_bytes_per_launch": sum(per_call) / len(per_call)}
+    Path(out_path).parent.mkdir(parents=True, exist_ok=True)
+    Path(out_path).write_text(json.dumps(summary, indent=2) + "\n")
+    print(json.dumps(summary, indent=2))
+    return 0
+
+
+def committed_traffic():
+    try:
+        return json.loads(PMC_TRAFFIC_FILE.read_text())
+    except (OSError, ValueError):
+        return None
+
+
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     parser.add_argument("--gpus", type=int, default=1)
@@ -205,11 +330,20 @@ def main() -> int:
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-gemm", action="store_true")
     parser.add_argument("--report", type=str, default="", help="write the detailed JSON report here")
+    parser.add_argument("--profile-pass", action="store_true",
+                        help="untimed dispatch sequence for rocprofv3 --pmc (calibration, 3 decode steps, GEMMs)")
+    parser.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                        help="turn two rocprofv3 --pmc counter_collection.csv files into the traffic file")
+    parser.add_argument("--traffic-out", type=str, default=str(PMC_TRAFFIC_FILE))
     args = parser.parse_args()
+    if args.summarize_pmc:
+        return summarize_pmc(args.summarize_pmc[0], args.summarize_pmc[1], args.traffic_out)
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported by this build "
               "(the W4G64 path has no multi-GPU component).", file=sys.stderr)
         return 2
+    if args.profile_pass:
+        return profile_pass()
 
     import torch
 
@@ -223,19 +357,9 @@ def main() -> int:
     log(f"device: {props.name} CUs={props.multi_processor_count}")
 
     # ---------------- decode workload ----------------
+    weights_np, copies, cases = decode_cases(torch, O, COPIES)
     shapes = O.QWEN2_SHAPES
-    weights_np = {name: O.symmetric_weights(n, k, O.BASE_SEED + n + k) for name, (n, k) in shapes.items()}
-    copies = {}
-    for name, (q, s, z) in weights_np.items():
-        base = (torch.from_numpy(q).cuda(), torch.from_numpy(s).cuda(), torch.from_numpy(z).cuda())
-        copies[name] = [tuple(t.clone() for t in base) for _ in range(COPIES)]
     distinct_mb = sum(sum(t.numel() * t.element_size() for t in c[0]) for c in copies.values()) * COPIES / 1e6
-    cases = []
-    for r_index, rows in enumerate(DECODE_ROWS):
-        for s_index, (name, (n, k)) in enumerate(shapes.items()):
-            x_np = O.activations(rows, k, seed=O.BASE_SEED + 1000 * rows + s_index, dtype="fp16")
-            cases.append({"name": name, "rows": rows, "n": n, "k": k, "x_np": x_np, "x": to_device(x_np, "fp16", torch),
-                          "copies": copies[name], "copy0": r_index, "bytes": algorithmic_bytes(rows, n, k)})
     step_bytes = sum(c["bytes"] for c in cases)
 
     # parity before timing
@@ -323,10 +447,18 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": None,
+            "traffic_source": None,
             "m1_mlp_GBps": round(m1_mlp_gbs, 2),
             "m1_mlp_frac": round(m1_mlp_gbs / HBM_PEAK_GBS, 4),
         },
     }
+
+    traffic = committed_traffic()
+    if traffic:
+        result["roofline"]["traffic"] = round(traffic["decode"]["traffic_bytes_per_launch"])
+        result["roofline"]["traffic_source"] = (f"{PMC_TRAFFIC_FILE.relative_to(REPO_ROOT)}: FETCH_SIZE + WRITE_SIZE "
+                                                f"per launch, scaled by the unpack-kernel calibration; algorithmic "
+                                                f"{traffic['decode']['algorithmic_bytes_per_launch']:.0f} B/launch")
 
     # ---------------- prefill GEMM ----------------
     if not args.no_gemm:
@@ -368,7 +500,8 @@ def main() -> int:
             "dtype": "bf16",
             "roofline": {"bound": "mfma", "kernel": "gemm2_kernel<bf16,128>", "achieved": round(tf, 2),
                          "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(tf / MFMA_PEAK_TFLOPS, 4),
-                         "traffic": None},
+                         "traffic": (round(traffic["gemm_2048"]["traffic_bytes_per_launch"])
+                                     if traffic and "gemm_2048" in traffic else None)},
             "per_shape": gemm_rows,
         }
 
