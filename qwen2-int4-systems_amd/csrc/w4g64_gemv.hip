@@ -46,6 +46,7 @@ constexpr int kWaves = 4;          // compute waves; one more wave stages the ac
 constexpr int kThreads = (kWaves + 1) * 64;
 constexpr int kMaxSteps = 16;      // group steps per lane in one workgroup
 constexpr int kStepBuckets[] = {2, 3, 6, 9, 12, 16};
+constexpr int kStageBatch = 8;    // activation items in flight per staging lane
 
 typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
 
@@ -116,31 +117,64 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
         }
     } else {
         // ---- staging wave: this workgroup's activations into LDS (slot order) ----
+        // Batches of kStageBatch items per lane: all loads of a batch are
+        // issued before any is consumed, so the wave has kStageBatch 16-byte
+        // loads in flight instead of one round trip per item.
         const int kbase = g0 * 64;
         const int items_per_row = cnt * 8;  // 8 values per item
-        for (int it = lane; it < a.M * items_per_row; it += 64) {
-            const int m = it / items_per_row;
-            const int c = it - m * items_per_row;
+        const int total = a.M * items_per_row;
+        for (int base = 0; base < total; base += 64 * kStageBatch) {
             if constexpr (XK != kF32) {
-                const u32x4 v = *(const u32x4*)((const uint16_t*)a.x + (int64_t)m * a.K + kbase + 8 * c);
-                *(u32x4*)(xs + m * row_stride + 8 * c) = permute_slots(v);
-            } else {
-                const float* src = (const float*)a.x + (int64_t)m * a.K + kbase + 8 * c;
-                const float4v f0 = *(const float4v*)src;
-                const float4v f1 = *(const float4v*)(src + 4);
-                uint16_t hi[8], mid[8], lo[8];
+                u32x4 v[kStageBatch];
 #pragma unroll
-                for (int e = 0; e < 8; ++e) split3_bf16(e < 4 ? f0[e] : f1[e - 4], hi[e], mid[e], lo[e]);
-                u32x4 ph, pm, pl;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    ph[e] = (uint32_t)hi[2 * e] | ((uint32_t)hi[2 * e + 1] << 16);
-                    pm[e] = (uint32_t)mid[2 * e] | ((uint32_t)mid[2 * e + 1] << 16);
-                    pl[e] = (uint32_t)lo[2 * e] | ((uint32_t)lo[2 * e + 1] << 16);
+                for (int u = 0; u < kStageBatch; ++u) {
+                    const int it = base + 64 * u + lane;
+                    const int itc = it < total ? it : total - 1;  // clamped: a valid address, result unused
+                    const int m = itc / items_per_row;
+                    const int c = itc - m * items_per_row;
+                    v[u] = *(const u32x4*)((const uint16_t*)a.x + (int64_t)m * a.K + kbase + 8 * c);
                 }
-                *(u32x4*)(xs + m * row_stride + 8 * c) = permute_slots(ph);
-                *(u32x4*)(xs + (a.M + m) * row_stride + 8 * c) = permute_slots(pm);
-                *(u32x4*)(xs + (2 * a.M + m) * row_stride + 8 * c) = permute_slots(pl);
+#pragma unroll
+                for (int u = 0; u < kStageBatch; ++u) {
+                    const int it = base + 64 * u + lane;
+                    if (it < total) {
+                        const int m = it / items_per_row;
+                        const int c = it - m * items_per_row;
+                        *(u32x4*)(xs + m * row_stride + 8 * c) = permute_slots(v[u]);
+                    }
+                }
+            } else {
+                float4v f[kStageBatch][2];
+#pragma unroll
+                for (int u = 0; u < kStageBatch; ++u) {
+                    const int it = base + 64 * u + lane;
+                    const int itc = it < total ? it : total - 1;
+                    const int m = itc / items_per_row;
+                    const int c = itc - m * items_per_row;
+                    const float* src = (const float*)a.x + (int64_t)m * a.K + kbase + 8 * c;
+                    f[u][0] = *(const float4v*)src;
+                    f[u][1] = *(const float4v*)(src + 4);
+                }
+#pragma unroll
+                for (int u = 0; u < kStageBatch; ++u) {
+                    const int it = base + 64 * u + lane;
+                    if (it >= total) continue;
+                    const int m = it / items_per_row;
+                    const int c = it - m * items_per_row;
+                    uint16_t hi[8], mid[8], lo[8];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) split3_bf16(e < 4 ? f[u][0][e] : f[u][1][e - 4], hi[e], mid[e], lo[e]);
+                    u32x4 ph, pm, pl;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        ph[e] = (uint32_t)hi[2 * e] | ((uint32_t)hi[2 * e + 1] << 16);
+                        pm[e] = (uint32_t)mid[2 * e] | ((uint32_t)mid[2 * e + 1] << 16);
+                        pl[e] = (uint32_t)lo[2 * e] | ((uint32_t)lo[2 * e + 1] << 16);
+                    }
+                    *(u32x4*)(xs + m * row_stride + 8 * c) = permute_slots(ph);
+                    *(u32x4*)(xs + (a.M + m) * row_stride + 8 * c) = permute_slots(pm);
+                    *(u32x4*)(xs + (2 * a.M + m) * row_stride + 8 * c) = permute_slots(pl);
+                }
             }
         }
         if constexpr (XK != kF16) {
@@ -150,7 +184,13 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
                 const int gl = idx - r * cnt;
                 const uint16_t* src = xs + r * row_stride + 64 * gl;
                 float s = 0.0f;
-                for (int k = 0; k < 64; ++k) s += bf16_bits_to_float(src[k]);
+#pragma unroll
+                for (int k = 0; k < 64; k += 8) {
+                    const u32x4 v = *(const u32x4*)(src + k);  // 16-byte LDS reads
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        s += __builtin_bit_cast(float, v[e] << 16) + __builtin_bit_cast(float, v[e] & 0xFFFF0000u);
+                }
                 sx[r * a.gps + gl] = s;
             }
         }
@@ -312,9 +352,51 @@ hipError_t launch_sw(const GemvArgs& args, const GemvPlan& plan, hipStream_t str
 
 }  // namespace
 
+namespace {
+constexpr int kRows16Buckets[] = {2, 3, 6, 9, 12, 18};  // steps of the 9..16-row kernel
+
+// 9..16 fp16/bf16 rows: one 16-feature block per workgroup, K split across
+// its waves (4, or 8 for long K); across workgroups only when a wave would
+// need more than 18 group steps.
+bool plan_rows16(int64_t rows, int64_t out_features, int64_t in_features, GemvPlan& plan) {
+    const int64_t groups = in_features / 64;
+    plan = GemvPlan{};
+    plan.kind = 1;
+    plan.waves = groups <= 48 ? 4 : 8;
+    plan.segments = 1;
+    plan.tiles = 1;
+    plan.n_blocks = (int)((out_features + 15) / 16);
+    int64_t splits = 1;
+    int64_t gps = groups;
+    while ((gps + plan.waves - 1) / plan.waves > 18) {
+        ++splits;
+        gps = (groups + splits - 1) / splits;
+    }
+    splits = (groups + gps - 1) / gps;
+    if (splits > 1 && plan.n_blocks > kGemvMaxColumnBlocks) return false;
+    plan.splits = (int)splits;
+    plan.groups_per_split = (int)gps;
+    const int64_t need = (gps + plan.waves - 1) / plan.waves;
+    plan.steps = 18;
+    for (int b : kRows16Buckets)
+        if (b >= need) {
+            plan.steps = b;
+            break;
+        }
+    plan.lds_bytes = 0;
+    plan.counter_bytes = splits > 1 ? kGemvCounterBytes : 0;
+    plan.workspace_bytes = splits > 1 ? plan.counter_bytes + splits * rows * out_features * 4 : 0;
+    return true;
+}
+}  // namespace
+
 GemvPlan plan_gemv(int64_t rows, int64_t out_features, int64_t in_features, int x_kind, int force_segments,
                    int force_splits) {
     GemvPlan plan{};
+    if (rows > 8 && rows <= 16 && (x_kind == kF16 || x_kind == kBF16) && force_segments <= 0 && force_splits <= 0 &&
+        plan_rows16(rows, out_features, in_features, plan))
+        return plan;
+    plan = GemvPlan{};
     const int64_t groups = in_features / 64;
     const int64_t parts = (x_kind == kF32) ? 3 : 1;
     const int64_t mv = rows * parts;
@@ -372,6 +454,10 @@ GemvPlan plan_gemv(int64_t rows, int64_t out_features, int64_t in_features, int 
 const char* gemv_kernel_name(const GemvPlan& plan, int x_kind) {
     static thread_local char name[64];
     static const char* kinds[] = {"?", "f16", "bf16", "f32"};
+    if (plan.kind == 1) {
+        snprintf(name, sizeof(name), "gemv16_kernel<%s,%d,%d>", kinds[x_kind & 3], plan.steps, plan.waves);
+        return name;
+    }
     snprintf(name, sizeof(name), "gemv_kernel<%s,%d,%d,%d>", kinds[x_kind & 3], plan.segments, plan.steps,
              plan.tiles);
     return name;
@@ -379,6 +465,7 @@ const char* gemv_kernel_name(const GemvPlan& plan, int x_kind) {
 
 hipError_t launch_gemv(const LinearProblem& p, const GemvPlan& plan, void* workspace, hipStream_t stream,
                        hipEvent_t start, hipEvent_t stop) {
+    if (plan.kind == 1) return launch_gemv16(p, plan, workspace, stream, start, stop);
     GemvArgs args{};
     args.x = p.x;
     args.qweight = p.qweight;

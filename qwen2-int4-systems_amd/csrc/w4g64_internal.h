@@ -32,9 +32,11 @@ constexpr int kGemvMaxRows = 16;
 constexpr int64_t kGemvCounterBytes = 64 * 1024;
 constexpr int64_t kGemvMaxColumnBlocks = kGemvCounterBytes / 4;  // 1,048,576 output features
 struct GemvPlan {
+    int kind;              // 0: segmented kernel (any rows); 1: 9..16-row kernel (fp16/bf16)
+    int waves;             // kind 1: waves per workgroup sharing one 16-feature block
     int segments;          // K segments per wave (16 / output features per wave)
     int steps;             // group steps per lane (compile-time bucket >= groups_per_split / segments)
-    int n_blocks;          // column blocks (4 * 16 / segments output features each)
+    int n_blocks;          // column blocks (kind 0: 4 * 16 / segments output features each; kind 1: 16)
     int splits;            // K splits across workgroups
     int groups_per_split;  // 64-wide K groups per split
     int tiles;             // 16-row MFMA A tiles (fp32 input uses 3 bf16 parts per row)
@@ -49,6 +51,8 @@ GemvPlan plan_gemv(int64_t rows, int64_t out_features, int64_t in_features, int 
 hipError_t launch_gemv(const LinearProblem& p, const GemvPlan& plan, void* workspace, hipStream_t stream,
                        hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
 const char* gemv_kernel_name(const GemvPlan& plan, int x_kind);
+hipError_t launch_gemv16(const LinearProblem& p, const GemvPlan& plan, void* workspace, hipStream_t stream,
+                         hipEvent_t start, hipEvent_t stop);
 
 // Prefill GEMM v2 (pipelined, fp16/bf16 activations).
 bool gemm2_supported(const LinearProblem& p);

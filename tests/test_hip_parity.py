@@ -280,6 +280,25 @@ def test_ragged_shapes(rows, n, k, dtype):
     check_linear(x, q, s, z, bias, n, k, dtype, bias_dtype="fp16")
 
 
+@pytest.mark.parametrize(
+    ("rows", "n", "k"),
+    [(9, 1536, 1536), (12, 256, 1536), (16, 8960, 1536), (16, 1536, 8960), (13, 72, 3072), (16, 40, 9280),
+     (10, 96, 64)],
+)
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+def test_decode_nine_to_sixteen_rows(rows, n, k, dtype):
+    """Rows 9..16 run the kernel that splits K across the waves of a workgroup;
+    k = 9280 (145 groups) also splits K across workgroups."""
+    from qwen_int4_hip import linear_kernel_name
+
+    assert linear_kernel_name(rows, n, k, torch.float16 if dtype == "fp16" else torch.bfloat16).startswith(
+        "gemv16_kernel")
+    q, s, z = weights("asym", n, k, rows * 7 + n + k)
+    x = O.activations(rows, k, seed=rows + 2 * n, dtype=dtype, outliers=True)
+    bias = O._from_f32(np.linspace(-0.5, 0.5, n, dtype=np.float32), dtype)
+    check_linear(x, q, s, z, bias, n, k, dtype, bias_dtype=dtype)
+
+
 def test_leading_dims_noncontiguous_and_empty_inputs():
     n, k = 96, 256
     q, s, z = weights("asym", n, k, 17)
