@@ -68,10 +68,13 @@ int w4g64_dequantize_canonical(const uint8_t* qweight, const uint16_t* scales, c
 
 /* Bytes of workspace w4g64_linear needs for this problem (0 = none).
  * Layout: a fixed 64 KiB area of per-column-block arrival counters, then the
- * fp32 split-K partial sums.  The counter area must be zero before the first
- * call and every call leaves it zero, so a caller allocates and clears one
- * workspace once (sized for its largest problem) and reuses it for every
- * shape.  Calls sharing a workspace must be ordered on one stream. */
+ * fp32 split-K partial sums (decode shapes that split K across workgroups;
+ * prefill shapes whose tiles do not fill whole rounds of the device's
+ * workgroup slots, up to 64 MiB of partials).  The counter area must be zero
+ * before the first call and every call leaves it zero, so a caller allocates
+ * and clears one workspace once (sized for its largest problem) and reuses it
+ * for every shape.  Calls sharing a workspace must be ordered on one stream.
+ * The prefill plan depends on the current device's CU count. */
 int64_t w4g64_linear_workspace_bytes(int64_t rows, int64_t out_features, int64_t in_features,
                                      int x_dtype);
 

@@ -79,7 +79,11 @@ int w4g64_dequantize_canonical(const uint8_t* qweight, const uint16_t* scales, c
 int64_t w4g64_linear_workspace_bytes(int64_t rows, int64_t out_features, int64_t in_features, int x_dtype) {
     if (rows <= 0 || out_features <= 0 || in_features <= 0 || in_features % 64) return 0;
     if (x_dtype != W4G64_DTYPE_F16 && x_dtype != W4G64_DTYPE_BF16 && x_dtype != W4G64_DTYPE_F32) return 0;
-    if (rows > w4g64::kGemvMaxRows) return 0;
+    if (rows > w4g64::kGemvMaxRows) {
+        w4g64::LinearProblem p{nullptr, x_dtype, nullptr, nullptr, nullptr, nullptr, 0, nullptr, rows, out_features,
+                               in_features};
+        return w4g64::gemm2_supported(p) ? w4g64::gemm2_workspace_bytes(rows, out_features, in_features) : 0;
+    }
     return w4g64::plan_gemv(rows, out_features, in_features, x_dtype).workspace_bytes;
 }
 
@@ -89,6 +93,15 @@ const char* w4g64_linear_kernel_name(int64_t rows, int64_t out_features, int64_t
     if (rows <= w4g64::kGemvMaxRows)
         return w4g64::gemv_kernel_name(w4g64::plan_gemv(rows, out_features, in_features, x_dtype), x_dtype);
     return w4g64::gemm_kernel_name(rows, out_features, in_features, x_dtype);
+}
+
+static int check_workspace(const void* workspace, int64_t have, int64_t need) {
+    if (need <= 0) return W4G64_STATUS_OK;
+    if (!workspace || have < need)
+        return fail(W4G64_STATUS_WORKSPACE, "workspace of %lld bytes required, got %lld", (long long)need,
+                    (long long)(workspace ? have : 0));
+    if (!aligned(workspace, 16)) return fail(W4G64_STATUS_WORKSPACE, "workspace must be 16-byte aligned");
+    return W4G64_STATUS_OK;
 }
 
 static int linear_impl(const void* x, int x_dtype, const uint8_t* qweight, const uint16_t* scales,
@@ -125,17 +138,16 @@ static int linear_impl(const void* x, int x_dtype, const uint8_t* qweight, const
             return fail(W4G64_STATUS_UNSUPPORTED, "decode path supports at most %lld output features",
                         (long long)(w4g64::kGemvMaxColumnBlocks * 64));
         const w4g64::GemvPlan plan = w4g64::plan_gemv(rows, out_features, in_features, x_dtype);
-        if (plan.workspace_bytes > 0) {
-            if (!workspace || workspace_bytes < plan.workspace_bytes)
-                return fail(W4G64_STATUS_WORKSPACE, "workspace of %lld bytes required, got %lld",
-                            (long long)plan.workspace_bytes, (long long)(workspace ? workspace_bytes : 0));
-            if (!aligned(workspace, 16)) return fail(W4G64_STATUS_WORKSPACE, "workspace must be 16-byte aligned");
-        }
+        if (int st = check_workspace(workspace, workspace_bytes, plan.workspace_bytes)) return st;
         return hip_status(w4g64::launch_gemv(p, plan, workspace, s, (hipEvent_t)start_event, (hipEvent_t)stop_event),
                           "gemv");
     }
-    if (w4g64::gemm2_supported(p))
-        return hip_status(w4g64::launch_gemm2(p, s, (hipEvent_t)start_event, (hipEvent_t)stop_event), "gemm");
+    if (w4g64::gemm2_supported(p)) {
+        const int64_t need = w4g64::gemm2_workspace_bytes(rows, out_features, in_features);
+        if (int st = check_workspace(workspace, workspace_bytes, need)) return st;
+        return hip_status(w4g64::launch_gemm2(p, workspace, s, (hipEvent_t)start_event, (hipEvent_t)stop_event),
+                          "gemm");
+    }
     return hip_status(w4g64::launch_gemm(p, s, (hipEvent_t)start_event, (hipEvent_t)stop_event), "gemm");
 }
 

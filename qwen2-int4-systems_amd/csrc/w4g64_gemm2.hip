@@ -61,7 +61,11 @@ struct Gemm2Args {
     int G;
     int tiles_m;
     int tiles_n;
-    int vec_out;  // y is 16-byte aligned and N % 8 == 0: 16-byte output stores
+    int vec_out;    // y is 16-byte aligned and N % 8 == 0: 16-byte output stores
+    int dp_tiles;   // tiles [0, dp_tiles): one workgroup each over the whole K range
+    int splits;     // tiles [dp_tiles, tiles): `splits` workgroups each, one K range apiece
+    int gps;        // groups per K range of a split tile
+    float* partials;  // [(tile - dp_tiles) * splits + piece][BM][kBN] fp32
 };
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
@@ -163,15 +167,28 @@ __global__ __launch_bounds__(256, 2) void gemm2_kernel(Gemm2Args a) {
     const int lane = tid & 63;
     const int wave = tid >> 6;
 
-    // ---- XCD-aware tile assignment ----
-    // Workgroup ids are dealt to the XCDs round robin (id % 8); give XCD x the
-    // contiguous tile range [start_x, start_x + count_x) -- a bijection.
-    const int tiles = a.tiles_m * a.tiles_n;
+    // ---- tile and K range of this workgroup ----
+    // Data-parallel tiles: workgroup ids are dealt to the XCDs round robin
+    // (id % 8); XCD x gets the contiguous tile range [start_x, start_x +
+    // count_x) -- a bijection on [0, dp_tiles) -- so an XCD's workgroups share
+    // activation row bands in their L2.  Split tiles follow: `splits`
+    // consecutive workgroups per tile, each over its own K range, writing fp32
+    // partial sums that a second kernel adds up in range order.
     const int bid = blockIdx.x;
-    const int xcd = bid % kXcds;
-    const int base = tiles / kXcds;
-    const int extra = tiles % kXcds;
-    const int t = xcd * base + (xcd < extra ? xcd : extra) + bid / kXcds;
+    int t, gbeg, gcnt, slot = -1;
+    if (bid < a.dp_tiles) {
+        const int xcd = bid % kXcds;
+        const int base = a.dp_tiles / kXcds;
+        const int extra = a.dp_tiles % kXcds;
+        t = xcd * base + (xcd < extra ? xcd : extra) + bid / kXcds;
+        gbeg = 0;
+        gcnt = a.G;
+    } else {
+        slot = bid - a.dp_tiles;
+        t = a.dp_tiles + slot / a.splits;
+        gbeg = (slot % a.splits) * a.gps;
+        gcnt = min(a.gps, a.G - gbeg);
+    }
     const int tile_m = t / a.tiles_n;
     const int tile_n = t - tile_m * a.tiles_n;
     const int64_t m0 = (int64_t)tile_m * BM;
@@ -186,7 +203,7 @@ __global__ __launch_bounds__(256, 2) void gemm2_kernel(Gemm2Args a) {
         const int chunk = (lane & 7) ^ a_swizzle(r);
         int64_t m = m0 + r;
         m = m < a.M ? m : a.M - 1;  // rows past M load a valid row; their outputs are not stored
-        a_src[d] = a.x + m * a.K + 8 * chunk;
+        a_src[d] = a.x + m * a.K + (int64_t)gbeg * 64 + 8 * chunk;
     }
     // weights: block bj, lane (j = lane % 32, q = lane / 32) -> column nw + 32 bj + j, bytes [16q, 16q + 16)
     const int j = lane & 31;
@@ -196,12 +213,12 @@ __global__ __launch_bounds__(256, 2) void gemm2_kernel(Gemm2Args a) {
     for (int bj = 0; bj < 2; ++bj) {
         int64_t n = nw + 32 * bj + j;
         n = n < a.N ? n : a.N - 1;
-        w_src[bj] = a.qweight + n * (a.K / 2) + 16 * q;
+        w_src[bj] = a.qweight + n * (a.K / 2) + (int64_t)gbeg * 32 + 16 * q;
     }
     // scale / zero of column nw + lane
     int64_t ncol = nw + lane;
     ncol = ncol < a.N ? ncol : a.N - 1;
-    const int64_t s_row = ncol * a.G;
+    const int64_t s_row = ncol * a.G + gbeg;  // scale / zero element of group gbeg
 
     auto issue = [&](int gg) {  // callers pass gg < G only
         unsigned char* st = smem[gg % kStages];
@@ -230,7 +247,7 @@ __global__ __launch_bounds__(256, 2) void gemm2_kernel(Gemm2Args a) {
 #pragma unroll
     for (int bj = 0; bj < 2; ++bj) {
         const int64_t n = nw + 32 * bj + j;
-        zpar[bj] = (int)(((n < a.N ? n : a.N - 1) * a.G) & 1);
+        zpar[bj] = (int)(((n < a.N ? n : a.N - 1) * a.G + gbeg) & 1);
     }
 
     // B fragments of step g, column block bj: this wave's packed columns,
@@ -302,7 +319,7 @@ __global__ __launch_bounds__(256, 2) void gemm2_kernel(Gemm2Args a) {
     // the number of operations issued after step s's (in-order completion).
     // Steps g + 3 < G run the branch-free body; the last (up to) three steps
     // the same body with the tighter waits and without refills.
-    const int G = a.G;
+    const int G = gcnt;  // steps of this workgroup's K range
     issue(0);
     if (G > 1) issue(1);
     if (G > 2) issue(2);
@@ -363,6 +380,21 @@ __global__ __launch_bounds__(256, 2) void gemm2_kernel(Gemm2Args a) {
     for (; g < G; ++g) step(g, std::true_type{});
     wait_vmcnt<0>();  // no DMA may still target this workgroup's LDS at exit
 
+    // ---- split tile: fp32 partial sums, added up by gemm2_reduce_kernel ----
+    // 32x32 accumulator layout (below); a store instruction writes two full
+    // 128-byte row segments.
+    if (slot >= 0) {
+        float* part = a.partials + (int64_t)slot * (BM * kBN) + 64 * wave + j;
+#pragma unroll
+        for (int bi = 0; bi < MB; ++bi)
+#pragma unroll
+            for (int bj = 0; bj < 2; ++bj)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    part[(32 * bi + 8 * (r / 4) + 4 * q + (r % 4)) * kBN + 32 * bj] = acc[bi][bj][r];
+        return;
+    }
+
     // ---- epilogue ----
     // 32x32 accumulator layout: column = lane % 32, row = 8 (r / 4) +
     // 4 (lane / 32) + r % 4.  Each wave stages its 64 output columns through
@@ -421,13 +453,140 @@ __global__ __launch_bounds__(256, 2) void gemm2_kernel(Gemm2Args a) {
     }
 }
 
+// Sum of the K-range partials of every split tile, in range order
+// (deterministic), plus bias, rounded to the output type.  One thread: 8
+// consecutive outputs of one tile row.
+template <int XK>
+__global__ __launch_bounds__(256) void gemm2_reduce_kernel(Gemm2Args a) {
+    constexpr int kPerTile = kBM * kBN / (256 * 8);  // workgroups per tile
+    const int idx = blockIdx.x / kPerTile;           // split tile index
+    const int e = ((blockIdx.x % kPerTile) * 256 + threadIdx.x) * 8;
+    const int row = e / kBN;
+    const int col = e % kBN;
+    const int t = a.dp_tiles + idx;
+    const int tile_m = t / a.tiles_n;
+    const int tile_n = t - tile_m * a.tiles_n;
+    const int64_t m = (int64_t)tile_m * kBM + row;
+    const int64_t n = (int64_t)tile_n * kBN + col;
+    if (m >= a.M || n >= a.N) return;
+    const float* src = a.partials + (int64_t)idx * a.splits * (kBM * kBN) + row * kBN + col;
+    float4v s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+    int piece = 0;
+    for (; piece + 4 <= a.splits; piece += 4) {  // four pieces' loads in flight, added in order
+        float4v v[4][2];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            v[u][0] = *(const float4v*)(src + (int64_t)(piece + u) * (kBM * kBN));
+            v[u][1] = *(const float4v*)(src + (int64_t)(piece + u) * (kBM * kBN) + 4);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            s0 += v[u][0];
+            s1 += v[u][1];
+        }
+    }
+    for (; piece < a.splits; ++piece) {
+        s0 += *(const float4v*)(src + (int64_t)piece * (kBM * kBN));
+        s1 += *(const float4v*)(src + (int64_t)piece * (kBM * kBN) + 4);
+    }
+    float out[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int64_t nn = n + i < a.N ? n + i : a.N - 1;
+        out[i] = (i < 4 ? s0[i] : s1[i - 4]) + load_bias(a.bias, a.bias_kind, nn);
+    }
+    uint16_t* y = (uint16_t*)a.y;
+    if (a.vec_out && n + 8 <= a.N) {
+        u32x4 v;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t lo = XK == kF16 ? float_to_half_bits(out[2 * i]) : float_to_bf16_bits(out[2 * i]);
+            const uint32_t hi = XK == kF16 ? float_to_half_bits(out[2 * i + 1]) : float_to_bf16_bits(out[2 * i + 1]);
+            v[i] = lo | (hi << 16);
+        }
+        *(u32x4*)(y + m * a.N + n) = v;
+    } else {
+        for (int i = 0; i < 8 && n + i < a.N; ++i) store_out<XK>(a.y, m * a.N + n + i, out[i]);
+    }
+}
+
+struct Gemm2Plan {
+    int tiles_m, tiles_n, dp_tiles, splits, gps, split_tiles;
+    int64_t partial_bytes;
+};
+
+// Workgroup slots of the device (two per CU), queried once per device.
+int gemm2_slots() {
+    static int slots[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+    if (slots[dev] == 0) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+        slots[dev] = 2 * cus;
+    }
+    return slots[dev];
+}
+
+// Choose data-parallel tiles and K splits.  Measured on MI355X: a K step
+// costs ~1.0 us with one workgroup per CU and ~1.54 us for the two that
+// share a CU; a round of workgroups costs ~6 us fixed (launch, pipeline
+// fill, epilogue); the reduction kernel ~2 us plus its partial-sum reads at
+// ~5 TB/s.  Full rounds of tiles stay data-parallel; the tiles of a last,
+// less than half full round -- or all tiles, when there are fewer than the
+// workgroup slots -- are split into the K-range count with the lowest
+// modelled time.
+Gemm2Plan plan_gemm2(int64_t rows, int64_t out_features, int64_t in_features) {
+    Gemm2Plan pl{};
+    pl.tiles_m = (int)((rows + kBM - 1) / kBM);
+    pl.tiles_n = (int)((out_features + kBN - 1) / kBN);
+    const int tiles = pl.tiles_m * pl.tiles_n;
+    const int G = (int)(in_features / 64);
+    const int slots = gemm2_slots();
+    const int cus = slots / 2;
+    int rem = tiles % slots;
+    if (tiles >= slots && (rem == 0 || 2 * rem > slots)) rem = 0;
+    pl.dp_tiles = tiles - rem;
+    pl.split_tiles = rem;
+    pl.splits = 1;
+    pl.gps = G;
+    if (rem > 0) {
+        auto step_us = [&](int wgs) { return wgs <= cus ? 1.0 : 1.54; };
+        double best = 6.0 + G * step_us(rem);  // unsplit
+        for (int sp = 2; sp <= G && rem * sp <= slots; ++sp) {
+            const int gps = (G + sp - 1) / sp;
+            const int used = (G + gps - 1) / gps;
+            const double t = 6.0 + gps * step_us(rem * used) + 2.0 + (double)rem * used * kBM * kBN * 4 / 5e6;
+            if (t < best) {
+                best = t;
+                pl.splits = used;
+                pl.gps = gps;
+            }
+        }
+    }
+    if (pl.splits == 1) {
+        pl.dp_tiles = tiles;
+        pl.split_tiles = 0;
+        pl.gps = G;
+    }
+    pl.partial_bytes = (int64_t)pl.split_tiles * pl.splits * kBM * kBN * 4;
+    return pl;
+}
+
 }  // namespace
+
+int64_t gemm2_workspace_bytes(int64_t rows, int64_t out_features, int64_t in_features) {
+    const Gemm2Plan pl = plan_gemm2(rows, out_features, in_features);
+    return pl.partial_bytes ? kGemvCounterBytes + pl.partial_bytes : 0;
+}
 
 bool gemm2_supported(const LinearProblem& p) {
     return (p.x_kind == kF16 || p.x_kind == kBF16);
 }
 
-hipError_t launch_gemm2(const LinearProblem& p, hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
+hipError_t launch_gemm2(const LinearProblem& p, void* workspace, hipStream_t stream, hipEvent_t start,
+                        hipEvent_t stop) {
+    const Gemm2Plan pl = plan_gemm2(p.rows, p.out_features, p.in_features);
     Gemm2Args args{};
     args.x = (const uint16_t*)p.x;
     args.qweight = p.qweight;
@@ -440,12 +599,29 @@ hipError_t launch_gemm2(const LinearProblem& p, hipStream_t stream, hipEvent_t s
     args.N = (int)p.out_features;
     args.K = (int)p.in_features;
     args.G = (int)(p.in_features / 64);
-    args.tiles_m = (int)((p.rows + kBM - 1) / kBM);
-    args.tiles_n = (int)((p.out_features + kBN - 1) / kBN);
+    args.tiles_m = pl.tiles_m;
+    args.tiles_n = pl.tiles_n;
     args.vec_out = (((uintptr_t)p.y & 15) == 0) && (p.out_features % 8 == 0);
-    dim3 grid((unsigned)(args.tiles_m * args.tiles_n));
-    if (p.x_kind == kF16) return launch_kernel(gemm2_kernel<kF16, kBM>, grid, dim3(256), 0, stream, start, stop, args);
-    return launch_kernel(gemm2_kernel<kBF16, kBM>, grid, dim3(256), 0, stream, start, stop, args);
+    args.dp_tiles = pl.dp_tiles;
+    args.splits = pl.splits;
+    args.gps = pl.gps;
+    // partials follow the workspace's counter area, which they must not touch
+    args.partials = pl.split_tiles ? (float*)((char*)workspace + kGemvCounterBytes) : nullptr;
+    const dim3 grid((unsigned)(pl.dp_tiles + pl.split_tiles * pl.splits));
+    const bool two = pl.split_tiles > 0;
+    constexpr int kPerTile = kBM * kBN / (256 * 8);
+    const dim3 rgrid((unsigned)(pl.split_tiles * kPerTile));
+    hipError_t err;
+    if (p.x_kind == kF16) {
+        err = launch_kernel(gemm2_kernel<kF16, kBM>, grid, dim3(256), 0, stream, start, two ? nullptr : stop, args);
+        if (err == hipSuccess && two)
+            err = launch_kernel(gemm2_reduce_kernel<kF16>, rgrid, dim3(256), 0, stream, nullptr, stop, args);
+    } else {
+        err = launch_kernel(gemm2_kernel<kBF16, kBM>, grid, dim3(256), 0, stream, start, two ? nullptr : stop, args);
+        if (err == hipSuccess && two)
+            err = launch_kernel(gemm2_reduce_kernel<kBF16>, rgrid, dim3(256), 0, stream, nullptr, stop, args);
+    }
+    return err;
 }
 
 }  // namespace w4g64

@@ -54,9 +54,14 @@ const char* gemv_kernel_name(const GemvPlan& plan, int x_kind);
 hipError_t launch_gemv16(const LinearProblem& p, const GemvPlan& plan, void* workspace, hipStream_t stream,
                          hipEvent_t start, hipEvent_t stop);
 
-// Prefill GEMM v2 (pipelined, fp16/bf16 activations).
+// Prefill GEMM v2 (pipelined, fp16/bf16 activations).  Tiles of a last,
+// mostly empty round of workgroups (or all tiles, when there are fewer than
+// the device's workgroup slots) are split along K; their fp32 partial sums
+// live in the workspace after the counter area and a second kernel adds
+// them up.
 bool gemm2_supported(const LinearProblem& p);
-hipError_t launch_gemm2(const LinearProblem& p, hipStream_t stream, hipEvent_t start = nullptr,
+int64_t gemm2_workspace_bytes(int64_t rows, int64_t out_features, int64_t in_features);
+hipError_t launch_gemm2(const LinearProblem& p, void* workspace, hipStream_t stream, hipEvent_t start = nullptr,
                         hipEvent_t stop = nullptr);
 
 // Prefill GEMM (rows > kGemvMaxRows).
