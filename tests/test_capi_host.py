@@ -76,7 +76,11 @@ def test_workspace_and_kernel_plan_queries():
     assert lib.w4g64_linear_workspace_bytes(4, 1536, 8960, _lib.DTYPE_F16) > 64 * 1024
     assert lib.w4g64_linear_workspace_bytes(16, 1536, 8960, _lib.DTYPE_F16) == 0
     assert lib.w4g64_linear_workspace_bytes(16, 40, 9280, _lib.DTYPE_BF16) == 64 * 1024 + 2 * 16 * 40 * 4
-    assert lib.w4g64_linear_workspace_bytes(2048, 8960, 1536, _lib.DTYPE_BF16) == 0
+    # prefill: 560 tiles of 128x256 on 512 workgroup slots (256 CUs, the default
+    # when no device answers): 512 data-parallel tiles, the other 48 split in 4
+    # K ranges with fp32 partials after the counter area; whole rounds need none
+    assert lib.w4g64_linear_workspace_bytes(2048, 8960, 1536, _lib.DTYPE_BF16) == 64 * 1024 + 48 * 4 * 128 * 256 * 4
+    assert lib.w4g64_linear_workspace_bytes(2048, 8192, 1536, _lib.DTYPE_BF16) == 0
     assert lib.w4g64_linear_workspace_bytes(1, 1536, 100, _lib.DTYPE_F16) == 0
     assert lib.w4g64_linear_kernel_name(1, 8960, 1536, _lib.DTYPE_F16).startswith(b"gemv_kernel<f16")
     assert lib.w4g64_linear_kernel_name(16, 1536, 8960, _lib.DTYPE_BF16) == b"gemv16_kernel<bf16,18,8>"
