@@ -15,8 +15,10 @@
 //     8 packed bytes it loads for its B column -- permuted into the slot
 //     order the nibble decode produces.  No staging wave, no workgroup barrier
 //     before the MFMAs;
-//   * all weight, scale, zero and activation loads of a lane are issued
-//     before the first MFMA, in step order, so step t waits only for its own;
+//   * all scale, zero, weight and activation loads of a lane are issued
+//     before the first MFMA (in that order), so the whole slice is in flight
+//     at once and the MFMA of step t waits only for loads issued before its
+//     own activations;
 //   * fp16: B = (code - zero) exact (1024 + n' magic, one v_pk_add_f16 per
 //     pair); bf16: B = 128 + n' exact, and the group result is corrected by
 //     -(136 + zero) * sum_k x[m,k]; that row sum comes from one more MFMA pair
@@ -70,51 +72,82 @@ __global__ __launch_bounds__(KW * 64) void gemv16_kernel(Gemv16Args a) {
     const uint16_t* xrow = (const uint16_t*)a.x + (int64_t)mrow * a.K + 16 * q;
     const int64_t sbase = (int64_t)nrow * a.G;
 
+    // Loads complete in order, so any use of a loaded value waits for every
+    // load issued before it.  All scale and zero loads go first (their decode
+    // may be scheduled early), then every weight load, then every activation
+    // load; no use is scheduled before the last load is issued.
+    // Long K ranges (more than 12 steps) load their activations in two
+    // phases, the second after the first half of the MFMAs, to stay within 256
+    // registers; the weights are always in flight at once.
+    constexpr int kPhases = STEPS > 12 ? 2 : 1;
+    constexpr int kChunk = (STEPS + kPhases - 1) / kPhases;
     u32x2 wq[STEPS];
-    u32x4 xa[STEPS][2];
-    float sc[STEPS];
-    int zr[STEPS];
+    uint32_t sraw[STEPS];
+    uint32_t zraw[STEPS];
+    auto group_of = [&](int t) {
+        const int gl = wave + KW * t;
+        return gl < cnt ? g0 + gl : g0;  // past the range: re-read group g0, zero scale below
+    };
 #pragma unroll
     for (int t = 0; t < STEPS; ++t) {
-        const int gl = wave + KW * t;
-        const int g = gl < cnt ? g0 + gl : g0;  // past the range: re-read group g0, zero scale below
-        wq[t] = __builtin_nontemporal_load((const u32x2*)(wrow + (int64_t)g * 32));
-        xa[t][0] = *(const u32x4*)(xrow + (int64_t)g * 64);
-        xa[t][1] = *(const u32x4*)(xrow + (int64_t)g * 64 + 8);
-        sc[t] = (nvalid && gl < cnt) ? half_bits_to_float(a.scales[sbase + g]) : 0.0f;
-        zr[t] = nibble_at(a.zeros, sbase + g);
+        const int64_t e = sbase + group_of(t);
+        sraw[t] = a.scales[e];
+        zraw[t] = (uint32_t)a.zeros[e >> 1] >> (4 * (e & 1));
     }
+#pragma unroll
+    for (int t = 0; t < STEPS; ++t)
+        wq[t] = __builtin_nontemporal_load((const u32x2*)(wrow + (int64_t)group_of(t) * 32));
 
     float4v acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int t = 0; t < STEPS; ++t) {
-        const u32x4 a0 = permute_slots(xa[t][0]);
-        const u32x4 a1 = permute_slots(xa[t][1]);
-        float4v d;
-        if constexpr (XK == kF16) {
-            const _Float16 zl = (_Float16)(1032 + zr[t]);
-            const _Float16 zh = (_Float16)(72 + zr[t]);
-            const half8 b0 = dequant8_f16_int(wq[t][0], half2v{zl, zl}, half2v{zh, zh});
-            const half8 b1 = dequant8_f16_int(wq[t][1], half2v{zl, zl}, half2v{zh, zh});
-            d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a0), b0, float4v{0.f, 0.f, 0.f, 0.f},
-                                                       0, 0, 0);
-            d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a1), b1, d, 0, 0, 0);
-        } else {
-            const bf16x8 b0 = dequant8_bf16_biased(wq[t][0]);
-            const bf16x8 b1 = dequant8_bf16_biased(wq[t][1]);
-            const bf16x8 ones = __builtin_bit_cast(bf16x8, u32x4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
-            d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a0), b0,
-                                                        float4v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-            d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a1), b1, d, 0, 0, 0);
-            float4v sx = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a0), ones,
-                                                                 float4v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-            sx = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a1), ones, sx, 0, 0, 0);
-            const float corr = 136.0f + (float)zr[t];
+    for (int ph = 0; ph < kPhases; ++ph) {
+        u32x4 xa[kChunk][2];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) d[r] = fmaf(-corr, sx[r], d[r]);
+        for (int c = 0; c < kChunk; ++c) {
+            const int t = ph * kChunk + c;
+            if (t < STEPS) {
+                xa[c][0] = *(const u32x4*)(xrow + (int64_t)group_of(t) * 64);
+                xa[c][1] = *(const u32x4*)(xrow + (int64_t)group_of(t) * 64 + 8);
+            }
         }
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) acc[r] = fmaf(sc[t], d[r], acc[r]);
+        for (int c = 0; c < kChunk; ++c) {
+            const int t = ph * kChunk + c;
+            if (t >= STEPS) continue;
+            const bool live = nvalid && wave + KW * t < cnt;
+            const float sct = live ? half_bits_to_float((uint16_t)sraw[t]) : 0.0f;
+            const int zn = (int)(zraw[t] & 0xF);
+            const int zrt = zn - ((zn & 8) << 1);
+            const u32x4 a0 = permute_slots(xa[c][0]);
+            const u32x4 a1 = permute_slots(xa[c][1]);
+            float4v d;
+            if constexpr (XK == kF16) {
+                const _Float16 zl = (_Float16)(1032 + zrt);
+                const _Float16 zh = (_Float16)(72 + zrt);
+                const half8 b0 = dequant8_f16_int(wq[t][0], half2v{zl, zl}, half2v{zh, zh});
+                const half8 b1 = dequant8_f16_int(wq[t][1], half2v{zl, zl}, half2v{zh, zh});
+                d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a0), b0,
+                                                           float4v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a1), b1, d, 0, 0, 0);
+            } else {
+                const bf16x8 b0 = dequant8_bf16_biased(wq[t][0]);
+                const bf16x8 b1 = dequant8_bf16_biased(wq[t][1]);
+                const bf16x8 ones =
+                    __builtin_bit_cast(bf16x8, u32x4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
+                d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a0), b0,
+                                                            float4v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a1), b1, d, 0, 0, 0);
+                float4v sx = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a0), ones,
+                                                                     float4v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                sx = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a1), ones, sx, 0, 0, 0);
+                const float corr = 136.0f + (float)zrt;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) d[r] = fmaf(-corr, sx[r], d[r]);
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[r] = fmaf(sct, d[r], acc[r]);
+        }
     }
 
     // ---- combine the waves' partial sums: D row = 4 q + r, column = j ----
