@@ -486,10 +486,11 @@ def build_c_oracle() -> Path:
 # ---------------------------------------------------------------------------
 
 def reference_linear_torch(x, qweight, scales, zeros, bias, *, out_features: int, in_features: int,
-                           group_size: int = 64):
+                           group_size: int = 64, return_f32: bool = False):
     """backends.py:73-98 over quantization.py:53-84 / :221-258, canonical
     packing, with torch CPU tensors: dequantize the whole weight to fp32,
-    fp32 matmul, fp32 bias, cast to ``x.dtype``."""
+    fp32 matmul, fp32 bias, cast to ``x.dtype`` (or kept in fp32 with
+    ``return_f32``, for error measurements)."""
     import torch
 
     groups = in_features // group_size
@@ -511,4 +512,5 @@ def reference_linear_torch(x, qweight, scales, zeros, bias, *, out_features: int
     output = x.reshape(-1, in_features).to(torch.float32) @ weight.t()
     if bias is not None:
         output = output + bias.to(torch.float32)
-    return output.reshape(*x.shape[:-1], out_features).to(x.dtype)
+    output = output.reshape(*x.shape[:-1], out_features)
+    return output if return_f32 else output.to(x.dtype)

@@ -11,11 +11,23 @@ from .kernels import (
     unpack_canonical_signed_int4_hip,
 )
 from .linear import QuantLinear
-from .quantization import PackingFormat
+from .quantization import (
+    PackingFormat,
+    dequantize_groupwise,
+    pack_int4,
+    quantize_asymmetric_rtn,
+    quantize_symmetric_rtn,
+    unpack_int4,
+)
 
 __all__ = [
     "PackingFormat",
     "QuantLinear",
+    "dequantize_groupwise",
+    "pack_int4",
+    "quantize_asymmetric_rtn",
+    "quantize_symmetric_rtn",
+    "unpack_int4",
     "SUPPORTED_BACKENDS",
     "dequantize_canonical_w4g64_hip",
     "hip_available",
