@@ -488,7 +488,7 @@ def build_c_oracle() -> Path:
 def reference_linear_torch(x, qweight, scales, zeros, bias, *, out_features: int, in_features: int,
                            group_size: int = 64, return_f32: bool = False):
     """backends.py:73-98 over quantization.py:53-84 / :221-258, canonical
-    packing, with torch CPU tensors: dequantize the whole weight to fp32,
+    packing, with torch tensors on any device: dequantize the whole weight to fp32,
     fp32 matmul, fp32 bias, cast to ``x.dtype`` (or kept in fp32 with
     ``return_f32``, for error measurements)."""
     import torch
@@ -499,7 +499,7 @@ def reference_linear_torch(x, qweight, scales, zeros, bias, *, out_features: int
         byte = packed.reshape(-1).to(torch.uint8)
         low = (byte & 0x0F).to(torch.int16)
         high = (byte >> 4).to(torch.int16)
-        out = torch.empty(byte.numel() * 2, dtype=torch.int8)
+        out = torch.empty(byte.numel() * 2, dtype=torch.int8, device=byte.device)
         out[0::2] = torch.where(low >= 8, low - 16, low).to(torch.int8)
         out[1::2] = torch.where(high >= 8, high - 16, high).to(torch.int8)
         return out[:count]
