@@ -25,6 +25,11 @@ Algorithmic bytes per call (M rows, N out, K in):
 The prefill GEMM (gate/up 8960x1536 and down 1536x8960 at rows 128/512/2048,
 bf16) is reported in the "gemm" object with its own roofline (MFMA bound).
 
+End to end ("e2e" object): the Qwen2-1.5B architecture with random-init
+weights over the HIP linears, batch 1, a 512-token random prompt, then 128
+greedy tokens with a static KV cache, each decode step one HIP graph replay:
+prefill and decode tokens/s.
+
 Weights and activations are generated on the GPU with the package's own
 quantizer (the mirror of src/qwen_int4/quantization.py).  The cpu_baseline
 leg runs the CPU restatement of the reference's torch backend on the host
@@ -363,6 +368,77 @@ def committed_traffic():
 
 
 # ---------------------------------------------------------------------------
+# End to end: Qwen2-1.5B architecture, 512-token prompt, 128 greedy tokens
+# ---------------------------------------------------------------------------
+
+QWEN2_1_5B = dict(hidden_size=1536, num_attention_heads=12, num_key_value_heads=2, head_dim=128,
+                  intermediate_size=8960, num_hidden_layers=28, vocab_size=151936, rms_norm_eps=1e-6,
+                  rope_theta=1_000_000.0)
+
+
+def build_model(torch, seed: int):
+    """Random-init Qwen2-1.5B (N(0, 0.02)); all 196 linears symmetric RTN W4G64."""
+    from types import SimpleNamespace
+
+    from qwen_int4_hip import QuantLinear, quantize_symmetric_rtn
+    from qwen_int4_hip.model import QwenInt4ForCausalLM
+
+    gen = torch.Generator(device="cuda").manual_seed(seed)
+    model = QwenInt4ForCausalLM(SimpleNamespace(**QWEN2_1_5B)).to("cuda")
+    with torch.no_grad():
+        emb = model.model.embed_tokens.weight
+        emb.copy_(torch.randn(emb.shape, generator=gen, device="cuda") * 0.02)
+        for module in model.modules():
+            if isinstance(module, QuantLinear):
+                w = torch.randn((module.out_features, module.in_features), generator=gen, device="cuda") * 0.02
+                q, s = quantize_symmetric_rtn(w, group_size=64)
+                module.qweight.copy_(q)
+                module.scales.copy_(s)
+                if module.bias is not None:
+                    module.bias.copy_(torch.randn(module.out_features, generator=gen, device="cuda") * 0.02)
+    return model.eval()
+
+
+def end_to_end(torch, prompt_len: int = 512, new_tokens: int = 128):
+    from qwen_int4_hip.generation import StaticGreedyDecoder
+
+    model = build_model(torch, BASE_SEED)
+    gen = torch.Generator().manual_seed(BASE_SEED + 4)
+    prompt = torch.randint(0, QWEN2_1_5B["vocab_size"], (1, prompt_len), generator=gen).cuda()
+    decoder = StaticGreedyDecoder(model, 1, prompt_len + new_tokens)
+    decoder.generate(prompt, 4)  # warm-up: kernels, workspaces, the decode-step graph
+    torch.cuda.synchronize()
+    decoder.length = 0
+    t0 = time.perf_counter()
+    decoder.prefill(prompt)
+    torch.cuda.synchronize()
+    prefill_s = time.perf_counter() - t0
+    tokens = [decoder.token.clone()]
+    t0 = time.perf_counter()
+    for _ in range(new_tokens - 1):
+        decoder.step()
+        tokens.append(decoder.token.clone())
+    torch.cuda.synchronize()
+    decode_s = time.perf_counter() - t0
+    linear_bytes = 28 * sum(algorithmic_bytes(1, n, k) for n, k in QWEN2_SHAPES.values())
+    head_bytes = QWEN2_1_5B["vocab_size"] * QWEN2_1_5B["hidden_size"] * 2
+    per_token = decode_s / (new_tokens - 1)
+    return {
+        "workload": (f"Qwen2-1.5B architecture (28 layers, hidden 1536, GQA 12/2 x 128, SwiGLU 8960, vocab 151936), "
+                     f"random-init N(0,0.02) weights, 196 symmetric RTN W4G64 linears, tied bf16 LM head; batch 1, "
+                     f"{prompt_len}-token random prompt then {new_tokens} greedy tokens, static KV cache, one HIP graph "
+                     f"replay per decode step"),
+        "prefill_ms": round(prefill_s * 1e3, 3),
+        "prefill_tokens_per_s": round(prompt_len / prefill_s, 1),
+        "decode_ms_per_token": round(per_token * 1e3, 4),
+        "decode_tokens_per_s": round(1.0 / per_token, 1),
+        "decode_weight_bytes_per_token": linear_bytes + head_bytes,
+        "decode_weight_GBps": round((linear_bytes + head_bytes) / per_token / 1e9, 1),
+        "generated_tokens": int(torch.cat(tokens, dim=1).numel()),
+    }
+
+
+# ---------------------------------------------------------------------------
 # main
 # ---------------------------------------------------------------------------
 
@@ -375,6 +451,7 @@ def main() -> int:
     parser.add_argument("--no-cpu-baseline", action="store_true",
                         help="skip the CPU baseline leg (and with it the parity check against the CPU reference)")
     parser.add_argument("--no-gemm", action="store_true")
+    parser.add_argument("--no-e2e", action="store_true", help="skip the end-to-end Qwen2-1.5B generation")
     parser.add_argument("--report", type=str, default="", help="write the detailed JSON report here")
     parser.add_argument("--profile-pass", action="store_true",
                         help="untimed dispatch sequence for rocprofv3 --pmc (calibration, 3 decode steps, GEMMs)")
@@ -539,6 +616,12 @@ def main() -> int:
                                      if gemm_traffic and "traffic_bytes_per_call" in gemm_traffic else None)},
             "per_shape": gemm_rows,
         }
+
+    if not args.no_e2e:
+        result["e2e"] = end_to_end(torch)
+        log(f"e2e: prefill {result['e2e']['prefill_ms']:.1f} ms ({result['e2e']['prefill_tokens_per_s']:.0f} tok/s), "
+            f"decode {result['e2e']['decode_ms_per_token']:.3f} ms/token ({result['e2e']['decode_tokens_per_s']:.0f} "
+            f"tok/s)")
 
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(cases, [c for c in gemm_cases if c["rows"] == 2048], torch)
