@@ -205,6 +205,27 @@ def kernel_durations(cases, reps, hip, torch):
     return durations
 
 
+def dense_library_gemm_ms(cases, torch, reps: int = 12):
+    """Median time (ms) of torch.matmul on each case's bf16 activations with a
+    dense bf16 [K, N] weight of the same shape: the vendor GEMM library's rate
+    on the same problem without dequantization (a calibration of what the
+    shapes allow, not a parity reference)."""
+    out = []
+    for c in cases:
+        x = c["x"]
+        w = torch.randn((c["k"], c["n"]), device="cuda", dtype=torch.float32).to(x.dtype).contiguous()
+        for _ in range(3):
+            torch.matmul(x, w)
+        events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+        for a, b in events:
+            a.record()
+            torch.matmul(x, w)
+            b.record()
+        torch.cuda.synchronize()
+        out.append(statistics.median(a.elapsed_time(b) for a, b in events))
+    return out
+
+
 # ---------------------------------------------------------------------------
 # CPU baseline (and the parity check against it)
 # ---------------------------------------------------------------------------
@@ -360,6 +381,79 @@ def summarize_pmc(fetch_csv: str, write_csv: str, out_path: str) -> int:
     return 0
 
 
+MFMA_PASS_COUNTERS = "GRBM_GUI_ACTIVE SQ_BUSY_CYCLES SQ_VALU_MFMA_BUSY_CYCLES SQ_BUSY_CU_CYCLES"
+XCDS = 8  # GRBM_GUI_ACTIVE is summed over the XCDs: cycles / XCDS / duration = shader clock
+
+
+def mfma_pass() -> int:
+    """Untimed dispatch sequence for rocprofv3 --pmc MFMA_PASS_COUNTERS: the
+    rows-2048 prefill GEMMs (4 calls per shape), then the same problems as
+    dense bf16 torch.matmul (4 calls per shape)."""
+    import torch
+
+    from qwen_int4_hip import hip_available, linear_canonical_w4g64_hip
+
+    if not hip_available():
+        raise SystemExit("bench.py needs a ROCm GPU and the built HIP library")
+    problems = []
+    for name in PREFILL_SHAPES:
+        n, k = QWEN2_SHAPES[name]
+        x = gen_activations(2048, k, BASE_SEED + 7 * 2048 + n, torch.bfloat16, torch)
+        problems.append((name, x, gen_weights(n, k, BASE_SEED + n + k, torch), n, k))
+    for _, x, w, _, _ in problems:
+        for _ in range(4):
+            linear_canonical_w4g64_hip(x, *w)
+    for _, x, _, n, k in problems:
+        dense = torch.randn((k, n), device="cuda", dtype=torch.float32).to(torch.bfloat16).contiguous()
+        for _ in range(4):
+            torch.matmul(x, dense)
+    torch.cuda.synchronize()
+    log(f"mfma pass done: {4 * len(problems)} W4G64 GEMM calls, {4 * len(problems)} dense bf16 matmuls")
+    return 0
+
+
+def summarize_mfma(csv_path: str, out_path: str, cus: int = 256) -> int:
+    """Per-kernel shader clock and MFMA busy fraction from an --mfma-pass
+    counter file: clock = GRBM_GUI_ACTIVE / XCDS / duration; MFMA busy =
+    SQ_VALU_MFMA_BUSY_CYCLES / (4 SIMDs x CUs x clock cycles)."""
+    import csv
+
+    per = {}
+    with open(csv_path, newline="") as fh:
+        for row in csv.DictReader(fh):
+            key = int(row["Dispatch_Id"])
+            d = per.setdefault(key, {"name": row["Kernel_Name"], "grid": row["Grid_Size"],
+                                     "ns": int(row["End_Timestamp"]) - int(row["Start_Timestamp"])})
+            d[row["Counter_Name"]] = d.get(row["Counter_Name"], 0.0) + float(row["Counter_Value"])
+    groups = {}
+    for key in sorted(per):
+        d = per[key]
+        if d.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0) <= 0:
+            continue
+        label = "W4G64 gemm2_kernel" if "gemm2_kernel" in d["name"] else d["name"].split("_MT")[0][:48]
+        groups.setdefault((label, d["grid"], d["SQ_VALU_MFMA_BUSY_CYCLES"]), []).append(d)
+    rows = []
+    for (label, grid, busy), ds in groups.items():
+        ds = ds[1:] if len(ds) > 1 else ds  # the first call of each group warms clocks and caches
+        ns = statistics.median(d["ns"] for d in ds)
+        cycles = statistics.median(d["GRBM_GUI_ACTIVE"] for d in ds) / XCDS
+        mfma_insts = busy / 32.0  # one v_mfma_*_32x32x16 bf16 keeps a SIMD busy for 32 cycles
+        flops = mfma_insts * 32 * 32 * 16 * 2
+        rows.append({"kernel": label, "grid": int(grid), "calls": len(ds), "duration_us": ns / 1e3,
+                     "clock_GHz": cycles / ns,
+                     "mfma_busy_frac": busy / (4 * cus * cycles), "flops": flops,
+                     "TFLOPs": flops / ns / 1e3, "frac_of_2p5PF": flops / ns / 1e3 / MFMA_PEAK_TFLOPS})
+    Path(out_path).parent.mkdir(parents=True, exist_ok=True)
+    Path(out_path).write_text(json.dumps(rows, indent=2) + "\n")
+    print("| kernel | grid (threads) | problem GFLOP | calls | duration (us) | clock (GHz) | MFMA busy | TFLOP/s | "
+          "of 2.5 PF |")
+    print("|---|---:|---:|---:|---:|---:|---:|---:|---:|")
+    for r in rows:
+        print(f"| {r['kernel']} | {r['grid']} | {r['flops'] / 1e9:.2f} | {r['calls']} | {r['duration_us']:.1f} | "
+              f"{r['clock_GHz']:.2f} | {r['mfma_busy_frac']:.1%} | {r['TFLOPs']:.0f} | {r['frac_of_2p5PF']:.1%} |")
+    return 0
+
+
 def committed_traffic():
     try:
         return json.loads(PMC_TRAFFIC_FILE.read_text())
@@ -458,15 +552,24 @@ def main() -> int:
     parser.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                         help="turn two rocprofv3 --pmc counter_collection.csv files into the traffic file")
     parser.add_argument("--traffic-out", type=str, default=str(PMC_TRAFFIC_FILE))
+    parser.add_argument("--mfma-pass", action="store_true",
+                        help=f"untimed rows-2048 GEMMs (W4G64, then dense bf16) for rocprofv3 --pmc "
+                             f"{MFMA_PASS_COUNTERS}")
+    parser.add_argument("--summarize-mfma", nargs=2, metavar=("COUNTER_CSV", "OUT_JSON"),
+                        help="shader clock and MFMA busy fraction per GEMM kernel from an --mfma-pass counter file")
     args = parser.parse_args()
     if args.summarize_pmc:
         return summarize_pmc(args.summarize_pmc[0], args.summarize_pmc[1], args.traffic_out)
+    if args.summarize_mfma:
+        return summarize_mfma(*args.summarize_mfma)
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported by this build "
               "(the W4G64 path has no multi-GPU component).", file=sys.stderr)
         return 2
     if args.profile_pass:
         return profile_pass()
+    if args.mfma_pass:
+        return mfma_pass()
 
     import torch
 
@@ -589,19 +692,25 @@ def main() -> int:
         for c in gemm_cases:
             c["out"] = linear_canonical_w4g64_hip(c["x"], *c["w"])
         gd = kernel_durations(gemm_cases, 8, hip, torch)
+        dense = dense_library_gemm_ms(gemm_cases, torch)
         gemm_rows = []
         flops_2048 = 0.0
         ms_2048 = 0.0
-        for c, d in zip(gemm_cases, gd):
+        dense_2048 = 0.0
+        for c, d, dense_ms in zip(gemm_cases, gd, dense):
             mean_ms = statistics.fmean(d)
             flops = 2.0 * c["rows"] * c["n"] * c["k"]
             tflops = flops / (mean_ms * 1e-3) / 1e12
             gemm_rows.append({"name": c["name"], "rows": c["rows"], "n": c["n"], "k": c["k"],
-                              "kernel_us_mean": mean_ms * 1e3, "TFLOPs": tflops})
-            log(f"  gemm {c['name']:9s} rows={c['rows']:4d}  {mean_ms * 1e3:8.2f} us  {tflops:7.1f} TFLOP/s")
+                              "kernel_us_mean": mean_ms * 1e3, "TFLOPs": tflops,
+                              "dense_bf16_library_us": dense_ms * 1e3,
+                              "dense_bf16_library_TFLOPs": flops / (dense_ms * 1e-3) / 1e12})
+            log(f"  gemm {c['name']:9s} rows={c['rows']:4d}  {mean_ms * 1e3:8.2f} us  {tflops:7.1f} TFLOP/s   "
+                f"(dense bf16 torch.matmul {dense_ms * 1e3:8.2f} us)")
             if c["rows"] == 2048:
                 flops_2048 += flops
                 ms_2048 += mean_ms
+                dense_2048 += dense_ms
         tf = flops_2048 / (ms_2048 * 1e-3) / 1e12
         gemm_traffic = traffic.get("gemm_2048") if traffic else None
         result["gemm"] = {
@@ -614,6 +723,9 @@ def main() -> int:
                          "frac": round(tf / MFMA_PEAK_TFLOPS, 4),
                          "traffic": (round(gemm_traffic["traffic_bytes_per_call"])
                                      if gemm_traffic and "traffic_bytes_per_call" in gemm_traffic else None)},
+            "dense_bf16_library_TFLOPs": round(flops_2048 / (dense_2048 * 1e-3) / 1e12, 2),
+            "dense_bf16_library": ("torch.matmul of the same bf16 activations with a dense bf16 [K, N] weight "
+                                   "(hipBLASLt): the vendor library's rate on the same shapes, without dequantization"),
             "per_shape": gemm_rows,
         }
 
