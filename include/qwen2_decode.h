@@ -1,0 +1,74 @@
+/*
+ * qwen2_decode.h -- C ABI of the fused decode-step kernels that sit between
+ * the W4G64 linears of a Qwen2 decoder layer (one token per sequence, bf16
+ * hidden states).  Same conventions as w4g64.h: plain device pointers, sizes,
+ * a HIP stream as `void*`, int status codes W4G64_STATUS_*, the message of a
+ * failed call in w4g64_last_error().  Nothing here allocates or synchronizes.
+ *
+ * With these, one decoder layer's decode step is eight launches:
+ *   add_rmsnorm -> W4G64 q|k|v (one N = (H + 2 KVH) * D launch, bias)
+ *   -> decode_attention -> W4G64 o_proj -> add_rmsnorm
+ *   -> W4G64 gate|up (one N = 2 I launch) -> silu_mul -> W4G64 down_proj (fp32 in).
+ */
+#ifndef QWEN_INT4_HIP_QWEN2_DECODE_H
+#define QWEN_INT4_HIP_QWEN2_DECODE_H
+
+#include <stdint.h>
+
+#include "w4g64.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Residual add + RMSNorm over `rows` rows of `hidden` bf16 values:
+ *   s        = x                                   (delta == NULL)
+ *            = bf16(x + bf16(delta))               (delta bf16 or fp32, as delta_dtype)
+ *   out_sum  = s                                   (may be NULL; may alias x)
+ *   out_norm = bf16(bf16(s * rsqrt(mean(s^2) + eps)) * weight)
+ * in fp32 arithmetic with the reference's two roundings.  hidden is a
+ * multiple of 8, at most 8192; all pointers 16-byte aligned.
+ * Replaces: RMSNorm.forward (src/qwen_int4/model.py:40-44) and the residual
+ *           adds of DecoderLayer.forward (model.py:149-154; the MLP output is
+ *           cast to bf16 first, model.py:136). */
+int qwen2_add_rmsnorm(const void* x, const void* delta, int delta_dtype, const void* weight, float eps,
+                      void* out_sum, void* out_norm, int64_t rows, int64_t hidden, void* stream);
+
+/* Bytes of workspace qwen2_decode_attention needs (arrival counters, then
+ * fp32 per-chunk partial results).  The counter area must be zero before the
+ * first call; every call leaves it zero.  Calls sharing a workspace must be
+ * ordered on one stream. */
+int64_t qwen2_decode_attention_workspace_bytes(int64_t batch, int64_t num_kv_heads, int64_t max_length);
+
+/* One decode step of grouped-query attention for `batch` sequences that all
+ * sit at the same position p = *position (a device int64; clamped to
+ * [0, max_length)):
+ *   qkv      bf16 [batch, (num_heads + 2 num_kv_heads) * head_dim]: the fused
+ *            q|k|v projection of the new token (bias included);
+ *   cos, sin bf16 [batch, head_dim]: the rotary factors of position p;
+ *   k_cache, v_cache bf16 [batch, num_kv_heads, max_length, head_dim].
+ * Rotates q and k as q * cos + rotate_half(q) * sin with bf16 rounding after
+ * each product and after the sum, writes the rotated key and the value at
+ * position p, and writes
+ *   out[b, h * head_dim + d] = bf16( softmax_t(q_h . k_t * scale) . v_t[d] ),
+ *   t = 0..p, query head h reading key/value head h / (num_heads / num_kv_heads),
+ * with fp32 scores, softmax and sums.  head_dim == 128,
+ * num_heads / num_kv_heads <= 8, max_length <= 17408.  The caches must be
+ * 16-byte aligned.
+ * Replaces: the rotary step and attention of QwenAttention.forward for one
+ *           cached token (src/qwen_int4/model.py:17-31, :61-122). */
+int qwen2_decode_attention(const void* qkv, const void* cos, const void* sin, void* k_cache, void* v_cache,
+                           const int64_t* position, void* out, int64_t batch, int64_t num_heads,
+                           int64_t num_kv_heads, int64_t head_dim, int64_t max_length, float scale,
+                           void* workspace, int64_t workspace_bytes, void* stream);
+
+/* out[r, i] = silu(gate) * up in fp32, gate = gate_up[r, i], up = gate_up[r, I + i]
+ * (bf16 inputs, the fused gate|up projection), silu(x) = x / (1 + exp(-x)).
+ * Replaces: the SwiGLU product of QwenMLP.forward (src/qwen_int4/model.py:133-136). */
+int qwen2_silu_mul(const void* gate_up, float* out, int64_t rows, int64_t intermediate, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QWEN_INT4_HIP_QWEN2_DECODE_H */

@@ -1,0 +1,552 @@
+// Fused decode-step kernels between the W4G64 linears of a Qwen2 decoder
+// layer (C ABI in include/qwen2_decode.h).  One token per sequence, bf16
+// hidden states; each kernel restates a block of src/qwen_int4/model.py with
+// the reference's roundings:
+//
+//   add_rmsnorm_kernel  one workgroup per row: residual add, fp32 sum of
+//                       squares, bf16(bf16(s * rsqrt(mean + eps)) * w)
+//                       (model.py:40-44, :149-154).
+//   attention_kernel    one workgroup per (sequence, key/value head, chunk of
+//                       64 positions).  It rotates the group's query heads
+//                       (and, in the chunk that holds the new position, the
+//                       new key, which it also writes to the cache with the
+//                       new value), stages the chunk's keys and values in LDS
+//                       (16-byte loads, rows padded to 272 B), computes fp32
+//                       scores, the chunk's softmax maximum and sum and its
+//                       probability-weighted value sums.  The last workgroup
+//                       of a (sequence, head) to arrive merges the chunks
+//                       (rescaled by exp(m_chunk - m)) and writes bf16
+//                       (model.py:61-122).
+//   silu_mul_kernel     silu(gate) * up in fp32 (model.py:133-136).
+//
+// The new key at position p is read by the chunk that holds p from LDS, never
+// from the cache, so no workgroup reads a cache row another one is writing.
+#include <math.h>
+#include <stdarg.h>
+
+#include "../../include/qwen2_decode.h"
+#include "w4g64_device.h"
+#include "w4g64_internal.h"
+
+namespace w4g64 {
+namespace {
+
+constexpr int kNormThreads = 256;
+constexpr int kNormIters = 4;  // hidden <= 256 threads x 8 elements x 4 = 8192
+
+constexpr int kHeadDim = 128;
+constexpr int kChunk = 64;        // positions per attention workgroup (one per lane of a wave)
+constexpr int kMaxGroup = 8;      // query heads per key/value head
+constexpr int kAttnThreads = 256;
+constexpr int kRowStride = kHeadDim + 8;  // bf16 elements per staged row (272 B)
+constexpr int kPartFloats = 2 * kMaxGroup + kMaxGroup * kHeadDim;  // m[8], l[8], acc[8][128]
+constexpr int kMergeBatch = 16;   // chunks whose partial sums one merge pass loads together
+// The merge keeps per-chunk statistics in the staging rows' LDS.
+constexpr int kMaxChunks = (kChunk * kRowStride * 2) / (2 * kMaxGroup * 4);
+constexpr int kMaxLength = kMaxChunks * kChunk;
+
+__device__ __forceinline__ float bf16_round(float v) { return bf16_bits_to_float(float_to_bf16_bits(v)); }
+
+// Thread t owns the 8-element pieces 8 t + 2048 i (i < kNormIters).  Every
+// load is unconditional at a clamped address and issued before any use (a
+// guarded load would be waited for on its own); pieces past the row end are
+// masked out of the sum and not stored.
+__global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(const uint16_t* x, const void* delta,
+                                                                   int delta_kind, const uint16_t* weight,
+                                                                   float eps, uint16_t* out_sum,
+                                                                   uint16_t* out_norm, int hidden) {
+    constexpr int kStride = kNormThreads * 8;
+    const int64_t base = (int64_t)blockIdx.x * hidden;
+    int col[kNormIters];
+    u32x4 xr[kNormIters], wr[kNormIters], dr[kNormIters][2];
+#pragma unroll
+    for (int i = 0; i < kNormIters; ++i) {
+        col[i] = 8 * (int)threadIdx.x + kStride * i;
+        const int c = min(col[i], hidden - 8);
+        xr[i] = *(const u32x4*)(x + base + c);
+        wr[i] = *(const u32x4*)(weight + c);
+        if (delta_kind == kBF16) {
+            dr[i][0] = *(const u32x4*)((const uint16_t*)delta + base + c);
+        } else if (delta_kind == kF32) {
+            dr[i][0] = *(const u32x4*)((const float*)delta + base + c);
+            dr[i][1] = *(const u32x4*)((const float*)delta + base + c + 4);
+        }
+    }
+    float v[kNormIters][8];
+    float sq = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kNormIters; ++i) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const uint32_t xw = xr[i][e / 2];
+            float s = bf16_bits_to_float(e & 1 ? xw >> 16 : xw & 0xFFFFu);
+            if (delta_kind == kBF16) {
+                const uint32_t dw = dr[i][0][e / 2];
+                s = bf16_round(s + bf16_bits_to_float(e & 1 ? dw >> 16 : dw & 0xFFFFu));
+            } else if (delta_kind == kF32) {
+                // (a scalar copy first: bit_cast of a vector element lvalue reads element 0)
+                const uint32_t bits = dr[i][e / 4][e % 4];
+                s = bf16_round(s + bf16_round(__builtin_bit_cast(float, bits)));
+            }
+            v[i][e] = s;
+            // the square is rounded before it is summed, as x.pow(2) is
+            if (col[i] < hidden) sq += __fmul_rn(s, s);
+        }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) sq += __shfl_xor(sq, off);
+    __shared__ float red[kNormThreads / 64];
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = sq;
+    __syncthreads();
+    float total = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kNormThreads / 64; ++w) total += red[w];
+    const float r = rsqrtf(total / (float)hidden + eps);
+#pragma unroll
+    for (int i = 0; i < kNormIters; ++i) {
+        if (col[i] >= hidden) continue;
+        u32x4 so, no;
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
+            const uint32_t ww = wr[i][e / 2];
+            const float n0 = bf16_round(v[i][e] * r) * bf16_bits_to_float(ww & 0xFFFFu);
+            const float n1 = bf16_round(v[i][e + 1] * r) * bf16_bits_to_float(ww >> 16);
+            so[e / 2] = float_to_bf16_bits(v[i][e]) | ((uint32_t)float_to_bf16_bits(v[i][e + 1]) << 16);
+            no[e / 2] = float_to_bf16_bits(n0) | ((uint32_t)float_to_bf16_bits(n1) << 16);
+        }
+        if (out_sum) *(u32x4*)(out_sum + base + col[i]) = so;
+        *(u32x4*)(out_norm + base + col[i]) = no;
+    }
+}
+
+struct AttnArgs {
+    const uint16_t* qkv;
+    const uint16_t* cos;
+    const uint16_t* sin;
+    uint16_t* k_cache;
+    uint16_t* v_cache;
+    const int64_t* position;
+    uint16_t* out;
+    int heads;
+    int kv_heads;
+    int max_len;
+    int chunks;
+    float scale;
+    unsigned* counters;  // [batch * kv_heads]
+    float* partials;     // [batch * kv_heads][chunks][kPartFloats]
+};
+
+// Element d of the rotated head vector: x * cos + rotate_half(x) * sin, with
+// rotate_half(x)[d] = -x[d + D/2] (d < D/2) or x[d - D/2], each product and
+// the sum rounded to bf16 (bf16 tensor arithmetic, model.py:17-19, :76-77).
+// x = vec[d], other = vec[d ^ D/2], c = cos[d], n = sin[d] (bf16 bits).
+__device__ __forceinline__ float rope_elem(uint16_t x, uint16_t other, uint16_t c, uint16_t n, int d) {
+    const float partner = d < kHeadDim / 2 ? -bf16_bits_to_float(other) : bf16_bits_to_float(other);
+    const float a = bf16_round(bf16_bits_to_float(x) * bf16_bits_to_float(c));
+    const float b = bf16_round(partner * bf16_bits_to_float(n));
+    return bf16_round(a + b);
+}
+
+// Wave-wide max / sum by DPP (quad swaps, half-row and row mirrors, row
+// broadcasts 15 and 31: lane 63 ends with the result), then a read of lane 63.
+__device__ __forceinline__ float dpp_step(float v, int ctrl_kind) {
+    const int x = __builtin_bit_cast(int, v);
+    int y;
+    switch (ctrl_kind) {
+        case 0: y = __builtin_amdgcn_update_dpp(x, x, 0xB1, 0xF, 0xF, false); break;   // quad_perm [1,0,3,2]
+        case 1: y = __builtin_amdgcn_update_dpp(x, x, 0x4E, 0xF, 0xF, false); break;   // quad_perm [2,3,0,1]
+        case 2: y = __builtin_amdgcn_update_dpp(x, x, 0x141, 0xF, 0xF, false); break;  // row_half_mirror
+        case 3: y = __builtin_amdgcn_update_dpp(x, x, 0x140, 0xF, 0xF, false); break;  // row_mirror
+        case 4: y = __builtin_amdgcn_update_dpp(x, x, 0x142, 0xA, 0xF, false); break;  // row_bcast15 -> rows 1, 3
+        default: y = __builtin_amdgcn_update_dpp(x, x, 0x143, 0xC, 0xF, false); break; // row_bcast31 -> rows 2, 3
+    }
+    return __builtin_bit_cast(float, y);
+}
+__device__ __forceinline__ float wave_max(float v) {
+    // lanes outside a row mask receive `old` = their own value: max is unchanged
+#pragma unroll
+    for (int k = 0; k < 6; ++k) v = fmaxf(v, dpp_step(v, k));
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) v += dpp_step(v, k);  // every lane: its row's sum
+    // rows 1 and 3 add the sums of rows 0 and 2, then rows 2 and 3 add row 1's
+    // (lanes outside the row mask receive the `old` operand, 0)
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x142, 0xA, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x143, 0xC, 0xF, false));
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
+// MFMA layout (v_mfma_f32_16x16x32_bf16): lane l = 16 q + j supplies A row j
+// and B column j with the 8 values of K slots [8 q, 8 q + 8); it receives
+// D[4 q + r][j], r < 4.
+//   scores: A = rotated queries (row = head, K = dimension), B = staged keys
+//           (column = position): wave w scores positions 16 w .. 16 w + 15,
+//           four MFMAs over the 128 dimensions;
+//   sums:   A = probabilities (row = head, K = position), split exactly enough
+//           into bf16 hi + lo, B = staged values transposed (column =
+//           dimension): wave w owns dimensions 32 w .. 32 w + 31, eight MFMAs.
+__global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
+    __shared__ __attribute__((aligned(16))) uint16_t qsb[16][kRowStride];     // rotated queries, bf16
+    __shared__ __attribute__((aligned(16))) uint16_t ks[kChunk][kRowStride];  // keys [position][dim]
+    __shared__ __attribute__((aligned(16))) uint16_t vt[kHeadDim][kChunk + 8];  // values [dim][position]
+    __shared__ __attribute__((aligned(16))) float pr[kMaxGroup][kChunk + 4];    // scores, then exp(s - m)
+    __shared__ float stat_m[kMaxGroup];
+    __shared__ float stat_l[kMaxGroup];
+    __shared__ int s_last;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int chunk = blockIdx.x % a.chunks;
+    const int kvh = (blockIdx.x / a.chunks) % a.kv_heads;
+    const int b = blockIdx.x / (a.chunks * a.kv_heads);
+    const int group = a.heads / a.kv_heads;
+    const uint16_t* qkv = a.qkv + (int64_t)b * (a.heads + 2 * a.kv_heads) * kHeadDim;
+    const uint16_t* cs = a.cos + (int64_t)b * kHeadDim;
+    const uint16_t* sn = a.sin + (int64_t)b * kHeadDim;
+    const int slot = b * a.kv_heads + kvh;
+    const int64_t cache_base = (int64_t)slot * a.max_len * kHeadDim;
+    float* part = a.partials + ((int64_t)slot * a.chunks + chunk) * kPartFloats;
+    const int mj = lane & 15;  // MFMA row / column of this lane
+    const int mq = lane >> 4;  // MFMA K-slot quarter of this lane
+
+    // ---- loads that do not depend on the position: queries, rotary factors, new key/value ----
+    constexpr int kQItems = kMaxGroup * kHeadDim / kAttnThreads;
+    uint16_t qx[kQItems], qp[kQItems], qc[kQItems], qn[kQItems];
+#pragma unroll
+    for (int i = 0; i < kQItems; ++i) {
+        const int e = tid + kAttnThreads * i;
+        const int g = min(e / kHeadDim, group - 1);
+        const int dd = e % kHeadDim;
+        const uint16_t* vec = qkv + (kvh * group + g) * kHeadDim;
+        qx[i] = vec[dd];
+        qp[i] = vec[dd ^ (kHeadDim / 2)];  // rotate_half partner
+        qc[i] = cs[dd];
+        qn[i] = sn[dd];
+    }
+    const uint16_t* kvec = qkv + (a.heads + kvh) * kHeadDim;
+    const int dk = tid % kHeadDim;
+    const uint16_t kx = kvec[dk];
+    const uint16_t kp = kvec[dk ^ (kHeadDim / 2)];
+    const uint16_t vx = qkv[(a.heads + a.kv_heads + kvh) * kHeadDim + dk];
+    int64_t p64 = *a.position;
+    p64 = p64 < 0 ? 0 : (p64 >= a.max_len ? a.max_len - 1 : p64);
+    const int pos = (int)p64;
+    const int t0 = chunk * kChunk;
+    const int nk = min(kChunk, pos + 1 - t0);  // positions of this chunk that are attended (<= 0: none)
+
+    if (nk > 0) {
+        // cached rows t0 .. t0 + cached - 1: piece e = tid + 256 i -> row e / 16, 16-byte column e % 16;
+        // rows past `cached` re-read a valid row of this chunk and are not used
+        const int cached = min(nk, pos - t0);
+        constexpr int kPieces = kChunk * (kHeadDim / 8) / kAttnThreads;
+        u32x4 kr[kPieces], vr[kPieces];
+#pragma unroll
+        for (int i = 0; i < kPieces; ++i) {
+            const int e = tid + kAttnThreads * i;
+            const int r = min(e / (kHeadDim / 8), max(cached - 1, 0));
+            const int64_t off = cache_base + (int64_t)(t0 + r) * kHeadDim + 8 * (e % (kHeadDim / 8));
+            kr[i] = *(const u32x4*)(a.k_cache + off);
+            vr[i] = *(const u32x4*)(a.v_cache + off);
+        }
+#pragma unroll
+        for (int i = 0; i < kQItems; ++i) {
+            const int e = tid + kAttnThreads * i;
+            if (e / kHeadDim < group)
+                qsb[e / kHeadDim][e % kHeadDim] = float_to_bf16_bits(rope_elem(qx[i], qp[i], qc[i], qn[i], e % kHeadDim));
+        }
+        if (pos - t0 < kChunk && tid < kHeadDim) {  // this chunk holds the new position
+            // qc[0] / qn[0] hold cos / sin of dimension (tid + 0) % 128 = tid
+            const uint16_t kb = float_to_bf16_bits(rope_elem(kx, kp, qc[0], qn[0], tid));
+            a.k_cache[cache_base + (int64_t)pos * kHeadDim + tid] = kb;
+            a.v_cache[cache_base + (int64_t)pos * kHeadDim + tid] = vx;
+            ks[pos - t0][tid] = kb;
+            vt[tid][pos - t0] = vx;
+        }
+#pragma unroll
+        for (int i = 0; i < kPieces; ++i) {
+            const int e = tid + kAttnThreads * i;
+            const int r = e / (kHeadDim / 8);
+            const int c = e % (kHeadDim / 8);
+            if (r < cached) {
+                *(u32x4*)&ks[r][8 * c] = kr[i];
+#pragma unroll
+                for (int h = 0; h < 8; ++h) vt[8 * c + h][r] = (uint16_t)(vr[i][h / 2] >> (16 * (h & 1)));
+            } else if (r >= nk) {  // unattended positions: zero values (their probability is 0)
+#pragma unroll
+                for (int h = 0; h < 8; ++h) vt[8 * c + h][r] = 0;
+            }
+        }
+        __syncthreads();
+
+        // ---- scores (MFMA): wave w, positions 16 w + mj ----
+        {
+            float4v sacc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int sl = 0; sl < kHeadDim / 32; ++sl) {
+                const u32x4 av = *(const u32x4*)&qsb[mj][32 * sl + 8 * mq];
+                const u32x4 bv = *(const u32x4*)&ks[16 * wave + mj][32 * sl + 8 * mq];
+                sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, av),
+                                                               __builtin_bit_cast(bf16x8, bv), sacc, 0, 0, 0);
+            }
+            const int j = 16 * wave + mj;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int g = 4 * mq + r;
+                if (g < group) pr[g][j] = j < nk ? sacc[r] * a.scale : -INFINITY;
+            }
+        }
+        __syncthreads();
+
+        // ---- chunk softmax statistics: wave w takes heads w, w + 4; lane = position ----
+        for (int g = wave; g < group; g += kAttnThreads / 64) {
+            const float sv = pr[g][lane];
+            const float m = wave_max(sv);
+            const float e = lane < nk ? expf(sv - m) : 0.0f;
+            pr[g][lane] = e;
+            const float l = wave_sum(e);
+            if (lane == 0) {
+                stat_m[g] = m;
+                stat_l[g] = l;
+            }
+        }
+        __syncthreads();
+
+        // ---- probability-weighted value sums (MFMA): wave w, dimensions 32 w .. 32 w + 31 ----
+        float4v oacc[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
+#pragma unroll
+        for (int sl = 0; sl < kChunk / 32; ++sl) {
+            u32x4 phi = {0u, 0u, 0u, 0u}, plo = {0u, 0u, 0u, 0u};
+            if (mj < group) {
+                const float4v p0 = *(const float4v*)&pr[mj][32 * sl + 8 * mq];
+                const float4v p1 = *(const float4v*)&pr[mj][32 * sl + 8 * mq + 4];
+#pragma unroll
+                for (int h = 0; h < 4; ++h) {
+                    const float x0 = h < 2 ? p0[2 * h] : p1[2 * h - 4];
+                    const float x1 = h < 2 ? p0[2 * h + 1] : p1[2 * h - 3];
+                    const uint16_t h0 = float_to_bf16_bits(x0), h1 = float_to_bf16_bits(x1);
+                    const uint16_t l0 = float_to_bf16_bits(x0 - bf16_bits_to_float(h0));
+                    const uint16_t l1 = float_to_bf16_bits(x1 - bf16_bits_to_float(h1));
+                    phi[h] = (uint32_t)h0 | ((uint32_t)h1 << 16);
+                    plo[h] = (uint32_t)l0 | ((uint32_t)l1 << 16);
+                }
+            }
+#pragma unroll
+            for (int cb = 0; cb < 2; ++cb) {
+                const u32x4 bv = *(const u32x4*)&vt[32 * wave + 16 * cb + mj][32 * sl + 8 * mq];
+                oacc[cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, phi),
+                                                                   __builtin_bit_cast(bf16x8, bv), oacc[cb], 0, 0, 0);
+                oacc[cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, plo),
+                                                                   __builtin_bit_cast(bf16x8, bv), oacc[cb], 0, 0, 0);
+            }
+        }
+        // partials travel through device-coherent atomic stores (the merging
+        // workgroup may run on another XCD)
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int g = 4 * mq + r;
+                if (g < group)
+                    __hip_atomic_store(part + 2 * kMaxGroup + g * kHeadDim + 32 * wave + 16 * cb + mj, oacc[cb][r],
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        if (tid < group) {
+            __hip_atomic_store(part + tid, stat_m[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(part + kMaxGroup + tid, stat_l[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+
+    // ---- arrival: the last workgroup of this (sequence, head) merges ----
+    // The wait completes this workgroup's partial stores before its arrival
+    // is counted; the merger loads only after its counter update returned.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0) {
+        const unsigned prev = __hip_atomic_fetch_add(a.counters + slot, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = prev == (unsigned)a.chunks - 1u;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    // Every device-coherent load travels to memory, so the merge issues all of
+    // them at once: the statistics into LDS and, per thread (dimension d,
+    // heads g0, g0 + 2, ...), the weighted sums of up to kMergeBatch chunks.
+    const int d = tid % kHeadDim;
+    const int g0 = tid / kHeadDim;
+    const int used = pos / kChunk + 1;  // chunks that hold positions 0..pos (all wrote partials)
+    const float* base = a.partials + (int64_t)slot * a.chunks * kPartFloats;
+    float v[kMergeBatch][kMaxGroup / 2];
+    auto load_batch = [&](int c0) {
+#pragma unroll
+        for (int u = 0; u < kMergeBatch; ++u)
+#pragma unroll
+            for (int i = 0; i < kMaxGroup / 2; ++i)
+                v[u][i] = (c0 + u < used && g0 + 2 * i < group)
+                              ? __hip_atomic_load(base + (c0 + u) * kPartFloats + 2 * kMaxGroup +
+                                                      (g0 + 2 * i) * kHeadDim + d,
+                                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                              : 0.0f;
+    };
+    load_batch(0);
+    float* stats = (float*)&ks[0][0];    // [used][2 * kMaxGroup]: m, l per head
+    float* scale_c = (float*)&vt[0][0];  // [used][kMaxGroup]: exp(m_c - m) / l
+    for (int e = tid; e < used * 2 * kMaxGroup; e += kAttnThreads)
+        stats[e] = __hip_atomic_load(base + (e / (2 * kMaxGroup)) * kPartFloats + e % (2 * kMaxGroup),
+                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    __shared__ float head_m[kMaxGroup], head_l[kMaxGroup];
+    if (tid < group) {
+        float m = -INFINITY;
+        for (int c = 0; c < used; ++c) m = fmaxf(m, stats[c * 2 * kMaxGroup + tid]);
+        float l = 0.0f;
+        for (int c = 0; c < used; ++c)
+            l = fmaf(stats[c * 2 * kMaxGroup + kMaxGroup + tid], expf(stats[c * 2 * kMaxGroup + tid] - m), l);
+        head_m[tid] = m;
+        head_l[tid] = l;
+    }
+    __syncthreads();
+    for (int e = tid; e < used * kMaxGroup; e += kAttnThreads) {
+        const int g = e % kMaxGroup;
+        if (g < group) scale_c[e] = expf(stats[(e / kMaxGroup) * 2 * kMaxGroup + g] - head_m[g]) / head_l[g];
+    }
+    __syncthreads();
+    float o[kMaxGroup / 2] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int c0 = 0; c0 < used; c0 += kMergeBatch) {
+        if (c0 > 0) load_batch(c0);
+#pragma unroll
+        for (int u = 0; u < kMergeBatch; ++u)
+#pragma unroll
+            for (int i = 0; i < kMaxGroup / 2; ++i)
+                if (c0 + u < used && g0 + 2 * i < group)
+                    o[i] = fmaf(v[u][i], scale_c[(c0 + u) * kMaxGroup + g0 + 2 * i], o[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < kMaxGroup / 2; ++i)
+        if (g0 + 2 * i < group)
+            a.out[(int64_t)b * a.heads * kHeadDim + (kvh * group + g0 + 2 * i) * kHeadDim + d] =
+                float_to_bf16_bits(o[i]);
+    if (tid == 0) __hip_atomic_store(a.counters + slot, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* gate_up, float* out, int64_t total,
+                                                       int inter) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= total) return;
+    const int64_t r = i / inter;
+    const int64_t c = i - r * inter;
+    const float g = bf16_bits_to_float(gate_up[r * 2 * inter + c]);
+    const float u = bf16_bits_to_float(gate_up[r * 2 * inter + inter + c]);
+    out[i] = (g / (1.0f + expf(-g))) * u;
+}
+
+int64_t attention_counter_bytes(int64_t batch, int64_t kv_heads) {
+    return (batch * kv_heads * (int64_t)sizeof(unsigned) + 255) / 256 * 256;
+}
+
+bool aligned16(const void* p) { return (((uintptr_t)p) & 15) == 0; }
+
+int launch_status(hipError_t err, const char* what) {
+    if (err != hipSuccess)
+        return set_error(W4G64_STATUS_HIP_ERROR, "%s launch failed: %s", what, hipGetErrorString(err));
+    return clear_error();
+}
+
+}  // namespace
+}  // namespace w4g64
+
+using namespace w4g64;
+
+extern "C" {
+
+int qwen2_add_rmsnorm(const void* x, const void* delta, int delta_dtype, const void* weight, float eps,
+                      void* out_sum, void* out_norm, int64_t rows, int64_t hidden, void* stream) {
+    if (rows < 0) return set_error(W4G64_STATUS_INVALID_VALUE, "rows must be non-negative, got %lld", (long long)rows);
+    if (hidden <= 0 || hidden % 8 || hidden > kNormThreads * 8 * kNormIters)
+        return set_error(W4G64_STATUS_INVALID_VALUE, "hidden must be a multiple of 8 in [8, %d], got %lld",
+                         kNormThreads * 8 * kNormIters, (long long)hidden);
+    if (delta && delta_dtype != W4G64_DTYPE_BF16 && delta_dtype != W4G64_DTYPE_F32)
+        return set_error(W4G64_STATUS_INVALID_DTYPE, "residual delta must be bf16 or fp32");
+    if (rows == 0) return clear_error();
+    if (!x || !weight || !out_norm)
+        return set_error(W4G64_STATUS_INVALID_VALUE, "x, weight and out_norm must be non-null device pointers");
+    if (!aligned16(x) || !aligned16(weight) || !aligned16(out_norm) || (out_sum && !aligned16(out_sum)) ||
+        (delta && !aligned16(delta)))
+        return set_error(W4G64_STATUS_INVALID_VALUE, "add_rmsnorm tensors must be 16-byte aligned");
+    if (rows > 0x7FFFFFFF) return set_error(W4G64_STATUS_INVALID_VALUE, "too many rows");
+    hipLaunchKernelGGL(add_rmsnorm_kernel, dim3((unsigned)rows), dim3(kNormThreads), 0, (hipStream_t)stream,
+                       (const uint16_t*)x, delta, delta ? delta_dtype : 0, (const uint16_t*)weight, eps,
+                       (uint16_t*)out_sum, (uint16_t*)out_norm, (int)hidden);
+    return launch_status(hipGetLastError(), "add_rmsnorm");
+}
+
+int64_t qwen2_decode_attention_workspace_bytes(int64_t batch, int64_t num_kv_heads, int64_t max_length) {
+    if (batch <= 0 || num_kv_heads <= 0 || max_length <= 0) return 0;
+    const int64_t chunks = (max_length + kChunk - 1) / kChunk;
+    return attention_counter_bytes(batch, num_kv_heads) +
+           batch * num_kv_heads * chunks * kPartFloats * (int64_t)sizeof(float);
+}
+
+int qwen2_decode_attention(const void* qkv, const void* cos, const void* sin, void* k_cache, void* v_cache,
+                           const int64_t* position, void* out, int64_t batch, int64_t num_heads,
+                           int64_t num_kv_heads, int64_t head_dim, int64_t max_length, float scale,
+                           void* workspace, int64_t workspace_bytes, void* stream) {
+    if (batch < 0) return set_error(W4G64_STATUS_INVALID_VALUE, "batch must be non-negative");
+    if (head_dim != kHeadDim)
+        return set_error(W4G64_STATUS_UNSUPPORTED, "head_dim must be %d, got %lld", kHeadDim, (long long)head_dim);
+    if (num_kv_heads <= 0 || num_heads <= 0 || num_heads % num_kv_heads != 0 ||
+        num_heads / num_kv_heads > kMaxGroup)
+        return set_error(W4G64_STATUS_INVALID_VALUE,
+                         "num_heads (%lld) must be a positive multiple of num_kv_heads (%lld), at most %d times",
+                         (long long)num_heads, (long long)num_kv_heads, kMaxGroup);
+    if (max_length <= 0 || max_length > kMaxLength)
+        return set_error(W4G64_STATUS_INVALID_VALUE, "max_length must be in [1, %d], got %lld", kMaxLength,
+                         (long long)max_length);
+    if (batch == 0) return clear_error();
+    if (!qkv || !cos || !sin || !k_cache || !v_cache || !position || !out)
+        return set_error(W4G64_STATUS_INVALID_VALUE, "all tensors must be non-null device pointers");
+    if (!aligned16(k_cache) || !aligned16(v_cache))
+        return set_error(W4G64_STATUS_INVALID_VALUE, "k_cache and v_cache must be 16-byte aligned");
+    const int64_t need = qwen2_decode_attention_workspace_bytes(batch, num_kv_heads, max_length);
+    if (!workspace || workspace_bytes < need)
+        return set_error(W4G64_STATUS_WORKSPACE, "attention workspace of %lld bytes required, got %lld",
+                         (long long)need, (long long)(workspace ? workspace_bytes : 0));
+    const int64_t chunks = (max_length + kChunk - 1) / kChunk;
+    const int64_t blocks = batch * num_kv_heads * chunks;
+    if (blocks > 0x7FFFFFFF) return set_error(W4G64_STATUS_INVALID_VALUE, "problem too large");
+    AttnArgs args;
+    args.qkv = (const uint16_t*)qkv;
+    args.cos = (const uint16_t*)cos;
+    args.sin = (const uint16_t*)sin;
+    args.k_cache = (uint16_t*)k_cache;
+    args.v_cache = (uint16_t*)v_cache;
+    args.position = position;
+    args.out = (uint16_t*)out;
+    args.heads = (int)num_heads;
+    args.kv_heads = (int)num_kv_heads;
+    args.max_len = (int)max_length;
+    args.chunks = (int)chunks;
+    args.scale = scale;
+    args.counters = (unsigned*)workspace;
+    args.partials = (float*)((char*)workspace + attention_counter_bytes(batch, num_kv_heads));
+    hipLaunchKernelGGL(attention_kernel, dim3((unsigned)blocks), dim3(kAttnThreads), 0, (hipStream_t)stream, args);
+    return launch_status(hipGetLastError(), "decode_attention");
+}
+
+int qwen2_silu_mul(const void* gate_up, float* out, int64_t rows, int64_t intermediate, void* stream) {
+    if (rows < 0 || intermediate <= 0 || intermediate > 0x3FFFFFFF)
+        return set_error(W4G64_STATUS_INVALID_VALUE, "rows must be non-negative and intermediate positive");
+    if (rows == 0) return clear_error();
+    if (!gate_up || !out) return set_error(W4G64_STATUS_INVALID_VALUE, "gate_up and out must be non-null");
+    const int64_t total = rows * intermediate;
+    const int64_t blocks = (total + 255) / 256;
+    if (blocks > 0x7FFFFFFF) return set_error(W4G64_STATUS_INVALID_VALUE, "problem too large");
+    hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
+                       (const uint16_t*)gate_up, out, total, (int)intermediate);
+    return launch_status(hipGetLastError(), "silu_mul");
+}
+
+}  // extern "C"

@@ -42,6 +42,19 @@ int hip_status(hipError_t err, const char* what) {
 
 }  // namespace
 
+int w4g64::set_error(int status, const char* fmt, ...) {
+    va_list args;
+    va_start(args, fmt);
+    vsnprintf(g_error, sizeof(g_error), fmt, args);
+    va_end(args);
+    return status;
+}
+
+int w4g64::clear_error() {
+    g_error[0] = '\0';
+    return W4G64_STATUS_OK;
+}
+
 extern "C" {
 
 int w4g64_abi_version(void) { return 1; }

@@ -82,6 +82,12 @@ hipError_t launch_kernel(F kernel, dim3 grid, dim3 block, size_t lds, hipStream_
     return hipGetLastError();
 }
 
+// Per-thread error string of the C ABI (defined with the w4g64_* entry
+// points): set_error formats the message and returns `status`; clear_error
+// empties it and returns 0.
+int set_error(int status, const char* fmt, ...);
+int clear_error();
+
 // Primitives.
 hipError_t launch_unpack(const uint8_t* packed, int8_t* out, int64_t elements, hipStream_t stream);
 hipError_t launch_dequant(const uint8_t* qweight, const uint16_t* scales, const uint8_t* zeros, float* out,

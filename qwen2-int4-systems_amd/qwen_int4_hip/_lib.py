@@ -1,4 +1,5 @@
-"""ctypes binding of ``libw4g64_hip.so`` (C ABI declared in include/w4g64.h).
+"""ctypes binding of ``libw4g64_hip.so`` (C ABI declared in include/w4g64.h and
+include/qwen2_decode.h).
 
 The library is loaded from the package directory only.  If it is missing the
 HIP backend is unavailable and every entry point raises -- there is no other
@@ -25,7 +26,7 @@ DTYPE_F16 = 1
 DTYPE_BF16 = 2
 DTYPE_F32 = 3
 
-# (name, restype, argtypes) for every symbol include/w4g64.h declares.
+# (name, restype, argtypes) for every symbol include/*.h declares.
 _p, _i64, _int = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
 SIGNATURES = {
     "w4g64_abi_version": (_int, []),
@@ -36,6 +37,11 @@ SIGNATURES = {
     "w4g64_linear": (_int, [_p, _int, _p, _p, _p, _p, _int, _p, _i64, _i64, _i64, _p, _i64, _p]),
     "w4g64_linear_timed": (_int, [_p, _int, _p, _p, _p, _p, _int, _p, _i64, _i64, _i64, _p, _i64, _p, _p, _p]),
     "w4g64_linear_kernel_name": (ctypes.c_char_p, [_i64, _i64, _i64, _int]),
+    # include/qwen2_decode.h
+    "qwen2_add_rmsnorm": (_int, [_p, _p, _int, _p, ctypes.c_float, _p, _p, _i64, _i64, _p]),
+    "qwen2_decode_attention_workspace_bytes": (_i64, [_i64, _i64, _i64]),
+    "qwen2_decode_attention": (_int, [_p] * 7 + [_i64] * 5 + [ctypes.c_float, _p, _i64, _p]),
+    "qwen2_silu_mul": (_int, [_p, _p, _i64, _i64, _p]),
 }
 
 _lock = threading.Lock()

@@ -14,6 +14,8 @@ from dataclasses import dataclass
 
 import torch
 
+from .decode import FusedDecodeStep
+
 
 @dataclass
 class CachedGenerationState:
@@ -105,10 +107,13 @@ def greedy_generate_cached(model, input_ids: torch.Tensor, *, max_new_tokens: in
 class StaticGreedyDecoder:
     """Greedy decoding of ``batch`` unpadded prompts of one length with a
     preallocated cache of ``max_length`` positions; every decode step is one
-    HIP graph replay (``use_graph``) of ``model.decode_static``."""
+    HIP graph replay (``use_graph``) of the fused decode step
+    (``decode.FusedDecodeStep``, eight launches per layer) or, with
+    ``fused=False``, of the module-level ``model.decode_static``."""
 
-    def __init__(self, model, batch: int, max_length: int, *, use_graph: bool = True) -> None:
+    def __init__(self, model, batch: int, max_length: int, *, use_graph: bool = True, fused: bool = True) -> None:
         self.model = model
+        self.fused = FusedDecodeStep(model, batch, max_length) if fused else None
         self.batch = batch
         self.max_length = max_length
         device = model.lm_head.weight.device
@@ -136,6 +141,8 @@ class StaticGreedyDecoder:
         return logits
 
     def _run(self) -> torch.Tensor:
+        if self.fused is not None:
+            return self.fused(self.token, self.position, self.caches)
         return self.model.decode_static(self.token, self.position, self.caches)
 
     def step(self, token: torch.Tensor | None = None) -> torch.Tensor:

@@ -20,22 +20,26 @@ from qwen_int4_hip.backends import SUPPORTED_BACKENDS, validate_canonical_w4g64_
 from qwen_int4_hip.linear import QuantLinear
 from qwen_int4_hip.quantization import PackingFormat
 
-HEADER = Path(__file__).resolve().parents[1] / "include" / "w4g64.h"
+HEADERS = sorted((Path(__file__).resolve().parents[1] / "include").glob("*.h"))
 
 pytestmark = pytest.mark.skipif(not _lib.library_built(), reason="HIP library not built (run __graft_entry__.build())")
 
 
 def _declared_functions():
-    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
-    return sorted(set(re.findall(r"\b(w4g64_[a-z0-9_]+)\s*\(", text)))
+    names = set()
+    for header in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", header.read_text(), flags=re.S)
+        names |= set(re.findall(r"\b((?:w4g64|qwen2)_[a-z0-9_]+)\s*\(", text))
+    return sorted(names)
 
 
 def test_library_exports_every_declared_symbol():
     lib = _lib.load()
+    assert {h.name for h in HEADERS} == {"w4g64.h", "qwen2_decode.h"}
     declared = _declared_functions()
-    assert declared, "no declarations parsed from include/w4g64.h"
+    assert declared, "no declarations parsed from include/*.h"
     for name in declared:
-        assert hasattr(lib, name), f"{name} declared in w4g64.h but not exported"
+        assert hasattr(lib, name), f"{name} declared in include/*.h but not exported"
     assert set(declared) == set(_lib.SIGNATURES), "ctypes signatures out of sync with the header"
     assert lib.w4g64_abi_version() == 1
 
@@ -66,6 +70,42 @@ def test_c_layer_rejects_before_launch():
     # dequant K not divisible by 64
     assert lib.w4g64_dequantize_canonical(p, p, p, p, 1, 96, null) == _lib.STATUS_INVALID_VALUE
     assert b"divisible" in lib.w4g64_last_error()
+
+
+def test_decode_step_entry_points_reject_before_launch():
+    lib = _lib.load()
+    null = None
+    buf = ctypes.create_string_buffer(4096)
+    p = ctypes.c_void_p((ctypes.addressof(buf) + 15) & ~15)
+    f = ctypes.c_float
+    # add_rmsnorm: hidden bounds, delta dtype, null pointers; zero rows is a no-op
+    assert lib.qwen2_add_rmsnorm(p, null, 0, p, f(1e-6), p, p, 1, 0, null) == _lib.STATUS_INVALID_VALUE
+    assert lib.qwen2_add_rmsnorm(p, null, 0, p, f(1e-6), p, p, 1, 8200, null) == _lib.STATUS_INVALID_VALUE
+    assert lib.qwen2_add_rmsnorm(p, null, 0, p, f(1e-6), p, p, 1, 100, null) == _lib.STATUS_INVALID_VALUE
+    odd2 = ctypes.c_void_p(p.value + 2)
+    assert lib.qwen2_add_rmsnorm(odd2, null, 0, p, f(1e-6), p, p, 1, 64, null) == _lib.STATUS_INVALID_VALUE
+    assert lib.qwen2_add_rmsnorm(p, p, _lib.DTYPE_F16, p, f(1e-6), p, p, 1, 64, null) == _lib.STATUS_INVALID_DTYPE
+    assert lib.qwen2_add_rmsnorm(null, null, 0, p, f(1e-6), p, p, 1, 64, null) == _lib.STATUS_INVALID_VALUE
+    assert lib.qwen2_add_rmsnorm(null, null, 0, null, f(1e-6), null, null, 0, 64, null) == _lib.STATUS_OK
+    # attention: head_dim, head grouping, workspace, alignment
+    ws = lib.qwen2_decode_attention_workspace_bytes(1, 2, 640)
+    assert ws == 256 + 1 * 2 * 10 * (16 + 8 * 128) * 4
+    assert lib.qwen2_decode_attention_workspace_bytes(0, 2, 640) == 0
+    args = [p] * 7
+    assert lib.qwen2_decode_attention(*args, 1, 12, 2, 64, 640, f(0.1), p, ws, null) == _lib.STATUS_UNSUPPORTED
+    assert lib.qwen2_decode_attention(*args, 1, 12, 5, 128, 640, f(0.1), p, ws, null) == _lib.STATUS_INVALID_VALUE
+    assert lib.qwen2_decode_attention(*args, 1, 18, 2, 128, 640, f(0.1), p, ws, null) == _lib.STATUS_INVALID_VALUE
+    assert lib.qwen2_decode_attention(*args, 1, 12, 2, 128, 640, f(0.1), p, ws - 4, null) == _lib.STATUS_WORKSPACE
+    assert lib.qwen2_decode_attention(*args, 1, 12, 2, 128, 17409, f(0.1), p, 1 << 30,
+                                      null) == _lib.STATUS_INVALID_VALUE
+    odd = ctypes.c_void_p(p.value + 2)
+    assert lib.qwen2_decode_attention(p, p, p, odd, p, p, p, 1, 12, 2, 128, 640, f(0.1), p, ws,
+                                      null) == _lib.STATUS_INVALID_VALUE
+    assert b"aligned" in lib.w4g64_last_error()
+    # silu_mul
+    assert lib.qwen2_silu_mul(p, p, 1, 0, null) == _lib.STATUS_INVALID_VALUE
+    assert lib.qwen2_silu_mul(null, p, 1, 64, null) == _lib.STATUS_INVALID_VALUE
+    assert lib.qwen2_silu_mul(null, null, 0, 64, null) == _lib.STATUS_OK
 
 
 def test_workspace_and_kernel_plan_queries():

@@ -124,8 +124,9 @@ def test_static_graph_decoder_matches_growing_cache_generation():
     model = build(SMALL, 13, "cuda")
     prompt = torch.randint(0, SMALL.vocab_size, (1, 17), generator=torch.Generator().manual_seed(3)).cuda()
     state = CachedGenerationState.prefill(model, prompt)
-    eager = StaticGreedyDecoder(model, 1, 64, use_graph=False)
-    graph = StaticGreedyDecoder(model, 1, 64, use_graph=True)
+    # head_dim 64: the module-level decode step (the fused one needs head_dim 128)
+    eager = StaticGreedyDecoder(model, 1, 64, use_graph=False, fused=False)
+    graph = StaticGreedyDecoder(model, 1, 64, use_graph=True, fused=False)
     assert cosine(eager.prefill(prompt), state.logits) == pytest.approx(1.0, abs=1e-12)
     graph.prefill(prompt)
     for _ in range(12):
@@ -136,7 +137,7 @@ def test_static_graph_decoder_matches_growing_cache_generation():
         assert torch.equal(a, b)  # graph replays run the eager kernels on the same inputs
         assert cosine(a, want) >= 0.9999
     # free-running greedy generation agrees with the growing cache on a well-separated run
-    ids = StaticGreedyDecoder(model, 1, 64).generate(prompt, 4)
+    ids = StaticGreedyDecoder(model, 1, 64, fused=False).generate(prompt, 4)
     assert ids.shape == (1, 21) and torch.equal(ids[:, :17], prompt)
 
 
