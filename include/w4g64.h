@@ -45,6 +45,11 @@ extern "C" {
 #define W4G64_DTYPE_BF16 2
 #define W4G64_DTYPE_F32 3
 
+/* Activation form of w4g64_linear_swiglu below, accepted (besides the dtypes
+ * above) by w4g64_linear_workspace_bytes and w4g64_linear_kernel_name: the
+ * SwiGLU product of a [gate | up] bf16 row (fp32). */
+#define W4G64_DTYPE_BF16_SWIGLU 5
+
 /* Version of this ABI (bumped on any signature or contract change). */
 int w4g64_abi_version(void);
 
@@ -101,6 +106,17 @@ int w4g64_linear_timed(const void* x, int x_dtype, const uint8_t* qweight, const
                        const uint8_t* zeros, const void* bias, int bias_dtype, void* y, int64_t rows,
                        int64_t out_features, int64_t in_features, void* workspace, int64_t workspace_bytes,
                        void* stream, void* start_event, void* stop_event);
+
+/* Decode-step fusion of the SwiGLU product into the down projection (rows
+ * 1..16): gate_up is [rows, 2 * in_features] bf16 (gate | up), the activation
+ * is h = silu(gate) * up in fp32 (silu(g) = g / (1 + exp(-g))), and
+ * y[rows, out] = h @ dequant(W)^T (+ bias) in fp32, as w4g64_linear on the
+ * fp32 h.  gate_up and qweight 16-byte aligned.
+ * Replaces: QwenMLP.forward's product and down projection
+ *           (src/qwen_int4/model.py:133-136). */
+int w4g64_linear_swiglu(const void* gate_up, const uint8_t* qweight, const uint16_t* scales, const uint8_t* zeros,
+                        const void* bias, int bias_dtype, float* y, int64_t rows, int64_t out_features,
+                        int64_t in_features, void* workspace, int64_t workspace_bytes, void* stream);
 
 /* Name of the kernel w4g64_linear launches for this problem (for profiles
  * and reports); never NULL. */

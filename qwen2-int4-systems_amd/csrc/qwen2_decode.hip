@@ -45,7 +45,6 @@ constexpr int kMergeBatch = 16;   // chunks whose partial sums one merge pass lo
 constexpr int kMaxChunks = (kChunk * kRowStride * 2) / (2 * kMaxGroup * 4);
 constexpr int kMaxLength = kMaxChunks * kChunk;
 
-__device__ __forceinline__ float bf16_round(float v) { return bf16_bits_to_float(float_to_bf16_bits(v)); }
 
 // Thread t owns the 8-element pieces 8 t + 2048 i (i < kNormIters).  Every
 // load is unconditional at a clamped address and issued before any use (a

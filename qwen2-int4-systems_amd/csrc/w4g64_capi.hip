@@ -89,8 +89,13 @@ int w4g64_dequantize_canonical(const uint8_t* qweight, const uint16_t* scales, c
                       "dequantize");
 }
 
+static bool fused_form(int x_dtype) { return x_dtype == W4G64_DTYPE_BF16_SWIGLU; }
+
 int64_t w4g64_linear_workspace_bytes(int64_t rows, int64_t out_features, int64_t in_features, int x_dtype) {
     if (rows <= 0 || out_features <= 0 || in_features <= 0 || in_features % 64) return 0;
+    if (fused_form(x_dtype))
+        return rows <= w4g64::kGemvMaxRows ? w4g64::plan_gemv(rows, out_features, in_features, x_dtype).workspace_bytes
+                                           : 0;
     if (x_dtype != W4G64_DTYPE_F16 && x_dtype != W4G64_DTYPE_BF16 && x_dtype != W4G64_DTYPE_F32) return 0;
     if (rows > w4g64::kGemvMaxRows) {
         w4g64::LinearProblem p{nullptr, x_dtype, nullptr, nullptr, nullptr, nullptr, 0, nullptr, rows, out_features,
@@ -102,6 +107,10 @@ int64_t w4g64_linear_workspace_bytes(int64_t rows, int64_t out_features, int64_t
 
 const char* w4g64_linear_kernel_name(int64_t rows, int64_t out_features, int64_t in_features, int x_dtype) {
     if (rows <= 0 || out_features <= 0 || in_features <= 0 || in_features % 64) return "none";
+    if (fused_form(x_dtype))
+        return rows <= w4g64::kGemvMaxRows
+                   ? w4g64::gemv_kernel_name(w4g64::plan_gemv(rows, out_features, in_features, x_dtype), x_dtype)
+                   : "none";
     if (x_dtype != W4G64_DTYPE_F16 && x_dtype != W4G64_DTYPE_BF16 && x_dtype != W4G64_DTYPE_F32) return "none";
     if (rows <= w4g64::kGemvMaxRows)
         return w4g64::gemv_kernel_name(w4g64::plan_gemv(rows, out_features, in_features, x_dtype), x_dtype);
@@ -177,6 +186,48 @@ int w4g64_linear_timed(const void* x, int x_dtype, const uint8_t* qweight, const
                        void* stream, void* start_event, void* stop_event) {
     return linear_impl(x, x_dtype, qweight, scales, zeros, bias, bias_dtype, y, rows, out_features, in_features,
                        workspace, workspace_bytes, stream, start_event, stop_event);
+}
+
+// Shared checks of the fused decode entry points (weights, bias, sizes).
+static int fused_common_checks(const uint8_t* qweight, const uint16_t* scales, const uint8_t* zeros,
+                               const void* bias, int bias_dtype, const void* y, int y_bytes, int64_t rows,
+                               int64_t out_features, int64_t in_features) {
+    if (bias_dtype != W4G64_DTYPE_NONE && bias_dtype != W4G64_DTYPE_F16 && bias_dtype != W4G64_DTYPE_BF16 &&
+        bias_dtype != W4G64_DTYPE_F32)
+        return fail(W4G64_STATUS_INVALID_DTYPE, "bias must have dtype float16, bfloat16, or float32");
+    if ((bias_dtype == W4G64_DTYPE_NONE) != (bias == nullptr))
+        return fail(W4G64_STATUS_INVALID_VALUE, "bias pointer and bias dtype disagree");
+    if (rows <= 0 || rows > w4g64::kGemvMaxRows)
+        return fail(W4G64_STATUS_INVALID_VALUE, "fused decode linears take 1..%d rows, got %lld", w4g64::kGemvMaxRows,
+                    (long long)rows);
+    if (in_features <= 0 || in_features % 64 || in_features > (1ll << 24))
+        return fail(W4G64_STATUS_INVALID_VALUE, "in_features must be a positive multiple of 64, got %lld",
+                    (long long)in_features);
+    if (out_features <= 0 || out_features > w4g64::kGemvMaxColumnBlocks * 64)
+        return fail(W4G64_STATUS_INVALID_VALUE, "out_features must be in [1, %lld], got %lld",
+                    (long long)(w4g64::kGemvMaxColumnBlocks * 64), (long long)out_features);
+    if (!qweight || !scales || !zeros || !y)
+        return fail(W4G64_STATUS_INVALID_VALUE, "qweight, scales, zeros and y must be non-null device pointers");
+    if (!aligned(qweight, 16)) return fail(W4G64_STATUS_INVALID_VALUE, "qweight must be 16-byte aligned");
+    if (!aligned(y, (uintptr_t)y_bytes) || !aligned(scales, 2))
+        return fail(W4G64_STATUS_INVALID_VALUE, "y and scales must be element aligned");
+    if (bias && !aligned(bias, (uintptr_t)element_bytes(bias_dtype)))
+        return fail(W4G64_STATUS_INVALID_VALUE, "bias must be element aligned");
+    return W4G64_STATUS_OK;
+}
+
+int w4g64_linear_swiglu(const void* gate_up, const uint8_t* qweight, const uint16_t* scales, const uint8_t* zeros,
+                        const void* bias, int bias_dtype, float* y, int64_t rows, int64_t out_features,
+                        int64_t in_features, void* workspace, int64_t workspace_bytes, void* stream) {
+    if (int st = fused_common_checks(qweight, scales, zeros, bias, bias_dtype, y, 4, rows, out_features, in_features))
+        return st;
+    if (!gate_up) return fail(W4G64_STATUS_INVALID_VALUE, "gate_up must be a non-null device pointer");
+    if (!aligned(gate_up, 16)) return fail(W4G64_STATUS_INVALID_VALUE, "gate_up must be 16-byte aligned");
+    w4g64::LinearProblem p{gate_up, w4g64::kSwiGLU, qweight, scales, zeros, bias, bias_dtype, y, rows, out_features,
+                           in_features};
+    const w4g64::GemvPlan plan = w4g64::plan_gemv(rows, out_features, in_features, w4g64::kSwiGLU);
+    if (int st = check_workspace(workspace, workspace_bytes, plan.workspace_bytes)) return st;
+    return hip_status(w4g64::launch_gemv(p, plan, workspace, (hipStream_t)stream), "gemv");
 }
 
 }  // extern "C"

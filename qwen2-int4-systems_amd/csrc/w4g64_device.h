@@ -28,7 +28,9 @@ typedef float float16v __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-enum XKind : int { kF16 = 1, kBF16 = 2, kF32 = 3 };
+// Activation kinds.  kSwiGLU forms the activation in the decode GEMV's
+// staging: silu(gate) * up in fp32 from a [gate | up] bf16 row (fp32 result).
+enum XKind : int { kF16 = 1, kBF16 = 2, kF32 = 3, kSwiGLU = 5 };
 
 // Slot order of the 8 values in an MFMA operand: slot p holds k = kSlotK[p].
 // (Used by host-side documentation/tests; kernels permute with v_perm.)
@@ -133,5 +135,7 @@ __device__ __forceinline__ void store_out(void* y, int64_t idx, float v) {
         ((float*)y)[idx] = v;
     }
 }
+
+__device__ __forceinline__ float bf16_round(float v) { return bf16_bits_to_float(float_to_bf16_bits(v)); }
 
 }  // namespace w4g64

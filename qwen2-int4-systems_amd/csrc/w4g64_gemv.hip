@@ -26,6 +26,9 @@
 //   * fp32 activations: every row is split exactly into three bf16 parts
 //     (hi + mid + lo == x) that form three virtual rows; the bf16 path runs
 //     on them and the parts are summed in fp32.
+//   * fused activation form (decode step of the decoder layer): kSwiGLU
+//     stages silu(gate) * up (fp32, as three bf16 parts) from a [gate | up]
+//     bf16 row.
 //   * every weight, scale and zero load of the lane is issued before the
 //     activations are staged, so the workgroup's whole weight slice is in
 //     flight at once.
@@ -73,7 +76,8 @@ template <int XK, int SW, int STEPS, int TILES>
 __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     __shared__ int s_last;
-    constexpr int kParts = (XK == kF32) ? 3 : 1;
+    constexpr int kParts = (XK == kF32 || XK == kSwiGLU) ? 3 : 1;
+    constexpr int kOut = XK == kSwiGLU ? kF32 : XK;  // output kind
     constexpr int R = 16 / SW;              // output features per wave
     constexpr int kBlockCols = kWaves * R;  // output features per workgroup
 
@@ -115,20 +119,26 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
             sc[t] = half_bits_to_float(a.scales[sbase + g]);
             zr[t] = nibble_at(a.zeros, sbase + g);
         }
-    } else {
-        // ---- staging wave: this workgroup's activations into LDS (slot order) ----
-        // Batches of kStageBatch items per lane: all loads of a batch are
-        // issued before any is consumed, so the wave has kStageBatch 16-byte
-        // loads in flight instead of one round trip per item.
+    }
+    // ---- staging: this workgroup's activations into LDS (slot order) ----
+    // Batches of kStageBatch items per lane: all loads of a batch are issued
+    // before any is consumed, so a lane has kStageBatch 16-byte loads in
+    // flight instead of one round trip per item.  The fp32-class kinds (exact
+    // bf16 split, silu) are ALU-heavy and every wave stages them (after
+    // issuing its weight loads); the other kinds use the staging wave alone.
+    constexpr bool kAllStage = (XK == kF32 || XK == kSwiGLU);
+    const int sid = kAllStage ? tid : lane;        // staging lane index
+    const int nst = kAllStage ? kThreads : 64;    // staging lanes
+    if (kAllStage || wave == kWaves) {
         const int kbase = g0 * 64;
         const int items_per_row = cnt * 8;  // 8 values per item
         const int total = a.M * items_per_row;
-        for (int base = 0; base < total; base += 64 * kStageBatch) {
-            if constexpr (XK != kF32) {
+        for (int base = 0; base < total; base += nst * kStageBatch) {
+            if constexpr (XK == kF16 || XK == kBF16) {
                 u32x4 v[kStageBatch];
 #pragma unroll
                 for (int u = 0; u < kStageBatch; ++u) {
-                    const int it = base + 64 * u + lane;
+                    const int it = base + nst * u + sid;
                     const int itc = it < total ? it : total - 1;  // clamped: a valid address, result unused
                     const int m = itc / items_per_row;
                     const int c = itc - m * items_per_row;
@@ -136,7 +146,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
                 }
 #pragma unroll
                 for (int u = 0; u < kStageBatch; ++u) {
-                    const int it = base + 64 * u + lane;
+                    const int it = base + nst * u + sid;
                     if (it < total) {
                         const int m = it / items_per_row;
                         const int c = it - m * items_per_row;
@@ -147,23 +157,46 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
                 float4v f[kStageBatch][2];
 #pragma unroll
                 for (int u = 0; u < kStageBatch; ++u) {
-                    const int it = base + 64 * u + lane;
+                    const int it = base + nst * u + sid;
                     const int itc = it < total ? it : total - 1;
                     const int m = itc / items_per_row;
                     const int c = itc - m * items_per_row;
-                    const float* src = (const float*)a.x + (int64_t)m * a.K + kbase + 8 * c;
-                    f[u][0] = *(const float4v*)src;
-                    f[u][1] = *(const float4v*)(src + 4);
+                    if constexpr (XK == kSwiGLU) {
+                        // x is [M, 2K]: gate | up (bf16); the product is formed once every load is issued
+                        const uint16_t* gu = (const uint16_t*)a.x + (int64_t)m * 2 * a.K + kbase + 8 * c;
+                        f[u][0] = __builtin_bit_cast(float4v, *(const u32x4*)gu);
+                        f[u][1] = __builtin_bit_cast(float4v, *(const u32x4*)(gu + a.K));
+                    } else {
+                        const float* src = (const float*)a.x + (int64_t)m * a.K + kbase + 8 * c;
+                        f[u][0] = *(const float4v*)src;
+                        f[u][1] = *(const float4v*)(src + 4);
+                    }
                 }
 #pragma unroll
                 for (int u = 0; u < kStageBatch; ++u) {
-                    const int it = base + 64 * u + lane;
+                    const int it = base + nst * u + sid;
                     if (it >= total) continue;
                     const int m = it / items_per_row;
                     const int c = it - m * items_per_row;
+                    float h[8];
+                    if constexpr (XK == kSwiGLU) {
+                        // h = silu(gate) * up in fp32, silu(g) = g / (1 + exp(-g)) (model.py:133-136)
+                        const u32x4 gv = __builtin_bit_cast(u32x4, f[u][0]);
+                        const u32x4 uv = __builtin_bit_cast(u32x4, f[u][1]);
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) {
+                            const uint32_t gw = gv[e / 2], uw = uv[e / 2];
+                            const float g = bf16_bits_to_float(e & 1 ? gw >> 16 : gw & 0xFFFFu);
+                            const float up = bf16_bits_to_float(e & 1 ? uw >> 16 : uw & 0xFFFFu);
+                            h[e] = (g / (1.0f + expf(-g))) * up;
+                        }
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) h[e] = e < 4 ? f[u][0][e] : f[u][1][e - 4];
+                    }
                     uint16_t hi[8], mid[8], lo[8];
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) split3_bf16(e < 4 ? f[u][0][e] : f[u][1][e - 4], hi[e], mid[e], lo[e]);
+                    for (int e = 0; e < 8; ++e) split3_bf16(h[e], hi[e], mid[e], lo[e]);
                     u32x4 ph, pm, pl;
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
@@ -177,9 +210,13 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
                 }
             }
         }
-        if constexpr (XK != kF16) {
-            // group sums of every staged row (this wave's own LDS writes are ordered before its reads)
-            for (int idx = lane; idx < cnt * a.mv; idx += 64) {
+    }
+    if constexpr (XK != kF16) {
+        // group sums of every staged row (a single staging wave's own LDS
+        // writes are ordered before its reads; several waves need a barrier)
+        if constexpr (kAllStage) __syncthreads();
+        if (kAllStage || wave == kWaves) {
+            for (int idx = sid; idx < cnt * a.mv; idx += nst) {
                 const int r = idx / cnt;
                 const int gl = idx - r * cnt;
                 const uint16_t* src = xs + r * row_stride + 64 * gl;
@@ -280,7 +317,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
             for (int s = 0; s < SW; ++s) v += red[((p * a.M + m) * kBlockCols + c) * SW + s];
         if (a.splits == 1) {
             v += load_bias(a.bias, a.bias_kind, nn);
-            store_out<XK>(a.y, (int64_t)m * a.N + nn, v);
+            store_out<kOut>(a.y, (int64_t)m * a.N + nn, v);
         } else {
             __hip_atomic_store(a.partials + ((int64_t)split * a.M + m) * a.N + nn, v, __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
@@ -313,7 +350,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
             v += __hip_atomic_load(a.partials + ((int64_t)s * a.M + m) * a.N + nn, __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
         v += load_bias(a.bias, a.bias_kind, nn);
-        store_out<XK>(a.y, (int64_t)m * a.N + nn, v);
+        store_out<kOut>(a.y, (int64_t)m * a.N + nn, v);
     }
     if (tid == 0) __hip_atomic_store(a.counters + nb, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -398,7 +435,7 @@ GemvPlan plan_gemv(int64_t rows, int64_t out_features, int64_t in_features, int 
         return plan;
     plan = GemvPlan{};
     const int64_t groups = in_features / 64;
-    const int64_t parts = (x_kind == kF32) ? 3 : 1;
+    const int64_t parts = (x_kind == kF32 || x_kind == kSwiGLU) ? 3 : 1;
     const int64_t mv = rows * parts;
     // Segments: as many as fit the 16 MFMA rows (mv * SW <= 16), then fewer
     // while that still leaves >= 1024 column blocks (more features per
@@ -453,12 +490,12 @@ GemvPlan plan_gemv(int64_t rows, int64_t out_features, int64_t in_features, int 
 
 const char* gemv_kernel_name(const GemvPlan& plan, int x_kind) {
     static thread_local char name[64];
-    static const char* kinds[] = {"?", "f16", "bf16", "f32"};
+    static const char* kinds[] = {"?", "f16", "bf16", "f32", "?", "swiglu_bf16"};
     if (plan.kind == 1) {
-        snprintf(name, sizeof(name), "gemv16_kernel<%s,%d,%d>", kinds[x_kind & 3], plan.steps, plan.waves);
+        snprintf(name, sizeof(name), "gemv16_kernel<%s,%d,%d>", kinds[x_kind >= 1 && x_kind <= 5 ? x_kind : 0], plan.steps, plan.waves);
         return name;
     }
-    snprintf(name, sizeof(name), "gemv_kernel<%s,%d,%d,%d>", kinds[x_kind & 3], plan.segments, plan.steps,
+    snprintf(name, sizeof(name), "gemv_kernel<%s,%d,%d,%d>", kinds[x_kind >= 1 && x_kind <= 5 ? x_kind : 0], plan.segments, plan.steps,
              plan.tiles);
     return name;
 }
@@ -480,7 +517,7 @@ hipError_t launch_gemv(const LinearProblem& p, const GemvPlan& plan, void* works
     args.G = (int)(p.in_features / 64);
     args.gps = plan.groups_per_split;
     args.splits = plan.splits;
-    args.mv = (int)(p.rows * (p.x_kind == kF32 ? 3 : 1));
+    args.mv = (int)(p.rows * (p.x_kind == kF32 || p.x_kind == kSwiGLU ? 3 : 1));
     args.counters = (unsigned*)workspace;
     args.partials = workspace ? (float*)((char*)workspace + plan.counter_bytes) : nullptr;
     switch (p.x_kind) {
@@ -488,6 +525,10 @@ hipError_t launch_gemv(const LinearProblem& p, const GemvPlan& plan, void* works
             return launch_sw<kF16, 1>(args, plan, stream, start, stop);
         case kBF16:
             return launch_sw<kBF16, 1>(args, plan, stream, start, stop);
+        case kSwiGLU:
+            if (plan.tiles == 1) return launch_sw<kSwiGLU, 1>(args, plan, stream, start, stop);
+            if (plan.tiles == 2) return launch_steps<kSwiGLU, 1, 2>(args, plan, stream, start, stop);
+            return launch_steps<kSwiGLU, 1, 3>(args, plan, stream, start, stop);
         default:
             // more than 16 virtual rows only occurs with one segment per wave
             if (plan.tiles == 1) return launch_sw<kF32, 1>(args, plan, stream, start, stop);

@@ -1,17 +1,17 @@
 """Fused single-token decode step of the Qwen2 decoder on the HIP kernels.
 
 Restates one cached-token pass of QwenModel / DecoderLayer
-(src/qwen_int4/model.py:61-154, :169-199) as eight launches per layer:
+(src/qwen_int4/model.py:61-154, :169-199) as seven launches per layer:
 
-    add_rmsnorm      residual add (bf16, with the MLP output cast to bf16
-                     first, model.py:136) + input/post-attention RMSNorm
-    W4G64 q|k|v      one GEMV over the three projections' rows, with bias
-    decode_attention rotary on q and the new k, cache write, GQA attention
+    add_rmsnorm          residual add of the previous MLP output (cast to bf16
+                         first, model.py:136) + input RMSNorm
+    W4G64 q|k|v          one GEMV over the three projections' rows, with bias
+    decode_attention     rotary on q and the new k, cache write, GQA attention
     W4G64 o_proj
-    add_rmsnorm
-    W4G64 gate|up    one GEMV over both projections' rows
-    silu_mul         fp32 silu(gate) * up
-    W4G64 down_proj  fp32 activations in, fp32 out
+    add_rmsnorm          residual add of the attention output + RMSNorm
+    W4G64 gate|up        one GEMV over both projections' rows
+    W4G64 down (swiglu)  silu(gate) * up in fp32, formed in the down
+                         projection's activation staging; fp32 out
 
 The fused projections are views: ``fuse_projections`` concatenates the
 q/k/v (and gate/up) buffers of each layer once and points the modules'
@@ -123,11 +123,11 @@ class FusedDecodeStep:
         self.attended = buf(self.heads * self.head_dim)
         self.o = buf(self.hidden)
         self.gate_up = buf(2 * self.inter)
-        self.h = buf(self.inter, torch.float32)
         self.down = buf(self.hidden, torch.float32)
-        shapes = [(self.qkv.shape[1], self.hidden, _lib.DTYPE_BF16), (self.hidden, self.heads * self.head_dim,
-                                                                      _lib.DTYPE_BF16),
-                  (2 * self.inter, self.hidden, _lib.DTYPE_BF16), (self.hidden, self.inter, _lib.DTYPE_F32)]
+        shapes = [(self.qkv.shape[1], self.hidden, _lib.DTYPE_BF16),
+                  (self.hidden, self.heads * self.head_dim, _lib.DTYPE_BF16),
+                  (2 * self.inter, self.hidden, _lib.DTYPE_BF16),
+                  (self.hidden, self.inter, _lib.DTYPE_BF16_SWIGLU)]
         ws = max(self.lib.w4g64_linear_workspace_bytes(batch, n, k, code) for n, k, code in shapes)
         self.workspace = torch.zeros(max(ws, 1), dtype=torch.uint8, device=device)
         aws = self.lib.qwen2_decode_attention_workspace_bytes(batch, self.kv_heads, max_length)
@@ -168,11 +168,11 @@ class FusedDecodeStep:
                          self.o, stream)
             self._norm(self.o, _lib.DTYPE_BF16, layer.post_attention_layernorm.weight, stream)
             self._linear(self.normed, _lib.DTYPE_BF16, fused["gate_up"], self.gate_up, stream)
-            _lib.check(self.lib.qwen2_silu_mul(_ptr(self.gate_up), _ptr(self.h), self.batch, self.inter, stream))
             down = layer.mlp.down_proj
-            self._linear(self.h, _lib.DTYPE_F32,
-                         {"qweight": down.qweight, "scales": down.scales, "zeros": down.zeros, "bias": None},
-                         self.down, stream)
+            _lib.check(self.lib.w4g64_linear_swiglu(
+                _ptr(self.gate_up), _ptr(down.qweight), _ptr(down.scales), _ptr(down.zeros), None, _lib.DTYPE_NONE,
+                _ptr(self.down), self.batch, self.hidden, self.inter, _ptr(self.workspace), self.workspace.numel(),
+                stream))
             delta, delta_code = self.down, _lib.DTYPE_F32
         self._norm(delta, delta_code, model.model.norm.weight, stream)
         return F.linear(self.normed, model.lm_head.weight).view(self.batch, 1, -1)

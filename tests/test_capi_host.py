@@ -108,6 +108,29 @@ def test_decode_step_entry_points_reject_before_launch():
     assert lib.qwen2_silu_mul(null, null, 0, 64, null) == _lib.STATUS_OK
 
 
+def test_fused_swiglu_linear_rejects_before_launch():
+    lib = _lib.load()
+    null = None
+    buf = ctypes.create_string_buffer(1 << 16)
+    base = (ctypes.addressof(buf) + 255) & ~255
+    p = ctypes.c_void_p(base)
+    f = ctypes.c_float
+    # swiglu linear: rows range, alignment, bias agreement
+    assert lib.w4g64_linear_swiglu(p, p, p, p, null, 0, p, 0, 64, 64, null, 0, null) == _lib.STATUS_INVALID_VALUE
+    assert lib.w4g64_linear_swiglu(ctypes.c_void_p(base + 8), p, p, p, null, 0, p, 1, 64, 64, null, 0,
+                                   null) == _lib.STATUS_INVALID_VALUE
+    assert lib.w4g64_linear_swiglu(p, p, p, p, p, 0, p, 1, 64, 64, null, 0, null) == _lib.STATUS_INVALID_VALUE
+    # the fused forms are valid workspace / kernel-name queries for decode rows only
+    assert lib.w4g64_linear_kernel_name(1, 1536, 8960, _lib.DTYPE_BF16_SWIGLU).decode().startswith(
+        "gemv_kernel<swiglu_bf16,")
+    assert lib.w4g64_linear_kernel_name(12, 1536, 8960, _lib.DTYPE_BF16_SWIGLU).decode().startswith(
+        "gemv_kernel<swiglu_bf16,")
+    assert lib.w4g64_linear_kernel_name(64, 1536, 8960, _lib.DTYPE_BF16_SWIGLU) == b"none"
+    assert lib.w4g64_linear_workspace_bytes(1, 64, 64, 4) == 0 and lib.w4g64_linear_kernel_name(1, 64, 64, 4) == b"none"
+    assert lib.w4g64_linear_workspace_bytes(1, 1536, 8960, _lib.DTYPE_BF16_SWIGLU) == \
+        lib.w4g64_linear_workspace_bytes(1, 1536, 8960, _lib.DTYPE_F32)
+
+
 def test_workspace_and_kernel_plan_queries():
     lib = _lib.load()
     # decode shapes that split K across workgroups need a workspace with the

@@ -135,6 +135,41 @@ def test_silu_mul_matches_torch(rows, inter):
     assert (out == want).float().mean().item() >= 0.99
 
 
+def _weights(n, k, seed, asymmetric=False):
+    from oracle import oracle as O
+
+    q, sc, z = (O.asymmetric_weights(n, k, seed) if asymmetric else O.symmetric_weights(n, k, seed))
+    return tuple(torch.from_numpy(t).cuda() for t in (q, sc, z))
+
+
+def _normwise(got, want):
+    return ((got.float() - want.float()).abs().max() / want.float().abs().max()).item()
+
+
+@pytest.mark.parametrize("rows", [1, 4, 9, 16])
+@pytest.mark.parametrize("n,k", [(1536, 8960), (100, 128), (256, 1536)])
+def test_linear_swiglu_matches_silu_then_reference_linear(rows, n, k):
+    """w4g64_linear_swiglu = fp32 silu(gate) * up (torch) followed by the
+    reference torch backend's fp32 linear (the oracle); the fp32 activations
+    run exactly (three bf16 parts), so the output agrees to fp32 summation
+    order (normwise 1e-5)."""
+    from oracle import oracle as O
+
+    lib = _lib.load()
+    g = _gen(rows * 17 + n + k)
+    gate_up = (torch.randn((rows, 2 * k), generator=g, device="cuda") * 3).to(torch.bfloat16)
+    h = torch.nn.functional.silu(gate_up[:, :k].float()) * gate_up[:, k:].float()
+    qw, sc, z = _weights(n, k, 9)
+    want = O.reference_linear_torch(h, qw, sc, z, None, out_features=n, in_features=k)
+    ws = torch.zeros(max(1, lib.w4g64_linear_workspace_bytes(rows, n, k, _lib.DTYPE_BF16_SWIGLU)),
+                     dtype=torch.uint8, device="cuda")
+    y = torch.empty((rows, n), dtype=torch.float32, device="cuda")
+    _lib.check(lib.w4g64_linear_swiglu(_p(gate_up), _p(qw), _p(sc), _p(z), None, 0, _p(y), rows, n, k, _p(ws),
+                                       ws.numel(), _stream()))
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(y).all()) and _normwise(y, want) <= 1e-5
+
+
 SMALL128 = SimpleNamespace(hidden_size=256, num_attention_heads=2, num_key_value_heads=1, head_dim=128,
                            intermediate_size=512, num_hidden_layers=3, vocab_size=512, rms_norm_eps=1e-6,
                            rope_theta=1_000_000.0)
