@@ -100,7 +100,7 @@ int64_t w4g64_linear_workspace_bytes(int64_t rows, int64_t out_features, int64_t
     if (rows > w4g64::kGemvMaxRows) {
         w4g64::LinearProblem p{nullptr, x_dtype, nullptr, nullptr, nullptr, nullptr, 0, nullptr, rows, out_features,
                                in_features};
-        return w4g64::gemm2_supported(p) ? w4g64::gemm2_workspace_bytes(rows, out_features, in_features) : 0;
+        return w4g64::gemm2_supported(p) ? w4g64::gemm2_workspace_bytes(rows, out_features, in_features, x_dtype) : 0;
     }
     return w4g64::plan_gemv(rows, out_features, in_features, x_dtype).workspace_bytes;
 }
@@ -164,13 +164,9 @@ static int linear_impl(const void* x, int x_dtype, const uint8_t* qweight, const
         return hip_status(w4g64::launch_gemv(p, plan, workspace, s, (hipEvent_t)start_event, (hipEvent_t)stop_event),
                           "gemv");
     }
-    if (w4g64::gemm2_supported(p)) {
-        const int64_t need = w4g64::gemm2_workspace_bytes(rows, out_features, in_features);
-        if (int st = check_workspace(workspace, workspace_bytes, need)) return st;
-        return hip_status(w4g64::launch_gemm2(p, workspace, s, (hipEvent_t)start_event, (hipEvent_t)stop_event),
-                          "gemm");
-    }
-    return hip_status(w4g64::launch_gemm(p, s, (hipEvent_t)start_event, (hipEvent_t)stop_event), "gemm");
+    const int64_t need = w4g64::gemm2_workspace_bytes(rows, out_features, in_features, x_dtype);
+    if (int st = check_workspace(workspace, workspace_bytes, need)) return st;
+    return hip_status(w4g64::launch_gemm2(p, workspace, s, (hipEvent_t)start_event, (hipEvent_t)stop_event), "gemm");
 }
 
 int w4g64_linear(const void* x, int x_dtype, const uint8_t* qweight, const uint16_t* scales, const uint8_t* zeros,

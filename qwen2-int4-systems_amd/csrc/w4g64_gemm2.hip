@@ -34,6 +34,12 @@
 //   * Tiles are assigned so that the workgroups of one XCD (ids congruent
 //     mod 8) cover consecutive tiles of one row band: they share the
 //     activation band in their L2.
+//   * fp32 activations: a first kernel splits each row into two bf16 planes,
+//     hi = RNE(x) and lo = RNE(x - hi) (16 significant bits, |x - hi - lo| <=
+//     2^-17 |x|, below the bf16-rounded dequantized weight's own 2^-9), laid
+//     out as one row [hi | lo] of 2K values in the workspace; the GEMM then
+//     runs over K' = 2K with weight group g mod G, so both planes meet the
+//     same dequantized weights, and stores fp32 outputs.
 #include <type_traits>
 
 #include "w4g64_device.h"
@@ -57,8 +63,9 @@ struct Gemm2Args {
     void* y;
     int M;
     int N;
-    int K;
-    int G;
+    int K;   // activation row length (2 in_features for fp32 activations)
+    int G;   // activation groups, K / 64
+    int wg;  // weight groups (in_features / 64): the K' step g reads weight group g mod wg
     int tiles_m;
     int tiles_n;
     int vec_out;    // y is 16-byte aligned and N % 8 == 0: 16-byte output stores
@@ -150,7 +157,7 @@ __device__ __forceinline__ u32x4 dequant_natural(uint32_t w, uint32_t zc_bits, u
     return out;
 }
 
-template <int XK, int BM>
+template <int XK, int BM, int OUTK>
 __global__ __launch_bounds__(256, 2) void gemm2_kernel(Gemm2Args a) {
     constexpr int MB = BM / 32;                 // 32-row MFMA blocks per wave
     constexpr int kABytes = BM * 128;           // BM rows x 64 fp16/bf16 values
@@ -213,26 +220,32 @@ __global__ __launch_bounds__(256, 2) void gemm2_kernel(Gemm2Args a) {
     for (int bj = 0; bj < 2; ++bj) {
         int64_t n = nw + 32 * bj + j;
         n = n < a.N ? n : a.N - 1;
-        w_src[bj] = a.qweight + n * (a.K / 2) + (int64_t)gbeg * 32 + 16 * q;
+        w_src[bj] = a.qweight + n * ((int64_t)a.wg * 32) + 16 * q;
     }
     // scale / zero of column nw + lane
     int64_t ncol = nw + lane;
     ncol = ncol < a.N ? ncol : a.N - 1;
-    const int64_t s_row = ncol * a.G + gbeg;  // scale / zero element of group gbeg
+    const int64_t s_row = ncol * a.wg;  // scale / zero element of weight group 0
+    // weight group of this workgroup's K step gg (one wrap at most: K' <= 2 in_features)
+    auto wgroup = [&](int gg) {
+        const int gabs = gbeg + gg;
+        return gabs >= a.wg ? gabs - a.wg : gabs;
+    };
 
     auto issue = [&](int gg) {  // callers pass gg < G only
         unsigned char* st = smem[gg % kStages];
+        const int gw = wgroup(gg);
 #pragma unroll
         for (int d = 0; d < kDma; ++d)
             __builtin_amdgcn_global_load_lds((const void*)(a_src[d] + (int64_t)gg * 64),
                                              (lds_ptr_t)(st + 1024 * (wave * kDma + d)), 16, 0, 0);
 #pragma unroll
         for (int bj = 0; bj < 2; ++bj)
-            __builtin_amdgcn_global_load_lds((const void*)(w_src[bj] + (int64_t)gg * 32),
+            __builtin_amdgcn_global_load_lds((const void*)(w_src[bj] + (int64_t)gw * 32),
                                              (lds_ptr_t)(st + kABytes + 2048 * wave + 1024 * bj), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds((const void*)(a.scales + s_row + gg),
+        __builtin_amdgcn_global_load_lds((const void*)(a.scales + s_row + gw),
                                          (lds_ptr_t)(st + kABytes + kWBytes + 256 * wave), 2, 0, 0);
-        __builtin_amdgcn_global_load_lds((const void*)(a.zeros + ((s_row + gg) >> 1)),
+        __builtin_amdgcn_global_load_lds((const void*)(a.zeros + ((s_row + gw) >> 1)),
                                          (lds_ptr_t)(st + kABytes + kWBytes + kSBytes + 256 * wave), 1, 0, 0);
     };
 
@@ -242,12 +255,12 @@ __global__ __launch_bounds__(256, 2) void gemm2_kernel(Gemm2Args a) {
 #pragma unroll
         for (int bj = 0; bj < 2; ++bj) acc[i][bj] = float16v{};
 
-    // parity of each of this lane's two dequant columns' zero element index at g = 0
+    // parity of each of this lane's two dequant columns' zero element index at weight group 0
     int zpar[2];
 #pragma unroll
     for (int bj = 0; bj < 2; ++bj) {
         const int64_t n = nw + 32 * bj + j;
-        zpar[bj] = (int)(((n < a.N ? n : a.N - 1) * a.G + gbeg) & 1);
+        zpar[bj] = (int)(((n < a.N ? n : a.N - 1) * a.wg) & 1);
     }
 
     // B fragments of step g, column block bj: this wave's packed columns,
@@ -267,7 +280,7 @@ __global__ __launch_bounds__(256, 2) void gemm2_kernel(Gemm2Args a) {
         return r;
     };
     auto dequant_b = [&](int g, int bj, const BRaw& r, u32x4 (&bf)[2][4]) {
-        int zn = (int)(((zpar[bj] ^ g) & 1) ? (r.zb >> 4) : (r.zb & 0xF));
+        int zn = (int)(((zpar[bj] ^ wgroup(g)) & 1) ? (r.zb >> 4) : (r.zb & 0xF));
         zn -= (zn & 8) << 1;
         const uint32_t zlo = 0x6408u + (uint32_t)zn;       // fp16 bits of 1032 + z
         const uint32_t zhi = 0x5480u + 16u * (uint32_t)zn;  // fp16 bits of 72 + z
@@ -403,6 +416,54 @@ __global__ __launch_bounds__(256, 2) void gemm2_kernel(Gemm2Args a) {
     // Row stride 144 B: the two lane halves (rows 4 apart) write disjoint
     // banks and the 16-byte reads stay aligned.
     block_barrier();  // every wave has finished reading the pipeline stages
+    if constexpr (OUTK == kF32) {
+        // fp32 outputs: the same staging with 4-byte values (row stride 272 B)
+        // and 16-byte stores of 4 outputs per lane
+        constexpr int kOutStride32 = 272;
+        constexpr int kHalfRows32 = BM / 2;
+        static_assert(4 * kHalfRows32 * kOutStride32 <= kStages * kStageBytes, "output staging exceeds LDS");
+        unsigned char* ost = &smem[0][0] + wave * kHalfRows32 * kOutStride32;
+        float bias_v[2];
+#pragma unroll
+        for (int bj = 0; bj < 2; ++bj) {
+            const int64_t n = nw + 32 * bj + j;
+            bias_v[bj] = n < a.N ? load_bias(a.bias, a.bias_kind, n) : 0.0f;
+        }
+        float* y = (float*)a.y;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+            for (int bi = 0; bi < MB / 2; ++bi)
+#pragma unroll
+                for (int bj = 0; bj < 2; ++bj)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int row = 32 * bi + 8 * (r / 4) + 4 * q + (r % 4);
+                        *(float*)(ost + row * kOutStride32 + 4 * (32 * bj + j)) =
+                            acc[h * (MB / 2) + bi][bj][r] + bias_v[bj];
+                    }
+            asm volatile("" ::: "memory");
+#pragma unroll
+            for (int i = 0; i < kHalfRows32 / 4; ++i) {
+                const int row = 4 * i + (lane >> 4);
+                const int c4 = lane & 15;
+                const u32x4 v = *(const u32x4*)(ost + row * kOutStride32 + 16 * c4);
+                const int64_t m = m0 + h * kHalfRows32 + row;
+                const int64_t n = nw + 4 * c4;
+                if (m < a.M) {
+                    if (a.vec_out && n + 4 <= a.N) {
+                        *(u32x4*)(y + m * a.N + n) = v;
+                    } else {
+#pragma unroll 1
+                        for (int e = 0; e < 4; ++e)
+                            if (n + e < a.N) y[m * a.N + n + e] = __builtin_bit_cast(float, (uint32_t)v[e]);
+                    }
+                }
+            }
+            asm volatile("" ::: "memory");
+        }
+        return;
+    }
     constexpr int kOutStride = 144;
     constexpr int kHalfRows = BM / 2;
     static_assert(4 * kHalfRows * kOutStride <= kStages * kStageBytes, "output staging exceeds LDS");
@@ -456,7 +517,7 @@ __global__ __launch_bounds__(256, 2) void gemm2_kernel(Gemm2Args a) {
 // Sum of the K-range partials of every split tile, in range order
 // (deterministic), plus bias, rounded to the output type.  One thread: 8
 // consecutive outputs of one tile row.
-template <int XK>
+template <int OUTK>
 __global__ __launch_bounds__(256) void gemm2_reduce_kernel(Gemm2Args a) {
     constexpr int kPerTile = kBM * kBN / (256 * 8);  // workgroups per tile
     const int idx = blockIdx.x / kPerTile;           // split tile index
@@ -495,18 +556,28 @@ __global__ __launch_bounds__(256) void gemm2_reduce_kernel(Gemm2Args a) {
         const int64_t nn = n + i < a.N ? n + i : a.N - 1;
         out[i] = (i < 4 ? s0[i] : s1[i - 4]) + load_bias(a.bias, a.bias_kind, nn);
     }
+    if constexpr (OUTK == kF32) {
+        float* y = (float*)a.y;
+        if (a.vec_out && n + 8 <= a.N) {
+            *(float4v*)(y + m * a.N + n) = float4v{out[0], out[1], out[2], out[3]};
+            *(float4v*)(y + m * a.N + n + 4) = float4v{out[4], out[5], out[6], out[7]};
+        } else {
+            for (int i = 0; i < 8 && n + i < a.N; ++i) y[m * a.N + n + i] = out[i];
+        }
+        return;
+    }
     uint16_t* y = (uint16_t*)a.y;
     if (a.vec_out && n + 8 <= a.N) {
         u32x4 v;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const uint32_t lo = XK == kF16 ? float_to_half_bits(out[2 * i]) : float_to_bf16_bits(out[2 * i]);
-            const uint32_t hi = XK == kF16 ? float_to_half_bits(out[2 * i + 1]) : float_to_bf16_bits(out[2 * i + 1]);
+            const uint32_t lo = OUTK == kF16 ? float_to_half_bits(out[2 * i]) : float_to_bf16_bits(out[2 * i]);
+            const uint32_t hi = OUTK == kF16 ? float_to_half_bits(out[2 * i + 1]) : float_to_bf16_bits(out[2 * i + 1]);
             v[i] = lo | (hi << 16);
         }
         *(u32x4*)(y + m * a.N + n) = v;
     } else {
-        for (int i = 0; i < 8 && n + i < a.N; ++i) store_out<XK>(a.y, m * a.N + n + i, out[i]);
+        for (int i = 0; i < 8 && n + i < a.N; ++i) store_out<OUTK>(a.y, m * a.N + n + i, out[i]);
     }
 }
 
@@ -573,20 +644,60 @@ Gemm2Plan plan_gemm2(int64_t rows, int64_t out_features, int64_t in_features) {
     return pl;
 }
 
+// Split of every fp32 activation row into [hi | lo] bf16 planes: one
+// thread per 8 consecutive values.
+__global__ __launch_bounds__(256) void split_planes_kernel(const float* x, uint16_t* planes, int64_t items, int K) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= items) return;
+    const int64_t e = i * 8;
+    const int64_t m = e / K;
+    const int64_t c = e - m * K;
+    const float4v f0 = *(const float4v*)(x + e);
+    const float4v f1 = *(const float4v*)(x + e + 4);
+    u32x4 hi, lo;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const float x0 = k < 2 ? f0[2 * k] : f1[2 * k - 4];
+        const float x1 = k < 2 ? f0[2 * k + 1] : f1[2 * k - 3];
+        const uint16_t h0 = float_to_bf16_bits(x0), h1 = float_to_bf16_bits(x1);
+        const uint16_t l0 = float_to_bf16_bits(x0 - bf16_bits_to_float(h0));
+        const uint16_t l1 = float_to_bf16_bits(x1 - bf16_bits_to_float(h1));
+        hi[k] = (uint32_t)h0 | ((uint32_t)h1 << 16);
+        lo[k] = (uint32_t)l0 | ((uint32_t)l1 << 16);
+    }
+    *(u32x4*)(planes + m * 2 * K + c) = hi;
+    *(u32x4*)(planes + m * 2 * K + K + c) = lo;
+}
+
+// Workspace: [counter area][split-tile partials][fp32 activations: bf16 planes, 256-byte aligned]
+int64_t planes_offset(const Gemm2Plan& pl) {
+    return (kGemvCounterBytes + pl.partial_bytes + 255) / 256 * 256;
+}
+
 }  // namespace
 
-int64_t gemm2_workspace_bytes(int64_t rows, int64_t out_features, int64_t in_features) {
-    const Gemm2Plan pl = plan_gemm2(rows, out_features, in_features);
+int64_t gemm2_workspace_bytes(int64_t rows, int64_t out_features, int64_t in_features, int x_kind) {
+    const bool f32 = x_kind == kF32;
+    const Gemm2Plan pl = plan_gemm2(rows, out_features, f32 ? 2 * in_features : in_features);
+    if (f32) return planes_offset(pl) + rows * in_features * 4;
     return pl.partial_bytes ? kGemvCounterBytes + pl.partial_bytes : 0;
 }
 
 bool gemm2_supported(const LinearProblem& p) {
-    return (p.x_kind == kF16 || p.x_kind == kBF16);
+    return p.x_kind == kF16 || p.x_kind == kBF16 || p.x_kind == kF32;
+}
+
+const char* gemm_kernel_name(int64_t, int64_t, int64_t, int x_kind) {
+    if (x_kind == kF16) return "gemm2_kernel<f16,128>";
+    if (x_kind == kBF16) return "gemm2_kernel<bf16,128>";
+    return "gemm2_kernel<bf16 hi|lo planes of f32,128>";
 }
 
 hipError_t launch_gemm2(const LinearProblem& p, void* workspace, hipStream_t stream, hipEvent_t start,
                         hipEvent_t stop) {
-    const Gemm2Plan pl = plan_gemm2(p.rows, p.out_features, p.in_features);
+    const bool f32 = p.x_kind == kF32;
+    const int64_t k_act = f32 ? 2 * p.in_features : p.in_features;  // activation row length
+    const Gemm2Plan pl = plan_gemm2(p.rows, p.out_features, k_act);
     Gemm2Args args{};
     args.x = (const uint16_t*)p.x;
     args.qweight = p.qweight;
@@ -597,11 +708,12 @@ hipError_t launch_gemm2(const LinearProblem& p, void* workspace, hipStream_t str
     args.y = p.y;
     args.M = (int)p.rows;
     args.N = (int)p.out_features;
-    args.K = (int)p.in_features;
-    args.G = (int)(p.in_features / 64);
+    args.K = (int)k_act;
+    args.G = (int)(k_act / 64);
+    args.wg = (int)(p.in_features / 64);
     args.tiles_m = pl.tiles_m;
     args.tiles_n = pl.tiles_n;
-    args.vec_out = (((uintptr_t)p.y & 15) == 0) && (p.out_features % 8 == 0);
+    args.vec_out = (((uintptr_t)p.y & 15) == 0) && (p.out_features % (f32 ? 4 : 8) == 0);
     args.dp_tiles = pl.dp_tiles;
     args.splits = pl.splits;
     args.gps = pl.gps;
@@ -613,13 +725,27 @@ hipError_t launch_gemm2(const LinearProblem& p, void* workspace, hipStream_t str
     const dim3 rgrid((unsigned)(pl.split_tiles * kPerTile));
     hipError_t err;
     if (p.x_kind == kF16) {
-        err = launch_kernel(gemm2_kernel<kF16, kBM>, grid, dim3(256), 0, stream, start, two ? nullptr : stop, args);
+        err = launch_kernel(gemm2_kernel<kF16, kBM, kF16>, grid, dim3(256), 0, stream, start, two ? nullptr : stop,
+                            args);
         if (err == hipSuccess && two)
             err = launch_kernel(gemm2_reduce_kernel<kF16>, rgrid, dim3(256), 0, stream, nullptr, stop, args);
-    } else {
-        err = launch_kernel(gemm2_kernel<kBF16, kBM>, grid, dim3(256), 0, stream, start, two ? nullptr : stop, args);
+    } else if (p.x_kind == kBF16) {
+        err = launch_kernel(gemm2_kernel<kBF16, kBM, kBF16>, grid, dim3(256), 0, stream, start, two ? nullptr : stop,
+                            args);
         if (err == hipSuccess && two)
             err = launch_kernel(gemm2_reduce_kernel<kBF16>, rgrid, dim3(256), 0, stream, nullptr, stop, args);
+    } else {
+        // fp32: [hi | lo] bf16 planes into the workspace, then the bf16 GEMM over 2K with fp32 output
+        uint16_t* planes = (uint16_t*)((char*)workspace + planes_offset(pl));
+        const int64_t items = p.rows * p.in_features / 8;
+        err = launch_kernel(split_planes_kernel, dim3((unsigned)((items + 255) / 256)), dim3(256), 0, stream, start,
+                            nullptr, (const float*)p.x, planes, items, (int)p.in_features);
+        args.x = planes;
+        if (err == hipSuccess)
+            err = launch_kernel(gemm2_kernel<kBF16, kBM, kF32>, grid, dim3(256), 0, stream, nullptr,
+                                two ? nullptr : stop, args);
+        if (err == hipSuccess && two)
+            err = launch_kernel(gemm2_reduce_kernel<kF32>, rgrid, dim3(256), 0, stream, nullptr, stop, args);
     }
     return err;
 }

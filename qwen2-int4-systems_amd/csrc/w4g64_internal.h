@@ -60,14 +60,10 @@ hipError_t launch_gemv16(const LinearProblem& p, const GemvPlan& plan, void* wor
 // live in the workspace after the counter area and a second kernel adds
 // them up.
 bool gemm2_supported(const LinearProblem& p);
-int64_t gemm2_workspace_bytes(int64_t rows, int64_t out_features, int64_t in_features);
+int64_t gemm2_workspace_bytes(int64_t rows, int64_t out_features, int64_t in_features, int x_kind);
+const char* gemm_kernel_name(int64_t rows, int64_t out_features, int64_t in_features, int x_kind);
 hipError_t launch_gemm2(const LinearProblem& p, void* workspace, hipStream_t stream, hipEvent_t start = nullptr,
                         hipEvent_t stop = nullptr);
-
-// Prefill GEMM (rows > kGemvMaxRows).
-hipError_t launch_gemm(const LinearProblem& p, hipStream_t stream, hipEvent_t start = nullptr,
-                       hipEvent_t stop = nullptr);
-const char* gemm_kernel_name(int64_t rows, int64_t out_features, int64_t in_features, int x_kind);
 
 // Launch a kernel; with events, hipExtLaunchKernelGGL records them at the
 // kernel's own start and end (what a profiler reports as its duration).

@@ -144,6 +144,10 @@ def test_workspace_and_kernel_plan_queries():
     # K ranges with fp32 partials after the counter area; whole rounds need none
     assert lib.w4g64_linear_workspace_bytes(2048, 8960, 1536, _lib.DTYPE_BF16) == 64 * 1024 + 48 * 4 * 128 * 256 * 4
     assert lib.w4g64_linear_workspace_bytes(2048, 8192, 1536, _lib.DTYPE_BF16) == 0
+    # fp32 GEMM activations: two bf16 planes (rows x 2 in_features x 2 B) after the counters and partials
+    ws32 = lib.w4g64_linear_workspace_bytes(512, 1536, 8960, _lib.DTYPE_F32)
+    assert 64 * 1024 + 512 * 8960 * 4 <= ws32 <= 64 * 1024 + (64 << 20) + 512 * 8960 * 4 + 256
+    assert lib.w4g64_linear_kernel_name(512, 1536, 8960, _lib.DTYPE_F32).startswith(b"gemm2_kernel<bf16 hi|lo")
     assert lib.w4g64_linear_workspace_bytes(1, 1536, 100, _lib.DTYPE_F16) == 0
     assert lib.w4g64_linear_kernel_name(1, 8960, 1536, _lib.DTYPE_F16).startswith(b"gemv_kernel<f16")
     assert lib.w4g64_linear_kernel_name(16, 1536, 8960, _lib.DTYPE_BF16) == b"gemv16_kernel<bf16,18,8>"

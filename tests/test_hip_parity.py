@@ -207,7 +207,7 @@ def test_awq_folded_weights_bf16(rows):
     check_linear(x, q, s, z, None, n, k, "bf16")
 
 
-@pytest.mark.parametrize("rows", [1, 3, 5, 6, 16, 17, 64])
+@pytest.mark.parametrize("rows", [1, 3, 5, 6, 16, 17, 64, 200, 512])
 def test_fp32_activations_run_natively(rows):
     # the reference routes fp32 to its torch oracle (backends.py:172-177); here it runs on the kernels
     n, k = SHAPES["down_proj"]
@@ -215,10 +215,20 @@ def test_fp32_activations_run_natively(rows):
     x = O.activations(rows, k, seed=O.BASE_SEED + 5 * rows, dtype="fp32")
     bias = np.linspace(-1, 1, n, dtype=np.float32)
     # decode splits fp32 exactly into three bf16 parts: near-fp32 accuracy;
-    # the GEMM multiplies bf16-rounded weights: bf16-level accuracy
+    # the GEMM (two bf16 planes of the activations) multiplies bf16-rounded
+    # weights: bf16-level accuracy
     normwise = 1e-5 if rows <= 16 else 1e-2
     tol = (1e-4, 1e-4) if rows <= 16 else (0.02, 0.05)
     check_linear(x, q, s, z, bias, n, k, "fp32", bias_dtype="fp32", normwise=normwise, tol=tol)
+
+
+@pytest.mark.parametrize("n,k,rows", [(200, 192, 40), (1000, 64, 300), (4, 128, 33)])
+def test_fp32_gemm_ragged_shapes(n, k, rows):
+    # output widths that are not a multiple of 4 (scalar fp32 stores), K = 64,
+    # and a single column tile
+    q, s, z = weights("awq", n, k, O.BASE_SEED + 3 * n + k)
+    x = O.activations(rows, k, seed=O.BASE_SEED + rows + n, dtype="fp32")
+    check_linear(x, q, s, z, None, n, k, "fp32", normwise=1e-2, tol=(0.02, 0.05))
 
 
 @pytest.mark.parametrize("rows", [2, 40])
