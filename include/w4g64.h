@@ -107,11 +107,13 @@ int w4g64_linear_timed(const void* x, int x_dtype, const uint8_t* qweight, const
                        int64_t out_features, int64_t in_features, void* workspace, int64_t workspace_bytes,
                        void* stream, void* start_event, void* stop_event);
 
-/* Decode-step fusion of the SwiGLU product into the down projection (rows
- * 1..16): gate_up is [rows, 2 * in_features] bf16 (gate | up), the activation
- * is h = silu(gate) * up in fp32 (silu(g) = g / (1 + exp(-g))), and
+/* Fusion of the SwiGLU product into the down projection: gate_up is
+ * [rows, 2 * in_features] bf16 (gate | up), the activation is
+ * h = silu(gate) * up in fp32 (silu(g) = g / (1 + exp(-g))), and
  * y[rows, out] = h @ dequant(W)^T (+ bias) in fp32, as w4g64_linear on the
- * fp32 h.  gate_up and qweight 16-byte aligned.
+ * fp32 h (decode rows 1..16: formed in the GEMV's activation staging; more
+ * rows: written as the GEMM's bf16 planes).  gate_up and qweight 16-byte
+ * aligned.
  * Replaces: QwenMLP.forward's product and down projection
  *           (src/qwen_int4/model.py:133-136). */
 int w4g64_linear_swiglu(const void* gate_up, const uint8_t* qweight, const uint16_t* scales, const uint8_t* zeros,

@@ -94,8 +94,9 @@ static bool fused_form(int x_dtype) { return x_dtype == W4G64_DTYPE_BF16_SWIGLU;
 int64_t w4g64_linear_workspace_bytes(int64_t rows, int64_t out_features, int64_t in_features, int x_dtype) {
     if (rows <= 0 || out_features <= 0 || in_features <= 0 || in_features % 64) return 0;
     if (fused_form(x_dtype))
-        return rows <= w4g64::kGemvMaxRows ? w4g64::plan_gemv(rows, out_features, in_features, x_dtype).workspace_bytes
-                                           : 0;
+        return rows <= w4g64::kGemvMaxRows
+                   ? w4g64::plan_gemv(rows, out_features, in_features, x_dtype).workspace_bytes
+                   : w4g64::gemm2_workspace_bytes(rows, out_features, in_features, x_dtype);
     if (x_dtype != W4G64_DTYPE_F16 && x_dtype != W4G64_DTYPE_BF16 && x_dtype != W4G64_DTYPE_F32) return 0;
     if (rows > w4g64::kGemvMaxRows) {
         w4g64::LinearProblem p{nullptr, x_dtype, nullptr, nullptr, nullptr, nullptr, 0, nullptr, rows, out_features,
@@ -110,7 +111,7 @@ const char* w4g64_linear_kernel_name(int64_t rows, int64_t out_features, int64_t
     if (fused_form(x_dtype))
         return rows <= w4g64::kGemvMaxRows
                    ? w4g64::gemv_kernel_name(w4g64::plan_gemv(rows, out_features, in_features, x_dtype), x_dtype)
-                   : "none";
+                   : w4g64::gemm_kernel_name(rows, out_features, in_features, x_dtype);
     if (x_dtype != W4G64_DTYPE_F16 && x_dtype != W4G64_DTYPE_BF16 && x_dtype != W4G64_DTYPE_F32) return "none";
     if (rows <= w4g64::kGemvMaxRows)
         return w4g64::gemv_kernel_name(w4g64::plan_gemv(rows, out_features, in_features, x_dtype), x_dtype);
@@ -193,9 +194,8 @@ static int fused_common_checks(const uint8_t* qweight, const uint16_t* scales, c
         return fail(W4G64_STATUS_INVALID_DTYPE, "bias must have dtype float16, bfloat16, or float32");
     if ((bias_dtype == W4G64_DTYPE_NONE) != (bias == nullptr))
         return fail(W4G64_STATUS_INVALID_VALUE, "bias pointer and bias dtype disagree");
-    if (rows <= 0 || rows > w4g64::kGemvMaxRows)
-        return fail(W4G64_STATUS_INVALID_VALUE, "fused decode linears take 1..%d rows, got %lld", w4g64::kGemvMaxRows,
-                    (long long)rows);
+    if (rows <= 0 || rows > (1ll << 30))
+        return fail(W4G64_STATUS_INVALID_VALUE, "rows must be positive, got %lld", (long long)rows);
     if (in_features <= 0 || in_features % 64 || in_features > (1ll << 24))
         return fail(W4G64_STATUS_INVALID_VALUE, "in_features must be a positive multiple of 64, got %lld",
                     (long long)in_features);
@@ -221,6 +221,11 @@ int w4g64_linear_swiglu(const void* gate_up, const uint8_t* qweight, const uint1
     if (!aligned(gate_up, 16)) return fail(W4G64_STATUS_INVALID_VALUE, "gate_up must be 16-byte aligned");
     w4g64::LinearProblem p{gate_up, w4g64::kSwiGLU, qweight, scales, zeros, bias, bias_dtype, y, rows, out_features,
                            in_features};
+    if (rows > w4g64::kGemvMaxRows) {
+        const int64_t need = w4g64::gemm2_workspace_bytes(rows, out_features, in_features, w4g64::kSwiGLU);
+        if (int st = check_workspace(workspace, workspace_bytes, need)) return st;
+        return hip_status(w4g64::launch_gemm2(p, workspace, (hipStream_t)stream), "gemm");
+    }
     const w4g64::GemvPlan plan = w4g64::plan_gemv(rows, out_features, in_features, w4g64::kSwiGLU);
     if (int st = check_workspace(workspace, workspace_bytes, plan.workspace_bytes)) return st;
     return hip_status(w4g64::launch_gemv(p, plan, workspace, (hipStream_t)stream), "gemv");

@@ -645,15 +645,33 @@ Gemm2Plan plan_gemm2(int64_t rows, int64_t out_features, int64_t in_features) {
 }
 
 // Split of every fp32 activation row into [hi | lo] bf16 planes: one
-// thread per 8 consecutive values.
-__global__ __launch_bounds__(256) void split_planes_kernel(const float* x, uint16_t* planes, int64_t items, int K) {
+// thread per 8 consecutive values.  XK = kF32: x is fp32 [M, K]; XK =
+// kSwiGLU: x is [M, 2K] bf16 (gate | up) and the activation is silu(gate) *
+// up in fp32, silu(g) = g / (1 + exp(-g)) (src/qwen_int4/model.py:133-136).
+template <int XK>
+__global__ __launch_bounds__(256) void split_planes_kernel(const void* x, uint16_t* planes, int64_t items, int K) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= items) return;
     const int64_t e = i * 8;
     const int64_t m = e / K;
     const int64_t c = e - m * K;
-    const float4v f0 = *(const float4v*)(x + e);
-    const float4v f1 = *(const float4v*)(x + e + 4);
+    float4v f0, f1;
+    if constexpr (XK == kSwiGLU) {
+        const uint16_t* gu = (const uint16_t*)x + m * 2 * K + c;
+        const u32x4 gv = *(const u32x4*)gu;
+        const u32x4 uv = *(const u32x4*)(gu + K);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const uint32_t gw = gv[t / 2], uw = uv[t / 2];
+            const float g = bf16_bits_to_float(t & 1 ? gw >> 16 : gw & 0xFFFFu);
+            const float u = bf16_bits_to_float(t & 1 ? uw >> 16 : uw & 0xFFFFu);
+            const float h = (g / (1.0f + expf(-g))) * u;
+            if (t < 4) f0[t] = h; else f1[t - 4] = h;
+        }
+    } else {
+        f0 = *(const float4v*)((const float*)x + e);
+        f1 = *(const float4v*)((const float*)x + e + 4);
+    }
     u32x4 hi, lo;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
@@ -677,25 +695,26 @@ int64_t planes_offset(const Gemm2Plan& pl) {
 }  // namespace
 
 int64_t gemm2_workspace_bytes(int64_t rows, int64_t out_features, int64_t in_features, int x_kind) {
-    const bool f32 = x_kind == kF32;
+    const bool f32 = x_kind == kF32 || x_kind == kSwiGLU;
     const Gemm2Plan pl = plan_gemm2(rows, out_features, f32 ? 2 * in_features : in_features);
     if (f32) return planes_offset(pl) + rows * in_features * 4;
     return pl.partial_bytes ? kGemvCounterBytes + pl.partial_bytes : 0;
 }
 
 bool gemm2_supported(const LinearProblem& p) {
-    return p.x_kind == kF16 || p.x_kind == kBF16 || p.x_kind == kF32;
+    return p.x_kind == kF16 || p.x_kind == kBF16 || p.x_kind == kF32 || p.x_kind == kSwiGLU;
 }
 
 const char* gemm_kernel_name(int64_t, int64_t, int64_t, int x_kind) {
     if (x_kind == kF16) return "gemm2_kernel<f16,128>";
     if (x_kind == kBF16) return "gemm2_kernel<bf16,128>";
+    if (x_kind == kSwiGLU) return "gemm2_kernel<bf16 hi|lo planes of silu(gate)*up,128>";
     return "gemm2_kernel<bf16 hi|lo planes of f32,128>";
 }
 
 hipError_t launch_gemm2(const LinearProblem& p, void* workspace, hipStream_t stream, hipEvent_t start,
                         hipEvent_t stop) {
-    const bool f32 = p.x_kind == kF32;
+    const bool f32 = p.x_kind == kF32 || p.x_kind == kSwiGLU;
     const int64_t k_act = f32 ? 2 * p.in_features : p.in_features;  // activation row length
     const Gemm2Plan pl = plan_gemm2(p.rows, p.out_features, k_act);
     Gemm2Args args{};
@@ -735,11 +754,17 @@ hipError_t launch_gemm2(const LinearProblem& p, void* workspace, hipStream_t str
         if (err == hipSuccess && two)
             err = launch_kernel(gemm2_reduce_kernel<kBF16>, rgrid, dim3(256), 0, stream, nullptr, stop, args);
     } else {
-        // fp32: [hi | lo] bf16 planes into the workspace, then the bf16 GEMM over 2K with fp32 output
+        // fp32 (or silu(gate) * up): [hi | lo] bf16 planes into the workspace, then the bf16 GEMM over 2K
+        // with fp32 output
         uint16_t* planes = (uint16_t*)((char*)workspace + planes_offset(pl));
         const int64_t items = p.rows * p.in_features / 8;
-        err = launch_kernel(split_planes_kernel, dim3((unsigned)((items + 255) / 256)), dim3(256), 0, stream, start,
-                            nullptr, (const float*)p.x, planes, items, (int)p.in_features);
+        const dim3 sgrid((unsigned)((items + 255) / 256));
+        if (p.x_kind == kSwiGLU)
+            err = launch_kernel(split_planes_kernel<kSwiGLU>, sgrid, dim3(256), 0, stream, start, nullptr, p.x, planes,
+                                items, (int)p.in_features);
+        else
+            err = launch_kernel(split_planes_kernel<kF32>, sgrid, dim3(256), 0, stream, start, nullptr, p.x, planes,
+                                items, (int)p.in_features);
         args.x = planes;
         if (err == hipSuccess)
             err = launch_kernel(gemm2_kernel<kBF16, kBM, kF32>, grid, dim3(256), 0, stream, nullptr,

@@ -176,3 +176,98 @@ class FusedDecodeStep:
             delta, delta_code = self.down, _lib.DTYPE_F32
         self._norm(delta, delta_code, model.model.norm.weight, stream)
         return F.linear(self.normed, model.lm_head.weight).view(self.batch, 1, -1)
+
+
+class FusedPrefill:
+    """Prompt pass of ``batch`` unpadded prompts of one length on the HIP
+    kernels, filling static caches [batch, kv_heads, max_length, head_dim]:
+    per layer add_rmsnorm, the fused q|k|v GEMM (bias), rotary and causal fp32
+    attention (torch, as ``QwenAttention.forward``), the o_proj GEMM,
+    add_rmsnorm, the fused gate|up GEMM and the SwiGLU down projection (its
+    product written as the GEMM's bf16 planes; fp32 out).  Returns the
+    logits [batch, length, vocab] of every prompt position, as the model's
+    forward does (src/qwen_int4/model.py:169-199, :231-245)."""
+
+    def __init__(self, model) -> None:
+        if not torch.cuda.is_available():
+            raise RuntimeError("the fused prefill requires a ROCm GPU")
+        self.lib = _lib.load()
+        self.model = model
+        self.fused = fuse_projections(model)
+        attn = model.model.layers[0].self_attn
+        self.heads, self.kv_heads, self.head_dim = attn.num_heads, attn.num_kv_heads, attn.head_dim
+        self.hidden = model.config.hidden_size
+        self.inter = model.config.intermediate_size
+        self.eps = float(model.model.norm.eps)
+        self._workspace = None
+
+    def _ws(self, nbytes: int) -> torch.Tensor:
+        if self._workspace is None or self._workspace.numel() < nbytes:
+            self._workspace = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=self.model.lm_head.weight.device)
+        return self._workspace
+
+    def __call__(self, input_ids: torch.Tensor, caches) -> torch.Tensor:
+        from .model import attend, rotate_half
+
+        model, lib = self.model, self.lib
+        batch, length = input_ids.shape
+        rows = batch * length
+        device = input_ids.device
+        stream = ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+        bf16 = torch.bfloat16
+        shapes = [(self.heads * self.head_dim + 2 * self.kv_heads * self.head_dim, self.hidden, _lib.DTYPE_BF16),
+                  (self.hidden, self.heads * self.head_dim, _lib.DTYPE_BF16),
+                  (2 * self.inter, self.hidden, _lib.DTYPE_BF16),
+                  (self.hidden, self.inter, _lib.DTYPE_BF16_SWIGLU)]
+        ws = self._ws(max(lib.w4g64_linear_workspace_bytes(rows, n, k, c) for n, k, c in shapes))
+        x = torch.index_select(model.model.embed_tokens.weight, 0, input_ids.reshape(-1))  # [rows, H]
+        normed = torch.empty_like(x)
+        qkv = torch.empty((rows, shapes[0][0]), dtype=bf16, device=device)
+        o = torch.empty_like(x)
+        gate_up = torch.empty((rows, 2 * self.inter), dtype=bf16, device=device)
+        down = torch.empty((rows, self.hidden), dtype=torch.float32, device=device)
+        positions = torch.arange(length, device=device).view(1, -1).expand(batch, length)
+        cos, sin = model.model.rotary_emb(positions, bf16)
+        cos, sin = cos.unsqueeze(1), sin.unsqueeze(1)
+        allowed = torch.ones((length, length), dtype=torch.bool, device=device).tril().view(1, 1, length, length)
+        h, kvh, d = self.heads, self.kv_heads, self.head_dim
+
+        def linear(inp, code, w, out):
+            bias = w["bias"]
+            _lib.check(lib.w4g64_linear(
+                _ptr(inp), code, _ptr(w["qweight"]), _ptr(w["scales"]), _ptr(w["zeros"]), _ptr(bias),
+                _lib.DTYPE_NONE if bias is None else _lib.DTYPE_BF16, _ptr(out), rows, out.shape[1], inp.shape[1],
+                _ptr(ws), ws.numel(), stream))
+
+        def norm(delta, code, weight):
+            _lib.check(lib.qwen2_add_rmsnorm(_ptr(x), _ptr(delta), code, _ptr(weight), ctypes.c_float(self.eps),
+                                             _ptr(x), _ptr(normed), rows, self.hidden, stream))
+
+        delta, delta_code = None, _lib.DTYPE_NONE
+        with torch.inference_mode():
+            for layer, fused, (k_cache, v_cache) in zip(model.model.layers, self.fused, caches):
+                norm(delta, delta_code, layer.input_layernorm.weight)
+                linear(normed, _lib.DTYPE_BF16, fused["qkv"], qkv)
+                q = qkv[:, : h * d].view(batch, length, h, d).transpose(1, 2)
+                k = qkv[:, h * d:(h + kvh) * d].view(batch, length, kvh, d).transpose(1, 2)
+                v = qkv[:, (h + kvh) * d:].view(batch, length, kvh, d).transpose(1, 2)
+                q = q * cos + rotate_half(q) * sin
+                k = k * cos + rotate_half(k) * sin
+                k_cache[:, :, :length].copy_(k)
+                v_cache[:, :, :length].copy_(v)
+                group = h // kvh
+                attended = attend(q, k.repeat_interleave(group, dim=1), v.repeat_interleave(group, dim=1), allowed,
+                                  d ** -0.5)
+                attended = attended.transpose(1, 2).reshape(rows, h * d)
+                op = layer.self_attn.o_proj
+                linear(attended, _lib.DTYPE_BF16, {"qweight": op.qweight, "scales": op.scales, "zeros": op.zeros,
+                                                   "bias": None}, o)
+                norm(o, _lib.DTYPE_BF16, layer.post_attention_layernorm.weight)
+                linear(normed, _lib.DTYPE_BF16, fused["gate_up"], gate_up)
+                dp = layer.mlp.down_proj
+                _lib.check(lib.w4g64_linear_swiglu(
+                    _ptr(gate_up), _ptr(dp.qweight), _ptr(dp.scales), _ptr(dp.zeros), None, _lib.DTYPE_NONE,
+                    _ptr(down), rows, self.hidden, self.inter, _ptr(ws), ws.numel(), stream))
+                delta, delta_code = down, _lib.DTYPE_F32
+            norm(delta, delta_code, model.model.norm.weight)
+            return F.linear(normed, model.lm_head.weight).view(batch, length, -1)

@@ -14,7 +14,7 @@ from dataclasses import dataclass
 
 import torch
 
-from .decode import FusedDecodeStep
+from .decode import FusedDecodeStep, FusedPrefill
 
 
 @dataclass
@@ -106,14 +106,15 @@ def greedy_generate_cached(model, input_ids: torch.Tensor, *, max_new_tokens: in
 
 class StaticGreedyDecoder:
     """Greedy decoding of ``batch`` unpadded prompts of one length with a
-    preallocated cache of ``max_length`` positions; every decode step is one
-    HIP graph replay (``use_graph``) of the fused decode step
-    (``decode.FusedDecodeStep``, eight launches per layer) or, with
-    ``fused=False``, of the module-level ``model.decode_static``."""
+    preallocated cache of ``max_length`` positions.  The prompt runs as
+    ``decode.FusedPrefill`` and every decode step is one HIP graph replay
+    (``use_graph``) of ``decode.FusedDecodeStep``; with ``fused=False``, the
+    module-level forward and ``model.decode_static`` instead."""
 
     def __init__(self, model, batch: int, max_length: int, *, use_graph: bool = True, fused: bool = True) -> None:
         self.model = model
         self.fused = FusedDecodeStep(model, batch, max_length) if fused else None
+        self.fused_prefill = FusedPrefill(model) if fused else None
         self.batch = batch
         self.max_length = max_length
         device = model.lm_head.weight.device
@@ -132,10 +133,13 @@ class StaticGreedyDecoder:
         if batch != self.batch or length >= self.max_length:
             raise ValueError("prompt batch or length does not fit this decoder")
         with torch.inference_mode():
-            logits, caches = self.model(input_ids, use_cache=True)
-            for (ks, vs), (k, v) in zip(self.caches, caches):
-                ks[:, :, :length].copy_(k)
-                vs[:, :, :length].copy_(v)
+            if self.fused_prefill is not None:
+                logits = self.fused_prefill(input_ids, self.caches)
+            else:
+                logits, caches = self.model(input_ids, use_cache=True)
+                for (ks, vs), (k, v) in zip(self.caches, caches):
+                    ks[:, :, :length].copy_(k)
+                    vs[:, :, :length].copy_(v)
         self.length = length
         self.token.copy_(logits[:, -1].argmax(dim=-1, keepdim=True))
         return logits

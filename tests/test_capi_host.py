@@ -125,7 +125,9 @@ def test_fused_swiglu_linear_rejects_before_launch():
         "gemv_kernel<swiglu_bf16,")
     assert lib.w4g64_linear_kernel_name(12, 1536, 8960, _lib.DTYPE_BF16_SWIGLU).decode().startswith(
         "gemv_kernel<swiglu_bf16,")
-    assert lib.w4g64_linear_kernel_name(64, 1536, 8960, _lib.DTYPE_BF16_SWIGLU) == b"none"
+    assert lib.w4g64_linear_kernel_name(64, 1536, 8960, _lib.DTYPE_BF16_SWIGLU).startswith(b"gemm2_kernel<bf16 hi|lo")
+    assert lib.w4g64_linear_workspace_bytes(512, 1536, 8960, _lib.DTYPE_BF16_SWIGLU) == \
+        lib.w4g64_linear_workspace_bytes(512, 1536, 8960, _lib.DTYPE_F32)
     assert lib.w4g64_linear_workspace_bytes(1, 64, 64, 4) == 0 and lib.w4g64_linear_kernel_name(1, 64, 64, 4) == b"none"
     assert lib.w4g64_linear_workspace_bytes(1, 1536, 8960, _lib.DTYPE_BF16_SWIGLU) == \
         lib.w4g64_linear_workspace_bytes(1, 1536, 8960, _lib.DTYPE_F32)

@@ -170,6 +170,29 @@ def test_linear_swiglu_matches_silu_then_reference_linear(rows, n, k):
     assert bool(torch.isfinite(y).all()) and _normwise(y, want) <= 1e-5
 
 
+@pytest.mark.parametrize("rows", [17, 64, 512])
+@pytest.mark.parametrize("n,k", [(1536, 8960), (100, 128)])
+def test_linear_swiglu_gemm_rows(rows, n, k):
+    """Prefill rows: the product is written as the GEMM's bf16 hi|lo planes and
+    multiplied by bf16-rounded dequantized weights -- the GEMM bar, normwise
+    1e-2."""
+    from oracle import oracle as O
+
+    lib = _lib.load()
+    g = _gen(rows * 13 + n + k)
+    gate_up = (torch.randn((rows, 2 * k), generator=g, device="cuda") * 3).to(torch.bfloat16)
+    h = torch.nn.functional.silu(gate_up[:, :k].float()) * gate_up[:, k:].float()
+    qw, sc, z = _weights(n, k, 11, asymmetric=True)
+    want = O.reference_linear_torch(h, qw, sc, z, None, out_features=n, in_features=k)
+    ws = torch.zeros(lib.w4g64_linear_workspace_bytes(rows, n, k, _lib.DTYPE_BF16_SWIGLU), dtype=torch.uint8,
+                     device="cuda")
+    y = torch.empty((rows, n), dtype=torch.float32, device="cuda")
+    _lib.check(lib.w4g64_linear_swiglu(_p(gate_up), _p(qw), _p(sc), _p(z), None, 0, _p(y), rows, n, k, _p(ws),
+                                       ws.numel(), _stream()))
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(y).all()) and _normwise(y, want) <= 1e-2
+
+
 SMALL128 = SimpleNamespace(hidden_size=256, num_attention_heads=2, num_key_value_heads=1, head_dim=128,
                            intermediate_size=512, num_hidden_layers=3, vocab_size=512, rms_norm_eps=1e-6,
                            rope_theta=1_000_000.0)
@@ -245,10 +268,27 @@ def test_fused_decode_step_matches_module_decode(batch):
         assert _cos(k0[:, :, :83], k1[:, :, :83]) >= 0.9999 and _cos(v0[:, :, :83], v1[:, :, :83]) >= 0.9999
 
 
+@pytest.mark.parametrize("batch,length", [(1, 40), (2, 17)])
+def test_fused_prefill_matches_module_forward(batch, length):
+    from qwen_int4_hip.decode import FusedPrefill
+
+    model = _build(SMALL128, 5 + batch)
+    prompt = torch.randint(0, SMALL128.vocab_size, (batch, length), generator=torch.Generator().manual_seed(7)).cuda()
+    with torch.inference_mode():
+        want, cache = model(prompt, use_cache=True)
+        caches = model.new_static_cache(batch, 64, "cuda")
+        got = FusedPrefill(model)(prompt, caches)
+    assert got.shape == want.shape and _cos(got, want) >= 0.9999
+    for (k0, v0), (k1, v1) in zip(cache, caches):
+        assert _cos(k1[:, :, :length], k0) >= 0.9999 and _cos(v1[:, :, :length], v0) >= 0.9999
+        assert not bool(k1[:, :, length:].any())  # positions past the prompt untouched
+
+
 def test_full_width_fused_decode_against_reference_backend():
-    """Qwen2-1.5B widths at 2 layers: the fused graph-replayed decode steps
-    stay within cosine 0.9999 of the model whose linears run the reference's
-    torch backend (the oracle's restatement, backends.py:73-98)."""
+    """Qwen2-1.5B widths at 2 layers: the fused prefill and the fused
+    graph-replayed decode steps stay within cosine 0.9999 of the model whose
+    linears run the reference's torch backend (the oracle's restatement,
+    backends.py:73-98)."""
     from test_model import QWEN2_1_5B, with_reference_linears
 
     from qwen_int4_hip.generation import StaticGreedyDecoder
@@ -259,8 +299,9 @@ def test_full_width_fused_decode_against_reference_backend():
     prompt = torch.randint(0, config.vocab_size, (1, 64), generator=torch.Generator().manual_seed(4)).cuda()
     decoder = StaticGreedyDecoder(model, 1, 96)
     with torch.inference_mode():
-        decoder.prefill(prompt)
+        got = decoder.prefill(prompt)
         want, cache = ref(prompt, use_cache=True)
+        assert _cos(got, want) >= 0.9999  # the fused prefill
         token = want[:, -1:].argmax(dim=-1)
         for _ in range(4):
             got = decoder.step(token)
