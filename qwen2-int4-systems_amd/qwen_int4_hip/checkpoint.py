@@ -1,0 +1,354 @@
+"""Packed W4G64 checkpoints: metadata contracts, strict loading, export.
+
+Restates the reference's checkpoint contract so that its RTN-v4 and AWQ-v6
+safetensors files load drop-in into ``QwenInt4ForCausalLM``:
+
+  * metadata of the symmetric RTN export (scripts/quantize_model.py:148-162)
+    and of the canonical asymmetric AWQ export (src/qwen_int4/export.py:38-57);
+  * ``load_quantized_checkpoint`` (src/qwen_int4/checkpoint.py:51-118): the
+    quantized tensors must match the model's buffers name for name and shape
+    for shape, AWQ files also carry their transformed norms and v_proj bias,
+    and non-zero zero points require an asymmetric contract -- with the same
+    checks and messages.  The tensors are read straight into the device of
+    the model's buffers (safetensors loads to that device; no host copy of
+    the whole file), and buffers that ``decode.fuse_projections`` turned into
+    views of fused q|k|v and gate|up buffers are written through;
+  * the frozen canonical AWQ v6 manifest and the checks on a v6 file's bytes
+    and metadata before it loads (src/qwen_int4/artifact_contract.py:52-167,
+    src/qwen_int4/checkpoint.py:121-140).
+
+Loading uses safetensors only (no pickle).
+"""
+
+from __future__ import annotations
+
+import hashlib
+import json
+import re
+from dataclasses import dataclass
+from pathlib import Path
+
+import torch
+from safetensors import safe_open
+from safetensors.torch import load_file, save_file
+
+from .quantization import (
+    CANONICAL_PACKING_METADATA,
+    SCALE_LAYOUT_METADATA,
+    WEIGHT_LAYOUT_METADATA,
+    PackingFormat,
+)
+
+# Pinned upstream identity of the reference's exports (src/qwen_int4/provenance.py:3-6).
+HF_MODEL_ID = "Qwen/Qwen2-1.5B"
+HF_MODEL_REVISION = "8a16abf2848eda07cc5253dec660bf1ce007ad7a"
+HF_TOKENIZER_REVISION = HF_MODEL_REVISION
+
+RTN_FORMAT_VERSION = "qwen-int4-v1"
+AWQ_FORMAT_VERSION = "qwen-int4-awq-v1"
+AWQ_TRANSFORMED_SUFFIXES = ("input_layernorm.weight", "post_attention_layernorm.weight", "v_proj.bias")
+QUANTIZED_SUFFIXES = (".qweight", ".scales", ".zeros")
+ZERO_LAYOUT_METADATA = "packed_row_major_[out_features,in_features/group_size]"
+ASYMMETRIC_ZERO_POINT_CONTRACTS = {
+    "canonical_signed_packed_per_group",
+    "asymmetric_canonical_signed_packed_per_group",
+}
+
+
+@dataclass(frozen=True)
+class LoadReport:
+    loaded_keys: int
+    skipped_non_quantized_keys: int
+
+
+def is_quantized_key(name: str) -> bool:
+    return name.endswith(QUANTIZED_SUFFIXES)
+
+
+def canonical_rtn_metadata(*, group_size: int = 64, method: str = "symmetric_rtn",
+                           source_model: str = HF_MODEL_ID, source_model_revision: str = HF_MODEL_REVISION,
+                           tokenizer_revision: str = HF_TOKENIZER_REVISION) -> dict[str, str]:
+    """Metadata of a symmetric RTN export (scripts/quantize_model.py:148-162)."""
+    if method not in ("symmetric_rtn", "activation_weighted_clip_rtn"):
+        raise ValueError(f"unknown RTN method {method!r}")
+    return {
+        "format_version": RTN_FORMAT_VERSION,
+        "source_model": source_model,
+        "source_model_revision": source_model_revision,
+        "tokenizer_revision": tokenizer_revision,
+        "quantization": method,
+        "bits": "4",
+        "activation_dtype": "bf16_or_fp16",
+        "group_size": str(group_size),
+        "code_range": "[-7,7]",
+        "packing": CANONICAL_PACKING_METADATA,
+        "weight_layout": WEIGHT_LAYOUT_METADATA,
+        "scale_layout": SCALE_LAYOUT_METADATA,
+        "zero_point": "none_symmetric",
+    }
+
+
+def canonical_awq_metadata(*, group_size: int = 128) -> dict[str, str]:
+    """Metadata of a canonical asymmetric AWQ export (src/qwen_int4/export.py:38-57)."""
+    if group_size not in {64, 128}:
+        raise ValueError("canonical AWQ supports group sizes 64 and 128")
+    return {
+        "format_version": AWQ_FORMAT_VERSION,
+        "source_model": HF_MODEL_ID,
+        "source_model_revision": HF_MODEL_REVISION,
+        "tokenizer_revision": HF_TOKENIZER_REVISION,
+        "quantization": "canonical_awq_w4a16_asymmetric",
+        "bits": "4",
+        "activation_dtype": "bf16_or_fp16",
+        "group_size": str(group_size),
+        "code_range": "[-8,7]",
+        "packing": CANONICAL_PACKING_METADATA,
+        "weight_layout": WEIGHT_LAYOUT_METADATA,
+        "scale_layout": SCALE_LAYOUT_METADATA,
+        "zero_point": "canonical_signed_packed_per_group",
+        "zero_layout": ZERO_LAYOUT_METADATA,
+        "status": "awaiting_gpu_reference",
+    }
+
+
+def checkpoint_metadata(path: str | Path) -> dict[str, str]:
+    with safe_open(str(path), framework="pt", device="cpu") as handle:
+        return handle.metadata() or {}
+
+
+def packing_from_checkpoint(path: str | Path) -> PackingFormat:
+    """Canonical only when the file says so; an unversioned file is legacy
+    (src/qwen_int4/checkpoint.py:36-41)."""
+    if checkpoint_metadata(path).get("packing", "") == CANONICAL_PACKING_METADATA:
+        return PackingFormat.CANONICAL
+    return PackingFormat.LEGACY_SIGNED_ADD
+
+
+def group_size_from_checkpoint(path: str | Path, default: int = 128) -> int:
+    value = checkpoint_metadata(path).get("group_size")
+    return default if value is None else int(value)
+
+
+def _buffer_device(model: torch.nn.Module) -> torch.device:
+    for name, tensor in model.state_dict().items():
+        if is_quantized_key(name):
+            return tensor.device
+    return torch.device("cpu")
+
+
+def load_quantized_checkpoint(model: torch.nn.Module, path: str | Path, *,
+                              device: torch.device | str | None = None) -> LoadReport:
+    """Strictly load the quantized tensors (and an AWQ file's transformed
+    state) into ``model`` (src/qwen_int4/checkpoint.py:51-118).  Tensors are
+    read directly onto ``device`` (default: where the model's quantized
+    buffers live)."""
+    path = Path(path)
+    if not path.is_file():
+        raise FileNotFoundError(path)
+    target = torch.device(device) if device is not None else _buffer_device(model)
+    checkpoint = load_file(str(path), device=str(target))
+    expected = model.state_dict()
+    expected_quantized = {key for key in expected if is_quantized_key(key)}
+    checkpoint_quantized = {key for key in checkpoint if is_quantized_key(key)}
+    missing = expected_quantized - checkpoint_quantized
+    unexpected = checkpoint_quantized - expected_quantized
+    mismatched = {
+        key: (tuple(expected[key].shape), tuple(checkpoint[key].shape))
+        for key in expected_quantized & checkpoint_quantized
+        if expected[key].shape != checkpoint[key].shape
+    }
+    if missing or unexpected or mismatched:
+        raise RuntimeError(
+            "checkpoint contract mismatch:\n"
+            f"  missing={sorted(missing)}\n"
+            f"  unexpected={sorted(unexpected)}\n"
+            f"  shape_mismatches={mismatched}"
+        )
+
+    metadata = checkpoint_metadata(path)
+    transformed: dict[str, torch.Tensor] = {}
+    if metadata.get("format_version") == AWQ_FORMAT_VERSION:
+        expected_transformed = {key for key in expected if key.endswith(AWQ_TRANSFORMED_SUFFIXES)}
+        checkpoint_transformed = {key for key in checkpoint if key.endswith(AWQ_TRANSFORMED_SUFFIXES)}
+        missing_t = expected_transformed - checkpoint_transformed
+        unexpected_t = checkpoint_transformed - expected_transformed
+        if missing_t or unexpected_t:
+            raise RuntimeError(
+                "AWQ transformed-state contract mismatch:\n"
+                f"  missing={sorted(missing_t)}\n"
+                f"  unexpected={sorted(unexpected_t)}"
+            )
+        transformed = {key: checkpoint[key] for key in checkpoint_transformed}
+
+    load_tensors = {**{key: checkpoint[key] for key in checkpoint_quantized}, **transformed}
+    # copy_ into the existing buffers (load_state_dict's default): views of
+    # fused projection buffers stay views and receive the data
+    incompatible = model.load_state_dict(load_tensors, strict=False)
+    if incompatible.unexpected_keys:
+        raise RuntimeError(f"quantized state_dict load failed: unexpected={sorted(incompatible.unexpected_keys)}")
+
+    nonzero_zero_points = [
+        name for name, tensor in model.named_buffers()
+        if name.endswith(".zeros") and torch.count_nonzero(tensor).item()
+    ]
+    if nonzero_zero_points and metadata.get("zero_point", "") not in ASYMMETRIC_ZERO_POINT_CONTRACTS:
+        raise RuntimeError(
+            "non-zero zero-points found without an asymmetric checkpoint contract: " + ", ".join(nonzero_zero_points)
+        )
+    return LoadReport(len(load_tensors), len(checkpoint) - len(load_tensors))
+
+
+def save_quantized_checkpoint(model: torch.nn.Module, path: str | Path, metadata: dict[str, str]) -> Path:
+    """Write ``model``'s quantized tensors (plus, for the AWQ format, its
+    transformed norms and v_proj biases) with ``metadata``; never overwrites."""
+    path = Path(path)
+    if path.exists():
+        raise FileExistsError(f"refusing to overwrite {path}")
+    awq = metadata.get("format_version") == AWQ_FORMAT_VERSION
+    tensors = {
+        key: value.detach().to("cpu").contiguous()
+        for key, value in model.state_dict().items()
+        if is_quantized_key(key) or (awq and key.endswith(AWQ_TRANSFORMED_SUFFIXES))
+    }
+    if not any(is_quantized_key(key) for key in tensors):
+        raise ValueError("model has no quantized tensors")
+    path.parent.mkdir(parents=True, exist_ok=True)
+    save_file(tensors, str(path), metadata=dict(metadata))
+    return path
+
+
+def sha256_file(path: str | Path) -> str:
+    """SHA-256 of a file, read in 1 MiB blocks (src/qwen_int4/artifact_contract.py:31-37)."""
+    digest = hashlib.sha256()
+    with Path(path).open("rb") as handle:
+        for block in iter(lambda: handle.read(1 << 20), b""):
+            digest.update(block)
+    return digest.hexdigest()
+
+
+AWQ_V6_ARTIFACT_ID = "qwen2-1.5b-w4g64-awq-canonical-v6"
+
+
+@dataclass(frozen=True)
+class CanonicalAWQV6Contract:
+    """What the frozen v6 manifest pins about the checkpoint file."""
+    manifest_path: Path
+    checkpoint_sha256: str
+    checkpoint_size_bytes: int
+    group_size: int
+    model_id: str
+    model_revision: str
+    tokenizer_revision: str
+
+
+# (dotted manifest field, required value, message on mismatch): the frozen
+# v6 manifest's fixed fields (src/qwen_int4/artifact_contract.py:60-101).
+_V6_MANIFEST_FIXED = (
+    ("schema_version", "qwen-int4-awq-artifact-manifest-v1", "unsupported canonical AWQ manifest schema"),
+    ("artifact_id", AWQ_V6_ARTIFACT_ID, "manifest is not the canonical AWQ v6 artifact"),
+    ("status", "frozen_phase_d_candidate", "canonical AWQ v6 manifest must remain frozen"),
+    ("quantization_contract.format_version", AWQ_FORMAT_VERSION, "canonical AWQ v6 format version mismatch"),
+    ("quantization_contract.bits", 4, "canonical AWQ v6 requires W4G64"),
+    ("quantization_contract.group_size", 64, "canonical AWQ v6 requires W4G64"),
+    ("quantization_contract.quantization", "canonical_awq_asymmetric",
+     "canonical AWQ v6 requires asymmetric quantization"),
+    ("quantization_contract.zero_point", "per-group asymmetric",
+     "canonical AWQ v6 requires per-group asymmetric zero points"),
+    ("quantization_contract.packing", "canonical signed INT4 packing",
+     "canonical AWQ v6 requires canonical signed INT4 packing"),
+    ("selection.selected_variant", "v6", "canonical AWQ v6 selection record mismatch"),
+    ("selection.rejected_variant", "v7", "canonical AWQ v6 selection record mismatch"),
+    ("selection.phase_e_eligibility", "correctness-only work; no performance claim is authorized by this manifest",
+     "manifest must retain the Phase E correctness-only restriction"),
+)
+
+
+def _manifest_field(manifest: object, dotted: str) -> object:
+    node = manifest
+    parts = dotted.split(".")
+    for depth, part in enumerate(parts):
+        if not isinstance(node, dict):
+            raise ValueError(f"manifest field {'.'.join(parts[:depth]) or 'root'!r} must be an object")
+        node = node.get(part)
+    return node
+
+
+def _manifest_string(manifest: object, dotted: str) -> str:
+    value = _manifest_field(manifest, dotted)
+    if not isinstance(value, str) or not value:
+        raise ValueError(f"manifest field {dotted!r} must be a non-empty string")
+    return value
+
+
+def load_canonical_awq_v6_contract(manifest_path: str | Path) -> CanonicalAWQV6Contract:
+    """Read the frozen v6 manifest and reject any drift from it
+    (src/qwen_int4/artifact_contract.py:52-111).  The manifest's evidence
+    records (the reference repository's own result files) are not checked."""
+    path = Path(manifest_path)
+    try:
+        manifest = json.loads(path.read_text(encoding="utf-8"))
+    except json.JSONDecodeError as error:
+        raise ValueError(f"invalid manifest JSON: {path}") from error
+    if not isinstance(manifest, dict):
+        raise ValueError("manifest field 'root' must be an object")
+    for field, value, message in _V6_MANIFEST_FIXED:
+        got = _manifest_field(manifest, field)
+        if got != value:
+            raise ValueError(message)
+    digest = _manifest_string(manifest, "artifact.sha256")
+    if re.fullmatch(r"[0-9a-f]{64}", digest) is None:
+        raise ValueError("artifact.sha256 must be a lowercase SHA-256 digest")
+    size = _manifest_field(manifest, "artifact.size_bytes")
+    if type(size) is not int or size <= 0:
+        raise ValueError("artifact.size_bytes must be a positive integer")
+    remote = _manifest_string(manifest, "artifact.remote_path")
+    if not (remote.startswith("/") and remote.endswith("/model.safetensors")):
+        raise ValueError("artifact.remote_path must be an absolute model.safetensors path")
+    return CanonicalAWQV6Contract(
+        manifest_path=path,
+        checkpoint_sha256=digest,
+        checkpoint_size_bytes=size,
+        group_size=64,
+        model_id=_manifest_string(manifest, "upstream.model_id"),
+        model_revision=_manifest_string(manifest, "upstream.model_revision"),
+        tokenizer_revision=_manifest_string(manifest, "upstream.tokenizer_revision"),
+    )
+
+
+def validate_canonical_awq_v6_checkpoint(path: str | Path, contract: CanonicalAWQV6Contract) -> dict[str, str]:
+    """Fail closed on the v6 checkpoint's bytes and metadata before any load
+    (src/qwen_int4/artifact_contract.py:140-167)."""
+    path = Path(path)
+    if not path.is_file():
+        raise FileNotFoundError(path)
+    if path.stat().st_size != contract.checkpoint_size_bytes:
+        raise ValueError("checkpoint size does not match the frozen v6 manifest")
+    if sha256_file(path) != contract.checkpoint_sha256:
+        raise ValueError("checkpoint SHA-256 does not match the frozen v6 manifest")
+    metadata = checkpoint_metadata(path)
+    # the export's metadata (export.py:38-57) minus its free-form fields,
+    # with the identity the manifest pins
+    expected = canonical_awq_metadata(group_size=contract.group_size)
+    del expected["activation_dtype"], expected["status"]
+    expected.update(source_model=contract.model_id, source_model_revision=contract.model_revision,
+                    tokenizer_revision=contract.tokenizer_revision)
+    mismatch = {key: (value, metadata.get(key)) for key, value in expected.items() if metadata.get(key) != value}
+    if mismatch:
+        raise ValueError(f"checkpoint metadata does not satisfy canonical AWQ v6: {mismatch}")
+    return metadata
+
+
+def load_canonical_awq_v6_checkpoint(model: torch.nn.Module, path: str | Path, contract: CanonicalAWQV6Contract, *,
+                                     device: torch.device | str | None = None) -> LoadReport:
+    """Check the file against the v6 contract and every quantized layer of
+    ``model`` for W4G64 canonical packing, then load
+    (src/qwen_int4/checkpoint.py:121-140)."""
+    validate_canonical_awq_v6_checkpoint(path, contract)
+    wrong = [
+        name for name, module in model.named_modules()
+        if hasattr(module, "qweight") and (getattr(module, "group_size", None) != contract.group_size
+                                           or getattr(module, "packing", None) is not PackingFormat.CANONICAL)
+    ]
+    if wrong:
+        raise RuntimeError("model does not satisfy canonical AWQ v6 W4G64 packing: " + ", ".join(wrong))
+    return load_quantized_checkpoint(model, path, device=device)
