@@ -5,10 +5,11 @@
  * a HIP stream as `void*`, int status codes W4G64_STATUS_*, the message of a
  * failed call in w4g64_last_error().  Nothing here allocates or synchronizes.
  *
- * With these, one decoder layer's decode step is eight launches:
+ * With these, one decoder layer's decode step is six launches:
  *   add_rmsnorm -> W4G64 q|k|v (one N = (H + 2 KVH) * D launch, bias)
  *   -> decode_attention -> W4G64 o_proj -> add_rmsnorm
- *   -> W4G64 gate|up (one N = 2 I launch) -> silu_mul -> W4G64 down_proj (fp32 in).
+ *   -> W4G64 gate|up (one N = 2 I launch) -> w4g64_linear_swiglu down_proj,
+ * and the step ends with add_rmsnorm -> lm_head (logits and greedy token).
  */
 #ifndef QWEN_INT4_HIP_QWEN2_DECODE_H
 #define QWEN_INT4_HIP_QWEN2_DECODE_H
@@ -66,6 +67,26 @@ int qwen2_decode_attention(const void* qkv, const void* cos, const void* sin, vo
  * (bf16 inputs, the fused gate|up projection), silu(x) = x / (1 + exp(-x)).
  * Replaces: the SwiGLU product of QwenMLP.forward (src/qwen_int4/model.py:133-136). */
 int qwen2_silu_mul(const void* gate_up, float* out, int64_t rows, int64_t intermediate, void* stream);
+
+/* Bytes of workspace qwen2_lm_head needs for its argmax (one key per row
+ * per workgroup; nothing in it survives a call); 0 for unsupported sizes.
+ * Calls sharing a workspace must be ordered on one stream. */
+int64_t qwen2_lm_head_workspace_bytes(int64_t rows, int64_t vocab, int64_t hidden);
+
+/* Dense bf16 LM head of a decode step, with the greedy choice (a second,
+ * one-workgroup-per-row launch on the same stream):
+ *   logits[r, v] = bf16( sum_k x[r, k] * weight[v, k] )   (fp32 sums)
+ *   argmax[r]    = the smallest v with the largest logits[r, v]
+ *                  (NaN counts as the largest; -0 equals +0)
+ * for x bf16 [rows, hidden], weight bf16 [vocab, hidden] (Qwen2's tied
+ * embedding), logits bf16 [rows, vocab], argmax int64 [rows] or NULL (then
+ * no workspace is needed).  rows <= 16, hidden a multiple of 128 and at most
+ * 4096; x and weight 16-byte aligned, workspace 8-byte aligned.
+ * Replaces: the tied lm_head projection of QwenInt4ForCausalLM
+ *           (src/qwen_int4/model.py:217-218, :243-245) and the greedy choice
+ *           logits[:, -1].argmax(dim=-1) (src/qwen_int4/generation.py:51). */
+int qwen2_lm_head(const void* x, const void* weight, void* logits, int64_t* argmax, int64_t rows, int64_t vocab,
+                  int64_t hidden, void* workspace, int64_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -132,6 +132,12 @@ class FusedDecodeStep:
         self.workspace = torch.zeros(max(ws, 1), dtype=torch.uint8, device=device)
         aws = self.lib.qwen2_decode_attention_workspace_bytes(batch, self.kv_heads, max_length)
         self.attn_workspace = torch.zeros(max(aws, 1), dtype=torch.uint8, device=device)
+        head = model.lm_head.weight
+        self.vocab = head.shape[0]
+        # the HIP LM head (with fused greedy argmax) covers up to 16 rows
+        hws = self.lib.qwen2_lm_head_workspace_bytes(batch, self.vocab, self.hidden)
+        self.hip_head = hws > 0 and head.dtype == bf16 and head.is_contiguous()
+        self.head_workspace = torch.zeros(max(hws, 1), dtype=torch.uint8, device=device)
 
     def _linear(self, x, code, weights, y, stream) -> None:
         bias = weights["bias"]
@@ -145,9 +151,12 @@ class FusedDecodeStep:
                                               ctypes.c_float(self.eps), _ptr(self.x), _ptr(self.normed),
                                               self.batch, self.hidden, stream))
 
-    def __call__(self, token_ids: torch.Tensor, position: torch.Tensor, caches) -> torch.Tensor:
+    def __call__(self, token_ids: torch.Tensor, position: torch.Tensor, caches,
+                 next_token: torch.Tensor | None = None) -> torch.Tensor:
         """Logits [batch, 1, vocab] of ``token_ids`` [batch, 1] at ``position``
-        (a 1-element int64 device tensor), extending ``caches``."""
+        (a 1-element int64 device tensor), extending ``caches``.  With
+        ``next_token`` (int64 [batch, 1], may be ``token_ids`` itself), the
+        greedy choice logits.argmax(-1) is written there."""
         model = self.model
         stream = ctypes.c_void_p(torch.cuda.current_stream(self.device).cuda_stream)
         torch.index_select(model.model.embed_tokens.weight, 0, token_ids.reshape(-1), out=self.x)
@@ -175,7 +184,19 @@ class FusedDecodeStep:
                 stream))
             delta, delta_code = self.down, _lib.DTYPE_F32
         self._norm(delta, delta_code, model.model.norm.weight, stream)
-        return F.linear(self.normed, model.lm_head.weight).view(self.batch, 1, -1)
+        if not self.hip_head:
+            logits = F.linear(self.normed, model.lm_head.weight)
+            if next_token is not None:
+                next_token.copy_(logits.argmax(dim=-1, keepdim=True))
+            return logits.view(self.batch, 1, -1)
+        logits = torch.empty((self.batch, self.vocab), dtype=torch.bfloat16, device=self.device)
+        if next_token is not None and (next_token.dtype != torch.int64 or next_token.numel() != self.batch
+                                       or not next_token.is_contiguous()):
+            raise ValueError("next_token must be a contiguous int64 tensor of batch elements")
+        _lib.check(self.lib.qwen2_lm_head(
+            _ptr(self.normed), _ptr(model.lm_head.weight), _ptr(logits), _ptr(next_token), self.batch, self.vocab,
+            self.hidden, _ptr(self.head_workspace), self.head_workspace.numel(), stream))
+        return logits.view(self.batch, 1, -1)
 
 
 class FusedPrefill:

@@ -144,9 +144,11 @@ class StaticGreedyDecoder:
         self.token.copy_(logits[:, -1].argmax(dim=-1, keepdim=True))
         return logits
 
-    def _run(self) -> torch.Tensor:
+    def _run(self, next_token: torch.Tensor | None) -> torch.Tensor:
+        """One decode step; the fused step also writes the greedy choice into
+        ``next_token`` (the module path leaves that to ``step``)."""
         if self.fused is not None:
-            return self.fused(self.token, self.position, self.caches)
+            return self.fused(self.token, self.position, self.caches, next_token)
         return self.model.decode_static(self.token, self.position, self.caches)
 
     def step(self, token: torch.Tensor | None = None) -> torch.Tensor:
@@ -158,25 +160,30 @@ class StaticGreedyDecoder:
         if token is not None:
             self.token.copy_(token)
         self.position.fill_(self.length)
+        fused = self.fused is not None
         with torch.inference_mode():
             if not self.use_graph:
-                self.logits = self._run()
+                self.logits = self._run(self.token if fused else None)
             elif self.graph is None:
                 # the capture stream lives as long as the graph: its workspace is keyed by it
                 self._stream = stream = torch.cuda.Stream()
                 stream.wait_stream(torch.cuda.current_stream())
                 with torch.cuda.stream(stream):
-                    self.logits = self._run()  # warm-up outside capture (allocates workspaces)
+                    # warm-up outside capture (allocates workspaces); its greedy
+                    # choice goes to a scratch tensor so the replay below reads
+                    # the same input token
+                    self._run(torch.empty_like(self.token) if fused else None)
                 torch.cuda.current_stream().wait_stream(stream)
                 torch.cuda.synchronize()
                 self.graph = torch.cuda.CUDAGraph()
                 with torch.cuda.graph(self.graph, stream=stream):  # same stream: same workspaces
-                    self.logits = self._run()
+                    self.logits = self._run(self.token if fused else None)
                 self.graph.replay()
             else:
                 self.graph.replay()
             self.length += 1
-            self.token.copy_(self.logits[:, -1].argmax(dim=-1, keepdim=True))
+            if not fused:
+                self.token.copy_(self.logits[:, -1].argmax(dim=-1, keepdim=True))
         return self.logits
 
     def generate(self, input_ids: torch.Tensor, max_new_tokens: int) -> torch.Tensor:

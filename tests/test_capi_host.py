@@ -106,6 +106,24 @@ def test_decode_step_entry_points_reject_before_launch():
     assert lib.qwen2_silu_mul(p, p, 1, 0, null) == _lib.STATUS_INVALID_VALUE
     assert lib.qwen2_silu_mul(null, p, 1, 64, null) == _lib.STATUS_INVALID_VALUE
     assert lib.qwen2_silu_mul(null, null, 0, 64, null) == _lib.STATUS_OK
+    # lm_head: rows <= 16, hidden a multiple of 128 up to 4096, workspace for the argmax
+    hws = lib.qwen2_lm_head_workspace_bytes(1, 151936, 1536)
+    assert hws == 1 * (151936 // 16) * 8  # one tile of 16 vocab rows per workgroup up to 8 rows
+    assert lib.qwen2_lm_head_workspace_bytes(2, 1000, 4096) == 2 * 63 * 8
+    assert lib.qwen2_lm_head_workspace_bytes(16, 1000, 1536) == 16 * 32 * 8  # two tiles above 8 rows
+    assert lib.qwen2_lm_head_workspace_bytes(16, 1000, 2560) == 16 * 63 * 8  # one where two do not fit
+    assert lib.qwen2_lm_head_workspace_bytes(17, 1000, 1536) == 0
+    assert lib.qwen2_lm_head_workspace_bytes(1, 1000, 100) == 0
+    i64 = ctypes.cast(p, ctypes.c_void_p)
+    assert lib.qwen2_lm_head(p, p, p, i64, 17, 1000, 1536, p, 1 << 20, null) == _lib.STATUS_INVALID_VALUE
+    assert lib.qwen2_lm_head(p, p, p, i64, 1, 1000, 1000, p, 1 << 20, null) == _lib.STATUS_INVALID_VALUE
+    assert lib.qwen2_lm_head(p, p, p, i64, 1, 1000, 4224, p, 1 << 20, null) == _lib.STATUS_INVALID_VALUE
+    assert lib.qwen2_lm_head(p, p, p, i64, 1, 0, 1536, p, 1 << 20, null) == _lib.STATUS_INVALID_VALUE
+    assert lib.qwen2_lm_head(p, null, p, i64, 1, 1000, 1536, p, 1 << 20, null) == _lib.STATUS_INVALID_VALUE
+    assert lib.qwen2_lm_head(odd, p, p, i64, 1, 1000, 1536, p, 1 << 20, null) == _lib.STATUS_INVALID_VALUE
+    assert lib.qwen2_lm_head(p, p, p, i64, 1, 151936, 1536, p, hws - 8, null) == _lib.STATUS_WORKSPACE
+    assert lib.qwen2_lm_head(p, p, p, i64, 1, 151936, 1536, null, hws, null) == _lib.STATUS_WORKSPACE
+    assert lib.qwen2_lm_head(null, null, null, null, 0, 1000, 1536, null, 0, null) == _lib.STATUS_OK
 
 
 def test_fused_swiglu_linear_rejects_before_launch():

@@ -193,6 +193,87 @@ def test_linear_swiglu_gemm_rows(rows, n, k):
     assert bool(torch.isfinite(y).all()) and _normwise(y, want) <= 1e-2
 
 
+def _lm_head(x, weight, with_argmax=True):
+    lib = _lib.load()
+    rows, hidden = x.shape
+    vocab = weight.shape[0]
+    logits = torch.full((rows, vocab), float("nan"), dtype=torch.bfloat16, device="cuda")
+    argmax = torch.full((rows,), -1, dtype=torch.int64, device="cuda") if with_argmax else None
+    nbytes = lib.qwen2_lm_head_workspace_bytes(rows, vocab, hidden)
+    assert nbytes > 0
+    workspace = torch.zeros(nbytes, dtype=torch.uint8, device="cuda")
+    _lib.check(lib.qwen2_lm_head(_p(x), _p(weight), _p(logits), _p(argmax), rows, vocab, hidden, _p(workspace),
+                                 nbytes, _stream()))
+    torch.cuda.synchronize()
+    return logits, argmax
+
+
+def _first_argmax(logits):
+    """torch.argmax's rule on bf16 rows, written out: the first index of the
+    largest value, NaN largest (torch documents the first occurrence)."""
+    values = logits.float()
+    nan = torch.isnan(values)
+    top = torch.where(nan.any(dim=1, keepdim=True), nan, values == values.max(dim=1, keepdim=True).values)
+    return top.float().argmax(dim=1)  # first True
+
+
+@pytest.mark.parametrize("rows,vocab,hidden", [(1, 151936, 1536), (2, 151936, 1536), (16, 4099, 1536),
+                                               (5, 1000, 896), (3, 257, 128), (1, 33, 4096), (7, 2048, 3584)])
+def test_lm_head_matches_fp64_and_argmax_is_torchs(rows, vocab, hidden):
+    g = _gen(rows * 1000 + hidden)
+    x = (torch.randn((rows, hidden), generator=g, device="cuda")).to(torch.bfloat16)
+    weight = (torch.randn((vocab, hidden), generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+    logits, argmax = _lm_head(x, weight)
+    exact = x.double() @ weight.double().T
+    # fp32 sums of exact bf16 products, one bf16 rounding: within half a bf16
+    # ulp of the exact value plus the fp32 summation error
+    bound = exact.abs() * 2.0 ** -8 + 1e-5 * (x.double().abs() @ weight.double().abs().T)
+    assert bool(((logits.double() - exact).abs() <= bound).all())
+    assert torch.equal(argmax, logits.argmax(dim=1))
+    assert torch.equal(argmax, _first_argmax(logits))
+    # without the argmax: same logits, no workspace needed
+    again, _ = _lm_head(x, weight, with_argmax=False)
+    assert torch.equal(again, logits)
+
+
+def test_lm_head_argmax_ties_and_nan():
+    hidden, vocab = 256, 3000
+    g = _gen(77)
+    weight = (torch.randn((vocab, hidden), generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+    # rows 2900, 40 and 1999 equal the largest row: ties resolve to the first
+    big = torch.full((hidden,), 0.5, dtype=torch.bfloat16, device="cuda")
+    for v in (2900, 40, 1999):
+        weight[v] = big
+    x = torch.ones((4, hidden), dtype=torch.bfloat16, device="cuda")
+    x[1] = -1.0  # all-negative ties: row 0 of the smallest weights wins instead
+    x[2, 5] = float("nan")  # every logit NaN: index 0
+    x[3] = 0.0  # every logit +0: index 0
+    logits, argmax = _lm_head(x, weight)
+    assert argmax[0].item() == 40
+    assert torch.equal(argmax, _first_argmax(logits))
+    assert argmax[2].item() == 0 and argmax[3].item() == 0
+
+
+def test_lm_head_repeated_calls_share_the_workspace():
+    """Back-to-back calls on one stream reuse one workspace."""
+    lib = _lib.load()
+    g = _gen(5)
+    weight = (torch.randn((151936, 1536), generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+    nbytes = lib.qwen2_lm_head_workspace_bytes(4, 151936, 1536)
+    workspace = torch.zeros(nbytes, dtype=torch.uint8, device="cuda")
+    outs = []
+    for seed in range(6):
+        x = torch.randn((4, 1536), generator=_gen(seed), device="cuda").to(torch.bfloat16)
+        logits = torch.empty((4, 151936), dtype=torch.bfloat16, device="cuda")
+        argmax = torch.empty(4, dtype=torch.int64, device="cuda")
+        _lib.check(lib.qwen2_lm_head(_p(x), _p(weight), _p(logits), _p(argmax), 4, 151936, 1536, _p(workspace),
+                                     nbytes, _stream()))
+        outs.append((logits, argmax))
+    torch.cuda.synchronize()
+    for logits, argmax in outs:
+        assert torch.equal(argmax, logits.argmax(dim=1))
+
+
 SMALL128 = SimpleNamespace(hidden_size=256, num_attention_heads=2, num_key_value_heads=1, head_dim=128,
                            intermediate_size=512, num_hidden_layers=3, vocab_size=512, rms_norm_eps=1e-6,
                            rope_theta=1_000_000.0)
@@ -264,6 +345,9 @@ def test_fused_decode_step_matches_module_decode(batch):
         replay = graph.step(token).clone()
         assert torch.equal(got, replay), step  # graph replays run the same kernels on the same inputs
         assert _cos(got, want) >= 0.9999, (step, _cos(got, want))
+        # the fused step's greedy choice is argmax of its own logits
+        assert torch.equal(fused.token, got[:, -1].argmax(dim=-1, keepdim=True)), step
+        assert torch.equal(graph.token, fused.token), step
     for (k0, v0), (k1, v1) in zip(module.caches, fused.caches):
         assert _cos(k0[:, :, :83], k1[:, :, :83]) >= 0.9999 and _cos(v0[:, :, :83], v1[:, :, :83]) >= 0.9999
 
