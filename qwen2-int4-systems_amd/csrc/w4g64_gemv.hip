@@ -29,9 +29,10 @@
 //   * fused activation form (decode step of the decoder layer): kSwiGLU
 //     stages silu(gate) * up (fp32, as three bf16 parts) from a [gate | up]
 //     bf16 row.
-//   * every weight, scale and zero load of the lane is issued before the
-//     activations are staged, so the workgroup's whole weight slice is in
-//     flight at once.
+//   * the compute waves issue every weight, scale and zero load at once
+//     (raw bits; decoded where the MFMA step uses them), so the workgroup's
+//     whole weight slice is in flight while separate staging waves (one, or
+//     four for the fp32-class kinds) bring the activations into LDS.
 //   * optional K split across workgroups (only for many rows x few output
 //     features): partial sums go through device-coherent (sc1) stores; the
 //     last workgroup to arrive for a column block, known from a per-block
@@ -46,10 +47,17 @@ namespace w4g64 {
 namespace {
 
 constexpr int kWaves = 4;          // compute waves; one more wave stages the activations
-constexpr int kThreads = (kWaves + 1) * 64;
+// Staging waves: one for fp16/bf16 activations; four for the fp32-class kinds,
+// whose staging (exact bf16 split, silu) is ALU-heavy.  Staging and weight
+// loads never share a wave: a wave's loads return in issue order, so a wave
+// holding both would see its activations only after its weight stream.
+constexpr int stage_waves(int xk) { return (xk == 3 || xk == 5) ? 4 : 1; }
+constexpr int gemv_threads(int xk) { return (kWaves + stage_waves(xk)) * 64; }
+constexpr int kMaxThreads = (kWaves + 4) * 64;
 constexpr int kMaxSteps = 16;      // group steps per lane in one workgroup
 constexpr int kStepBuckets[] = {2, 3, 6, 9, 12, 16};
-constexpr int kStageBatch = 8;    // activation items in flight per staging lane
+// activation items in flight per staging lane (the four-wave kinds need fewer)
+constexpr int stage_batch(int xk) { return (xk == 3 || xk == 5) ? 4 : 8; }
 
 typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
 
@@ -73,7 +81,7 @@ struct GemvArgs {
 };
 
 template <int XK, int SW, int STEPS, int TILES>
-__global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
+__global__ __launch_bounds__(kMaxThreads) void gemv_kernel(GemvArgs a) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     __shared__ int s_last;
     constexpr int kParts = (XK == kF32 || XK == kSwiGLU) ? 3 : 1;
@@ -101,10 +109,102 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
     const bool nvalid = n < a.N;
     const int nrow = nvalid ? n : 0;
     u32x2 wq[STEPS];
-    float sc[STEPS];
-    int zr[STEPS];
+    // raw scale bits and zero bytes: decoded where used, so that issuing a
+    // step's loads never waits for an earlier step's data
+    uint32_t sraw[STEPS];
+    uint32_t zraw[STEPS];
     const uint8_t* wrow = a.qweight + (int64_t)nrow * (a.K / 2) + 8 * q;
     const int64_t sbase = (int64_t)nrow * a.G;
+
+    // ---- loads: weights (compute waves), activations (staging waves) ----
+    // Staging works in batches of kStageBatch items per staging lane: every
+    // load of a batch is issued before any is consumed.
+    constexpr int kThreads = gemv_threads(XK);
+    constexpr int kStageBatch = stage_batch(XK);
+    constexpr int kVecs = (XK == kF16 || XK == kBF16) ? 1 : 2;  // 16-byte loads per item
+    const int sid = tid - kWaves * 64;           // staging lane index
+    constexpr int nst = stage_waves(XK) * 64;    // staging lanes
+    const bool stager = wave >= kWaves;
+    const int kbase = g0 * 64;
+    const int items_per_row = cnt * 8;  // 8 values per item
+    const int total = a.M * items_per_row;
+    const float inv_items = 1.0f / (float)items_per_row;
+    // item -> (row m, item c in the row); it < 2^24, so the float quotient is
+    // off by at most one
+    auto item_rc = [&](int it, int& m, int& c) {
+        m = (int)((float)it * inv_items);
+        c = it - m * items_per_row;
+        if (c < 0) { --m; c += items_per_row; }
+        else if (c >= items_per_row) { ++m; c -= items_per_row; }
+    };
+    u32x4 v[kStageBatch][kVecs];
+    auto stage_load = [&](int base) {
+#pragma unroll
+        for (int u = 0; u < kStageBatch; ++u) {
+            // clamped: a valid address whose result is not stored (an
+            // unconditional load keeps the batch branch-free)
+            const int it = min(base + nst * u + sid, total - 1);
+            {
+                int m, c;
+                item_rc(it, m, c);
+                if constexpr (XK == kF16 || XK == kBF16) {
+                    v[u][0] = *(const u32x4*)((const uint16_t*)a.x + (int64_t)m * a.K + kbase + 8 * c);
+                } else if constexpr (XK == kSwiGLU) {
+                    // x is [M, 2K]: gate | up (bf16)
+                    const uint16_t* gu = (const uint16_t*)a.x + (int64_t)m * 2 * a.K + kbase + 8 * c;
+                    v[u][0] = *(const u32x4*)gu;
+                    v[u][1] = *(const u32x4*)(gu + a.K);
+                } else {
+                    const float* src = (const float*)a.x + (int64_t)m * a.K + kbase + 8 * c;
+                    v[u][0] = *(const u32x4*)src;
+                    v[u][1] = *(const u32x4*)(src + 4);
+                }
+            }
+        }
+    };
+    auto stage_store = [&](int base) {
+#pragma unroll
+        for (int u = 0; u < kStageBatch; ++u) {
+            const int it = base + nst * u + sid;
+            if (it >= total) continue;
+            int m, c;
+            item_rc(it, m, c);
+            if constexpr (XK == kF16 || XK == kBF16) {
+                *(u32x4*)(xs + m * row_stride + 8 * c) = permute_slots(v[u][0]);
+            } else {
+                float h[8];
+                if constexpr (XK == kSwiGLU) {
+                    // h = silu(gate) * up in fp32, silu(g) = g / (1 + exp(-g)) (model.py:133-136)
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const uint32_t gw = v[u][0][e / 2], uw = v[u][1][e / 2];
+                        const float g = bf16_bits_to_float(e & 1 ? gw >> 16 : gw & 0xFFFFu);
+                        const float up = bf16_bits_to_float(e & 1 ? uw >> 16 : uw & 0xFFFFu);
+                        h[e] = (g / (1.0f + expf(-g))) * up;
+                    }
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const uint32_t bits = v[u][e / 4][e % 4];  // element to a scalar before the cast
+                        h[e] = __builtin_bit_cast(float, bits);
+                    }
+                }
+                uint16_t hi[8], mid[8], lo[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) split3_bf16(h[e], hi[e], mid[e], lo[e]);
+                u32x4 ph, pm, pl;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    ph[e] = (uint32_t)hi[2 * e] | ((uint32_t)hi[2 * e + 1] << 16);
+                    pm[e] = (uint32_t)mid[2 * e] | ((uint32_t)mid[2 * e + 1] << 16);
+                    pl[e] = (uint32_t)lo[2 * e] | ((uint32_t)lo[2 * e + 1] << 16);
+                }
+                *(u32x4*)(xs + m * row_stride + 8 * c) = permute_slots(ph);
+                *(u32x4*)(xs + (a.M + m) * row_stride + 8 * c) = permute_slots(pm);
+                *(u32x4*)(xs + (2 * a.M + m) * row_stride + 8 * c) = permute_slots(pl);
+            }
+        }
+    };
 
     if (wave < kWaves) {
         // ---- compute waves: issue every weight / scale / zero load, step by step ----
@@ -116,106 +216,22 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
             const int gl = sj + SW * t;
             const int g = gl < cnt ? g0 + gl : g0;
             wq[t] = __builtin_nontemporal_load((const u32x2*)(wrow + (int64_t)g * 32));
-            sc[t] = half_bits_to_float(a.scales[sbase + g]);
-            zr[t] = nibble_at(a.zeros, sbase + g);
+            sraw[t] = a.scales[sbase + g];
+            zraw[t] = a.zeros[(sbase + g) >> 1];
         }
     }
     // ---- staging: this workgroup's activations into LDS (slot order) ----
-    // Batches of kStageBatch items per lane: all loads of a batch are issued
-    // before any is consumed, so a lane has kStageBatch 16-byte loads in
-    // flight instead of one round trip per item.  The fp32-class kinds (exact
-    // bf16 split, silu) are ALU-heavy and every wave stages them (after
-    // issuing its weight loads); the other kinds use the staging wave alone.
-    constexpr bool kAllStage = (XK == kF32 || XK == kSwiGLU);
-    const int sid = kAllStage ? tid : lane;        // staging lane index
-    const int nst = kAllStage ? kThreads : 64;    // staging lanes
-    if (kAllStage || wave == kWaves) {
-        const int kbase = g0 * 64;
-        const int items_per_row = cnt * 8;  // 8 values per item
-        const int total = a.M * items_per_row;
+    if (stager) {
         for (int base = 0; base < total; base += nst * kStageBatch) {
-            if constexpr (XK == kF16 || XK == kBF16) {
-                u32x4 v[kStageBatch];
-#pragma unroll
-                for (int u = 0; u < kStageBatch; ++u) {
-                    const int it = base + nst * u + sid;
-                    const int itc = it < total ? it : total - 1;  // clamped: a valid address, result unused
-                    const int m = itc / items_per_row;
-                    const int c = itc - m * items_per_row;
-                    v[u] = *(const u32x4*)((const uint16_t*)a.x + (int64_t)m * a.K + kbase + 8 * c);
-                }
-#pragma unroll
-                for (int u = 0; u < kStageBatch; ++u) {
-                    const int it = base + nst * u + sid;
-                    if (it < total) {
-                        const int m = it / items_per_row;
-                        const int c = it - m * items_per_row;
-                        *(u32x4*)(xs + m * row_stride + 8 * c) = permute_slots(v[u]);
-                    }
-                }
-            } else {
-                float4v f[kStageBatch][2];
-#pragma unroll
-                for (int u = 0; u < kStageBatch; ++u) {
-                    const int it = base + nst * u + sid;
-                    const int itc = it < total ? it : total - 1;
-                    const int m = itc / items_per_row;
-                    const int c = itc - m * items_per_row;
-                    if constexpr (XK == kSwiGLU) {
-                        // x is [M, 2K]: gate | up (bf16); the product is formed once every load is issued
-                        const uint16_t* gu = (const uint16_t*)a.x + (int64_t)m * 2 * a.K + kbase + 8 * c;
-                        f[u][0] = __builtin_bit_cast(float4v, *(const u32x4*)gu);
-                        f[u][1] = __builtin_bit_cast(float4v, *(const u32x4*)(gu + a.K));
-                    } else {
-                        const float* src = (const float*)a.x + (int64_t)m * a.K + kbase + 8 * c;
-                        f[u][0] = *(const float4v*)src;
-                        f[u][1] = *(const float4v*)(src + 4);
-                    }
-                }
-#pragma unroll
-                for (int u = 0; u < kStageBatch; ++u) {
-                    const int it = base + nst * u + sid;
-                    if (it >= total) continue;
-                    const int m = it / items_per_row;
-                    const int c = it - m * items_per_row;
-                    float h[8];
-                    if constexpr (XK == kSwiGLU) {
-                        // h = silu(gate) * up in fp32, silu(g) = g / (1 + exp(-g)) (model.py:133-136)
-                        const u32x4 gv = __builtin_bit_cast(u32x4, f[u][0]);
-                        const u32x4 uv = __builtin_bit_cast(u32x4, f[u][1]);
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) {
-                            const uint32_t gw = gv[e / 2], uw = uv[e / 2];
-                            const float g = bf16_bits_to_float(e & 1 ? gw >> 16 : gw & 0xFFFFu);
-                            const float up = bf16_bits_to_float(e & 1 ? uw >> 16 : uw & 0xFFFFu);
-                            h[e] = (g / (1.0f + expf(-g))) * up;
-                        }
-                    } else {
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) h[e] = e < 4 ? f[u][0][e] : f[u][1][e - 4];
-                    }
-                    uint16_t hi[8], mid[8], lo[8];
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) split3_bf16(h[e], hi[e], mid[e], lo[e]);
-                    u32x4 ph, pm, pl;
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        ph[e] = (uint32_t)hi[2 * e] | ((uint32_t)hi[2 * e + 1] << 16);
-                        pm[e] = (uint32_t)mid[2 * e] | ((uint32_t)mid[2 * e + 1] << 16);
-                        pl[e] = (uint32_t)lo[2 * e] | ((uint32_t)lo[2 * e + 1] << 16);
-                    }
-                    *(u32x4*)(xs + m * row_stride + 8 * c) = permute_slots(ph);
-                    *(u32x4*)(xs + (a.M + m) * row_stride + 8 * c) = permute_slots(pm);
-                    *(u32x4*)(xs + (2 * a.M + m) * row_stride + 8 * c) = permute_slots(pl);
-                }
-            }
+            stage_load(base);
+            stage_store(base);
         }
     }
     if constexpr (XK != kF16) {
         // group sums of every staged row (a single staging wave's own LDS
         // writes are ordered before its reads; several waves need a barrier)
-        if constexpr (kAllStage) __syncthreads();
-        if (kAllStage || wave == kWaves) {
+        if constexpr (stage_waves(XK) > 1) __syncthreads();
+        if (stager) {
             for (int idx = sid; idx < cnt * a.mv; idx += nst) {
                 const int r = idx / cnt;
                 const int gl = idx - r * cnt;
@@ -223,10 +239,10 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
                 float s = 0.0f;
 #pragma unroll
                 for (int k = 0; k < 64; k += 8) {
-                    const u32x4 v = *(const u32x4*)(src + k);  // 16-byte LDS reads
+                    const u32x4 xv = *(const u32x4*)(src + k);  // 16-byte LDS reads
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
-                        s += __builtin_bit_cast(float, v[e] << 16) + __builtin_bit_cast(float, v[e] & 0xFFFF0000u);
+                        s += __builtin_bit_cast(float, xv[e] << 16) + __builtin_bit_cast(float, xv[e] & 0xFFFF0000u);
                 }
                 sx[r * a.gps + gl] = s;
             }
@@ -239,27 +255,40 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
 #pragma unroll
     for (int tt = 0; tt < TILES; ++tt) acc[tt] = float4v{0.f, 0.f, 0.f, 0.f};
 
+    // Branch-free: every LDS read is in bounds and unconditional, so the
+    // reads of a step need no exec-mask branches around them.  Out-of-range
+    // operands read staged (finite) data instead of zeros: A rows past the
+    // virtual rows only feed D rows the epilogue drops, and a step past the K
+    // range has zero scale.  (Reading several steps ahead measured slower:
+    // the registers cost more occupancy than the overlap gained.)
     if (wave < kWaves) {
+        // The empty asm keeps the scale and zero decoding below this point:
+        // hoisted next to the loads, it would make every step's load issue
+        // wait for the scale.
 #pragma unroll
-    for (int t = 0; t < STEPS; ++t) {
-        {
-            const float scale = (nvalid && sj + SW * t < cnt) ? sc[t] : 0.0f;  // zero: no contribution
+        for (int t = 0; t < STEPS; ++t) asm volatile("" : "+v"(sraw[t]), "+v"(zraw[t]));
+#pragma unroll
+        for (int t = 0; t < STEPS; ++t) {
+            const uint32_t s_bits = sraw[t], z_bits = zraw[t];
+            const int gl = sj + SW * t;  // this lane's group, local to the K range
+            const float scale = (nvalid && gl < cnt) ? half_bits_to_float((uint16_t)s_bits) : 0.0f;
+            const int gz = gl < cnt ? g0 + gl : g0;  // the group this step loaded
+            const int zn = (((sbase + gz) & 1) ? (z_bits >> 4) : z_bits) & 0xF;
+            const int zr_t = zn - ((zn & 8) << 1);
+            const int glc = min(gl, cnt - 1);
 #pragma unroll
             for (int tt = 0; tt < TILES; ++tt) {
                 // A operand of this lane: A row il = virtual row m, segment sa.
                 const int il = 16 * tt + (lane & 15);
-                const int m = il / SW;
-                const int ga = il % SW + SW * t;  // the A row's group, local to this K range
-                u16x8 a0 = {}, a1 = {};
-                if (m < a.mv && ga < cnt) {
-                    const uint16_t* src = xs + m * row_stride + 64 * ga + 16 * q;
-                    a0 = *(const u16x8*)src;
-                    a1 = *(const u16x8*)(src + 8);
-                }
+                const int m = min(il / SW, a.mv - 1);
+                const int ga = min(il % SW + SW * t, cnt - 1);  // the A row's group, local to the K range
+                const uint16_t* src = xs + m * row_stride + 64 * ga + 16 * q;
+                const u16x8 a0 = *(const u16x8*)src;
+                const u16x8 a1 = *(const u16x8*)(src + 8);
                 float4v d;
                 if constexpr (XK == kF16) {
-                    const _Float16 zl = (_Float16)(1032 + zr[t]);
-                    const _Float16 zh = (_Float16)(72 + zr[t]);
+                    const _Float16 zl = (_Float16)(1032 + zr_t);
+                    const _Float16 zh = (_Float16)(72 + zr_t);
                     const half8 b0 = dequant8_f16_int(wq[t][0], half2v{zl, zl}, half2v{zh, zh});
                     const half8 b1 = dequant8_f16_int(wq[t][1], half2v{zl, zl}, half2v{zh, zh});
                     d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a0), b0,
@@ -273,20 +302,17 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
                     d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a1), b1, d, 0, 0, 0);
                     // D rows i = 16 tt + 4 q + r.  The rows kept later share this
                     // lane's segment, so their group is this lane's group gl.
-                    const float corr = 136.0f + (float)zr[t];
-                    const int gl = sj + SW * t;
+                    const float corr = 136.0f + (float)zr_t;
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
-                        const int mi = (16 * tt + 4 * q + r) / SW;
-                        const float s_x = (mi < a.mv && gl < cnt) ? sx[mi * a.gps + gl] : 0.0f;
-                        d[r] = fmaf(-corr, s_x, d[r]);
+                        const int mi = min((16 * tt + 4 * q + r) / SW, a.mv - 1);
+                        d[r] = fmaf(-corr, sx[mi * a.gps + glc], d[r]);
                     }
                 }
 #pragma unroll
                 for (int r = 0; r < 4; ++r) acc[tt][r] = fmaf(scale, d[r], acc[tt][r]);
             }
         }
-    }
     }
 
     // ---- epilogue: keep the block diagonal, sum segments and fp32 parts ----
@@ -358,7 +384,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
 template <int XK, int SW, int STEPS, int TILES>
 hipError_t launch_typed(const GemvArgs& args, const GemvPlan& plan, hipStream_t stream, hipEvent_t start,
                         hipEvent_t stop) {
-    return launch_kernel(gemv_kernel<XK, SW, STEPS, TILES>, dim3(plan.n_blocks, plan.splits), dim3(kThreads),
+    return launch_kernel(gemv_kernel<XK, SW, STEPS, TILES>, dim3(plan.n_blocks, plan.splits), dim3(gemv_threads(XK)),
                          (size_t)plan.lds_bytes, stream, start, stop, args);
 }
 
@@ -427,38 +453,24 @@ bool plan_rows16(int64_t rows, int64_t out_features, int64_t in_features, GemvPl
 }
 }  // namespace
 
-GemvPlan plan_gemv(int64_t rows, int64_t out_features, int64_t in_features, int x_kind, int force_segments,
-                   int force_splits) {
+namespace {
+constexpr int64_t kDeviceCUs = 256;  // MI355X compute units
+
+// The segmented kernel's plan for `sw` segments and at least `min_splits` K
+// splits (more when a lane would need more than kMaxSteps group steps or
+// the staged activations would not fit the 60 KB LDS budget).
+GemvPlan plan_segmented(int64_t rows, int64_t out_features, int64_t in_features, int x_kind, int64_t sw,
+                        int64_t min_splits) {
     GemvPlan plan{};
-    if (rows > 8 && rows <= 16 && (x_kind == kF16 || x_kind == kBF16) && force_segments <= 0 && force_splits <= 0 &&
-        plan_rows16(rows, out_features, in_features, plan))
-        return plan;
-    plan = GemvPlan{};
     const int64_t groups = in_features / 64;
-    const int64_t parts = (x_kind == kF32 || x_kind == kSwiGLU) ? 3 : 1;
-    const int64_t mv = rows * parts;
-    // Segments: as many as fit the 16 MFMA rows (mv * SW <= 16), then fewer
-    // while that still leaves >= 1024 column blocks (more features per
-    // workgroup = more reuse of the staged activations).
-    int64_t sw = 1;
-    while (sw < 16 && mv * sw * 2 <= 16) sw *= 2;
-    auto blocks_for = [&](int64_t s) {
-        const int64_t cols = kWaves * (16 / s);
-        return (out_features + cols - 1) / cols;
-    };
-    while (sw > 1 && blocks_for(sw / 2) >= 1024) sw /= 2;
-    if (force_segments > 0) sw = force_segments;
+    const int64_t mv = rows * ((x_kind == kF32 || x_kind == kSwiGLU) ? 3 : 1);
+    const int64_t cols = kWaves * (16 / sw);
     plan.segments = (int)sw;
     plan.tiles = (int)((mv * sw + 15) / 16);
-    plan.n_blocks = (int)blocks_for(sw);
-    // K splits: a lane holds at most kMaxSteps group steps; with few column
-    // blocks and many rows, split further so that >= 256 workgroups run.
-    int64_t splits = (groups + sw * kMaxSteps - 1) / (sw * kMaxSteps);
-    while (plan.n_blocks * splits < 256 && splits * 2 <= groups && groups / (splits * 2) >= sw) splits *= 2;
-    if (force_splits > 0) splits = force_splits;
+    plan.n_blocks = (int)((out_features + cols - 1) / cols);
+    int64_t splits = min_splits > 0 ? min_splits : 1;
     int64_t gps = (groups + splits - 1) / splits;
-    // Staged activations (virtual rows x split width, 16-bit) plus the group
-    // sums must fit a 60 KB dynamic-LDS budget (64 KB per workgroup).
+    // staged activations (virtual rows x split width, 16-bit) plus the group sums
     auto lds_for = [&](int64_t g) {
         const int64_t stage = mv * (g * 64 + 8) * 2 + mv * g * 4;
         const int64_t red = mv * kWaves * 16 * 4;
@@ -482,6 +494,35 @@ GemvPlan plan_gemv(int64_t rows, int64_t out_features, int64_t in_features, int 
     plan.counter_bytes = splits > 1 ? kGemvCounterBytes : 0;
     plan.workspace_bytes = splits > 1 ? plan.counter_bytes + splits * rows * out_features * 4 : 0;
     return plan;
+}
+}  // namespace
+
+GemvPlan plan_gemv(int64_t rows, int64_t out_features, int64_t in_features, int x_kind, int force_segments,
+                   int force_splits) {
+    GemvPlan plan{};
+    if (rows > 8 && rows <= 16 && (x_kind == kF16 || x_kind == kBF16) && force_segments <= 0 && force_splits <= 0 &&
+        plan_rows16(rows, out_features, in_features, plan))
+        return plan;
+    const int64_t groups = in_features / 64;
+    const int64_t mv = rows * ((x_kind == kF32 || x_kind == kSwiGLU) ? 3 : 1);
+    // Segments: as many as fit the 16 MFMA rows (mv * SW <= 16), then fewer
+    // while that still leaves >= 1024 column blocks (more features per
+    // workgroup = more reuse of the staged activations).
+    int64_t sw = 1;
+    while (sw < 16 && mv * sw * 2 <= 16) sw *= 2;
+    auto blocks_for = [&](int64_t s) {
+        const int64_t cols = kWaves * (16 / s);
+        return (out_features + cols - 1) / cols;
+    };
+    while (sw > 1 && blocks_for(sw / 2) >= 1024) sw /= 2;
+    if (force_segments > 0 || force_splits > 0)
+        return plan_segmented(rows, out_features, in_features, x_kind, force_segments > 0 ? force_segments : sw,
+                              force_splits);
+    // K splits: a lane holds at most kMaxSteps group steps; with few column
+    // blocks and many rows, split further so that >= 256 workgroups run.
+    int64_t splits = (groups + sw * kMaxSteps - 1) / (sw * kMaxSteps);
+    while (blocks_for(sw) * splits < kDeviceCUs && splits * 2 <= groups && groups / (splits * 2) >= sw) splits *= 2;
+    return plan_segmented(rows, out_features, in_features, x_kind, sw, splits);
 }
 
 GemvPlan plan_gemv(int64_t rows, int64_t out_features, int64_t in_features, int x_kind) {
