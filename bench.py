@@ -517,6 +517,7 @@ def end_to_end(torch, prompt_len: int = 512, new_tokens: int = 128):
     linear_bytes = 28 * sum(algorithmic_bytes(1, n, k) for n, k in QWEN2_SHAPES.values())
     head_bytes = QWEN2_1_5B["vocab_size"] * QWEN2_1_5B["hidden_size"] * 2
     per_token = decode_s / (new_tokens - 1)
+    head = lm_head_rate(torch, decoder, head_bytes)
     return {
         "workload": (f"Qwen2-1.5B architecture (28 layers, hidden 1536, GQA 12/2 x 128, SwiGLU 8960, vocab 151936), "
                      f"random-init N(0,0.02) weights, 196 symmetric RTN W4G64 linears, tied bf16 LM head; batch 1, "
@@ -529,7 +530,47 @@ def end_to_end(torch, prompt_len: int = 512, new_tokens: int = 128):
         "decode_weight_bytes_per_token": linear_bytes + head_bytes,
         "decode_weight_GBps": round((linear_bytes + head_bytes) / per_token / 1e9, 1),
         "generated_tokens": int(torch.cat(tokens, dim=1).numel()),
+        "lm_head": head,
     }
+
+
+def log_e2e(e2e) -> None:
+    log(f"e2e: prefill {e2e['prefill_ms']:.1f} ms ({e2e['prefill_tokens_per_s']:.0f} tok/s), "
+        f"decode {e2e['decode_ms_per_token']:.3f} ms/token ({e2e['decode_tokens_per_s']:.0f} tok/s)")
+    if e2e.get("lm_head"):
+        h = e2e["lm_head"]
+        log(f"e2e LM head: {h['us_per_call']:.1f} us per call, {h['GBps']:.0f} GB/s ({100 * h['frac']:.1f}% of 8 TB/s)")
+
+
+def lm_head_rate(torch, decoder, head_bytes: int, reps: int = 64):
+    """The decode step's LM head (tied bf16 151936 x 1536 GEMV plus the greedy
+    argmax: qwen2_lm_head) timed alone: `reps` back-to-back calls on the
+    step's own buffers between two events on the stream they run on."""
+    import ctypes
+
+    fused = decoder.fused
+    if fused is None or not fused.hip_head:
+        return None
+    weight = fused.model.lm_head.weight
+    logits = torch.empty((fused.batch, fused.vocab), dtype=torch.bfloat16, device="cuda")
+    token = torch.empty(fused.batch, dtype=torch.int64, device="cuda")
+    ptr = lambda t: ctypes.c_void_p(t.data_ptr())
+    stream = torch.cuda.current_stream()
+    call = lambda: fused.lib.qwen2_lm_head(ptr(fused.normed), ptr(weight), ptr(logits), ptr(token), fused.batch,
+                                           fused.vocab, fused.hidden, ptr(fused.head_workspace),
+                                           fused.head_workspace.numel(), ctypes.c_void_p(stream.cuda_stream))
+    for _ in range(4):
+        assert call() == 0
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(reps):
+        call()
+    stop.record(stream)
+    torch.cuda.synchronize()
+    us = start.elapsed_time(stop) * 1e3 / reps
+    gbs = head_bytes / (us * 1e-6) / 1e9
+    return {"kernels": "lm_head_kernel<3,1> + lm_head_argmax_kernel", "us_per_call": round(us, 2),
+            "weight_bytes": head_bytes, "GBps": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
 
 
 # ---------------------------------------------------------------------------
@@ -546,6 +587,8 @@ def main() -> int:
                         help="skip the CPU baseline leg (and with it the parity check against the CPU reference)")
     parser.add_argument("--no-gemm", action="store_true")
     parser.add_argument("--no-e2e", action="store_true", help="skip the end-to-end Qwen2-1.5B generation")
+    parser.add_argument("--e2e-only", action="store_true",
+                        help="run only the end-to-end generation and print its object (for kernel-trace profiles)")
     parser.add_argument("--report", type=str, default="", help="write the detailed JSON report here")
     parser.add_argument("--profile-pass", action="store_true",
                         help="untimed dispatch sequence for rocprofv3 --pmc (calibration, 3 decode steps, GEMMs)")
@@ -580,6 +623,11 @@ def main() -> int:
     hip = Hip()
     props = torch.cuda.get_device_properties(0)
     log(f"device: {props.name} CUs={props.multi_processor_count}")
+    if args.e2e_only:
+        e2e = end_to_end(torch)
+        log_e2e(e2e)
+        print(json.dumps({"e2e": e2e}), flush=True)
+        return 0
 
     # ---------------- decode workload ----------------
     base, copies, cases = decode_cases(torch, COPIES)
@@ -731,9 +779,7 @@ def main() -> int:
 
     if not args.no_e2e:
         result["e2e"] = end_to_end(torch)
-        log(f"e2e: prefill {result['e2e']['prefill_ms']:.1f} ms ({result['e2e']['prefill_tokens_per_s']:.0f} tok/s), "
-            f"decode {result['e2e']['decode_ms_per_token']:.3f} ms/token ({result['e2e']['decode_tokens_per_s']:.0f} "
-            f"tok/s)")
+        log_e2e(result["e2e"])
 
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(cases, [c for c in gemm_cases if c["rows"] == 2048], torch)
