@@ -374,6 +374,8 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
     // Every device-coherent load travels to memory, so the merge issues all of
     // them at once: the statistics into LDS and, per thread (dimension d,
     // heads g0, g0 + 2, ...), the weighted sums of up to kMergeBatch chunks.
+    // Loads of chunks past `used` (or heads past `group`) re-read a valid
+    // partial; their scale is zero, so the accumulation needs no branches.
     const int d = tid % kHeadDim;
     const int g0 = tid / kHeadDim;
     const int used = pos / kChunk + 1;  // chunks that hold positions 0..pos (all wrote partials)
@@ -384,33 +386,34 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
         for (int u = 0; u < kMergeBatch; ++u)
 #pragma unroll
             for (int i = 0; i < kMaxGroup / 2; ++i)
-                v[u][i] = (c0 + u < used && g0 + 2 * i < group)
-                              ? __hip_atomic_load(base + (c0 + u) * kPartFloats + 2 * kMaxGroup +
-                                                      (g0 + 2 * i) * kHeadDim + d,
-                                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                              : 0.0f;
+                v[u][i] = __hip_atomic_load(base + min(c0 + u, used - 1) * kPartFloats + 2 * kMaxGroup +
+                                                min(g0 + 2 * i, group - 1) * kHeadDim + d,
+                                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     };
     load_batch(0);
     float* stats = (float*)&ks[0][0];    // [used][2 * kMaxGroup]: m, l per head
-    float* scale_c = (float*)&vt[0][0];  // [used][kMaxGroup]: exp(m_c - m) / l
+    float* scale_c = (float*)&vt[0][0];  // [kMaxChunks][kMaxGroup]: exp(m_c - m) / l, zero past `used`
     for (int e = tid; e < used * 2 * kMaxGroup; e += kAttnThreads)
         stats[e] = __hip_atomic_load(base + (e / (2 * kMaxGroup)) * kPartFloats + e % (2 * kMaxGroup),
                                      __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
-    __shared__ float head_m[kMaxGroup], head_l[kMaxGroup];
-    if (tid < group) {
+    // per head g (wave w takes heads w, w + 4): lanes walk the chunks; the
+    // head's maximum and rescaled sum are wave reductions.  Heads past
+    // `group` get zero scales (their clamped loads then add nothing).
+    for (int g = wave; g < kMaxGroup; g += kAttnThreads / 64) {
+        if (g >= group) {
+            for (int c = lane; c < kMaxChunks; c += 64) scale_c[c * kMaxGroup + g] = 0.0f;
+            continue;
+        }
         float m = -INFINITY;
-        for (int c = 0; c < used; ++c) m = fmaxf(m, stats[c * 2 * kMaxGroup + tid]);
+        for (int c = lane; c < used; c += 64) m = fmaxf(m, stats[c * 2 * kMaxGroup + g]);
+        m = wave_max(m);
         float l = 0.0f;
-        for (int c = 0; c < used; ++c)
-            l = fmaf(stats[c * 2 * kMaxGroup + kMaxGroup + tid], expf(stats[c * 2 * kMaxGroup + tid] - m), l);
-        head_m[tid] = m;
-        head_l[tid] = l;
-    }
-    __syncthreads();
-    for (int e = tid; e < used * kMaxGroup; e += kAttnThreads) {
-        const int g = e % kMaxGroup;
-        if (g < group) scale_c[e] = expf(stats[(e / kMaxGroup) * 2 * kMaxGroup + g] - head_m[g]) / head_l[g];
+        for (int c = lane; c < used; c += 64)
+            l = fmaf(stats[c * 2 * kMaxGroup + kMaxGroup + g], expf(stats[c * 2 * kMaxGroup + g] - m), l);
+        l = wave_sum(l);
+        for (int c = lane; c < kMaxChunks; c += 64)
+            scale_c[c * kMaxGroup + g] = c < used ? expf(stats[c * 2 * kMaxGroup + g] - m) / l : 0.0f;
     }
     __syncthreads();
     float o[kMaxGroup / 2] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -419,9 +422,11 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
 #pragma unroll
         for (int u = 0; u < kMergeBatch; ++u)
 #pragma unroll
-            for (int i = 0; i < kMaxGroup / 2; ++i)
-                if (c0 + u < used && g0 + 2 * i < group)
-                    o[i] = fmaf(v[u][i], scale_c[(c0 + u) * kMaxGroup + g0 + 2 * i], o[i]);
+            for (int i = 0; i < kMaxGroup / 2; ++i) {
+                float sc = scale_c[min(c0 + u, kMaxChunks - 1) * kMaxGroup + min(g0 + 2 * i, kMaxGroup - 1)];
+                sc = c0 + u < used ? sc : 0.0f;
+                o[i] = fmaf(v[u][i], sc, o[i]);
+            }
     }
 #pragma unroll
     for (int i = 0; i < kMaxGroup / 2; ++i)
