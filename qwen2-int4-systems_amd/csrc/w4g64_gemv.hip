@@ -518,10 +518,20 @@ GemvPlan plan_gemv(int64_t rows, int64_t out_features, int64_t in_features, int 
     if (force_segments > 0 || force_splits > 0)
         return plan_segmented(rows, out_features, in_features, x_kind, force_segments > 0 ? force_segments : sw,
                               force_splits);
-    // K splits: a lane holds at most kMaxSteps group steps; with few column
-    // blocks and many rows, split further so that >= 256 workgroups run.
+    // K splits: a lane holds at most kMaxSteps group steps.  With few column
+    // blocks, split further to fill the chip -- but a split adds a cross-
+    // workgroup merge, which only pays while each lane keeps >= 5 group steps
+    // (fp16/bf16, measured: q at 4 rows 6.3 -> 5.0 us unsplit, down at 4 rows
+    // 11.2 -> 9.6 us with 6 splits instead of 3).  The fp32-class kinds stage
+    // their activations at a higher cost per workgroup and keep the old rule
+    // (the SwiGLU down projection at 1 row: 3 splits 9.9 us, 6 splits 11.2 us).
     int64_t splits = (groups + sw * kMaxSteps - 1) / (sw * kMaxSteps);
-    while (blocks_for(sw) * splits < kDeviceCUs && splits * 2 <= groups && groups / (splits * 2) >= sw) splits *= 2;
+    if (mv == rows) {
+        while (blocks_for(sw) * splits < 2 * kDeviceCUs && splits * 2 <= groups && groups >= splits * 2 * sw * 5)
+            splits *= 2;
+    } else {
+        while (blocks_for(sw) * splits < kDeviceCUs && splits * 2 <= groups && groups / (splits * 2) >= sw) splits *= 2;
+    }
     return plan_segmented(rows, out_features, in_features, x_kind, sw, splits);
 }
 
