@@ -436,6 +436,14 @@ bool plan_rows16(int64_t rows, int64_t out_features, int64_t in_features, GemvPl
         gps = (groups + splits - 1) / splits;
     }
     splits = (groups + gps - 1) / gps;
+    // Long K with few column blocks: split across workgroups while a wave
+    // keeps more than 6 group steps (down projection 1536 x 8960 at 16 rows:
+    // 96 workgroups 18.5 us, 4 splits 14.9 us; short K loses to the merge).
+    while (plan.n_blocks * splits < 256 && (gps + plan.waves - 1) / plan.waves > 6) {
+        splits *= 2;
+        gps = (groups + splits - 1) / splits;
+        splits = (groups + gps - 1) / gps;
+    }
     if (splits > 1 && plan.n_blocks > kGemvMaxColumnBlocks) return false;
     plan.splits = (int)splits;
     plan.groups_per_split = (int)gps;
