@@ -23,7 +23,9 @@
 //     pair); bf16: B = 128 + n' exact, and the group result is corrected by
 //     -(136 + zero) * sum_k x[m,k]; that row sum comes from one more MFMA pair
 //     against an all-ones B, which leaves it in the accumulator's own layout.
-//   * a K split across workgroups (only for K > 18 * 8 * 64) uses the same
+//   * a K split across workgroups (when a wave would otherwise hold more than
+//     18 group steps, or for long K with few column blocks: while a wave keeps
+//     more than 6 steps and fewer than 256 workgroups run) uses the same
 //     coherent last-arriver protocol as the segmented kernel.
 #include "w4g64_device.h"
 #include "w4g64_internal.h"
