@@ -369,3 +369,47 @@ def test_load_straight_to_the_gpu_matches_a_host_load(tmp_path: Path):
     prompt = torch.randint(0, config.vocab_size, (1, 16), generator=torch.Generator().manual_seed(3)).cuda()
     with torch.inference_mode():
         assert torch.equal(host(prompt), device(prompt))
+
+
+@pytest.mark.gpu
+def test_exported_awq_checkpoint_round_trips_through_the_fused_decoder(tmp_path: Path):
+    """A model quantized on the GPU (asymmetric codes, transformed norms and
+    v_proj bias), exported, and loaded into a fresh model whose projections
+    were fused for decode, generates exactly what the source model generates:
+    same prompt logits, same greedy tokens through the graph-replayed step."""
+    from qwen_int4_hip.generation import StaticGreedyDecoder
+    from qwen_int4_hip.quantization import quantize_asymmetric_rtn
+
+    config = SimpleNamespace(num_hidden_layers=2, **QWEN2_1_5B)
+    gen = torch.Generator(device="cuda").manual_seed(23)
+    source = QwenInt4ForCausalLM(config).cuda()
+    with torch.no_grad():
+        source.model.embed_tokens.weight.copy_(torch.randn(source.model.embed_tokens.weight.shape, generator=gen,
+                                                           device="cuda") * 0.02)
+        for name, module in source.named_modules():
+            if isinstance(module, QuantLinear):
+                w = torch.randn((module.out_features, module.in_features), generator=gen, device="cuda") * 0.02
+                q, s, z = quantize_asymmetric_rtn(w, group_size=64)
+                module.qweight.copy_(q)
+                module.scales.copy_(s)
+                module.zeros.copy_(z)
+                if module.bias is not None:
+                    module.bias.copy_(torch.randn(module.out_features, generator=gen, device="cuda") * 0.02)
+        for name, p in source.named_parameters():
+            if name.endswith("layernorm.weight"):
+                p.copy_(torch.rand(p.shape, generator=gen, device="cuda") + 0.5)
+    path = save_quantized_checkpoint(source, tmp_path / "awq" / "model.safetensors", canonical_awq_metadata(group_size=64))
+    target = QwenInt4ForCausalLM(config).cuda()
+    with torch.no_grad():
+        target.model.embed_tokens.weight.copy_(source.model.embed_tokens.weight)
+    fuse_projections(target)
+    assert load_quantized_checkpoint(target, path).loaded_keys == 2 * (7 * 3 + 3)
+    prompt = torch.randint(0, config.vocab_size, (1, 24), generator=torch.Generator().manual_seed(1)).cuda()
+    a = StaticGreedyDecoder(source, 1, 48)
+    b = StaticGreedyDecoder(target, 1, 48)
+    with torch.inference_mode():
+        la, lb = a.prefill(prompt), b.prefill(prompt)
+        assert torch.equal(la, lb)
+        for _ in range(8):
+            assert torch.equal(a.step(), b.step())
+            assert torch.equal(a.token, b.token)
