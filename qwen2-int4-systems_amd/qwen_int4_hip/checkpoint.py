@@ -15,7 +15,9 @@ safetensors files load drop-in into ``QwenInt4ForCausalLM``:
     views of fused q|k|v and gate|up buffers are written through;
   * the frozen canonical AWQ v6 manifest and the checks on a v6 file's bytes
     and metadata before it loads (src/qwen_int4/artifact_contract.py:52-167,
-    src/qwen_int4/checkpoint.py:121-140).
+    src/qwen_int4/checkpoint.py:121-140);
+  * the base-model tensors the checkpoint does not carry (embedding, norms,
+    q/k/v biases, tied LM head) -- src/qwen_int4/checkpoint.py:143-175.
 
 Loading uses safetensors only (no pickle).
 """
@@ -196,6 +198,38 @@ def load_quantized_checkpoint(model: torch.nn.Module, path: str | Path, *,
             "non-zero zero-points found without an asymmetric checkpoint contract: " + ", ".join(nonzero_zero_points)
         )
     return LoadReport(len(load_tensors), len(checkpoint) - len(load_tensors))
+
+
+# Non-quantized tensors every model needs from its base model (the checkpoint
+# carries only the quantized linears and, for AWQ, the transformed norms and
+# v_proj bias) -- src/qwen_int4/checkpoint.py:157-165.
+_REQUIRED_BASE_KEYS = ("model.embed_tokens.weight", "model.norm.weight", "lm_head.weight")
+_REQUIRED_BASE_SUFFIXES = ("layernorm.weight", "q_proj.bias", "k_proj.bias", "v_proj.bias")
+
+
+def extract_non_quantized_state(base_model: torch.nn.Module, target_model: torch.nn.Module) -> dict[str, torch.Tensor]:
+    """The base model's tensors that `target_model` holds outside its quantized
+    buffers (embedding, norms, q/k/v biases, tied LM head), as host copies,
+    matched by name and shape; fails if a required one is absent
+    (src/qwen_int4/checkpoint.py:143-169)."""
+    source = base_model.state_dict()
+    wanted = [key for key in target_model.state_dict() if not is_quantized_key(key)]
+    target_shapes = {key: tensor.shape for key, tensor in target_model.state_dict().items()}
+    state = {key: source[key].detach().to("cpu").clone() for key in wanted
+             if key in source and source[key].shape == target_shapes[key]}
+    required = {key for key in wanted
+                if key in _REQUIRED_BASE_KEYS or key.endswith(_REQUIRED_BASE_SUFFIXES)}
+    missing = sorted(required - set(state))
+    if missing:
+        raise RuntimeError(f"HF base model is missing required non-quantized tensors: {missing}")
+    return state
+
+
+def load_non_quantized_state(model: torch.nn.Module, state: dict[str, torch.Tensor]) -> None:
+    """Copy base-model tensors into `model` (src/qwen_int4/checkpoint.py:172-175)."""
+    incompatible = model.load_state_dict(state, strict=False)
+    if incompatible.unexpected_keys:
+        raise RuntimeError(f"unexpected HF base keys: {sorted(incompatible.unexpected_keys)}")
 
 
 def save_quantized_checkpoint(model: torch.nn.Module, path: str | Path, metadata: dict[str, str]) -> Path:

@@ -25,10 +25,12 @@ from qwen_int4_hip.checkpoint import (
     canonical_awq_metadata,
     canonical_rtn_metadata,
     checkpoint_metadata,
+    extract_non_quantized_state,
     group_size_from_checkpoint,
     is_quantized_key,
     load_canonical_awq_v6_checkpoint,
     load_canonical_awq_v6_contract,
+    load_non_quantized_state,
     load_quantized_checkpoint,
     packing_from_checkpoint,
     save_quantized_checkpoint,
@@ -253,6 +255,34 @@ def test_load_writes_through_fused_projection_views(tmp_path: Path):
                            torch.cat([mlp.gate_proj.scales, mlp.up_proj.scales]))
 
 
+# --- base-model state ---------------------------------------------------------
+
+def test_non_quantized_state_is_taken_from_the_base_model():
+    config = SimpleNamespace(num_hidden_layers=2, **dict(QWEN2_1_5B, hidden_size=128, num_attention_heads=2,
+                                                         num_key_value_heads=1, head_dim=64, intermediate_size=256,
+                                                         vocab_size=64))
+    base = _fill(QwenInt4ForCausalLM(config), 31)
+    target = QwenInt4ForCausalLM(config)
+    state = extract_non_quantized_state(base, target)
+    assert not any(is_quantized_key(k) for k in state)
+    assert {"model.embed_tokens.weight", "model.norm.weight", "lm_head.weight",
+            "model.layers.1.self_attn.k_proj.bias", "model.layers.0.post_attention_layernorm.weight"} <= set(state)
+    assert all(v.device.type == "cpu" for v in state.values())
+    load_non_quantized_state(target, state)
+    _assert_same_state(base, target, list(state))
+    assert not torch.equal(base.model.layers[0].mlp.up_proj.qweight, target.model.layers[0].mlp.up_proj.qweight)
+    # a base model without a required tensor is rejected
+    class NoNorm(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.model = nn.Module()
+            self.model.embed_tokens = nn.Embedding(64, 128)
+    with pytest.raises(RuntimeError, match="missing required non-quantized tensors"):
+        extract_non_quantized_state(NoNorm(), target)
+    with pytest.raises(RuntimeError, match="unexpected HF base keys"):
+        load_non_quantized_state(target, {"model.extra.weight": torch.zeros(1)})
+
+
 # --- frozen v6 manifest ------------------------------------------------------
 
 def _v6_checkpoint(tmp_path: Path, metadata: dict[str, str]) -> tuple[Path, CanonicalAWQV6Contract]:
@@ -400,9 +430,9 @@ def test_exported_awq_checkpoint_round_trips_through_the_fused_decoder(tmp_path:
                 p.copy_(torch.rand(p.shape, generator=gen, device="cuda") + 0.5)
     path = save_quantized_checkpoint(source, tmp_path / "awq" / "model.safetensors", canonical_awq_metadata(group_size=64))
     target = QwenInt4ForCausalLM(config).cuda()
-    with torch.no_grad():
-        target.model.embed_tokens.weight.copy_(source.model.embed_tokens.weight)
     fuse_projections(target)
+    # the reference's load order (src/qwen_int4/cli.py:92-95): base-model tensors, then the checkpoint
+    load_non_quantized_state(target, extract_non_quantized_state(source, target))
     assert load_quantized_checkpoint(target, path).loaded_keys == 2 * (7 * 3 + 3)
     prompt = torch.randint(0, config.vocab_size, (1, 24), generator=torch.Generator().manual_seed(1)).cuda()
     a = StaticGreedyDecoder(source, 1, 48)
