@@ -29,10 +29,15 @@
 //   * fused activation form (decode step of the decoder layer): kSwiGLU
 //     stages silu(gate) * up (fp32, as three bf16 parts) from a [gate | up]
 //     bf16 row.
-//   * the compute waves issue every weight, scale and zero load at once
-//     (raw bits; decoded where the MFMA step uses them), so the workgroup's
-//     whole weight slice is in flight while separate staging waves (one, or
-//     four for the fp32-class kinds) bring the activations into LDS.
+//   * every wave first issues its share of the workgroup's activation loads,
+//     then every weight, scale and zero load of its steps (raw bits; decoded
+//     where the MFMA step uses them).  A wave's loads return in issue order,
+//     so the activations arrive first; they go to LDS (with the bf16 group
+//     sums reduced across lanes) and a barrier over LDS alone lets every wave
+//     start on its first weight step while the rest of the weights stream in.
+//   * each wave owns whole output features (all their segments and fp32
+//     parts), so the epilogue reduces within the wave, with no workgroup
+//     barrier.
 //   * optional K split across workgroups (only for many rows x few output
 //     features): partial sums go through device-coherent (sc1) stores; the
 //     last workgroup to arrive for a column block, known from a per-block
@@ -46,18 +51,10 @@
 namespace w4g64 {
 namespace {
 
-constexpr int kWaves = 4;          // compute waves; one more wave stages the activations
-// Staging waves: one for fp16/bf16 activations; four for the fp32-class kinds,
-// whose staging (exact bf16 split, silu) is ALU-heavy.  Staging and weight
-// loads never share a wave: a wave's loads return in issue order, so a wave
-// holding both would see its activations only after its weight stream.
-constexpr int stage_waves(int xk) { return (xk == 3 || xk == 5) ? 4 : 1; }
-constexpr int gemv_threads(int xk) { return (kWaves + stage_waves(xk)) * 64; }
-constexpr int kMaxThreads = (kWaves + 4) * 64;
-constexpr int kMaxSteps = 16;      // group steps per lane in one workgroup
+constexpr int kWaves = 4;  // waves per workgroup
+constexpr int kThreads = kWaves * 64;
+constexpr int kMaxSteps = 16;  // group steps per lane in one workgroup
 constexpr int kStepBuckets[] = {2, 3, 6, 9, 12, 16};
-// activation items in flight per staging lane (the four-wave kinds need fewer)
-constexpr int stage_batch(int xk) { return (xk == 3 || xk == 5) ? 4 : 8; }
 
 typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
 
@@ -80,14 +77,33 @@ struct GemvArgs {
     unsigned* counters;  // [column blocks]
 };
 
+// Activation items (8 values each) a lane stages: M x groups-per-split x 8
+// items over the workgroup's lanes, where M <= 16 TILES / (SW parts) and
+// groups-per-split <= SW STEPS.
+template <int XK, int STEPS, int TILES>
+constexpr int stage_items() {
+    constexpr int parts = (XK == kF32 || XK == kSwiGLU) ? 3 : 1;
+    return (TILES * STEPS + 2 * parts - 1) / (2 * parts);
+}
+
+// Sum over the 8 lanes 8i..8i+7; every one of them gets the same bits.
+__device__ __forceinline__ float sum8_lanes(float s) {
+    s += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, s), 0xB1, 0xF, 0xF, false));
+    s += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, s), 0x4E, 0xF, 0xF, false));
+    s += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, s), 0x141, 0xF, 0xF, false));
+    return s;
+}
+
 template <int XK, int SW, int STEPS, int TILES>
-__global__ __launch_bounds__(kMaxThreads) void gemv_kernel(GemvArgs a) {
+__global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     __shared__ int s_last;
     constexpr int kParts = (XK == kF32 || XK == kSwiGLU) ? 3 : 1;
     constexpr int kOut = XK == kSwiGLU ? kF32 : XK;  // output kind
     constexpr int R = 16 / SW;              // output features per wave
     constexpr int kBlockCols = kWaves * R;  // output features per workgroup
+    constexpr int kStage = stage_items<XK, STEPS, TILES>();
+    constexpr int kVecs = (XK == kF16 || XK == kBF16) ? 1 : 2;  // 16-byte loads per item
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -99,6 +115,7 @@ __global__ __launch_bounds__(kMaxThreads) void gemv_kernel(GemvArgs a) {
     const int row_stride = a.gps * 64 + 8;  // 16-bit elements per staged row (+16 B pad)
     uint16_t* xs = (uint16_t*)smem;         // [mv][row_stride], slot order
     float* sx = (float*)(smem + (size_t)a.mv * row_stride * 2);  // [mv][gps] group sums (bf16/fp32)
+    float* red = sx + a.mv * a.gps;                               // [mv][kBlockCols][SW]
 
     // ---- this lane's column: output feature n, segment sj ----
     const int j = lane & 15;
@@ -116,141 +133,133 @@ __global__ __launch_bounds__(kMaxThreads) void gemv_kernel(GemvArgs a) {
     const uint8_t* wrow = a.qweight + (int64_t)nrow * (a.K / 2) + 8 * q;
     const int64_t sbase = (int64_t)nrow * a.G;
 
-    // ---- loads: weights (compute waves), activations (staging waves) ----
-    // Staging works in batches of kStageBatch items per staging lane: every
-    // load of a batch is issued before any is consumed.
-    constexpr int kThreads = gemv_threads(XK);
-    constexpr int kStageBatch = stage_batch(XK);
-    constexpr int kVecs = (XK == kF16 || XK == kBF16) ? 1 : 2;  // 16-byte loads per item
-    const int sid = tid - kWaves * 64;           // staging lane index
-    constexpr int nst = stage_waves(XK) * 64;    // staging lanes
-    const bool stager = wave >= kWaves;
+    // ---- 1. activation loads: item it = kThreads u + tid (8 values of row m) ----
+    // Lanes past the last item take the item at the same place in the last
+    // group instead, so they load, sum and store exactly what that group's
+    // own lanes do (identical bytes to the same addresses): no branch
+    // anywhere before the MFMA loop.
     const int kbase = g0 * 64;
-    const int items_per_row = cnt * 8;  // 8 values per item
+    const int items_per_row = cnt * 8;
     const int total = a.M * items_per_row;
     const float inv_items = 1.0f / (float)items_per_row;
     // item -> (row m, item c in the row); it < 2^24, so the float quotient is
     // off by at most one
-    auto item_rc = [&](int it, int& m, int& c) {
+    auto item_rc = [&](int it, int& m, int& c) {  // branch-free
         m = (int)((float)it * inv_items);
         c = it - m * items_per_row;
-        if (c < 0) { --m; c += items_per_row; }
-        else if (c >= items_per_row) { ++m; c -= items_per_row; }
+        const int adj = (int)(c >= items_per_row) - (int)(c < 0);
+        m += adj;
+        c -= adj * items_per_row;
     };
-    u32x4 v[kStageBatch][kVecs];
-    auto stage_load = [&](int base) {
+    u32x4 v[kStage][kVecs];
 #pragma unroll
-        for (int u = 0; u < kStageBatch; ++u) {
-            // clamped: a valid address whose result is not stored (an
-            // unconditional load keeps the batch branch-free)
-            const int it = min(base + nst * u + sid, total - 1);
-            {
-                int m, c;
-                item_rc(it, m, c);
-                if constexpr (XK == kF16 || XK == kBF16) {
-                    v[u][0] = *(const u32x4*)((const uint16_t*)a.x + (int64_t)m * a.K + kbase + 8 * c);
-                } else if constexpr (XK == kSwiGLU) {
-                    // x is [M, 2K]: gate | up (bf16)
-                    const uint16_t* gu = (const uint16_t*)a.x + (int64_t)m * 2 * a.K + kbase + 8 * c;
-                    v[u][0] = *(const u32x4*)gu;
-                    v[u][1] = *(const u32x4*)(gu + a.K);
-                } else {
-                    const float* src = (const float*)a.x + (int64_t)m * a.K + kbase + 8 * c;
-                    v[u][0] = *(const u32x4*)src;
-                    v[u][1] = *(const u32x4*)(src + 4);
-                }
-            }
+    for (int u = 0; u < kStage; ++u) {
+        const int it = kThreads * u + tid;
+        int m, c;
+        item_rc(it < total ? it : total - 8 + (tid & 7), m, c);
+        if constexpr (XK == kF16 || XK == kBF16) {
+            v[u][0] = *(const u32x4*)((const uint16_t*)a.x + (int64_t)m * a.K + kbase + 8 * c);
+        } else if constexpr (XK == kSwiGLU) {
+            // x is [M, 2K]: gate | up (bf16)
+            const uint16_t* gu = (const uint16_t*)a.x + (int64_t)m * 2 * a.K + kbase + 8 * c;
+            v[u][0] = *(const u32x4*)gu;
+            v[u][1] = *(const u32x4*)(gu + a.K);
+        } else {
+            const float* src = (const float*)a.x + (int64_t)m * a.K + kbase + 8 * c;
+            v[u][0] = *(const u32x4*)src;
+            v[u][1] = *(const u32x4*)(src + 4);
         }
-    };
-    auto stage_store = [&](int base) {
+    }
+    // (the empty asm statements with a memory clobber fix the issue order)
+    asm volatile("" ::: "memory");
+
+    // ---- 2. weight / scale / zero loads of every step ----
+    // Unconditional (steps past the K range re-read group g0 and get a zero
+    // scale), in step order, so that step t is complete once the lane's first
+    // 3 (t + 1) weight-side loads have returned.
 #pragma unroll
-        for (int u = 0; u < kStageBatch; ++u) {
-            const int it = base + nst * u + sid;
-            if (it >= total) continue;
-            int m, c;
-            item_rc(it, m, c);
-            if constexpr (XK == kF16 || XK == kBF16) {
-                *(u32x4*)(xs + m * row_stride + 8 * c) = permute_slots(v[u][0]);
+    for (int t = 0; t < STEPS; ++t) {
+        const int gl = sj + SW * t;
+        const int g = gl < cnt ? g0 + gl : g0;
+        wq[t] = __builtin_nontemporal_load((const u32x2*)(wrow + (int64_t)g * 32));
+        sraw[t] = a.scales[sbase + g];
+        zraw[t] = a.zeros[(sbase + g) >> 1];
+        asm volatile("" ::: "memory");
+    }
+    // Nothing that uses the activations may move above the last load issue.
+#pragma unroll
+    for (int u = 0; u < kStage; ++u)
+#pragma unroll
+        for (int k = 0; k < kVecs; ++k) asm volatile("" : "+v"(v[u][k]));
+
+    // ---- 3. activations into LDS (slot order) and group sums ----
+    // The 8 items of one (row, group) sit in lanes 8i..8i+7 of one u, so a
+    // group sum is a reduction over those 8 lanes, and all 8 store it.
+#pragma unroll
+    for (int u = 0; u < kStage; ++u) {
+        const int it = kThreads * u + tid;
+        int m, c;
+        item_rc(it < total ? it : total - 8 + (tid & 7), m, c);
+        const int gl = c >> 3;
+        if constexpr (XK == kF16) {
+            *(u32x4*)(xs + m * row_stride + 8 * c) = permute_slots(v[u][0]);
+        } else if constexpr (XK == kBF16) {
+            float s = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                s += __builtin_bit_cast(float, v[u][0][e] << 16) + __builtin_bit_cast(float, v[u][0][e] & 0xFFFF0000u);
+            s = sum8_lanes(s);
+            *(u32x4*)(xs + m * row_stride + 8 * c) = permute_slots(v[u][0]);
+            sx[m * a.gps + gl] = s;
+        } else {
+            float h[8];
+            if constexpr (XK == kSwiGLU) {
+                // h = silu(gate) * up in fp32, silu(g) = g / (1 + exp(-g)) (model.py:133-136)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const uint32_t gw = v[u][0][e / 2], uw = v[u][1][e / 2];
+                    const float g = bf16_bits_to_float(e & 1 ? gw >> 16 : gw & 0xFFFFu);
+                    const float up = bf16_bits_to_float(e & 1 ? uw >> 16 : uw & 0xFFFFu);
+                    h[e] = (g / (1.0f + expf(-g))) * up;
+                }
             } else {
-                float h[8];
-                if constexpr (XK == kSwiGLU) {
-                    // h = silu(gate) * up in fp32, silu(g) = g / (1 + exp(-g)) (model.py:133-136)
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        const uint32_t gw = v[u][0][e / 2], uw = v[u][1][e / 2];
-                        const float g = bf16_bits_to_float(e & 1 ? gw >> 16 : gw & 0xFFFFu);
-                        const float up = bf16_bits_to_float(e & 1 ? uw >> 16 : uw & 0xFFFFu);
-                        h[e] = (g / (1.0f + expf(-g))) * up;
-                    }
-                } else {
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        const uint32_t bits = v[u][e / 4][e % 4];  // element to a scalar before the cast
-                        h[e] = __builtin_bit_cast(float, bits);
-                    }
+                for (int e = 0; e < 8; ++e) {
+                    const uint32_t bits = v[u][e / 4][e % 4];  // element to a scalar before the cast
+                    h[e] = __builtin_bit_cast(float, bits);
                 }
-                uint16_t hi[8], mid[8], lo[8];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) split3_bf16(h[e], hi[e], mid[e], lo[e]);
-                u32x4 ph, pm, pl;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    ph[e] = (uint32_t)hi[2 * e] | ((uint32_t)hi[2 * e + 1] << 16);
-                    pm[e] = (uint32_t)mid[2 * e] | ((uint32_t)mid[2 * e + 1] << 16);
-                    pl[e] = (uint32_t)lo[2 * e] | ((uint32_t)lo[2 * e + 1] << 16);
-                }
-                *(u32x4*)(xs + m * row_stride + 8 * c) = permute_slots(ph);
-                *(u32x4*)(xs + (a.M + m) * row_stride + 8 * c) = permute_slots(pm);
-                *(u32x4*)(xs + (2 * a.M + m) * row_stride + 8 * c) = permute_slots(pl);
             }
-        }
-    };
-
-    if (wave < kWaves) {
-        // ---- compute waves: issue every weight / scale / zero load, step by step ----
-        // Unconditional loads (steps past the K range re-read group g0 and get a
-        // zero scale), interleaved so that step t is complete once the lane's
-        // first 3 (t + 1) loads have returned.
+            uint16_t hi[8], mid[8], lo[8];
 #pragma unroll
-        for (int t = 0; t < STEPS; ++t) {
-            const int gl = sj + SW * t;
-            const int g = gl < cnt ? g0 + gl : g0;
-            wq[t] = __builtin_nontemporal_load((const u32x2*)(wrow + (int64_t)g * 32));
-            sraw[t] = a.scales[sbase + g];
-            zraw[t] = a.zeros[(sbase + g) >> 1];
-        }
-    }
-    // ---- staging: this workgroup's activations into LDS (slot order) ----
-    if (stager) {
-        for (int base = 0; base < total; base += nst * kStageBatch) {
-            stage_load(base);
-            stage_store(base);
-        }
-    }
-    if constexpr (XK != kF16) {
-        // group sums of every staged row (a single staging wave's own LDS
-        // writes are ordered before its reads; several waves need a barrier)
-        if constexpr (stage_waves(XK) > 1) __syncthreads();
-        if (stager) {
-            for (int idx = sid; idx < cnt * a.mv; idx += nst) {
-                const int r = idx / cnt;
-                const int gl = idx - r * cnt;
-                const uint16_t* src = xs + r * row_stride + 64 * gl;
-                float s = 0.0f;
+            for (int e = 0; e < 8; ++e) split3_bf16(h[e], hi[e], mid[e], lo[e]);
+            u32x4 pp[3];
+            float ps[3] = {0.0f, 0.0f, 0.0f};
 #pragma unroll
-                for (int k = 0; k < 64; k += 8) {
-                    const u32x4 xv = *(const u32x4*)(src + k);  // 16-byte LDS reads
+            for (int e = 0; e < 4; ++e) {
+                pp[0][e] = (uint32_t)hi[2 * e] | ((uint32_t)hi[2 * e + 1] << 16);
+                pp[1][e] = (uint32_t)mid[2 * e] | ((uint32_t)mid[2 * e + 1] << 16);
+                pp[2][e] = (uint32_t)lo[2 * e] | ((uint32_t)lo[2 * e + 1] << 16);
+            }
 #pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        s += __builtin_bit_cast(float, xv[e] << 16) + __builtin_bit_cast(float, xv[e] & 0xFFFF0000u);
-                }
-                sx[r * a.gps + gl] = s;
+            for (int p = 0; p < 3; ++p) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    ps[p] += __builtin_bit_cast(float, pp[p][e] << 16) + __builtin_bit_cast(float, pp[p][e] & 0xFFFF0000u);
+                ps[p] = sum8_lanes(ps[p]);
+            }
+#pragma unroll
+            for (int p = 0; p < 3; ++p) {
+                *(u32x4*)(xs + (p * a.M + m) * row_stride + 8 * c) = permute_slots(pp[p]);
+                sx[(p * a.M + m) * a.gps + gl] = ps[p];
             }
         }
     }
-    __syncthreads();
+    // A barrier over LDS alone: the weight loads stay in flight through it.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 
-    // ---- MFMA over the group steps (compute waves) ----
+    // ---- 4. MFMA over the group steps ----
     float4v acc[TILES];
 #pragma unroll
     for (int tt = 0; tt < TILES; ++tt) acc[tt] = float4v{0.f, 0.f, 0.f, 0.f};
@@ -261,14 +270,25 @@ __global__ __launch_bounds__(kMaxThreads) void gemv_kernel(GemvArgs a) {
     // virtual rows only feed D rows the epilogue drops, and a step past the K
     // range has zero scale.  (Reading several steps ahead measured slower:
     // the registers cost more occupancy than the overlap gained.)
-    if (wave < kWaves) {
-        // The empty asm keeps the scale and zero decoding below this point:
-        // hoisted next to the loads, it would make every step's load issue
-        // wait for the scale.
-#pragma unroll
-        for (int t = 0; t < STEPS; ++t) asm volatile("" : "+v"(sraw[t]), "+v"(zraw[t]));
+    {
 #pragma unroll
         for (int t = 0; t < STEPS; ++t) {
+            // A operands of this step from LDS first (A row il = virtual row
+            // m, segment il % SW) ...
+            u16x8 a0[TILES], a1[TILES];
+#pragma unroll
+            for (int tt = 0; tt < TILES; ++tt) {
+                const int il = 16 * tt + (lane & 15);
+                const int m = min(il / SW, a.mv - 1);
+                const int ga = min(il % SW + SW * t, cnt - 1);  // the A row's group, local to the K range
+                const uint16_t* src = xs + m * row_stride + 64 * ga + 16 * q;
+                a0[tt] = *(const u16x8*)src;
+                a1[tt] = *(const u16x8*)(src + 8);
+            }
+            // ... then wait for this step's weight, scale and zero alone: the
+            // empty asm keeps their decoding here (hoisted next to the loads,
+            // it would make the later loads' issue wait for these).
+            asm volatile("" : "+v"(wq[t]), "+v"(sraw[t]), "+v"(zraw[t]));
             const uint32_t s_bits = sraw[t], z_bits = zraw[t];
             const int gl = sj + SW * t;  // this lane's group, local to the K range
             const float scale = (nvalid && gl < cnt) ? half_bits_to_float((uint16_t)s_bits) : 0.0f;
@@ -278,28 +298,21 @@ __global__ __launch_bounds__(kMaxThreads) void gemv_kernel(GemvArgs a) {
             const int glc = min(gl, cnt - 1);
 #pragma unroll
             for (int tt = 0; tt < TILES; ++tt) {
-                // A operand of this lane: A row il = virtual row m, segment sa.
-                const int il = 16 * tt + (lane & 15);
-                const int m = min(il / SW, a.mv - 1);
-                const int ga = min(il % SW + SW * t, cnt - 1);  // the A row's group, local to the K range
-                const uint16_t* src = xs + m * row_stride + 64 * ga + 16 * q;
-                const u16x8 a0 = *(const u16x8*)src;
-                const u16x8 a1 = *(const u16x8*)(src + 8);
                 float4v d;
                 if constexpr (XK == kF16) {
                     const _Float16 zl = (_Float16)(1032 + zr_t);
                     const _Float16 zh = (_Float16)(72 + zr_t);
                     const half8 b0 = dequant8_f16_int(wq[t][0], half2v{zl, zl}, half2v{zh, zh});
                     const half8 b1 = dequant8_f16_int(wq[t][1], half2v{zl, zl}, half2v{zh, zh});
-                    d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a0), b0,
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a0[tt]), b0,
                                                                float4v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                    d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a1), b1, d, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a1[tt]), b1, d, 0, 0, 0);
                 } else {
                     const bf16x8 b0 = dequant8_bf16_biased(wq[t][0]);
                     const bf16x8 b1 = dequant8_bf16_biased(wq[t][1]);
-                    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a0), b0,
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a0[tt]), b0,
                                                                 float4v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a1), b1, d, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a1[tt]), b1, d, 0, 0, 0);
                     // D rows i = 16 tt + 4 q + r.  The rows kept later share this
                     // lane's segment, so their group is this lane's group gl.
                     const float corr = 136.0f + (float)zr_t;
@@ -315,10 +328,9 @@ __global__ __launch_bounds__(kMaxThreads) void gemv_kernel(GemvArgs a) {
         }
     }
 
-    // ---- epilogue: keep the block diagonal, sum segments and fp32 parts ----
-    __syncthreads();            // activations no longer read
-    float* red = (float*)smem;  // [mv][kBlockCols][SW]
-    if (wave < kWaves)
+    // ---- 5. epilogue (per wave): keep the block diagonal, sum segments and parts ----
+    // The wave writes and reads only its own features' slots of `red`; LDS
+    // operations of one wave complete in order, so no barrier is needed.
 #pragma unroll
     for (int tt = 0; tt < TILES; ++tt) {
 #pragma unroll
@@ -328,12 +340,10 @@ __global__ __launch_bounds__(kMaxThreads) void gemv_kernel(GemvArgs a) {
             if (i % SW == sj && m < a.mv) red[(m * kBlockCols + wave * R + rj) * SW + sj] = acc[tt][r];
         }
     }
-    __syncthreads();
-
     const int col0 = nb * kBlockCols;
-    for (int idx = tid; idx < a.M * kBlockCols; idx += kThreads) {
-        const int m = idx / kBlockCols;
-        const int c = idx - m * kBlockCols;
+    for (int idx = lane; idx < a.M * R; idx += 64) {
+        const int m = idx / R;
+        const int c = wave * R + (idx - m * R);
         const int nn = col0 + c;
         if (nn >= a.N) continue;
         float v = 0.0f;
@@ -384,7 +394,9 @@ __global__ __launch_bounds__(kMaxThreads) void gemv_kernel(GemvArgs a) {
 template <int XK, int SW, int STEPS, int TILES>
 hipError_t launch_typed(const GemvArgs& args, const GemvPlan& plan, hipStream_t stream, hipEvent_t start,
                         hipEvent_t stop) {
-    return launch_kernel(gemv_kernel<XK, SW, STEPS, TILES>, dim3(plan.n_blocks, plan.splits), dim3(gemv_threads(XK)),
+    // the staging capacity of this instantiation (the planner never exceeds it)
+    if ((int64_t)args.M * args.gps * 8 > (int64_t)stage_items<XK, STEPS, TILES>() * kThreads) return hipErrorInvalidValue;
+    return launch_kernel(gemv_kernel<XK, SW, STEPS, TILES>, dim3(plan.n_blocks, plan.splits), dim3(kThreads),
                          (size_t)plan.lds_bytes, stream, start, stop, args);
 }
 
@@ -478,12 +490,9 @@ GemvPlan plan_segmented(int64_t rows, int64_t out_features, int64_t in_features,
     plan.n_blocks = (int)((out_features + cols - 1) / cols);
     int64_t splits = min_splits > 0 ? min_splits : 1;
     int64_t gps = (groups + splits - 1) / splits;
-    // staged activations (virtual rows x split width, 16-bit) plus the group sums
-    auto lds_for = [&](int64_t g) {
-        const int64_t stage = mv * (g * 64 + 8) * 2 + mv * g * 4;
-        const int64_t red = mv * kWaves * 16 * 4;
-        return stage > red ? stage : red;
-    };
+    // staged activations (virtual rows x split width, 16-bit), the group
+    // sums and the epilogue's per-segment results
+    auto lds_for = [&](int64_t g) { return mv * (g * 64 + 8) * 2 + mv * g * 4 + mv * kWaves * 16 * 4; };
     while (lds_for(gps) > 60 * 1024 || (gps + sw - 1) / sw > kMaxSteps) {
         ++splits;
         gps = (groups + splits - 1) / splits;
