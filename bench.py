@@ -13,10 +13,13 @@ replays K step graphs back to back between two device synchronizations.
 value = algorithmic bytes of the step / step time.
 
 The roofline object is for the kernels that do the decode work (all 21
-calls): their durations are measured live with HIP events that
-hipExtLaunchKernelGGL records at each kernel's own start and end (the same
-figure rocprofv3 --kernel-trace reports), on the stream the kernel runs on;
-achieved = algorithmic bytes / summed kernel durations.
+calls): each call's average launch duration is measured live the way the
+step runs -- a HIP graph of 32 back-to-back launches of that call (rotating
+over the weight copies), replayed between HIP events recorded on the replay
+stream -- and agrees with the per-kernel durations rocprofv3 --kernel-trace
+reports for graph replays; achieved = algorithmic bytes / summed average
+durations.  (Launched one at a time with start/stop events of their own,
+the same kernels measure ~0.6 us longer each.)
 
 Algorithmic bytes per call (M rows, N out, K in):
     N*K/2 + 2*N*K/64 + N*K/128 + 2*M*K + 2*M*N
@@ -105,12 +108,17 @@ class Hip:
         self.lib.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
         self.lib.hipEventSynchronize.argtypes = [ctypes.c_void_p]
         self.lib.hipEventDestroy.argtypes = [ctypes.c_void_p]
+        self.lib.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
 
     def event(self) -> ctypes.c_void_p:
         ev = ctypes.c_void_p()
         if self.lib.hipEventCreate(ctypes.byref(ev)) != 0:
             raise RuntimeError("hipEventCreate failed")
         return ev
+
+    def record(self, event, stream) -> None:
+        if self.lib.hipEventRecord(event, stream) != 0:
+            raise RuntimeError("hipEventRecord failed")
 
     def elapsed_ms(self, start, stop) -> float:
         self.lib.hipEventSynchronize(stop)
@@ -202,6 +210,42 @@ def kernel_durations(cases, reps, hip, torch):
     for a, b in pairs:
         hip.lib.hipEventDestroy(a)
         hip.lib.hipEventDestroy(b)
+    return durations
+
+
+def graph_kernel_durations(cases, reps, hip, torch, launches: int = 32):
+    """Per-case average launch duration (ms), measured the way the decode step
+    runs: one HIP graph per case holding `launches` back-to-back calls
+    (rotating over the weight copies), replayed `reps` times between HIP
+    events recorded on the replay stream; each sample is one replay's
+    elapsed time / `launches`."""
+    from qwen_int4_hip.kernels import linear_canonical_w4g64_hip
+
+    side = torch.cuda.Stream()
+    stream = ctypes.c_void_p(side.cuda_stream)
+    durations = []
+    with torch.cuda.stream(side):
+        for case in cases:
+            x, copies = case["x"], case["copies"]
+            ws = [copies[(case["copy0"] + 3 * i) % len(copies)] for i in range(launches)]
+            linear_canonical_w4g64_hip(x, *ws[0])  # workspace and kernel set-up outside capture
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=side):
+                for w in ws:
+                    linear_canonical_w4g64_hip(x, *w)
+            g.replay()
+            events = [(hip.event(), hip.event()) for _ in range(reps)]
+            for a, b in events:
+                hip.record(a, stream)
+                g.replay()
+                hip.record(b, stream)
+            torch.cuda.synchronize()
+            durations.append([hip.elapsed_ms(a, b) / launches for a, b in events])
+            for a, b in events:
+                hip.lib.hipEventDestroy(a)
+                hip.lib.hipEventDestroy(b)
+            del g
     return durations
 
 
@@ -582,7 +626,7 @@ def main() -> int:
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=512)
     parser.add_argument("--warmup", type=int, default=64)
-    parser.add_argument("--kernel-reps", type=int, default=32, help="event-timed calls per case")
+    parser.add_argument("--kernel-reps", type=int, default=32, help="timed graph replays per decode case (32 launches each); event-timed calls per GEMM case")
     parser.add_argument("--no-cpu-baseline", action="store_true",
                         help="skip the CPU baseline leg (and with it the parity check against the CPU reference)")
     parser.add_argument("--no-gemm", action="store_true")
@@ -663,8 +707,8 @@ def main() -> int:
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
     log(f"decode: {ms_per_step * 1e3:.1f} us/step, {value:.1f} GB/s whole-step ({step_bytes / 1e6:.1f} MB/step)")
 
-    # live per-kernel durations (events recorded by the kernel launch itself)
-    durations = kernel_durations(cases, args.kernel_reps, hip, torch)
+    # live per-kernel durations: HIP events around graph replays of each shape
+    durations = graph_kernel_durations(cases, args.kernel_reps, hip, torch)
     per_case = []
     kernel_ms_total = 0.0
     for c, d in zip(cases, durations):

@@ -427,51 +427,54 @@ hipError_t launch_sw(const GemvArgs& args, const GemvPlan& plan, hipStream_t str
 
 }  // namespace
 
-namespace {
 constexpr int kRows16Buckets[] = {2, 3, 6, 9, 12, 18};  // steps of the 9..16-row kernel
 
-// 9..16 fp16/bf16 rows: one 16-feature block per workgroup, K split across
-// its waves (4, or 8 for long K); across workgroups only when a wave would
-// need more than 18 group steps.
-bool plan_rows16(int64_t rows, int64_t out_features, int64_t in_features, GemvPlan& plan) {
+// 9..16 fp16/bf16 rows: fblocks 16-feature blocks per workgroup, `waves`
+// waves per block taking its K range's groups round robin; the range's
+// activations are staged in LDS (at most ~60 KB: 28 groups at 16 rows).
+// Measured at 16 rows (fp16, cold weights): K = 1536 runs best as one block
+// of 8 waves (3 steps; gate 8960x1536 8.4 us, q 1536x1536 4.2 us); K = 8960
+// as two blocks of 4 waves over the 5 K splits the LDS budget needs (down
+// 1536x8960 11.2 us).  More splits, or 8 waves over 6+ steps (133 VGPRs: one
+// such workgroup per CU, two dispatch rounds), measured slower.
+bool plan_rows16(int64_t rows, int64_t out_features, int64_t in_features, GemvPlan& plan, int force_fblocks,
+                 int force_waves, int force_splits) {
+    if (rows < 9 || rows > 16) return false;
     const int64_t groups = in_features / 64;
     plan = GemvPlan{};
     plan.kind = 1;
-    plan.waves = groups <= 48 ? 4 : 8;
     plan.segments = 1;
     plan.tiles = 1;
-    plan.n_blocks = (int)((out_features + 15) / 16);
-    int64_t splits = 1;
-    int64_t gps = groups;
-    while ((gps + plan.waves - 1) / plan.waves > 18) {
+    const bool short_k = groups <= 48;
+    plan.fblocks = force_fblocks > 0 ? force_fblocks : (short_k ? 1 : 2);
+    plan.waves = force_waves > 0 ? force_waves : (plan.fblocks == 1 ? (short_k ? 8 : 4) : 4);
+    const int fb = plan.fblocks, kw = plan.waves;
+    if (!((fb == 1 && (kw == 4 || kw == 8)) || (fb == 2 && (kw == 2 || kw == 4)) || (fb == 4 && (kw == 1 || kw == 2))))
+        return false;
+    plan.n_blocks = (int)((out_features + 16 * fb - 1) / (16 * fb));
+    auto lds_for = [&](int64_t g) { return rows * (g * 64 + 8) * 2 + rows * g * 4; };
+    int64_t splits = force_splits > 0 ? force_splits : 1;
+    int64_t gps = (groups + splits - 1) / splits;
+    while (lds_for(gps) > 60 * 1024 || (gps + kw - 1) / kw > 18) {
         ++splits;
         gps = (groups + splits - 1) / splits;
     }
     splits = (groups + gps - 1) / gps;
-    // Long K with few column blocks: split across workgroups while a wave
-    // keeps more than 6 group steps (down projection 1536 x 8960 at 16 rows:
-    // 96 workgroups 18.5 us, 4 splits 14.9 us; short K loses to the merge).
-    while (plan.n_blocks * splits < 256 && (gps + plan.waves - 1) / plan.waves > 6) {
-        splits *= 2;
-        gps = (groups + splits - 1) / splits;
-        splits = (groups + gps - 1) / gps;
-    }
     if (splits > 1 && plan.n_blocks > kGemvMaxColumnBlocks) return false;
     plan.splits = (int)splits;
     plan.groups_per_split = (int)gps;
-    const int64_t need = (gps + plan.waves - 1) / plan.waves;
+    const int64_t need = (gps + kw - 1) / kw;
     plan.steps = 18;
     for (int b : kRows16Buckets)
         if (b >= need) {
             plan.steps = b;
             break;
         }
-    plan.lds_bytes = 0;
+    plan.lds_bytes = lds_for(gps);
     plan.counter_bytes = splits > 1 ? kGemvCounterBytes : 0;
     plan.workspace_bytes = splits > 1 ? plan.counter_bytes + splits * rows * out_features * 4 : 0;
     return true;
 }
-}  // namespace
 
 namespace {
 constexpr int64_t kDeviceCUs = 256;  // MI355X compute units
@@ -518,7 +521,7 @@ GemvPlan plan_gemv(int64_t rows, int64_t out_features, int64_t in_features, int 
                    int force_splits) {
     GemvPlan plan{};
     if (rows > 8 && rows <= 16 && (x_kind == kF16 || x_kind == kBF16) && force_segments <= 0 && force_splits <= 0 &&
-        plan_rows16(rows, out_features, in_features, plan))
+        plan_rows16(rows, out_features, in_features, plan, 0, 0, 0))
         return plan;
     const int64_t groups = in_features / 64;
     const int64_t mv = rows * ((x_kind == kF32 || x_kind == kSwiGLU) ? 3 : 1);
@@ -560,7 +563,8 @@ const char* gemv_kernel_name(const GemvPlan& plan, int x_kind) {
     static thread_local char name[64];
     static const char* kinds[] = {"?", "f16", "bf16", "f32", "?", "swiglu_bf16"};
     if (plan.kind == 1) {
-        snprintf(name, sizeof(name), "gemv16_kernel<%s,%d,%d>", kinds[x_kind >= 1 && x_kind <= 5 ? x_kind : 0], plan.steps, plan.waves);
+        snprintf(name, sizeof(name), "gemv16_kernel<%s,%d,%d,%d>", kinds[x_kind >= 1 && x_kind <= 5 ? x_kind : 0], plan.steps,
+                 plan.waves, plan.fblocks);
         return name;
     }
     snprintf(name, sizeof(name), "gemv_kernel<%s,%d,%d,%d>", kinds[x_kind >= 1 && x_kind <= 5 ? x_kind : 0], plan.segments, plan.steps,

@@ -1,37 +1,36 @@
 // Decode path for 9..16 activation rows (fp16 / bf16): fused unpack +
-// dequant + GEMV with the K range split across the waves of a workgroup.
+// dequant + GEMV, the activations staged once per workgroup in LDS.
 //
 // y[m, n] = sum_g scale[n,g] * sum_{k in g} x[m,k] * (code[n,k] - zero[n,g])   (+ bias[n])
 // (src/qwen_int4/backends.py:73-98, group scale applied once per group in fp32).
 //
 // With 9..16 rows the activation rows fill the 16 A rows of
 // v_mfma_f32_16x16x32_{f16,bf16} on their own, so:
-//   * a workgroup owns one block of 16 output features (the 16 B columns);
-//     its KW waves take the groups of its K range round robin (wave w takes
-//     g0 + w, g0 + w + KW, ...), and their partial sums meet in LDS;
-//   * every lane loads its A fragment straight from global memory (the
-//     activations are small and stay in L2): row lane % 16, the 16 values
-//     [16 q, 16 q + 16) of the group, q = lane / 16 -- the same K values as the
-//     8 packed bytes it loads for its B column -- permuted into the slot
-//     order the nibble decode produces.  No staging wave, no workgroup barrier
-//     before the MFMAs;
-//   * all scale, zero, weight and activation loads of a lane are issued
-//     before the first MFMA (in that order), so the whole slice is in flight
-//     at once and the MFMA of step t waits only for loads issued before its
-//     own activations;
+//   * a workgroup owns FB blocks of 16 output features (the 16 B columns of
+//     a wave's MFMA); KW waves work on each block and take the groups of the
+//     workgroup's K range round robin (wave kw takes g0 + kw, g0 + kw + KW,
+//     ...); their partial sums meet in LDS at the end;
+//   * the activations of the K range (rows x groups x 64 values) are staged
+//     once per workgroup: every lane first issues its share of dense 16-byte
+//     loads, then every weight, scale and zero load of its steps.  A wave's
+//     loads return in issue order, so the activations arrive first; they go
+//     to LDS in MFMA slot order (bf16: with the group sums for the zero
+//     correction, reduced over 8 lanes), and a barrier over LDS alone lets
+//     the MFMA steps start while the weights still stream in.  Staging
+//     FB blocks' worth of features per workgroup divides the activation
+//     traffic (M / 4 bytes of activations per weight byte per block) by FB;
 //   * fp16: B = (code - zero) exact (1024 + n' magic, one v_pk_add_f16 per
 //     pair); bf16: B = 128 + n' exact, and the group result is corrected by
-//     -(136 + zero) * sum_k x[m,k]; that row sum comes from one more MFMA pair
-//     against an all-ones B, which leaves it in the accumulator's own layout.
-//   * a K split across workgroups (when a wave would otherwise hold more than
-//     18 group steps, or for long K with few column blocks: while a wave keeps
-//     more than 6 steps and fewer than 256 workgroups run) uses the same
-//     coherent last-arriver protocol as the segmented kernel.
+//     -(136 + zero) * sum_{k in g} x[m,k].
+//   * a K split across workgroups (long K: the staged range must fit LDS)
+//     uses the same coherent last-arriver protocol as the segmented kernel.
 #include "w4g64_device.h"
 #include "w4g64_internal.h"
 
 namespace w4g64 {
 namespace {
+
+typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
 
 struct Gemv16Args {
     const void* x;
@@ -51,133 +50,183 @@ struct Gemv16Args {
     unsigned* counters;  // [column blocks]
 };
 
-template <int XK, int STEPS, int KW>
-__global__ __launch_bounds__(KW * 64) void gemv16_kernel(Gemv16Args a) {
-    __shared__ float red[KW][16][16];  // [wave][row][feature]
+// Activation items (8 values) a lane stages: 16 rows x KW STEPS groups x 8
+// items over KW FB waves.
+template <int STEPS, int FB>
+constexpr int stage_items16() {
+    return (2 * STEPS + FB - 1) / FB;
+}
+
+// Sum over the 8 lanes 8i..8i+7; every one of them gets the same bits.
+__device__ __forceinline__ float sum8_lanes16(float s) {
+    s += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, s), 0xB1, 0xF, 0xF, false));
+    s += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, s), 0x4E, 0xF, 0xF, false));
+    s += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, s), 0x141, 0xF, 0xF, false));
+    return s;
+}
+
+template <int XK, int STEPS, int KW, int FB>
+__global__ __launch_bounds__(KW * FB * 64) void gemv16_kernel(Gemv16Args a) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    __shared__ float red[KW * FB][16][16];  // [wave][row][feature]
     __shared__ int s_last;
+    constexpr int kThreads16 = KW * FB * 64;
+    constexpr int kStage = stage_items16<STEPS, FB>();
+    constexpr int kCols = 16 * FB;  // output features per workgroup
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
+    const int fb = wave % FB;  // this wave's 16-feature block
+    const int kw = wave / FB;  // this wave's share of the groups
     const int nb = blockIdx.x;
     const int split = blockIdx.y;
     const int g0 = split * a.gps;
     const int cnt = min(a.gps, a.G - g0);
+    const int row_stride = a.gps * 64 + 8;  // 16-bit elements per staged row (+16 B pad)
+    uint16_t* xs = (uint16_t*)smem;         // [M][row_stride], slot order
+    float* sx = (float*)(smem + (size_t)a.M * row_stride * 2);  // [M][gps] group sums (bf16)
 
     const int j = lane & 15;  // B column = output feature, A row = activation row
     const int q = lane >> 4;  // 16-value quarter of the group
-    const int n = nb * 16 + j;
+    const int n = nb * kCols + fb * 16 + j;
     const bool nvalid = n < a.N;
     const int nrow = nvalid ? n : 0;
-    const int mrow = j < a.M ? j : a.M - 1;  // rows past M load a valid row; their outputs are dropped
     const uint8_t* wrow = a.qweight + (int64_t)nrow * (a.K / 2) + 8 * q;
-    const uint16_t* xrow = (const uint16_t*)a.x + (int64_t)mrow * a.K + 16 * q;
     const int64_t sbase = (int64_t)nrow * a.G;
 
-    // Loads complete in order, so any use of a loaded value waits for every
-    // load issued before it.  All scale and zero loads go first (their decode
-    // may be scheduled early), then every weight load, then every activation
-    // load; no use is scheduled before the last load is issued.
-    // Long K ranges (more than 12 steps) load their activations in two
-    // phases, the second after the first half of the MFMAs, to stay within 256
-    // registers; the weights are always in flight at once.
-    constexpr int kPhases = STEPS > 12 ? 2 : 1;
-    constexpr int kChunk = (STEPS + kPhases - 1) / kPhases;
+    // ---- 1. activation loads: item it = kThreads16 u + tid (8 values of row m) ----
+    // Lanes past the last item take the item at the same place in the last
+    // group, so they load, sum and store exactly what that group's own lanes
+    // do: no branch anywhere before the MFMA loop.
+    const int kbase = g0 * 64;
+    const int items_per_row = cnt * 8;
+    const int total = a.M * items_per_row;
+    const float inv_items = 1.0f / (float)items_per_row;
+    auto item_rc = [&](int it, int& m, int& c) {  // branch-free; it < 2^24
+        m = (int)((float)it * inv_items);
+        c = it - m * items_per_row;
+        const int adj = (int)(c >= items_per_row) - (int)(c < 0);
+        m += adj;
+        c -= adj * items_per_row;
+    };
+    u32x4 v[kStage];
+#pragma unroll
+    for (int u = 0; u < kStage; ++u) {
+        const int it = kThreads16 * u + tid;
+        int m, c;
+        item_rc(it < total ? it : total - 8 + (tid & 7), m, c);
+        v[u] = *(const u32x4*)((const uint16_t*)a.x + (int64_t)m * a.K + kbase + 8 * c);
+    }
+    // (the empty asm statements with a memory clobber fix the issue order)
+    asm volatile("" ::: "memory");
+
+    // ---- 2. weight / scale / zero loads of every step, in step order ----
+    // Steps past the K range re-read group g0 and get a zero scale.
     u32x2 wq[STEPS];
     uint32_t sraw[STEPS];
     uint32_t zraw[STEPS];
-    auto group_of = [&](int t) {
-        const int gl = wave + KW * t;
-        return gl < cnt ? g0 + gl : g0;  // past the range: re-read group g0, zero scale below
-    };
 #pragma unroll
     for (int t = 0; t < STEPS; ++t) {
-        const int64_t e = sbase + group_of(t);
-        sraw[t] = a.scales[e];
-        zraw[t] = (uint32_t)a.zeros[e >> 1] >> (4 * (e & 1));
+        const int gl = kw + KW * t;
+        const int g = gl < cnt ? g0 + gl : g0;
+        wq[t] = __builtin_nontemporal_load((const u32x2*)(wrow + (int64_t)g * 32));
+        sraw[t] = a.scales[sbase + g];
+        zraw[t] = a.zeros[(sbase + g) >> 1];
+        asm volatile("" ::: "memory");
     }
+    // Nothing that uses the activations may move above the last load issue.
 #pragma unroll
-    for (int t = 0; t < STEPS; ++t)
-        wq[t] = __builtin_nontemporal_load((const u32x2*)(wrow + (int64_t)group_of(t) * 32));
+    for (int u = 0; u < kStage; ++u) asm volatile("" : "+v"(v[u]));
 
+    // ---- 3. activations into LDS (slot order); bf16 group sums ----
+#pragma unroll
+    for (int u = 0; u < kStage; ++u) {
+        const int it = kThreads16 * u + tid;
+        int m, c;
+        item_rc(it < total ? it : total - 8 + (tid & 7), m, c);
+        *(u32x4*)(xs + m * row_stride + 8 * c) = permute_slots(v[u]);
+        if constexpr (XK == kBF16) {
+            float s = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                s += __builtin_bit_cast(float, v[u][e] << 16) + __builtin_bit_cast(float, v[u][e] & 0xFFFF0000u);
+            s = sum8_lanes16(s);
+            sx[m * a.gps + (c >> 3)] = s;
+        }
+    }
+    // A barrier over LDS alone: the weight loads stay in flight through it.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+
+    // ---- 4. MFMA over the steps: A row = activation row (rows past M read row M - 1) ----
+    const int mrow = min(j, a.M - 1);
     float4v acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int ph = 0; ph < kPhases; ++ph) {
-        u32x4 xa[kChunk][2];
+    for (int t = 0; t < STEPS; ++t) {
+        const int gl = kw + KW * t;
+        const int glc = min(gl, cnt - 1);
+        const uint16_t* src = xs + mrow * row_stride + 64 * glc + 16 * q;
+        const u16x8 a0 = *(const u16x8*)src;
+        const u16x8 a1 = *(const u16x8*)(src + 8);
+        // wait for this step's weight, scale and zero alone; the empty asm keeps
+        // their decoding here
+        asm volatile("" : "+v"(wq[t]), "+v"(sraw[t]), "+v"(zraw[t]));
+        const float sct = (nvalid && gl < cnt) ? half_bits_to_float((uint16_t)sraw[t]) : 0.0f;
+        const int gz = gl < cnt ? g0 + gl : g0;  // the group this step loaded
+        const int zn = (((sbase + gz) & 1) ? (zraw[t] >> 4) : zraw[t]) & 0xF;
+        const int zrt = zn - ((zn & 8) << 1);
+        float4v d;
+        if constexpr (XK == kF16) {
+            const _Float16 zl = (_Float16)(1032 + zrt);
+            const _Float16 zh = (_Float16)(72 + zrt);
+            const half8 b0 = dequant8_f16_int(wq[t][0], half2v{zl, zl}, half2v{zh, zh});
+            const half8 b1 = dequant8_f16_int(wq[t][1], half2v{zl, zl}, half2v{zh, zh});
+            d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a0), b0,
+                                                       float4v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+            d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a1), b1, d, 0, 0, 0);
+        } else {
+            const bf16x8 b0 = dequant8_bf16_biased(wq[t][0]);
+            const bf16x8 b1 = dequant8_bf16_biased(wq[t][1]);
+            d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a0), b0,
+                                                        float4v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+            d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a1), b1, d, 0, 0, 0);
+            // D row 4 q + r = activation row; its group sum over this step's group
+            const float corr = 136.0f + (float)zrt;
 #pragma unroll
-        for (int c = 0; c < kChunk; ++c) {
-            const int t = ph * kChunk + c;
-            if (t < STEPS) {
-                xa[c][0] = *(const u32x4*)(xrow + (int64_t)group_of(t) * 64);
-                xa[c][1] = *(const u32x4*)(xrow + (int64_t)group_of(t) * 64 + 8);
-            }
+            for (int r = 0; r < 4; ++r) d[r] = fmaf(-corr, sx[min(4 * q + r, a.M - 1) * a.gps + glc], d[r]);
         }
-        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int c = 0; c < kChunk; ++c) {
-            const int t = ph * kChunk + c;
-            if (t >= STEPS) continue;
-            const bool live = nvalid && wave + KW * t < cnt;
-            const float sct = live ? half_bits_to_float((uint16_t)sraw[t]) : 0.0f;
-            const int zn = (int)(zraw[t] & 0xF);
-            const int zrt = zn - ((zn & 8) << 1);
-            const u32x4 a0 = permute_slots(xa[c][0]);
-            const u32x4 a1 = permute_slots(xa[c][1]);
-            float4v d;
-            if constexpr (XK == kF16) {
-                const _Float16 zl = (_Float16)(1032 + zrt);
-                const _Float16 zh = (_Float16)(72 + zrt);
-                const half8 b0 = dequant8_f16_int(wq[t][0], half2v{zl, zl}, half2v{zh, zh});
-                const half8 b1 = dequant8_f16_int(wq[t][1], half2v{zl, zl}, half2v{zh, zh});
-                d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a0), b0,
-                                                           float4v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a1), b1, d, 0, 0, 0);
-            } else {
-                const bf16x8 b0 = dequant8_bf16_biased(wq[t][0]);
-                const bf16x8 b1 = dequant8_bf16_biased(wq[t][1]);
-                const bf16x8 ones =
-                    __builtin_bit_cast(bf16x8, u32x4{0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u});
-                d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a0), b0,
-                                                            float4v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a1), b1, d, 0, 0, 0);
-                float4v sx = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a0), ones,
-                                                                     float4v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                sx = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a1), ones, sx, 0, 0, 0);
-                const float corr = 136.0f + (float)zrt;
-#pragma unroll
-                for (int r = 0; r < 4; ++r) d[r] = fmaf(-corr, sx[r], d[r]);
-            }
-#pragma unroll
-            for (int r = 0; r < 4; ++r) acc[r] = fmaf(sct, d[r], acc[r]);
-        }
+        for (int r = 0; r < 4; ++r) acc[r] = fmaf(sct, d[r], acc[r]);
     }
 
-    // ---- combine the waves' partial sums: D row = 4 q + r, column = j ----
+    // ---- 5. combine the KW waves of each block: D row = 4 q + r, column = j ----
 #pragma unroll
     for (int r = 0; r < 4; ++r) red[wave][4 * q + r][j] = acc[r];
     __syncthreads();
 
-    float v = 0.0f;
-    const int m = tid >> 4;  // threads 0..255: (row, feature)
-    const int c = tid & 15;
-    const int nn = nb * 16 + c;
-    const bool mine = tid < 256 && m < a.M && nn < a.N;
-    if (tid < 256) {
+    const int col0 = nb * kCols;
+    for (int idx = tid; idx < a.M * kCols; idx += kThreads16) {
+        const int m = idx / kCols;
+        const int c = idx - m * kCols;
+        const int nn = col0 + c;
+        if (nn >= a.N) continue;
+        float s = 0.0f;
 #pragma unroll
-        for (int w = 0; w < KW; ++w) v += red[w][m][c];  // fixed order: deterministic
+        for (int w = 0; w < KW; ++w) s += red[w * FB + c / 16][m][c % 16];  // fixed order: deterministic
+        if (a.splits == 1)
+            store_out<XK>(a.y, (int64_t)m * a.N + nn, s + load_bias(a.bias, a.bias_kind, nn));
+        else
+            __hip_atomic_store(a.partials + ((int64_t)split * a.M + m) * a.N + nn, s, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
     }
-    if (a.splits == 1) {
-        if (mine) store_out<XK>(a.y, (int64_t)m * a.N + nn, v + load_bias(a.bias, a.bias_kind, nn));
-        return;
-    }
+    if (a.splits == 1) return;
 
     // ---- K split across workgroups: the last arrival of the block reduces ----
     // Partials travel through device-coherent (sc1) atomic stores and loads;
     // the wait completes this workgroup's partial stores before its arrival is
     // counted, and the reducer loads only after its counter update returned.
-    if (mine)
-        __hip_atomic_store(a.partials + ((int64_t)split * a.M + m) * a.N + nn, v, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
@@ -188,7 +237,11 @@ __global__ __launch_bounds__(KW * 64) void gemv16_kernel(Gemv16Args a) {
     __syncthreads();
     if (!s_last) return;
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-    if (mine) {
+    for (int idx = tid; idx < a.M * kCols; idx += kThreads16) {
+        const int m = idx / kCols;
+        const int c = idx - m * kCols;
+        const int nn = col0 + c;
+        if (nn >= a.N) continue;
         float s = 0.0f;
         for (int sp = 0; sp < a.splits; ++sp)
             s += __hip_atomic_load(a.partials + ((int64_t)sp * a.M + m) * a.N + nn, __ATOMIC_RELAXED,
@@ -198,18 +251,40 @@ __global__ __launch_bounds__(KW * 64) void gemv16_kernel(Gemv16Args a) {
     if (tid == 0) __hip_atomic_store(a.counters + nb, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <int XK, int KW>
+template <int XK, int STEPS, int KW, int FB>
+hipError_t launch16(const Gemv16Args& args, const GemvPlan& plan, hipStream_t stream, hipEvent_t start,
+                    hipEvent_t stop) {
+    // the staging capacity of this instantiation (the planner never exceeds it)
+    if ((int64_t)args.M * args.gps * 8 > (int64_t)stage_items16<STEPS, FB>() * KW * FB * 64 || args.gps > KW * STEPS)
+        return hipErrorInvalidValue;
+    return launch_kernel(gemv16_kernel<XK, STEPS, KW, FB>, dim3(plan.n_blocks, plan.splits), dim3(KW * FB * 64),
+                         (size_t)plan.lds_bytes, stream, start, stop, args);
+}
+
+template <int XK, int KW, int FB>
 hipError_t launch_steps16(const Gemv16Args& args, const GemvPlan& plan, hipStream_t stream, hipEvent_t start,
                           hipEvent_t stop) {
-    const dim3 grid(plan.n_blocks, plan.splits);
     switch (plan.steps) {
-        case 2: return launch_kernel(gemv16_kernel<XK, 2, KW>, grid, dim3(KW * 64), 0, stream, start, stop, args);
-        case 3: return launch_kernel(gemv16_kernel<XK, 3, KW>, grid, dim3(KW * 64), 0, stream, start, stop, args);
-        case 6: return launch_kernel(gemv16_kernel<XK, 6, KW>, grid, dim3(KW * 64), 0, stream, start, stop, args);
-        case 9: return launch_kernel(gemv16_kernel<XK, 9, KW>, grid, dim3(KW * 64), 0, stream, start, stop, args);
-        case 12: return launch_kernel(gemv16_kernel<XK, 12, KW>, grid, dim3(KW * 64), 0, stream, start, stop, args);
-        default: return launch_kernel(gemv16_kernel<XK, 18, KW>, grid, dim3(KW * 64), 0, stream, start, stop, args);
+        case 2: return launch16<XK, 2, KW, FB>(args, plan, stream, start, stop);
+        case 3: return launch16<XK, 3, KW, FB>(args, plan, stream, start, stop);
+        case 6: return launch16<XK, 6, KW, FB>(args, plan, stream, start, stop);
+        case 9: return launch16<XK, 9, KW, FB>(args, plan, stream, start, stop);
+        case 12: return launch16<XK, 12, KW, FB>(args, plan, stream, start, stop);
+        default: return launch16<XK, 18, KW, FB>(args, plan, stream, start, stop);
     }
+}
+
+template <int XK>
+hipError_t launch_shape16(const Gemv16Args& args, const GemvPlan& plan, hipStream_t stream, hipEvent_t start,
+                          hipEvent_t stop) {
+    // (KW, FB) pairs the planner produces
+    if (plan.fblocks == 1 && plan.waves == 4) return launch_steps16<XK, 4, 1>(args, plan, stream, start, stop);
+    if (plan.fblocks == 1 && plan.waves == 8) return launch_steps16<XK, 8, 1>(args, plan, stream, start, stop);
+    if (plan.fblocks == 2 && plan.waves == 2) return launch_steps16<XK, 2, 2>(args, plan, stream, start, stop);
+    if (plan.fblocks == 2 && plan.waves == 4) return launch_steps16<XK, 4, 2>(args, plan, stream, start, stop);
+    if (plan.fblocks == 4 && plan.waves == 1) return launch_steps16<XK, 1, 4>(args, plan, stream, start, stop);
+    if (plan.fblocks == 4 && plan.waves == 2) return launch_steps16<XK, 2, 4>(args, plan, stream, start, stop);
+    return hipErrorInvalidValue;
 }
 
 }  // namespace
@@ -232,11 +307,8 @@ hipError_t launch_gemv16(const LinearProblem& p, const GemvPlan& plan, void* wor
     args.splits = plan.splits;
     args.counters = (unsigned*)workspace;
     args.partials = workspace ? (float*)((char*)workspace + plan.counter_bytes) : nullptr;
-    if (p.x_kind == kF16)
-        return plan.waves == 8 ? launch_steps16<kF16, 8>(args, plan, stream, start, stop)
-                               : launch_steps16<kF16, 4>(args, plan, stream, start, stop);
-    return plan.waves == 8 ? launch_steps16<kBF16, 8>(args, plan, stream, start, stop)
-                           : launch_steps16<kBF16, 4>(args, plan, stream, start, stop);
+    if (p.x_kind == kF16) return launch_shape16<kF16>(args, plan, stream, start, stop);
+    return launch_shape16<kBF16>(args, plan, stream, start, stop);
 }
 
 }  // namespace w4g64

@@ -33,7 +33,8 @@ constexpr int64_t kGemvCounterBytes = 64 * 1024;
 constexpr int64_t kGemvMaxColumnBlocks = kGemvCounterBytes / 4;  // 1,048,576 output features
 struct GemvPlan {
     int kind;              // 0: segmented kernel (any rows); 1: 9..16-row kernel (fp16/bf16)
-    int waves;             // kind 1: waves per workgroup sharing one 16-feature block
+    int waves;             // kind 1: waves per 16-feature block (they split its K range)
+    int fblocks;           // kind 1: 16-feature blocks per workgroup
     int segments;          // K segments per wave (16 / output features per wave)
     int steps;             // group steps per lane (compile-time bucket >= groups_per_split / segments)
     int n_blocks;          // column blocks (kind 0: 4 * 16 / segments output features each; kind 1: 16)
@@ -51,6 +52,11 @@ GemvPlan plan_gemv(int64_t rows, int64_t out_features, int64_t in_features, int 
 hipError_t launch_gemv(const LinearProblem& p, const GemvPlan& plan, void* workspace, hipStream_t stream,
                        hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
 const char* gemv_kernel_name(const GemvPlan& plan, int x_kind);
+// The 9..16-row kernel's plan with its shape forced (> 0: feature blocks per
+// workgroup, waves per block, K splits) -- for tuning sweeps.  false if the
+// rows or the shape do not fit it.
+bool plan_rows16(int64_t rows, int64_t out_features, int64_t in_features, GemvPlan& plan, int force_fblocks,
+                 int force_waves, int force_splits);
 hipError_t launch_gemv16(const LinearProblem& p, const GemvPlan& plan, void* workspace, hipStream_t stream,
                          hipEvent_t start, hipEvent_t stop);
 

@@ -154,14 +154,14 @@ def test_fused_swiglu_linear_rejects_before_launch():
 def test_workspace_and_kernel_plan_queries():
     lib = _lib.load()
     # decode shapes that split K across workgroups need a workspace with the
-    # fixed 64 KiB counter area; 9..16 rows split K across the waves of one
-    # workgroup, and across workgroups only while a wave keeps > 6 group steps
-    # and fewer than 256 workgroups run (long K: 140 groups over 96 blocks -> 4
-    # splits of 35 groups); short K needs no workspace
+    # fixed 64 KiB counter area; 9..16 rows stage the K range's activations in
+    # LDS (~60 KB: at most 28 groups at 16 rows), so long K splits across
+    # workgroups (140 groups -> 5 splits of 28; 145 groups -> 6 of 25); short
+    # K needs no workspace
     assert lib.w4g64_linear_workspace_bytes(4, 1536, 8960, _lib.DTYPE_F16) > 64 * 1024
-    assert lib.w4g64_linear_workspace_bytes(16, 1536, 8960, _lib.DTYPE_F16) == 64 * 1024 + 4 * 16 * 1536 * 4
+    assert lib.w4g64_linear_workspace_bytes(16, 1536, 8960, _lib.DTYPE_F16) == 64 * 1024 + 5 * 16 * 1536 * 4
     assert lib.w4g64_linear_workspace_bytes(16, 1536, 1536, _lib.DTYPE_F16) == 0
-    assert lib.w4g64_linear_workspace_bytes(16, 40, 9280, _lib.DTYPE_BF16) == 64 * 1024 + 4 * 16 * 40 * 4
+    assert lib.w4g64_linear_workspace_bytes(16, 40, 9280, _lib.DTYPE_BF16) == 64 * 1024 + 6 * 16 * 40 * 4
     # prefill: 560 tiles of 128x256 on 512 workgroup slots (256 CUs, the default
     # when no device answers): 512 data-parallel tiles, the other 48 split in 4
     # K ranges with fp32 partials after the counter area; whole rounds need none
@@ -173,7 +173,8 @@ def test_workspace_and_kernel_plan_queries():
     assert lib.w4g64_linear_kernel_name(512, 1536, 8960, _lib.DTYPE_F32).startswith(b"gemm2_kernel<bf16 hi|lo")
     assert lib.w4g64_linear_workspace_bytes(1, 1536, 100, _lib.DTYPE_F16) == 0
     assert lib.w4g64_linear_kernel_name(1, 8960, 1536, _lib.DTYPE_F16).startswith(b"gemv_kernel<f16")
-    assert lib.w4g64_linear_kernel_name(16, 1536, 8960, _lib.DTYPE_BF16) == b"gemv16_kernel<bf16,6,8>"
+    assert lib.w4g64_linear_kernel_name(16, 1536, 8960, _lib.DTYPE_BF16) == b"gemv16_kernel<bf16,9,4,2>"
+    assert lib.w4g64_linear_kernel_name(16, 8960, 1536, _lib.DTYPE_F16) == b"gemv16_kernel<f16,3,8,1>"
     assert lib.w4g64_linear_kernel_name(16, 1536, 8960, _lib.DTYPE_F32).startswith(b"gemv_kernel<f32")
     assert lib.w4g64_linear_kernel_name(2048, 8960, 1536, _lib.DTYPE_BF16).startswith(b"gemm2_kernel<bf16")
     assert lib.w4g64_linear_kernel_name(1, 8960, 1536, 7) == b"none"

@@ -297,8 +297,10 @@ def test_ragged_shapes(rows, n, k, dtype):
 )
 @pytest.mark.parametrize("dtype", ["fp16", "bf16"])
 def test_decode_nine_to_sixteen_rows(rows, n, k, dtype):
-    """Rows 9..16 run the kernel that splits K across the waves of a workgroup;
-    k = 9280 (145 groups) also splits K across workgroups."""
+    """Rows 9..16 run the kernel that stages the activations in LDS and splits
+    K across the waves of each 16-feature block; long K (8960, 9280, and 3072
+    at 13 rows) also splits K across workgroups, and long K puts two feature
+    blocks in a workgroup (n = 40: the second block is partly past N)."""
     from qwen_int4_hip import linear_kernel_name
 
     assert linear_kernel_name(rows, n, k, torch.float16 if dtype == "fp16" else torch.bfloat16).startswith(
