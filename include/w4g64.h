@@ -50,6 +50,15 @@ extern "C" {
  * SwiGLU product of a [gate | up] bf16 row (fp32). */
 #define W4G64_DTYPE_BF16_SWIGLU 5
 
+/* Decode-step forms (1..16 rows):
+ *   W4G64_DTYPE_BF16_PLANES: activation form of w4g64_linear -- x is bf16
+ *     [3, rows, in_features], three planes whose fp32 sum (hi + mid + lo) is
+ *     the activation, as w4g64_linear_gate_up_planes writes them; y is fp32.
+ *   W4G64_DTYPE_BF16_GATE_UP: query code (w4g64_linear_workspace_bytes,
+ *     w4g64_linear_kernel_name) for w4g64_linear_gate_up_planes. */
+#define W4G64_DTYPE_BF16_PLANES 6
+#define W4G64_DTYPE_BF16_GATE_UP 7
+
 /* Version of this ABI (bumped on any signature or contract change). */
 int w4g64_abi_version(void);
 
@@ -86,6 +95,8 @@ int64_t w4g64_linear_workspace_bytes(int64_t rows, int64_t out_features, int64_t
 /* y[rows, out] = x[rows, in] @ dequant(W)^T (+ bias), fp32 accumulation,
  * stored in x's dtype.  x: fp16/bf16/fp32 contiguous row-major; bias: NONE,
  * fp16, bf16 or fp32 [out]; y: same dtype as x.  rows >= 1; in % 64 == 0.
+ * With x_dtype W4G64_DTYPE_BF16_PLANES (1..16 rows) x holds the three bf16
+ * planes of an fp32 activation and y is fp32.
  * rows <= 16 runs the decode GEMV, larger rows the MFMA GEMM.
  * Pointers must be 16-byte aligned (scales and bias: element aligned).
  * Replaces: linear_canonical_w4g64_triton (src/qwen_int4/triton_kernels.py:206-268)
@@ -119,6 +130,23 @@ int w4g64_linear_timed(const void* x, int x_dtype, const uint8_t* qweight, const
 int w4g64_linear_swiglu(const void* gate_up, const uint8_t* qweight, const uint16_t* scales, const uint8_t* zeros,
                         const void* bias, int bias_dtype, float* y, int64_t rows, int64_t out_features,
                         int64_t in_features, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Fused gate|up projection of a decode step (1..16 rows) with the SwiGLU
+ * product in its epilogue.  The weight is the two projections' rows stacked,
+ * out_features = 2 I (gate rows 0..I-1, then up rows I..2I-1); x is bf16
+ * [rows, in_features].  For every row m and i < I:
+ *   gate = bf16(x . W[i] + bias[i]),  up = bf16(x . W[I + i] + bias[I + i])
+ *   h    = silu(gate) * up in fp32, silu(v) = v / (1 + exp(-v))
+ * stored as its exact three-way bf16 split into planes bf16 [3, rows, I]
+ * (planes[0] + planes[1] + planes[2] == h; planes[0] is h truncated to bf16,
+ * planes[1] the remainder truncated, planes[2] the rest), the activation form
+ * W4G64_DTYPE_BF16_PLANES of the down projection.  Workspace: query with
+ * W4G64_DTYPE_BF16_GATE_UP.  x and qweight 16-byte aligned.
+ * Replaces: the gate/up projections and the SwiGLU product of
+ *           QwenMLP.forward (src/qwen_int4/model.py:133-135). */
+int w4g64_linear_gate_up_planes(const void* x, const uint8_t* qweight, const uint16_t* scales, const uint8_t* zeros,
+                                const void* bias, int bias_dtype, void* planes, int64_t rows, int64_t out_features,
+                                int64_t in_features, void* workspace, int64_t workspace_bytes, void* stream);
 
 /* Name of the kernel w4g64_linear launches for this problem (for profiles
  * and reports); never NULL. */

@@ -57,7 +57,7 @@ int w4g64::clear_error() {
 
 extern "C" {
 
-int w4g64_abi_version(void) { return 1; }
+int w4g64_abi_version(void) { return 2; }
 
 const char* w4g64_last_error(void) { return g_error; }
 
@@ -90,9 +90,20 @@ int w4g64_dequantize_canonical(const uint8_t* qweight, const uint16_t* scales, c
 }
 
 static bool fused_form(int x_dtype) { return x_dtype == W4G64_DTYPE_BF16_SWIGLU; }
+// decode-only forms (1..16 rows): planes input, paired gate|up output
+static bool decode_form(int x_dtype) {
+    return x_dtype == W4G64_DTYPE_BF16_PLANES || x_dtype == W4G64_DTYPE_BF16_GATE_UP;
+}
+static w4g64::GemvPlan decode_form_plan(int64_t rows, int64_t out_features, int64_t in_features, int x_dtype) {
+    return x_dtype == W4G64_DTYPE_BF16_GATE_UP ? w4g64::plan_gemv_paired(rows, out_features, in_features)
+                                               : w4g64::plan_gemv(rows, out_features, in_features, w4g64::kPlanes);
+}
 
 int64_t w4g64_linear_workspace_bytes(int64_t rows, int64_t out_features, int64_t in_features, int x_dtype) {
     if (rows <= 0 || out_features <= 0 || in_features <= 0 || in_features % 64) return 0;
+    if (decode_form(x_dtype))
+        return rows <= w4g64::kGemvMaxRows ? decode_form_plan(rows, out_features, in_features, x_dtype).workspace_bytes
+                                           : 0;
     if (fused_form(x_dtype))
         return rows <= w4g64::kGemvMaxRows
                    ? w4g64::plan_gemv(rows, out_features, in_features, x_dtype).workspace_bytes
@@ -108,6 +119,11 @@ int64_t w4g64_linear_workspace_bytes(int64_t rows, int64_t out_features, int64_t
 
 const char* w4g64_linear_kernel_name(int64_t rows, int64_t out_features, int64_t in_features, int x_dtype) {
     if (rows <= 0 || out_features <= 0 || in_features <= 0 || in_features % 64) return "none";
+    if (decode_form(x_dtype))
+        return rows <= w4g64::kGemvMaxRows
+                   ? w4g64::gemv_kernel_name(decode_form_plan(rows, out_features, in_features, x_dtype),
+                                             x_dtype == W4G64_DTYPE_BF16_GATE_UP ? w4g64::kBF16 : w4g64::kPlanes)
+                   : "none";
     if (fused_form(x_dtype))
         return rows <= w4g64::kGemvMaxRows
                    ? w4g64::gemv_kernel_name(w4g64::plan_gemv(rows, out_features, in_features, x_dtype), x_dtype)
@@ -130,8 +146,12 @@ static int check_workspace(const void* workspace, int64_t have, int64_t need) {
 static int linear_impl(const void* x, int x_dtype, const uint8_t* qweight, const uint16_t* scales,
                        const uint8_t* zeros, const void* bias, int bias_dtype, void* y, int64_t rows,
                        int64_t out_features, int64_t in_features, void* workspace, int64_t workspace_bytes, void* stream, void* start_event, void* stop_event) {
-    if (x_dtype != W4G64_DTYPE_F16 && x_dtype != W4G64_DTYPE_BF16 && x_dtype != W4G64_DTYPE_F32)
+    const bool planes = x_dtype == W4G64_DTYPE_BF16_PLANES;
+    if (x_dtype != W4G64_DTYPE_F16 && x_dtype != W4G64_DTYPE_BF16 && x_dtype != W4G64_DTYPE_F32 && !planes)
         return fail(W4G64_STATUS_INVALID_DTYPE, "activations must have dtype float16, bfloat16, or float32");
+    if (planes && rows > w4g64::kGemvMaxRows)
+        return fail(W4G64_STATUS_INVALID_VALUE, "the bf16-planes activation form takes 1..%d rows, got %lld",
+                    w4g64::kGemvMaxRows, (long long)rows);
     if (bias_dtype != W4G64_DTYPE_NONE && bias_dtype != W4G64_DTYPE_F16 && bias_dtype != W4G64_DTYPE_BF16 &&
         bias_dtype != W4G64_DTYPE_F32)
         return fail(W4G64_STATUS_INVALID_DTYPE, "bias must have dtype float16, bfloat16, or float32");
@@ -149,18 +169,19 @@ static int linear_impl(const void* x, int x_dtype, const uint8_t* qweight, const
         return fail(W4G64_STATUS_INVALID_VALUE, "x, qweight, scales, zeros and y must be non-null device pointers");
     if (!aligned(x, 16) || !aligned(qweight, 16))
         return fail(W4G64_STATUS_INVALID_VALUE, "x and qweight must be 16-byte aligned");
-    if (!aligned(y, (uintptr_t)element_bytes(x_dtype)) || !aligned(scales, 2))
+    if (!aligned(y, (uintptr_t)(planes ? 4 : element_bytes(x_dtype))) || !aligned(scales, 2))
         return fail(W4G64_STATUS_INVALID_VALUE, "y and scales must be element aligned");
     if (bias && !aligned(bias, (uintptr_t)element_bytes(bias_dtype)))
         return fail(W4G64_STATUS_INVALID_VALUE, "bias must be element aligned");
 
-    w4g64::LinearProblem p{x, x_dtype, qweight, scales, zeros, bias, bias_dtype, y, rows, out_features, in_features};
+    w4g64::LinearProblem p{x, planes ? (int)w4g64::kPlanes : x_dtype, qweight, scales, zeros, bias, bias_dtype, y, rows,
+                           out_features, in_features};
     hipStream_t s = (hipStream_t)stream;
     if (rows <= w4g64::kGemvMaxRows) {
         if (out_features > w4g64::kGemvMaxColumnBlocks * 64)
             return fail(W4G64_STATUS_UNSUPPORTED, "decode path supports at most %lld output features",
                         (long long)(w4g64::kGemvMaxColumnBlocks * 64));
-        const w4g64::GemvPlan plan = w4g64::plan_gemv(rows, out_features, in_features, x_dtype);
+        const w4g64::GemvPlan plan = w4g64::plan_gemv(rows, out_features, in_features, p.x_kind);
         if (int st = check_workspace(workspace, workspace_bytes, plan.workspace_bytes)) return st;
         return hip_status(w4g64::launch_gemv(p, plan, workspace, s, (hipEvent_t)start_event, (hipEvent_t)stop_event),
                           "gemv");
@@ -227,6 +248,27 @@ int w4g64_linear_swiglu(const void* gate_up, const uint8_t* qweight, const uint1
         return hip_status(w4g64::launch_gemm2(p, workspace, (hipStream_t)stream), "gemm");
     }
     const w4g64::GemvPlan plan = w4g64::plan_gemv(rows, out_features, in_features, w4g64::kSwiGLU);
+    if (int st = check_workspace(workspace, workspace_bytes, plan.workspace_bytes)) return st;
+    return hip_status(w4g64::launch_gemv(p, plan, workspace, (hipStream_t)stream), "gemv");
+}
+
+int w4g64_linear_gate_up_planes(const void* x, const uint8_t* qweight, const uint16_t* scales, const uint8_t* zeros,
+                                const void* bias, int bias_dtype, void* planes, int64_t rows, int64_t out_features,
+                                int64_t in_features, void* workspace, int64_t workspace_bytes, void* stream) {
+    if (int st = fused_common_checks(qweight, scales, zeros, bias, bias_dtype, planes, 2, rows, out_features,
+                                     in_features))
+        return st;
+    if (rows > w4g64::kGemvMaxRows)
+        return fail(W4G64_STATUS_INVALID_VALUE, "the paired gate|up projection takes 1..%d rows, got %lld",
+                    w4g64::kGemvMaxRows, (long long)rows);
+    if (out_features % 2)
+        return fail(W4G64_STATUS_INVALID_VALUE, "out_features must be even (gate rows then up rows), got %lld",
+                    (long long)out_features);
+    if (!x) return fail(W4G64_STATUS_INVALID_VALUE, "x must be a non-null device pointer");
+    if (!aligned(x, 16)) return fail(W4G64_STATUS_INVALID_VALUE, "x must be 16-byte aligned");
+    w4g64::LinearProblem p{x, w4g64::kBF16, qweight, scales, zeros, bias, bias_dtype, planes, rows, out_features,
+                           in_features, 1};
+    const w4g64::GemvPlan plan = w4g64::plan_gemv_paired(rows, out_features, in_features);
     if (int st = check_workspace(workspace, workspace_bytes, plan.workspace_bytes)) return st;
     return hip_status(w4g64::launch_gemv(p, plan, workspace, (hipStream_t)stream), "gemv");
 }

@@ -30,7 +30,7 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 // Activation kinds.  kSwiGLU forms the activation in the decode GEMV's
 // staging: silu(gate) * up in fp32 from a [gate | up] bf16 row (fp32 result).
-enum XKind : int { kF16 = 1, kBF16 = 2, kF32 = 3, kSwiGLU = 5 };
+enum XKind : int { kF16 = 1, kBF16 = 2, kF32 = 3, kSwiGLU = 5, kPlanes = 6 };
 
 // Slot order of the 8 values in an MFMA operand: slot p holds k = kSlotK[p].
 // (Used by host-side documentation/tests; kernels permute with v_perm.)
@@ -95,8 +95,11 @@ __device__ __forceinline__ uint16_t float_to_bf16_bits(float f) {
 }
 
 // Exact three-way split of an fp32 value into bf16 parts (hi + mid + lo == x
-// for every normal x whose parts stay normal), by truncation.
+// for every normal x whose parts stay normal), by truncation.  No FP
+// contraction here: fused into a caller's product (fma(a, b, -hi)), the first
+// remainder would belong to the unrounded a * b rather than to x.
 __device__ __forceinline__ void split3_bf16(float x, uint16_t& hi, uint16_t& mid, uint16_t& lo) {
+#pragma clang fp contract(off)
     uint32_t xb = __builtin_bit_cast(uint32_t, x);
     uint32_t hb = xb & 0xFFFF0000u;
     float r1 = x - __builtin_bit_cast(float, hb);
@@ -111,6 +114,7 @@ __device__ __forceinline__ void split3_bf16(float x, uint16_t& hi, uint16_t& mid
 // Two-way split for the GEMM (16 significant bits; the bf16 weight tile
 // carries 8): hi by truncation, lo rounded.
 __device__ __forceinline__ void split2_bf16(float x, uint16_t& hi, uint16_t& lo) {
+#pragma clang fp contract(off)
     uint32_t xb = __builtin_bit_cast(uint32_t, x);
     uint32_t hb = xb & 0xFFFF0000u;
     float r1 = x - __builtin_bit_cast(float, hb);

@@ -24,11 +24,19 @@
 //   * bf16 activations: B = 128 + n' (exact in bf16); the group result is
 //     corrected by -(136 + zero) * sum_{k in g} x[m,k] before scaling.
 //   * fp32 activations: every row is split exactly into three bf16 parts
-//     (hi + mid + lo == x) that form three virtual rows; the bf16 path runs
-//     on them and the parts are summed in fp32.
+//     (hi + mid + lo == x), staged as three planes; each group step runs the
+//     three planes through the MFMA against the same decoded weights, into
+//     one fp32 accumulator (the parts lengthen K, not the A rows, so one row
+//     still leaves 16 segments per wave).
 //   * fused activation form (decode step of the decoder layer): kSwiGLU
 //     stages silu(gate) * up (fp32, as three bf16 parts) from a [gate | up]
-//     bf16 row.
+//     bf16 row; kPlanes stages the three parts from three bf16 planes
+//     written by the paired gate|up epilogue (below), with no arithmetic.
+//   * paired epilogue (fused gate|up projection of the decoder layer, bf16):
+//     a wave's R features are R/2 gate rows i and the R/2 up rows I + i of
+//     the same i, so the wave computes h = silu(bf16(gate)) * bf16(up) in
+//     fp32 (model.py:133-135) once per value and stores its exact three-way
+//     bf16 split (hi + mid + lo == h) as three planes [3][M][I].
 //   * every wave first issues its share of the workgroup's activation loads,
 //     then every weight, scale and zero load of its steps (raw bits; decoded
 //     where the MFMA step uses them).  A wave's loads return in issue order,
@@ -72,18 +80,18 @@ struct GemvArgs {
     int G;       // K / 64
     int gps;     // groups per K split
     int splits;  // K splits across workgroups
-    int mv;      // virtual A rows (M, or 3M for fp32 input)
+    int mv;      // A rows in use (= M)
     float* partials;     // [splits][M][N]
     unsigned* counters;  // [column blocks]
+    int paired;          // paired gate|up epilogue (y = bf16 planes [3][M][N/2])
 };
 
 // Activation items (8 values each) a lane stages: M x groups-per-split x 8
-// items over the workgroup's lanes, where M <= 16 TILES / (SW parts) and
-// groups-per-split <= SW STEPS.
+// items over the workgroup's lanes, where M <= 16 TILES / SW (planes kind:
+// 3 M <= 16 TILES / SW) and groups-per-split <= SW STEPS.
 template <int XK, int STEPS, int TILES>
 constexpr int stage_items() {
-    constexpr int parts = (XK == kF32 || XK == kSwiGLU) ? 3 : 1;
-    return (TILES * STEPS + 2 * parts - 1) / (2 * parts);
+    return XK == kPlanes ? (TILES * STEPS + 5) / 6 : (TILES * STEPS + 1) / 2;
 }
 
 // Sum over the 8 lanes 8i..8i+7; every one of them gets the same bits.
@@ -94,16 +102,38 @@ __device__ __forceinline__ float sum8_lanes(float s) {
     return s;
 }
 
+// h = silu(bf16(g)) * bf16(up) in fp32 (the projections' outputs are bf16,
+// model.py:133-135; silu(x) = x / (1 + exp(-x))), stored as its exact
+// three-way bf16 split: planes [3][M][I], hi + mid + lo == h.
+__device__ __forceinline__ void store_silu_planes(void* y, int m, int i, int M, int I, float g, float up) {
+    const float gb = bf16_round(g), ub = bf16_round(up);
+    const float h = (gb / (1.0f + expf(-gb))) * ub;
+    uint16_t hi, mid, lo;
+    split3_bf16(h, hi, mid, lo);
+    uint16_t* planes = (uint16_t*)y;
+    const int64_t at = (int64_t)m * I + i, plane = (int64_t)M * I;
+    planes[at] = hi;
+    planes[plane + at] = mid;
+    planes[2 * plane + at] = lo;
+}
+
 template <int XK, int SW, int STEPS, int TILES>
 __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     __shared__ int s_last;
-    constexpr int kParts = (XK == kF32 || XK == kSwiGLU) ? 3 : 1;
-    constexpr int kOut = XK == kSwiGLU ? kF32 : XK;  // output kind
+    // fp32-class activations are staged as three bf16 planes; the fp32 and
+    // SwiGLU kinds run them along K (three MFMA pairs per group step into
+    // separate accumulators), the planes kind as A rows (virtual row p M + m,
+    // a third of the LDS reads and MFMAs per weight byte; the epilogue sums
+    // the three rows' results)
+    constexpr int kStaged = (XK == kF32 || XK == kSwiGLU || XK == kPlanes) ? 3 : 1;
+    constexpr int kParts = (XK == kF32 || XK == kSwiGLU) ? 3 : 1;  // along K
+    constexpr int kRowParts = XK == kPlanes ? 3 : 1;                // as A rows
+    constexpr int kOut = (XK == kSwiGLU || XK == kPlanes) ? kF32 : XK;  // output kind
     constexpr int R = 16 / SW;              // output features per wave
     constexpr int kBlockCols = kWaves * R;  // output features per workgroup
     constexpr int kStage = stage_items<XK, STEPS, TILES>();
-    constexpr int kVecs = (XK == kF16 || XK == kBF16) ? 1 : 2;  // 16-byte loads per item
+    constexpr int kVecs = (XK == kF16 || XK == kBF16) ? 1 : (XK == kPlanes ? 3 : 2);  // 16-byte loads per item
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -113,17 +143,32 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
     const int g0 = split * a.gps;
     const int cnt = min(a.gps, a.G - g0);  // groups in this workgroup's K range
     const int row_stride = a.gps * 64 + 8;  // 16-bit elements per staged row (+16 B pad)
-    uint16_t* xs = (uint16_t*)smem;         // [mv][row_stride], slot order
-    float* sx = (float*)(smem + (size_t)a.mv * row_stride * 2);  // [mv][gps] group sums (bf16/fp32)
-    float* red = sx + a.mv * a.gps;                               // [mv][kBlockCols][SW]
+    const int planes = kStaged * a.M;       // staged rows: part p of row m is plane row p M + m
+    uint16_t* xs = (uint16_t*)smem;         // [planes][row_stride], slot order
+    float* sx = (float*)(smem + (size_t)planes * row_stride * 2);  // [planes][gps] group sums (bf16/fp32)
+    float* red = sx + planes * a.gps;                               // [M][kBlockCols][SW]
 
     // ---- this lane's column: output feature n, segment sj ----
     const int j = lane & 15;
     const int q = lane >> 4;
     const int rj = j / SW;
     const int sj = j % SW;
-    const int n = nb * kBlockCols + wave * R + rj;
-    const bool nvalid = n < a.N;
+    // Output feature of slot (nb, wave, rj): slot order, or -- paired -- the
+    // wave's first R/2 slots are gate rows i and the last R/2 the up rows
+    // I + i of the same i (I = N / 2).
+    const int half_n = a.N >> 1;
+    auto slot_feature = [&](int slot_in_block, int& i_out) {
+        const int w = slot_in_block / R, r = slot_in_block % R;
+        if (!a.paired) {
+            i_out = nb * kBlockCols + slot_in_block;
+            return i_out;
+        }
+        i_out = (nb * kBlockCols + w * R) / 2 + r % (R / 2 > 0 ? R / 2 : 1);
+        return (r >= R / 2 ? half_n : 0) + i_out;
+    };
+    int n_i;
+    const int n = slot_feature(wave * R + rj, n_i);
+    const bool nvalid = a.paired ? n_i < half_n : n < a.N;
     const int nrow = nvalid ? n : 0;
     u32x2 wq[STEPS];
     // raw scale bits and zero bytes: decoded where used, so that issuing a
@@ -164,6 +209,11 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
             const uint16_t* gu = (const uint16_t*)a.x + (int64_t)m * 2 * a.K + kbase + 8 * c;
             v[u][0] = *(const u32x4*)gu;
             v[u][1] = *(const u32x4*)(gu + a.K);
+        } else if constexpr (XK == kPlanes) {
+            // x is [3][M][K] bf16: the hi, mid and lo parts
+#pragma unroll
+            for (int pl = 0; pl < 3; ++pl)
+                v[u][pl] = *(const u32x4*)((const uint16_t*)a.x + ((int64_t)pl * a.M + m) * a.K + kbase + 8 * c);
         } else {
             const float* src = (const float*)a.x + (int64_t)m * a.K + kbase + 8 * c;
             v[u][0] = *(const u32x4*)src;
@@ -211,6 +261,17 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
             s = sum8_lanes(s);
             *(u32x4*)(xs + m * row_stride + 8 * c) = permute_slots(v[u][0]);
             sx[m * a.gps + gl] = s;
+        } else if constexpr (XK == kPlanes) {
+#pragma unroll
+            for (int pl = 0; pl < 3; ++pl) {
+                float ps = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    ps += __builtin_bit_cast(float, v[u][pl][e] << 16) + __builtin_bit_cast(float, v[u][pl][e] & 0xFFFF0000u);
+                ps = sum8_lanes(ps);
+                *(u32x4*)(xs + (pl * a.M + m) * row_stride + 8 * c) = permute_slots(v[u][pl]);
+                sx[(pl * a.M + m) * a.gps + gl] = ps;
+            }
         } else {
             float h[8];
             if constexpr (XK == kSwiGLU) {
@@ -260,9 +321,14 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 
     // ---- 4. MFMA over the group steps ----
-    float4v acc[TILES];
+    // One accumulator per fp32 part: the bf16 path's biased codes make each
+    // part's group result a difference of two large terms, so the parts are
+    // kept apart until the end (their magnitudes differ by 2^8 and 2^16).
+    float4v acc[TILES][kParts];
 #pragma unroll
-    for (int tt = 0; tt < TILES; ++tt) acc[tt] = float4v{0.f, 0.f, 0.f, 0.f};
+    for (int tt = 0; tt < TILES; ++tt)
+#pragma unroll
+        for (int p = 0; p < kParts; ++p) acc[tt][p] = float4v{0.f, 0.f, 0.f, 0.f};
 
     // Branch-free: every LDS read is in bounds and unconditional, so the
     // reads of a step need no exec-mask branches around them.  Out-of-range
@@ -273,17 +339,20 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
     {
 #pragma unroll
         for (int t = 0; t < STEPS; ++t) {
-            // A operands of this step from LDS first (A row il = virtual row
-            // m, segment il % SW) ...
-            u16x8 a0[TILES], a1[TILES];
+            // A operands of this step from LDS first (A row il = row m,
+            // segment il % SW; one operand pair per fp32 part) ...
+            u16x8 a0[TILES][kParts], a1[TILES][kParts];
 #pragma unroll
             for (int tt = 0; tt < TILES; ++tt) {
                 const int il = 16 * tt + (lane & 15);
                 const int m = min(il / SW, a.mv - 1);
                 const int ga = min(il % SW + SW * t, cnt - 1);  // the A row's group, local to the K range
-                const uint16_t* src = xs + m * row_stride + 64 * ga + 16 * q;
-                a0[tt] = *(const u16x8*)src;
-                a1[tt] = *(const u16x8*)(src + 8);
+#pragma unroll
+                for (int p = 0; p < kParts; ++p) {
+                    const uint16_t* src = xs + (p * a.M + m) * row_stride + 64 * ga + 16 * q;
+                    a0[tt][p] = *(const u16x8*)src;
+                    a1[tt][p] = *(const u16x8*)(src + 8);
+                }
             }
             // ... then wait for this step's weight, scale and zero alone: the
             // empty asm keeps their decoding here (hoisted next to the loads,
@@ -298,37 +367,56 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
             const int glc = min(gl, cnt - 1);
 #pragma unroll
             for (int tt = 0; tt < TILES; ++tt) {
-                float4v d;
+                float4v d[kParts];
                 if constexpr (XK == kF16) {
                     const _Float16 zl = (_Float16)(1032 + zr_t);
                     const _Float16 zh = (_Float16)(72 + zr_t);
                     const half8 b0 = dequant8_f16_int(wq[t][0], half2v{zl, zl}, half2v{zh, zh});
                     const half8 b1 = dequant8_f16_int(wq[t][1], half2v{zl, zl}, half2v{zh, zh});
-                    d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a0[tt]), b0,
-                                                               float4v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                    d = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a1[tt]), b1, d, 0, 0, 0);
+                    d[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a0[tt][0]), b0,
+                                                                  float4v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    d[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, a1[tt][0]), b1, d[0], 0, 0, 0);
                 } else {
                     const bf16x8 b0 = dequant8_bf16_biased(wq[t][0]);
                     const bf16x8 b1 = dequant8_bf16_biased(wq[t][1]);
-                    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a0[tt]), b0,
-                                                                float4v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a1[tt]), b1, d, 0, 0, 0);
+#pragma unroll
+                    for (int p = 0; p < kParts; ++p) {
+                        d[p] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a0[tt][p]), b0,
+                                                                       float4v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                        d[p] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a1[tt][p]), b1, d[p], 0,
+                                                                       0, 0);
+                    }
                     // D rows i = 16 tt + 4 q + r.  The rows kept later share this
                     // lane's segment, so their group is this lane's group gl.
                     const float corr = 136.0f + (float)zr_t;
+                    if constexpr (SW >= 4) {
+                        // the lane's 4 D rows 4q..4q+3 lie in one segment block: one row mi
+                        const int mi = min((16 * tt + 4 * q) / SW, a.mv - 1);
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const int mi = min((16 * tt + 4 * q + r) / SW, a.mv - 1);
-                        d[r] = fmaf(-corr, sx[mi * a.gps + glc], d[r]);
+                        for (int p = 0; p < kParts; ++p) {
+                            const float gs = sx[(p * a.M + mi) * a.gps + glc];
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) d[p][r] = fmaf(-corr, gs, d[p][r]);
+                        }
+                    } else {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const int mi = min((16 * tt + 4 * q + r) / SW, a.mv - 1);
+#pragma unroll
+                            for (int p = 0; p < kParts; ++p)
+                                d[p][r] = fmaf(-corr, sx[(p * a.M + mi) * a.gps + glc], d[p][r]);
+                        }
                     }
                 }
 #pragma unroll
-                for (int r = 0; r < 4; ++r) acc[tt][r] = fmaf(scale, d[r], acc[tt][r]);
+                for (int p = 0; p < kParts; ++p)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc[tt][p][r] = fmaf(scale, d[p][r], acc[tt][p][r]);
             }
         }
     }
 
-    // ---- 5. epilogue (per wave): keep the block diagonal, sum segments and parts ----
+    // ---- 5. epilogue (per wave): keep the block diagonal, sum the segments ----
     // The wave writes and reads only its own features' slots of `red`; LDS
     // operations of one wave complete in order, so no barrier is needed.
 #pragma unroll
@@ -337,20 +425,43 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
         for (int r = 0; r < 4; ++r) {
             const int i = 16 * tt + 4 * q + r;
             const int m = i / SW;
-            if (i % SW == sj && m < a.mv) red[(m * kBlockCols + wave * R + rj) * SW + sj] = acc[tt][r];
+            float v = acc[tt][0][r];
+#pragma unroll
+            for (int p = 1; p < kParts; ++p) v += acc[tt][p][r];
+            if (i % SW == sj && m < a.mv) red[(m * kBlockCols + wave * R + rj) * SW + sj] = v;
         }
     }
     const int col0 = nb * kBlockCols;
+    if (a.paired && a.splits == 1) {
+        // gate and up of the same i are in this wave: h straight to the planes
+        for (int idx = lane; idx < a.M * (R / 2); idx += 64) {
+            const int m = idx / (R / 2);
+            const int c = idx - m * (R / 2);
+            int i;
+            slot_feature(wave * R + c, i);
+            if (i >= half_n) continue;
+            float g = 0.0f, up = 0.0f;
+#pragma unroll
+            for (int s = 0; s < SW; ++s) {
+                g += red[(m * kBlockCols + wave * R + c) * SW + s];
+                up += red[(m * kBlockCols + wave * R + R / 2 + c) * SW + s];
+            }
+            store_silu_planes(a.y, m, i, a.M, half_n, g + load_bias(a.bias, a.bias_kind, i),
+                              up + load_bias(a.bias, a.bias_kind, half_n + i));
+        }
+        return;
+    }
     for (int idx = lane; idx < a.M * R; idx += 64) {
         const int m = idx / R;
         const int c = wave * R + (idx - m * R);
-        const int nn = col0 + c;
-        if (nn >= a.N) continue;
+        int i;
+        const int nn = slot_feature(c, i);
+        if (a.paired ? i >= half_n : nn >= a.N) continue;
         float v = 0.0f;
 #pragma unroll
-        for (int p = 0; p < kParts; ++p)
+        for (int rp = 0; rp < kRowParts; ++rp)
 #pragma unroll
-            for (int s = 0; s < SW; ++s) v += red[((p * a.M + m) * kBlockCols + c) * SW + s];
+            for (int s = 0; s < SW; ++s) v += red[((rp * a.M + m) * kBlockCols + c) * SW + s];
         if (a.splits == 1) {
             v += load_bias(a.bias, a.bias_kind, nn);
             store_out<kOut>(a.y, (int64_t)m * a.N + nn, v);
@@ -376,17 +487,30 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
     __syncthreads();
     if (!s_last) return;
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-    for (int idx = tid; idx < a.M * kBlockCols; idx += kThreads) {
-        const int m = idx / kBlockCols;
-        const int c = idx - m * kBlockCols;
-        const int nn = col0 + c;
-        if (nn >= a.N) continue;
+    auto reduce_partials = [&](int m, int nn) {
         float v = 0.0f;
         for (int s = 0; s < a.splits; ++s)
             v += __hip_atomic_load(a.partials + ((int64_t)s * a.M + m) * a.N + nn, __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
-        v += load_bias(a.bias, a.bias_kind, nn);
-        store_out<kOut>(a.y, (int64_t)m * a.N + nn, v);
+        return v + load_bias(a.bias, a.bias_kind, nn);
+    };
+    if (a.paired) {
+        for (int idx = tid; idx < a.M * (kBlockCols / 2); idx += kThreads) {
+            const int m = idx / (kBlockCols / 2);
+            const int pc = idx - m * (kBlockCols / 2);  // pair: wave pc / (R/2), offset pc % (R/2)
+            int i;
+            slot_feature((pc / (R / 2)) * R + pc % (R / 2), i);
+            if (i >= half_n) continue;
+            store_silu_planes(a.y, m, i, a.M, half_n, reduce_partials(m, i), reduce_partials(m, half_n + i));
+        }
+    } else {
+        for (int idx = tid; idx < a.M * kBlockCols; idx += kThreads) {
+            const int m = idx / kBlockCols;
+            const int c = idx - m * kBlockCols;
+            const int nn = col0 + c;
+            if (nn >= a.N) continue;
+            store_out<kOut>(a.y, (int64_t)m * a.N + nn, reduce_partials(m, nn));
+        }
     }
     if (tid == 0) __hip_atomic_store(a.counters + nb, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -486,7 +610,8 @@ GemvPlan plan_segmented(int64_t rows, int64_t out_features, int64_t in_features,
                         int64_t min_splits) {
     GemvPlan plan{};
     const int64_t groups = in_features / 64;
-    const int64_t mv = rows * ((x_kind == kF32 || x_kind == kSwiGLU) ? 3 : 1);
+    const int64_t mv = rows * (x_kind == kPlanes ? 3 : 1);
+    const int64_t planes = rows * ((x_kind == kF32 || x_kind == kSwiGLU || x_kind == kPlanes) ? 3 : 1);
     const int64_t cols = kWaves * (16 / sw);
     plan.segments = (int)sw;
     plan.tiles = (int)((mv * sw + 15) / 16);
@@ -495,7 +620,7 @@ GemvPlan plan_segmented(int64_t rows, int64_t out_features, int64_t in_features,
     int64_t gps = (groups + splits - 1) / splits;
     // staged activations (virtual rows x split width, 16-bit), the group
     // sums and the epilogue's per-segment results
-    auto lds_for = [&](int64_t g) { return mv * (g * 64 + 8) * 2 + mv * g * 4 + mv * kWaves * 16 * 4; };
+    auto lds_for = [&](int64_t g) { return planes * (g * 64 + 8) * 2 + planes * g * 4 + mv * kWaves * 16 * 4; };
     while (lds_for(gps) > 60 * 1024 || (gps + sw - 1) / sw > kMaxSteps) {
         ++splits;
         gps = (groups + splits - 1) / splits;
@@ -524,7 +649,8 @@ GemvPlan plan_gemv(int64_t rows, int64_t out_features, int64_t in_features, int 
         plan_rows16(rows, out_features, in_features, plan, 0, 0, 0))
         return plan;
     const int64_t groups = in_features / 64;
-    const int64_t mv = rows * ((x_kind == kF32 || x_kind == kSwiGLU) ? 3 : 1);
+    const int64_t mv = rows * (x_kind == kPlanes ? 3 : 1);
+    const bool fp32_class = x_kind == kF32 || x_kind == kSwiGLU;
     // Segments: as many as fit the 16 MFMA rows (mv * SW <= 16), then fewer
     // while that still leaves >= 1024 column blocks (more features per
     // workgroup = more reuse of the staged activations).
@@ -546,7 +672,7 @@ GemvPlan plan_gemv(int64_t rows, int64_t out_features, int64_t in_features, int 
     // their activations at a higher cost per workgroup and keep the old rule
     // (the SwiGLU down projection at 1 row: 3 splits 9.9 us, 6 splits 11.2 us).
     int64_t splits = (groups + sw * kMaxSteps - 1) / (sw * kMaxSteps);
-    if (mv == rows) {
+    if (!fp32_class) {
         while (blocks_for(sw) * splits < 2 * kDeviceCUs && splits * 2 <= groups && groups >= splits * 2 * sw * 5)
             splits *= 2;
     } else {
@@ -559,15 +685,22 @@ GemvPlan plan_gemv(int64_t rows, int64_t out_features, int64_t in_features, int 
     return plan_gemv(rows, out_features, in_features, x_kind, 0, 0);
 }
 
+GemvPlan plan_gemv_paired(int64_t rows, int64_t out_features, int64_t in_features) {
+    GemvPlan plan = plan_gemv(rows, out_features, in_features, kBF16, 0, 0);
+    if (plan.kind == 1 || plan.segments > 8)
+        plan = plan_gemv(rows, out_features, in_features, kBF16, plan.kind == 1 ? 1 : 8, 0);
+    return plan;
+}
+
 const char* gemv_kernel_name(const GemvPlan& plan, int x_kind) {
     static thread_local char name[64];
-    static const char* kinds[] = {"?", "f16", "bf16", "f32", "?", "swiglu_bf16"};
+    static const char* kinds[] = {"?", "f16", "bf16", "f32", "?", "swiglu_bf16", "planes_bf16"};
     if (plan.kind == 1) {
-        snprintf(name, sizeof(name), "gemv16_kernel<%s,%d,%d,%d>", kinds[x_kind >= 1 && x_kind <= 5 ? x_kind : 0], plan.steps,
+        snprintf(name, sizeof(name), "gemv16_kernel<%s,%d,%d,%d>", kinds[x_kind >= 1 && x_kind <= 6 ? x_kind : 0], plan.steps,
                  plan.waves, plan.fblocks);
         return name;
     }
-    snprintf(name, sizeof(name), "gemv_kernel<%s,%d,%d,%d>", kinds[x_kind >= 1 && x_kind <= 5 ? x_kind : 0], plan.segments, plan.steps,
+    snprintf(name, sizeof(name), "gemv_kernel<%s,%d,%d,%d>", kinds[x_kind >= 1 && x_kind <= 6 ? x_kind : 0], plan.segments, plan.steps,
              plan.tiles);
     return name;
 }
@@ -589,7 +722,10 @@ hipError_t launch_gemv(const LinearProblem& p, const GemvPlan& plan, void* works
     args.G = (int)(p.in_features / 64);
     args.gps = plan.groups_per_split;
     args.splits = plan.splits;
-    args.mv = (int)(p.rows * (p.x_kind == kF32 || p.x_kind == kSwiGLU ? 3 : 1));
+    args.mv = (int)(p.rows * (p.x_kind == kPlanes ? 3 : 1));
+    if (plan.tiles != 1 && p.x_kind != kPlanes) return hipErrorInvalidValue;  // rows <= 16 fit one A tile
+    args.paired = p.paired;
+    if (p.paired && (p.x_kind != kBF16 || plan.segments > 8 || (p.out_features & 1))) return hipErrorInvalidValue;
     args.counters = (unsigned*)workspace;
     args.partials = workspace ? (float*)((char*)workspace + plan.counter_bytes) : nullptr;
     switch (p.x_kind) {
@@ -598,14 +734,14 @@ hipError_t launch_gemv(const LinearProblem& p, const GemvPlan& plan, void* works
         case kBF16:
             return launch_sw<kBF16, 1>(args, plan, stream, start, stop);
         case kSwiGLU:
-            if (plan.tiles == 1) return launch_sw<kSwiGLU, 1>(args, plan, stream, start, stop);
-            if (plan.tiles == 2) return launch_steps<kSwiGLU, 1, 2>(args, plan, stream, start, stop);
-            return launch_steps<kSwiGLU, 1, 3>(args, plan, stream, start, stop);
+            return launch_sw<kSwiGLU, 1>(args, plan, stream, start, stop);
+        case kPlanes:
+            // 3 rows x rows: more than 16 virtual rows only with one segment per wave
+            if (plan.tiles == 1) return launch_sw<kPlanes, 1>(args, plan, stream, start, stop);
+            if (plan.tiles == 2) return launch_steps<kPlanes, 1, 2>(args, plan, stream, start, stop);
+            return launch_steps<kPlanes, 1, 3>(args, plan, stream, start, stop);
         default:
-            // more than 16 virtual rows only occurs with one segment per wave
-            if (plan.tiles == 1) return launch_sw<kF32, 1>(args, plan, stream, start, stop);
-            if (plan.tiles == 2) return launch_steps<kF32, 1, 2>(args, plan, stream, start, stop);
-            return launch_steps<kF32, 1, 3>(args, plan, stream, start, stop);
+            return launch_sw<kF32, 1>(args, plan, stream, start, stop);
     }
 }
 

@@ -26,6 +26,8 @@ DTYPE_F16 = 1
 DTYPE_BF16 = 2
 DTYPE_F32 = 3
 DTYPE_BF16_SWIGLU = 5  # activation form of w4g64_linear_swiglu (workspace / kernel-name queries)
+DTYPE_BF16_PLANES = 6  # three bf16 planes of an fp32 activation (w4g64_linear, 1..16 rows, fp32 out)
+DTYPE_BF16_GATE_UP = 7  # workspace / kernel-name queries of w4g64_linear_gate_up_planes
 
 # (name, restype, argtypes) for every symbol include/*.h declares.
 _p, _i64, _int = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
@@ -39,6 +41,7 @@ SIGNATURES = {
     "w4g64_linear_timed": (_int, [_p, _int, _p, _p, _p, _p, _int, _p, _i64, _i64, _i64, _p, _i64, _p, _p, _p]),
     "w4g64_linear_kernel_name": (ctypes.c_char_p, [_i64, _i64, _i64, _int]),
     "w4g64_linear_swiglu": (_int, [_p, _p, _p, _p, _p, _int, _p, _i64, _i64, _i64, _p, _i64, _p]),
+    "w4g64_linear_gate_up_planes": (_int, [_p, _p, _p, _p, _p, _int, _p, _i64, _i64, _i64, _p, _i64, _p]),
     # include/qwen2_decode.h
     "qwen2_add_rmsnorm": (_int, [_p, _p, _int, _p, ctypes.c_float, _p, _p, _i64, _i64, _p]),
     "qwen2_decode_attention_workspace_bytes": (_i64, [_i64, _i64, _i64]),

@@ -9,9 +9,13 @@ Restates one cached-token pass of QwenModel / DecoderLayer
     decode_attention     rotary on q and the new k, cache write, GQA attention
     W4G64 o_proj
     add_rmsnorm          residual add of the attention output + RMSNorm
-    W4G64 gate|up        one GEMV over both projections' rows
-    W4G64 down (swiglu)  silu(gate) * up in fp32, formed in the down
-                         projection's activation staging; fp32 out
+    W4G64 gate|up        one GEMV over both projections' rows; its epilogue
+                         pairs gate row i with up row I + i and stores
+                         silu(gate) * up (fp32, model.py:133-135) as three
+                         exact bf16 planes (batches of 1..16)
+    W4G64 down           the planes as its activation (three parts along K);
+                         fp32 out (larger batches: the down projection forms
+                         the product itself from the bf16 gate|up output)
 
 The fused projections are views: ``fuse_projections`` concatenates the
 q/k/v (and gate/up) buffers of each layer once and points the modules'
@@ -122,12 +126,17 @@ class FusedDecodeStep:
         self.qkv = buf((self.heads + 2 * self.kv_heads) * self.head_dim)
         self.attended = buf(self.heads * self.head_dim)
         self.o = buf(self.hidden)
-        self.gate_up = buf(2 * self.inter)
+        # 1..16 rows: the gate|up epilogue writes silu(gate) * up as planes
+        self.paired = batch <= 16
+        if self.paired:
+            self.planes = torch.empty((3, batch, self.inter), dtype=bf16, device=device)
+        else:
+            self.gate_up = buf(2 * self.inter)
         self.down = buf(self.hidden, torch.float32)
         shapes = [(self.qkv.shape[1], self.hidden, _lib.DTYPE_BF16),
                   (self.hidden, self.heads * self.head_dim, _lib.DTYPE_BF16),
-                  (2 * self.inter, self.hidden, _lib.DTYPE_BF16),
-                  (self.hidden, self.inter, _lib.DTYPE_BF16_SWIGLU)]
+                  (2 * self.inter, self.hidden, _lib.DTYPE_BF16_GATE_UP if self.paired else _lib.DTYPE_BF16),
+                  (self.hidden, self.inter, _lib.DTYPE_BF16_PLANES if self.paired else _lib.DTYPE_BF16_SWIGLU)]
         ws = max(self.lib.w4g64_linear_workspace_bytes(batch, n, k, code) for n, k, code in shapes)
         self.workspace = torch.zeros(max(ws, 1), dtype=torch.uint8, device=device)
         aws = self.lib.qwen2_decode_attention_workspace_bytes(batch, self.kv_heads, max_length)
@@ -176,12 +185,23 @@ class FusedDecodeStep:
                          {"qweight": o_proj.qweight, "scales": o_proj.scales, "zeros": o_proj.zeros, "bias": None},
                          self.o, stream)
             self._norm(self.o, _lib.DTYPE_BF16, layer.post_attention_layernorm.weight, stream)
-            self._linear(self.normed, _lib.DTYPE_BF16, fused["gate_up"], self.gate_up, stream)
             down = layer.mlp.down_proj
-            _lib.check(self.lib.w4g64_linear_swiglu(
-                _ptr(self.gate_up), _ptr(down.qweight), _ptr(down.scales), _ptr(down.zeros), None, _lib.DTYPE_NONE,
-                _ptr(self.down), self.batch, self.hidden, self.inter, _ptr(self.workspace), self.workspace.numel(),
-                stream))
+            if self.paired:
+                gu = fused["gate_up"]
+                _lib.check(self.lib.w4g64_linear_gate_up_planes(
+                    _ptr(self.normed), _ptr(gu["qweight"]), _ptr(gu["scales"]), _ptr(gu["zeros"]), _ptr(gu["bias"]),
+                    _lib.DTYPE_NONE if gu["bias"] is None else _lib.DTYPE_BF16, _ptr(self.planes), self.batch,
+                    2 * self.inter, self.hidden, _ptr(self.workspace), self.workspace.numel(), stream))
+                _lib.check(self.lib.w4g64_linear(
+                    _ptr(self.planes), _lib.DTYPE_BF16_PLANES, _ptr(down.qweight), _ptr(down.scales),
+                    _ptr(down.zeros), None, _lib.DTYPE_NONE, _ptr(self.down), self.batch, self.hidden, self.inter,
+                    _ptr(self.workspace), self.workspace.numel(), stream))
+            else:
+                self._linear(self.normed, _lib.DTYPE_BF16, fused["gate_up"], self.gate_up, stream)
+                _lib.check(self.lib.w4g64_linear_swiglu(
+                    _ptr(self.gate_up), _ptr(down.qweight), _ptr(down.scales), _ptr(down.zeros), None,
+                    _lib.DTYPE_NONE, _ptr(self.down), self.batch, self.hidden, self.inter, _ptr(self.workspace),
+                    self.workspace.numel(), stream))
             delta, delta_code = self.down, _lib.DTYPE_F32
         self._norm(delta, delta_code, model.model.norm.weight, stream)
         if not self.hip_head:

@@ -41,7 +41,7 @@ def test_library_exports_every_declared_symbol():
     for name in declared:
         assert hasattr(lib, name), f"{name} declared in include/*.h but not exported"
     assert set(declared) == set(_lib.SIGNATURES), "ctypes signatures out of sync with the header"
-    assert lib.w4g64_abi_version() == 1
+    assert lib.w4g64_abi_version() == 2
 
 
 def test_c_layer_rejects_before_launch():
@@ -151,6 +151,37 @@ def test_fused_swiglu_linear_rejects_before_launch():
         lib.w4g64_linear_workspace_bytes(1, 1536, 8960, _lib.DTYPE_F32)
 
 
+def test_gate_up_planes_and_planes_form_reject_before_launch():
+    lib = _lib.load()
+    null = None
+    buf = ctypes.create_string_buffer(1 << 16)
+    base = (ctypes.addressof(buf) + 255) & ~255
+    p = ctypes.c_void_p(base)
+    gate_up = lib.w4g64_linear_gate_up_planes
+    # rows 1..16 only; out_features even (gate rows then up rows); x aligned; bias agreement
+    assert gate_up(p, p, p, p, null, 0, p, 17, 128, 64, null, 0, null) == _lib.STATUS_INVALID_VALUE
+    assert gate_up(p, p, p, p, null, 0, p, 0, 128, 64, null, 0, null) == _lib.STATUS_INVALID_VALUE
+    assert gate_up(p, p, p, p, null, 0, p, 1, 127, 64, null, 0, null) == _lib.STATUS_INVALID_VALUE
+    assert "even" in lib.w4g64_last_error().decode()
+    assert gate_up(ctypes.c_void_p(base + 8), p, p, p, null, 0, p, 1, 128, 64, null, 0, null) == \
+        _lib.STATUS_INVALID_VALUE
+    assert gate_up(p, p, p, p, p, 0, p, 1, 128, 64, null, 0, null) == _lib.STATUS_INVALID_VALUE
+    # the planes activation form of w4g64_linear: 1..16 rows, fp32-aligned output
+    planes = _lib.DTYPE_BF16_PLANES
+    assert lib.w4g64_linear(p, planes, p, p, p, null, 0, p, 17, 64, 64, null, 0, null) == _lib.STATUS_INVALID_VALUE
+    assert lib.w4g64_linear(p, planes, p, p, p, null, 0, ctypes.c_void_p(base + 2), 1, 64, 64, null, 0,
+                            null) == _lib.STATUS_INVALID_VALUE
+    # queries: decode rows only; the M = 1 MLP shapes need no K split (no workspace)
+    assert lib.w4g64_linear_kernel_name(1, 1536, 8960, planes) == b"gemv_kernel<planes_bf16,16,9,1>"
+    assert lib.w4g64_linear_workspace_bytes(1, 1536, 8960, planes) == 0
+    assert lib.w4g64_linear_kernel_name(1, 17920, 1536, _lib.DTYPE_BF16_GATE_UP) == b"gemv_kernel<bf16,4,6,1>"
+    assert lib.w4g64_linear_workspace_bytes(1, 17920, 1536, _lib.DTYPE_BF16_GATE_UP) == 0
+    assert lib.w4g64_linear_kernel_name(17, 1536, 8960, planes) == b"none"
+    assert lib.w4g64_linear_workspace_bytes(17, 17920, 1536, _lib.DTYPE_BF16_GATE_UP) == 0
+    # 9..16 rows pair inside the segmented kernel (one segment per wave)
+    assert lib.w4g64_linear_kernel_name(16, 17920, 1536, _lib.DTYPE_BF16_GATE_UP).startswith(b"gemv_kernel<bf16,1,")
+
+
 def test_workspace_and_kernel_plan_queries():
     lib = _lib.load()
     # decode shapes that split K across workgroups need a workspace with the
@@ -177,7 +208,7 @@ def test_workspace_and_kernel_plan_queries():
     assert lib.w4g64_linear_kernel_name(16, 8960, 1536, _lib.DTYPE_F16) == b"gemv16_kernel<f16,3,8,1>"
     assert lib.w4g64_linear_kernel_name(16, 1536, 8960, _lib.DTYPE_F32).startswith(b"gemv_kernel<f32")
     assert lib.w4g64_linear_kernel_name(2048, 8960, 1536, _lib.DTYPE_BF16).startswith(b"gemm2_kernel<bf16")
-    assert lib.w4g64_linear_kernel_name(1, 8960, 1536, 7) == b"none"
+    assert lib.w4g64_linear_kernel_name(1, 8960, 1536, 8) == b"none"
 
 
 def test_status_mapping_uses_reference_exception_types():

@@ -170,6 +170,77 @@ def test_linear_swiglu_matches_silu_then_reference_linear(rows, n, k):
     assert bool(torch.isfinite(y).all()) and _normwise(y, want) <= 1e-5
 
 
+def _split3(h):
+    """Exact three-way bf16 split of fp32 h by truncation: planes [3, ...]
+    with hi + mid + lo == h (the decomposition the GEMV kernels stage)."""
+    mask = torch.tensor(-65536, dtype=torch.int32, device=h.device)  # 0xFFFF0000
+    hi = (h.contiguous().view(torch.int32) & mask).view(torch.float32)
+    r1 = h - hi
+    mid = (r1.view(torch.int32) & mask).view(torch.float32)
+    lo = r1 - mid
+    top = lambda t: (t.view(torch.int32) >> 16).to(torch.int16).view(torch.bfloat16)
+    return torch.stack([top(hi), top(mid), top(lo)])
+
+
+@pytest.mark.parametrize("rows", [1, 4, 9, 16])
+@pytest.mark.parametrize("n,k", [(1536, 8960), (100, 128), (256, 1536)])
+def test_linear_planes_form_matches_reference_linear(rows, n, k):
+    """w4g64_linear with the bf16-planes activation form = the reference torch
+    backend's fp32 linear of the planes' sum (the oracle); the planes are the
+    exact split, so the output agrees to fp32 summation order (normwise 1e-5)."""
+    from oracle import oracle as O
+
+    lib = _lib.load()
+    g = _gen(rows * 23 + n + k)
+    h = torch.randn((rows, k), generator=g, device="cuda") * 2
+    planes = _split3(h)
+    assert torch.equal(planes.float().sum(0), h)
+    qw, sc, z = _weights(n, k, 13, asymmetric=True)
+    want = O.reference_linear_torch(h, qw, sc, z, None, out_features=n, in_features=k)
+    ws = torch.zeros(max(1, lib.w4g64_linear_workspace_bytes(rows, n, k, _lib.DTYPE_BF16_PLANES)),
+                     dtype=torch.uint8, device="cuda")
+    y = torch.empty((rows, n), dtype=torch.float32, device="cuda")
+    _lib.check(lib.w4g64_linear(_p(planes), _lib.DTYPE_BF16_PLANES, _p(qw), _p(sc), _p(z), None, 0, _p(y), rows, n,
+                                k, _p(ws), ws.numel(), _stream()))
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(y).all()) and _normwise(y, want) <= 1e-5
+
+
+@pytest.mark.parametrize("rows", [1, 4, 9, 16])
+@pytest.mark.parametrize("inter,k", [(8960, 1536), (100, 128), (72, 192)])
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_gate_up_planes_matches_reference_swiglu_product(rows, inter, k, with_bias):
+    """w4g64_linear_gate_up_planes over a stacked [gate; up] weight writes
+    h = silu(bf16(gate)) * bf16(up) (model.py:133-135) as the exact bf16
+    split of its fp32 value: the planes reassemble to h exactly, and h agrees
+    with the oracle's projections (bf16 outputs, as the reference's) followed
+    by torch's silu and product -- to the bf16 rounding of gate and up that
+    a different fp32 summation order can flip (normwise 1e-2, the GEMM bar)."""
+    from oracle import oracle as O
+
+    lib = _lib.load()
+    g = _gen(rows * 31 + inter + k)
+    x = (torch.randn((rows, k), generator=g, device="cuda")).to(torch.bfloat16)
+    gw = _weights(inter, k, 17)
+    uw = _weights(inter, k, 19, asymmetric=True)
+    qw, sc, z = (torch.cat([a.reshape(-1), b.reshape(-1)]) for a, b in zip(gw, uw))
+    sc = sc.view(2 * inter, k // 64)
+    bias = (torch.randn(2 * inter, generator=g, device="cuda") * 0.5).to(torch.bfloat16) if with_bias else None
+    ws = torch.zeros(max(1, lib.w4g64_linear_workspace_bytes(rows, 2 * inter, k, _lib.DTYPE_BF16_GATE_UP)),
+                     dtype=torch.uint8, device="cuda")
+    planes = torch.empty((3, rows, inter), dtype=torch.bfloat16, device="cuda")
+    _lib.check(lib.w4g64_linear_gate_up_planes(_p(x), _p(qw), _p(sc), _p(z), _p(bias),
+                                               _lib.DTYPE_BF16 if with_bias else _lib.DTYPE_NONE, _p(planes), rows,
+                                               2 * inter, k, _p(ws), ws.numel(), _stream()))
+    torch.cuda.synchronize()
+    h = planes.float().sum(0)
+    assert torch.equal(_split3(h), planes)
+    gate = O.reference_linear_torch(x, *gw, None if bias is None else bias[:inter], out_features=inter, in_features=k)
+    up = O.reference_linear_torch(x, *uw, None if bias is None else bias[inter:], out_features=inter, in_features=k)
+    want = torch.nn.functional.silu(gate.float()) * up.float()
+    assert bool(torch.isfinite(h).all()) and _normwise(h, want) <= 1e-2
+
+
 @pytest.mark.parametrize("rows", [17, 64, 512])
 @pytest.mark.parametrize("n,k", [(1536, 8960), (100, 128)])
 def test_linear_swiglu_gemm_rows(rows, n, k):
