@@ -171,9 +171,11 @@ def test_gate_up_planes_and_planes_form_reject_before_launch():
     assert lib.w4g64_linear(p, planes, p, p, p, null, 0, p, 17, 64, 64, null, 0, null) == _lib.STATUS_INVALID_VALUE
     assert lib.w4g64_linear(p, planes, p, p, p, null, 0, ctypes.c_void_p(base + 2), 1, 64, 64, null, 0,
                             null) == _lib.STATUS_INVALID_VALUE
-    # queries: decode rows only; the M = 1 MLP shapes need no K split (no workspace)
-    assert lib.w4g64_linear_kernel_name(1, 1536, 8960, planes) == b"gemv_kernel<planes_bf16,16,9,1>"
-    assert lib.w4g64_linear_workspace_bytes(1, 1536, 8960, planes) == 0
+    # queries: decode rows only.  The planes are 3 M virtual A rows (4 segments
+    # at M = 1), so the 1536 x 8960 down projection splits K 6 ways (fp32
+    # partials after the counter area); the paired gate|up needs no split
+    assert lib.w4g64_linear_kernel_name(1, 1536, 8960, planes) == b"gemv_kernel<planes_bf16,4,6,1>"
+    assert lib.w4g64_linear_workspace_bytes(1, 1536, 8960, planes) == 64 * 1024 + 6 * 1536 * 4
     assert lib.w4g64_linear_kernel_name(1, 17920, 1536, _lib.DTYPE_BF16_GATE_UP) == b"gemv_kernel<bf16,4,6,1>"
     assert lib.w4g64_linear_workspace_bytes(1, 17920, 1536, _lib.DTYPE_BF16_GATE_UP) == 0
     assert lib.w4g64_linear_kernel_name(17, 1536, 8960, planes) == b"none"
