@@ -148,6 +148,28 @@ int w4g64_linear_gate_up_planes(const void* x, const uint8_t* qweight, const uin
                                 const void* bias, int bias_dtype, void* planes, int64_t rows, int64_t out_features,
                                 int64_t in_features, void* workspace, int64_t workspace_bytes, void* stream);
 
+/* Decode linear (one row, bf16: batch-1 decode) with the decoder's residual add and
+ * RMSNorm formed in its activation staging:
+ *   s      = bf16(residual + bf16(delta))          (delta bf16 or fp32)
+ *   x      = bf16(bf16(s * rsqrt(mean(s^2) + eps)) * norm_weight)
+ *   y      = x @ dequant(W)^T (+ bias), bf16 [rows, out_features]
+ *            -- or, with gate_up_planes != 0, the planes of
+ *            w4g64_linear_gate_up_planes (W the stacked [gate; up] rows)
+ *   out_sum = s (bf16 [rows, in_features]; must not overlap residual).
+ * Squares are rounded before their fp32 sum (as x.pow(2)); the same
+ * arithmetic as qwen2_add_rmsnorm followed by w4g64_linear (or the gate|up
+ * planes entry).  The whole row is staged by every workgroup, so the plan
+ * must not split K (W4G64_STATUS_UNSUPPORTED otherwise); no workspace.
+ * Pointers 16-byte aligned.
+ * Replaces: RMSNorm.forward (src/qwen_int4/model.py:40-44), the residual adds
+ *           of DecoderLayer.forward (:149-154) and the linear that follows
+ *           each norm (q/k/v, model.py:70-72; gate/up, :133-135). */
+int w4g64_linear_rmsnorm(const void* residual, const void* delta, int delta_dtype, const void* norm_weight, float eps,
+                         void* out_sum, const uint8_t* qweight, const uint16_t* scales, const uint8_t* zeros,
+                         const void* bias, int bias_dtype, void* y, int gate_up_planes, int64_t rows,
+                         int64_t out_features, int64_t in_features, void* workspace, int64_t workspace_bytes,
+                         void* stream);
+
 /* Name of the kernel w4g64_linear launches for this problem (for profiles
  * and reports); never NULL. */
 const char* w4g64_linear_kernel_name(int64_t rows, int64_t out_features, int64_t in_features,

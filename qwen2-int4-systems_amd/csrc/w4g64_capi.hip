@@ -252,6 +252,46 @@ int w4g64_linear_swiglu(const void* gate_up, const uint8_t* qweight, const uint1
     return hip_status(w4g64::launch_gemv(p, plan, workspace, (hipStream_t)stream), "gemv");
 }
 
+int w4g64_linear_rmsnorm(const void* residual, const void* delta, int delta_dtype, const void* norm_weight, float eps,
+                         void* out_sum, const uint8_t* qweight, const uint16_t* scales, const uint8_t* zeros,
+                         const void* bias, int bias_dtype, void* y, int gate_up_planes, int64_t rows,
+                         int64_t out_features, int64_t in_features, void* workspace, int64_t workspace_bytes,
+                         void* stream) {
+    if (int st = fused_common_checks(qweight, scales, zeros, bias, bias_dtype, y, 2, rows, out_features, in_features))
+        return st;
+    if (rows != 1)
+        return fail(W4G64_STATUS_INVALID_VALUE, "the fused RMSNorm linear takes one row, got %lld", (long long)rows);
+    if (delta_dtype != W4G64_DTYPE_BF16 && delta_dtype != W4G64_DTYPE_F32)
+        return fail(W4G64_STATUS_INVALID_DTYPE, "delta must have dtype bfloat16 or float32");
+    if (!residual || !delta || !norm_weight || !out_sum)
+        return fail(W4G64_STATUS_INVALID_VALUE, "residual, delta, norm_weight and out_sum must be non-null");
+    if (!aligned(residual, 16) || !aligned(delta, 16) || !aligned(norm_weight, 16) || !aligned(out_sum, 16))
+        return fail(W4G64_STATUS_INVALID_VALUE, "residual, delta, norm_weight and out_sum must be 16-byte aligned");
+    const int64_t row_bytes = rows * in_features * 2;
+    const char* r0 = (const char*)residual;
+    const char* o0 = (const char*)out_sum;
+    if (o0 < r0 + row_bytes && r0 < o0 + row_bytes)
+        return fail(W4G64_STATUS_INVALID_VALUE, "out_sum must not overlap residual (every workgroup reads it)");
+    if (gate_up_planes && out_features % 2)
+        return fail(W4G64_STATUS_INVALID_VALUE, "out_features must be even (gate rows then up rows), got %lld",
+                    (long long)out_features);
+    const int kind = delta_dtype == W4G64_DTYPE_BF16 ? w4g64::kNormB : w4g64::kNormF;
+    w4g64::LinearProblem p{residual, kind, qweight, scales, zeros, bias, bias_dtype, y, rows, out_features,
+                           in_features, gate_up_planes ? 1 : 0};
+    p.norm_delta = delta;
+    p.norm_weight = (const uint16_t*)norm_weight;
+    p.norm_eps = eps;
+    p.norm_out_sum = out_sum;
+    const w4g64::GemvPlan plan = gate_up_planes ? w4g64::plan_gemv_paired(rows, out_features, in_features, kind)
+                                                : w4g64::plan_gemv(rows, out_features, in_features, kind);
+    if (plan.kind != 0 || plan.splits != 1)
+        return fail(W4G64_STATUS_UNSUPPORTED,
+                    "the fused RMSNorm linear needs the whole row in one workgroup (in_features %lld too long)",
+                    (long long)in_features);
+    if (int st = check_workspace(workspace, workspace_bytes, plan.workspace_bytes)) return st;
+    return hip_status(w4g64::launch_gemv(p, plan, workspace, (hipStream_t)stream), "gemv");
+}
+
 int w4g64_linear_gate_up_planes(const void* x, const uint8_t* qweight, const uint16_t* scales, const uint8_t* zeros,
                                 const void* bias, int bias_dtype, void* planes, int64_t rows, int64_t out_features,
                                 int64_t in_features, void* workspace, int64_t workspace_bytes, void* stream) {

@@ -30,7 +30,12 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 // Activation kinds.  kSwiGLU forms the activation in the decode GEMV's
 // staging: silu(gate) * up in fp32 from a [gate | up] bf16 row (fp32 result).
-enum XKind : int { kF16 = 1, kBF16 = 2, kF32 = 3, kSwiGLU = 5, kPlanes = 6 };
+enum XKind : int {
+    kF16 = 1, kBF16 = 2, kF32 = 3, kSwiGLU = 5, kPlanes = 6,
+    // bf16 activations formed in the decode GEMV's staging as RMSNorm(residual
+    // + delta), delta bf16 (kNormB) or fp32 (kNormF); internal kinds
+    kNormB = 7, kNormF = 8
+};
 
 // Slot order of the 8 values in an MFMA operand: slot p holds k = kSlotK[p].
 // (Used by host-side documentation/tests; kernels permute with v_perm.)

@@ -84,13 +84,20 @@ struct GemvArgs {
     float* partials;     // [splits][M][N]
     unsigned* counters;  // [column blocks]
     int paired;          // paired gate|up epilogue (y = bf16 planes [3][M][N/2])
+    // RMSNorm prologue (kNormB / kNormF): x is the residual stream
+    const void* delta;
+    const uint16_t* norm_w;
+    float eps;
+    uint16_t* out_sum;
 };
 
 // Activation items (8 values each) a lane stages: M x groups-per-split x 8
 // items over the workgroup's lanes, where M <= 16 TILES / SW (planes kind:
 // 3 M <= 16 TILES / SW) and groups-per-split <= SW STEPS.
-template <int XK, int STEPS, int TILES>
+// The RMSNorm kinds take one row: SW STEPS groups x 8 items over 256 lanes.
+template <int XK, int SW, int STEPS, int TILES>
 constexpr int stage_items() {
+    if constexpr (XK == kNormB || XK == kNormF) return (SW * STEPS + 31) / 32;
     return XK == kPlanes ? (TILES * STEPS + 5) / 6 : (TILES * STEPS + 1) / 2;
 }
 
@@ -129,11 +136,13 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
     constexpr int kStaged = (XK == kF32 || XK == kSwiGLU || XK == kPlanes) ? 3 : 1;
     constexpr int kParts = (XK == kF32 || XK == kSwiGLU) ? 3 : 1;  // along K
     constexpr int kRowParts = XK == kPlanes ? 3 : 1;                // as A rows
-    constexpr int kOut = (XK == kSwiGLU || XK == kPlanes) ? kF32 : XK;  // output kind
+    constexpr bool kNorm = XK == kNormB || XK == kNormF;
+    constexpr int kOut = (XK == kSwiGLU || XK == kPlanes) ? kF32 : (kNorm ? kBF16 : XK);  // output kind
     constexpr int R = 16 / SW;              // output features per wave
     constexpr int kBlockCols = kWaves * R;  // output features per workgroup
-    constexpr int kStage = stage_items<XK, STEPS, TILES>();
-    constexpr int kVecs = (XK == kF16 || XK == kBF16) ? 1 : (XK == kPlanes ? 3 : 2);  // 16-byte loads per item
+    constexpr int kStage = stage_items<XK, SW, STEPS, TILES>();
+    // 16-byte loads per item (norm kinds: residual, delta, norm weight)
+    constexpr int kVecs = (XK == kF16 || XK == kBF16) ? 1 : (XK == kPlanes || XK == kNormB ? 3 : (XK == kNormF ? 4 : 2));
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -214,6 +223,17 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
 #pragma unroll
             for (int pl = 0; pl < 3; ++pl)
                 v[u][pl] = *(const u32x4*)((const uint16_t*)a.x + ((int64_t)pl * a.M + m) * a.K + kbase + 8 * c);
+        } else if constexpr (kNorm) {
+            // residual (bf16), delta (bf16 or fp32), norm weight (bf16); the K range is the whole row
+            v[u][0] = *(const u32x4*)((const uint16_t*)a.x + (int64_t)m * a.K + 8 * c);
+            if constexpr (XK == kNormB) {
+                v[u][1] = *(const u32x4*)((const uint16_t*)a.delta + (int64_t)m * a.K + 8 * c);
+            } else {
+                const float* dsrc = (const float*)a.delta + (int64_t)m * a.K + 8 * c;
+                v[u][1] = *(const u32x4*)dsrc;
+                v[u][2] = *(const u32x4*)(dsrc + 4);
+            }
+            v[u][kVecs - 1] = *(const u32x4*)(a.norm_w + 8 * c);
         } else {
             const float* src = (const float*)a.x + (int64_t)m * a.K + kbase + 8 * c;
             v[u][0] = *(const u32x4*)src;
@@ -242,6 +262,79 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
 #pragma unroll
         for (int k = 0; k < kVecs; ++k) asm volatile("" : "+v"(v[u][k]));
 
+    // ---- 3a. RMSNorm prologue (model.py:40-44, residual adds :149-154) ----
+    // s = bf16(x + bf16(delta)); the activation is bf16(bf16(s * r) * w) with
+    // r = rsqrt(mean(s^2) + eps) over the whole row (squares rounded before
+    // the fp32 sum, as x.pow(2) is).  Workgroup (0, 0) stores s.
+    if constexpr (kNorm) {
+        float* nsq = red + a.mv * kBlockCols * SW;  // [M][items per row] partial sums of squares
+        float* rinv = nsq + a.M * items_per_row;    // [M]
+        const bool writer = nb == 0 && split == 0;
+#pragma unroll
+        for (int u = 0; u < kStage; ++u) {
+            const int it = kThreads * u + tid;
+            const int itc = it < total ? it : total - 8 + (tid & 7);
+            int m, c;
+            item_rc(itc, m, c);
+            float ps = 0.0f;
+            u32x4 sb;
+#pragma unroll
+            for (int e = 0; e < 8; e += 2) {
+                float sv[2];
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const uint32_t xw = v[u][0][e / 2];
+                    const float xv = bf16_bits_to_float(h ? xw >> 16 : xw & 0xFFFFu);
+                    float dv;
+                    if constexpr (XK == kNormB) {
+                        const uint32_t dw = v[u][1][e / 2];
+                        dv = bf16_bits_to_float(h ? dw >> 16 : dw & 0xFFFFu);
+                    } else {
+                        const uint32_t bits = v[u][1 + (e + h) / 4][(e + h) % 4];  // element to a scalar first
+                        dv = bf16_round(__builtin_bit_cast(float, bits));
+                    }
+                    sv[h] = bf16_round(xv + dv);
+                    ps += __fmul_rn(sv[h], sv[h]);
+                }
+                sb[e / 2] = float_to_bf16_bits(sv[0]) | ((uint32_t)float_to_bf16_bits(sv[1]) << 16);
+            }
+            v[u][0] = sb;  // s replaces the residual item
+            nsq[itc] = ps;
+            if (writer) *(u32x4*)(a.out_sum + (int64_t)m * a.K + 8 * c) = sb;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+        if (wave == 0) {
+            for (int m = 0; m < a.M; ++m) {
+                float sq = 0.0f;
+                for (int l = lane; l < items_per_row; l += 64) sq += nsq[m * items_per_row + l];
+#pragma unroll
+                for (int off = 32; off > 0; off >>= 1) sq += __shfl_xor(sq, off);
+                if (lane == 0) rinv[m] = rsqrtf(sq / (float)a.K + a.eps);
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+#pragma unroll
+        for (int u = 0; u < kStage; ++u) {
+            const int it = kThreads * u + tid;
+            int m, c;
+            item_rc(it < total ? it : total - 8 + (tid & 7), m, c);
+            const float r = rinv[m];
+            u32x4 nbits;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t sw2 = v[u][0][e], ww = v[u][kVecs - 1][e];
+                const float n0 = bf16_round(bf16_bits_to_float(sw2 & 0xFFFFu) * r) * bf16_bits_to_float(ww & 0xFFFFu);
+                const float n1 = bf16_round(bf16_bits_to_float(sw2 >> 16) * r) * bf16_bits_to_float(ww >> 16);
+                nbits[e] = float_to_bf16_bits(n0) | ((uint32_t)float_to_bf16_bits(n1) << 16);
+            }
+            v[u][0] = nbits;  // the bf16 activation item
+        }
+    }
+
     // ---- 3. activations into LDS (slot order) and group sums ----
     // The 8 items of one (row, group) sit in lanes 8i..8i+7 of one u, so a
     // group sum is a reduction over those 8 lanes, and all 8 store it.
@@ -253,7 +346,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
         const int gl = c >> 3;
         if constexpr (XK == kF16) {
             *(u32x4*)(xs + m * row_stride + 8 * c) = permute_slots(v[u][0]);
-        } else if constexpr (XK == kBF16) {
+        } else if constexpr (XK == kBF16 || kNorm) {
             float s = 0.0f;
 #pragma unroll
             for (int e = 0; e < 4; ++e)
@@ -519,7 +612,7 @@ template <int XK, int SW, int STEPS, int TILES>
 hipError_t launch_typed(const GemvArgs& args, const GemvPlan& plan, hipStream_t stream, hipEvent_t start,
                         hipEvent_t stop) {
     // the staging capacity of this instantiation (the planner never exceeds it)
-    if ((int64_t)args.M * args.gps * 8 > (int64_t)stage_items<XK, STEPS, TILES>() * kThreads) return hipErrorInvalidValue;
+    if ((int64_t)args.M * args.gps * 8 > (int64_t)stage_items<XK, SW, STEPS, TILES>() * kThreads) return hipErrorInvalidValue;
     return launch_kernel(gemv_kernel<XK, SW, STEPS, TILES>, dim3(plan.n_blocks, plan.splits), dim3(kThreads),
                          (size_t)plan.lds_bytes, stream, start, stop, args);
 }
@@ -620,7 +713,11 @@ GemvPlan plan_segmented(int64_t rows, int64_t out_features, int64_t in_features,
     int64_t gps = (groups + splits - 1) / splits;
     // staged activations (virtual rows x split width, 16-bit), the group
     // sums and the epilogue's per-segment results
-    auto lds_for = [&](int64_t g) { return planes * (g * 64 + 8) * 2 + planes * g * 4 + mv * kWaves * 16 * 4; };
+    // (norm kinds: plus the per-item partial sums of squares and the row factors)
+    const int64_t norm_extra = (x_kind == kNormB || x_kind == kNormF) ? rows * (in_features / 64) * 8 * 4 + rows * 4 : 0;
+    auto lds_for = [&](int64_t g) {
+        return planes * (g * 64 + 8) * 2 + planes * g * 4 + mv * kWaves * 16 * 4 + norm_extra;
+    };
     while (lds_for(gps) > 60 * 1024 || (gps + sw - 1) / sw > kMaxSteps) {
         ++splits;
         gps = (groups + splits - 1) / splits;
@@ -685,22 +782,23 @@ GemvPlan plan_gemv(int64_t rows, int64_t out_features, int64_t in_features, int 
     return plan_gemv(rows, out_features, in_features, x_kind, 0, 0);
 }
 
-GemvPlan plan_gemv_paired(int64_t rows, int64_t out_features, int64_t in_features) {
-    GemvPlan plan = plan_gemv(rows, out_features, in_features, kBF16, 0, 0);
+GemvPlan plan_gemv_paired(int64_t rows, int64_t out_features, int64_t in_features, int x_kind) {
+    GemvPlan plan = plan_gemv(rows, out_features, in_features, x_kind, 0, 0);
     if (plan.kind == 1 || plan.segments > 8)
-        plan = plan_gemv(rows, out_features, in_features, kBF16, plan.kind == 1 ? 1 : 8, 0);
+        plan = plan_gemv(rows, out_features, in_features, x_kind, plan.kind == 1 ? 1 : 8, 0);
     return plan;
 }
 
 const char* gemv_kernel_name(const GemvPlan& plan, int x_kind) {
     static thread_local char name[64];
-    static const char* kinds[] = {"?", "f16", "bf16", "f32", "?", "swiglu_bf16", "planes_bf16"};
+    static const char* kinds[] = {"?", "f16", "bf16", "f32", "?", "swiglu_bf16", "planes_bf16", "rmsnorm_bf16",
+                                  "rmsnorm_f32delta"};
     if (plan.kind == 1) {
-        snprintf(name, sizeof(name), "gemv16_kernel<%s,%d,%d,%d>", kinds[x_kind >= 1 && x_kind <= 6 ? x_kind : 0], plan.steps,
+        snprintf(name, sizeof(name), "gemv16_kernel<%s,%d,%d,%d>", kinds[x_kind >= 1 && x_kind <= 8 ? x_kind : 0], plan.steps,
                  plan.waves, plan.fblocks);
         return name;
     }
-    snprintf(name, sizeof(name), "gemv_kernel<%s,%d,%d,%d>", kinds[x_kind >= 1 && x_kind <= 6 ? x_kind : 0], plan.segments, plan.steps,
+    snprintf(name, sizeof(name), "gemv_kernel<%s,%d,%d,%d>", kinds[x_kind >= 1 && x_kind <= 8 ? x_kind : 0], plan.segments, plan.steps,
              plan.tiles);
     return name;
 }
@@ -725,7 +823,16 @@ hipError_t launch_gemv(const LinearProblem& p, const GemvPlan& plan, void* works
     args.mv = (int)(p.rows * (p.x_kind == kPlanes ? 3 : 1));
     if (plan.tiles != 1 && p.x_kind != kPlanes) return hipErrorInvalidValue;  // rows <= 16 fit one A tile
     args.paired = p.paired;
-    if (p.paired && (p.x_kind != kBF16 || plan.segments > 8 || (p.out_features & 1))) return hipErrorInvalidValue;
+    const bool norm = p.x_kind == kNormB || p.x_kind == kNormF;
+    if (p.paired && ((p.x_kind != kBF16 && !norm) || plan.segments > 8 || (p.out_features & 1)))
+        return hipErrorInvalidValue;
+    // the norm prologue needs the whole row in every workgroup
+    if (norm && (plan.kind != 0 || plan.splits != 1 || !p.norm_delta || !p.norm_weight || !p.norm_out_sum))
+        return hipErrorInvalidValue;
+    args.delta = p.norm_delta;
+    args.norm_w = p.norm_weight;
+    args.eps = p.norm_eps;
+    args.out_sum = (uint16_t*)p.norm_out_sum;
     args.counters = (unsigned*)workspace;
     args.partials = workspace ? (float*)((char*)workspace + plan.counter_bytes) : nullptr;
     switch (p.x_kind) {
@@ -735,6 +842,10 @@ hipError_t launch_gemv(const LinearProblem& p, const GemvPlan& plan, void* works
             return launch_sw<kBF16, 1>(args, plan, stream, start, stop);
         case kSwiGLU:
             return launch_sw<kSwiGLU, 1>(args, plan, stream, start, stop);
+        case kNormB:
+            return launch_sw<kNormB, 1>(args, plan, stream, start, stop);
+        case kNormF:
+            return launch_sw<kNormF, 1>(args, plan, stream, start, stop);
         case kPlanes:
             // 3 rows x rows: more than 16 virtual rows only with one segment per wave
             if (plan.tiles == 1) return launch_sw<kPlanes, 1>(args, plan, stream, start, stop);

@@ -21,6 +21,13 @@ struct LinearProblem {
     int64_t out_features;
     int64_t in_features;
     int paired = 0;  // decode GEMV: paired gate|up epilogue writing SiLU-product planes
+    // decode GEMV, x_kind kNormB / kNormF: x is the residual stream (bf16); the
+    // activation is RMSNorm(x + delta) (weight, eps), and x + delta (bf16) is
+    // stored to norm_out_sum by one workgroup
+    const void* norm_delta = nullptr;
+    const uint16_t* norm_weight = nullptr;
+    float norm_eps = 0.0f;
+    void* norm_out_sum = nullptr;
 };
 
 // Decode GEMV (rows <= kGemvMaxRows).
@@ -56,7 +63,7 @@ const char* gemv_kernel_name(const GemvPlan& plan, int x_kind);
 // Plan of the paired gate|up GEMV (bf16, out_features = 2 I rows: gate then
 // up): the segmented kernel with at most 8 segments, so that every wave holds
 // whole (gate, up) pairs.
-GemvPlan plan_gemv_paired(int64_t rows, int64_t out_features, int64_t in_features);
+GemvPlan plan_gemv_paired(int64_t rows, int64_t out_features, int64_t in_features, int x_kind = kBF16);
 // The 9..16-row kernel's plan with its shape forced (> 0: feature blocks per
 // workgroup, waves per block, K splits) -- for tuning sweeps.  false if the
 // rows or the shape do not fit it.

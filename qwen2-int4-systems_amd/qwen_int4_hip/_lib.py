@@ -42,6 +42,8 @@ SIGNATURES = {
     "w4g64_linear_kernel_name": (ctypes.c_char_p, [_i64, _i64, _i64, _int]),
     "w4g64_linear_swiglu": (_int, [_p, _p, _p, _p, _p, _int, _p, _i64, _i64, _i64, _p, _i64, _p]),
     "w4g64_linear_gate_up_planes": (_int, [_p, _p, _p, _p, _p, _int, _p, _i64, _i64, _i64, _p, _i64, _p]),
+    "w4g64_linear_rmsnorm": (_int, [_p, _p, _int, _p, ctypes.c_float, _p, _p, _p, _p, _p, _int, _p, _int, _i64, _i64,
+                                    _i64, _p, _i64, _p]),
     # include/qwen2_decode.h
     "qwen2_add_rmsnorm": (_int, [_p, _p, _int, _p, ctypes.c_float, _p, _p, _i64, _i64, _p]),
     "qwen2_decode_attention_workspace_bytes": (_i64, [_i64, _i64, _i64]),

@@ -1,7 +1,10 @@
 """Fused single-token decode step of the Qwen2 decoder on the HIP kernels.
 
 Restates one cached-token pass of QwenModel / DecoderLayer
-(src/qwen_int4/model.py:61-154, :169-199) as seven launches per layer:
+(src/qwen_int4/model.py:61-154, :169-199) as seven launches per layer (five
+at batch 1, where each add_rmsnorm but the first is formed in the staging of
+the linear that follows it, ``w4g64_linear_rmsnorm``, and the residual
+stream alternates between two buffers):
 
     add_rmsnorm          residual add of the previous MLP output (cast to bf16
                          first, model.py:136) + input RMSNorm
@@ -122,6 +125,10 @@ class FusedDecodeStep:
             return torch.empty((batch, cols), dtype=dtype, device=device)
 
         self.x = buf(self.hidden)          # residual stream
+        # batch 1: the norms fuse into the next linear, whose workgroups all
+        # read the residual while one writes the updated one -- a second buffer
+        self.fused_norm = batch == 1
+        self.x_alt = buf(self.hidden) if self.fused_norm else None
         self.normed = buf(self.hidden)
         self.qkv = buf((self.heads + 2 * self.kv_heads) * self.head_dim)
         self.attended = buf(self.heads * self.head_dim)
@@ -155,10 +162,20 @@ class FusedDecodeStep:
             _lib.DTYPE_NONE if bias is None else _lib.DTYPE_BF16, _ptr(y), self.batch, y.shape[1], x.shape[1],
             _ptr(self.workspace), self.workspace.numel(), stream))
 
-    def _norm(self, delta, delta_code, weight, stream) -> None:
-        _lib.check(self.lib.qwen2_add_rmsnorm(_ptr(self.x), _ptr(delta), delta_code, _ptr(weight),
-                                              ctypes.c_float(self.eps), _ptr(self.x), _ptr(self.normed),
+    def _norm_at(self, residual, delta, delta_code, weight, stream) -> None:
+        """residual <- residual + delta (in place), self.normed <- RMSNorm of it."""
+        _lib.check(self.lib.qwen2_add_rmsnorm(_ptr(residual), _ptr(delta), delta_code, _ptr(weight),
+                                              ctypes.c_float(self.eps), _ptr(residual), _ptr(self.normed),
                                               self.batch, self.hidden, stream))
+
+    def _norm_linear(self, residual, delta, delta_code, norm_weight, weights, y, planes, out_sum, stream) -> None:
+        bias = weights["bias"]
+        _lib.check(self.lib.w4g64_linear_rmsnorm(
+            _ptr(residual), _ptr(delta), delta_code, _ptr(norm_weight), ctypes.c_float(self.eps), _ptr(out_sum),
+            _ptr(weights["qweight"]), _ptr(weights["scales"]), _ptr(weights["zeros"]), _ptr(bias),
+            _lib.DTYPE_NONE if bias is None else _lib.DTYPE_BF16, _ptr(y), 1 if planes else 0, self.batch,
+            2 * self.inter if planes else y.shape[1], self.hidden, _ptr(self.workspace), self.workspace.numel(),
+            stream))
 
     def __call__(self, token_ids: torch.Tensor, position: torch.Tensor, caches,
                  next_token: torch.Tensor | None = None) -> torch.Tensor:
@@ -173,9 +190,15 @@ class FusedDecodeStep:
         cos = cos.reshape(self.batch, self.head_dim).contiguous()
         sin = sin.reshape(self.batch, self.head_dim).contiguous()
         delta, delta_code = None, _lib.DTYPE_NONE
+        cur, other = self.x, self.x_alt  # residual stream (fused norms: read cur, write other)
         for layer, fused, (k_cache, v_cache) in zip(model.model.layers, self.fused, caches):
-            self._norm(delta, delta_code, layer.input_layernorm.weight, stream)
-            self._linear(self.normed, _lib.DTYPE_BF16, fused["qkv"], self.qkv, stream)
+            if self.fused_norm and delta is not None:
+                self._norm_linear(cur, delta, delta_code, layer.input_layernorm.weight, fused["qkv"], self.qkv,
+                                  False, other, stream)
+                cur, other = other, cur
+            else:
+                self._norm_at(cur, delta, delta_code, layer.input_layernorm.weight, stream)
+                self._linear(self.normed, _lib.DTYPE_BF16, fused["qkv"], self.qkv, stream)
             _lib.check(self.lib.qwen2_decode_attention(
                 _ptr(self.qkv), _ptr(cos), _ptr(sin), _ptr(k_cache), _ptr(v_cache), _ptr(position),
                 _ptr(self.attended), self.batch, self.heads, self.kv_heads, self.head_dim, k_cache.shape[2],
@@ -184,14 +207,20 @@ class FusedDecodeStep:
             self._linear(self.attended, _lib.DTYPE_BF16,
                          {"qweight": o_proj.qweight, "scales": o_proj.scales, "zeros": o_proj.zeros, "bias": None},
                          self.o, stream)
-            self._norm(self.o, _lib.DTYPE_BF16, layer.post_attention_layernorm.weight, stream)
             down = layer.mlp.down_proj
-            if self.paired:
+            if self.fused_norm:
+                self._norm_linear(cur, self.o, _lib.DTYPE_BF16, layer.post_attention_layernorm.weight,
+                                  fused["gate_up"], self.planes, True, other, stream)
+                cur, other = other, cur
+            else:
+                self._norm_at(cur, self.o, _lib.DTYPE_BF16, layer.post_attention_layernorm.weight, stream)
+            if self.paired and not self.fused_norm:
                 gu = fused["gate_up"]
                 _lib.check(self.lib.w4g64_linear_gate_up_planes(
                     _ptr(self.normed), _ptr(gu["qweight"]), _ptr(gu["scales"]), _ptr(gu["zeros"]), _ptr(gu["bias"]),
                     _lib.DTYPE_NONE if gu["bias"] is None else _lib.DTYPE_BF16, _ptr(self.planes), self.batch,
                     2 * self.inter, self.hidden, _ptr(self.workspace), self.workspace.numel(), stream))
+            if self.paired:
                 _lib.check(self.lib.w4g64_linear(
                     _ptr(self.planes), _lib.DTYPE_BF16_PLANES, _ptr(down.qweight), _ptr(down.scales),
                     _ptr(down.zeros), None, _lib.DTYPE_NONE, _ptr(self.down), self.batch, self.hidden, self.inter,
@@ -203,7 +232,7 @@ class FusedDecodeStep:
                     _lib.DTYPE_NONE, _ptr(self.down), self.batch, self.hidden, self.inter, _ptr(self.workspace),
                     self.workspace.numel(), stream))
             delta, delta_code = self.down, _lib.DTYPE_F32
-        self._norm(delta, delta_code, model.model.norm.weight, stream)
+        self._norm_at(cur, delta, delta_code, model.model.norm.weight, stream)
         if not self.hip_head:
             logits = F.linear(self.normed, model.lm_head.weight)
             if next_token is not None:

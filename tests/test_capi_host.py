@@ -180,6 +180,21 @@ def test_gate_up_planes_and_planes_form_reject_before_launch():
     assert lib.w4g64_linear_workspace_bytes(1, 17920, 1536, _lib.DTYPE_BF16_GATE_UP) == 0
     assert lib.w4g64_linear_kernel_name(17, 1536, 8960, planes) == b"none"
     assert lib.w4g64_linear_workspace_bytes(17, 17920, 1536, _lib.DTYPE_BF16_GATE_UP) == 0
+    # the fused RMSNorm linear: one row, bf16/fp32 delta, out_sum apart from the residual, even planes rows
+    rn = lib.w4g64_linear_rmsnorm
+    f = ctypes.c_float(1e-6)
+    other = ctypes.c_void_p(base + 4096)
+    assert rn(p, p, _lib.DTYPE_BF16, p, f, other, p, p, p, null, 0, p, 0, 2, 128, 64, null, 0, null) == \
+        _lib.STATUS_INVALID_VALUE
+    assert rn(p, p, _lib.DTYPE_F16, p, f, other, p, p, p, null, 0, p, 0, 1, 128, 64, null, 0, null) == \
+        _lib.STATUS_INVALID_DTYPE
+    assert rn(p, p, _lib.DTYPE_BF16, p, f, ctypes.c_void_p(base + 64), p, p, p, null, 0, p, 0, 1, 128, 64, null, 0,
+              null) == _lib.STATUS_INVALID_VALUE
+    assert "overlap" in lib.w4g64_last_error().decode()
+    assert rn(p, p, _lib.DTYPE_F32, p, f, other, p, p, p, null, 0, p, 1, 1, 127, 64, null, 0, null) == \
+        _lib.STATUS_INVALID_VALUE
+    assert rn(p, null, _lib.DTYPE_F32, p, f, other, p, p, p, null, 0, p, 0, 1, 128, 64, null, 0, null) == \
+        _lib.STATUS_INVALID_VALUE
     # 9..16 rows pair inside the segmented kernel (one segment per wave)
     assert lib.w4g64_linear_kernel_name(16, 17920, 1536, _lib.DTYPE_BF16_GATE_UP).startswith(b"gemv_kernel<bf16,1,")
 

@@ -66,6 +66,53 @@ def test_add_rmsnorm_matches_torch(rows, hidden, delta_dtype):
     assert torch.equal(x2, want_sum)
 
 
+@pytest.mark.parametrize("delta_dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("form,n,k", [("linear", 2048, 1536), ("linear", 200, 640), ("planes", 8960, 1536),
+                                      ("planes", 72, 192)])
+def test_linear_rmsnorm_matches_norm_then_linear(delta_dtype, form, n, k):
+    """w4g64_linear_rmsnorm (one row) = qwen2_add_rmsnorm followed by the
+    plain linear (or the gate|up planes entry): the residual sum bit-exact
+    (torch's bf16 add), the activation to the norm's own bar (the fp32 sum of
+    squares runs in another order), so the outputs agree to the bf16 rounding
+    that can flip (normwise 1e-2; most outputs identical)."""
+    lib = _lib.load()
+    g = _gen(n + k + (1 if delta_dtype == torch.float32 else 0))
+    x = (torch.randn((1, k), generator=g, device="cuda") * 3).to(torch.bfloat16)
+    delta = (torch.randn((1, k), generator=g, device="cuda") * 2).to(delta_dtype)
+    norm = RMSNorm(k, 1e-6).cuda()
+    with torch.no_grad():
+        norm.weight.copy_((torch.rand(k, generator=g, device="cuda") + 0.5).to(torch.bfloat16))
+    qw, sc, z = _weights(n, k, 23, asymmetric=True)
+    bias = (torch.randn(n, generator=g, device="cuda") * 0.3).to(torch.bfloat16) if form == "linear" else None
+    dcode = _lib.DTYPE_BF16 if delta_dtype == torch.bfloat16 else _lib.DTYPE_F32
+    planes = form == "planes"
+    y = (torch.empty((3, 1, n // 2), dtype=torch.bfloat16, device="cuda") if planes
+         else torch.empty((1, n), dtype=torch.bfloat16, device="cuda"))
+    out_sum = torch.empty_like(x)
+    ws = torch.zeros(1 << 20, dtype=torch.uint8, device="cuda")
+    _lib.check(lib.w4g64_linear_rmsnorm(_p(x), _p(delta), dcode, _p(norm.weight), ctypes.c_float(1e-6), _p(out_sum),
+                                        _p(qw), _p(sc), _p(z), _p(bias), _lib.DTYPE_BF16 if bias is not None else 0,
+                                        _p(y), 1 if planes else 0, 1, n, k, _p(ws), ws.numel(), _stream()))
+    # the separate kernels
+    ref_sum, normed = torch.empty_like(x), torch.empty_like(x)
+    _lib.check(lib.qwen2_add_rmsnorm(_p(x), _p(delta), dcode, _p(norm.weight), ctypes.c_float(1e-6), _p(ref_sum),
+                                     _p(normed), 1, k, _stream()))
+    want = torch.empty_like(y)
+    if planes:
+        _lib.check(lib.w4g64_linear_gate_up_planes(_p(normed), _p(qw), _p(sc), _p(z), None, 0, _p(want), 1, n, k,
+                                                   _p(ws), ws.numel(), _stream()))
+    else:
+        _lib.check(lib.w4g64_linear(_p(normed), _lib.DTYPE_BF16, _p(qw), _p(sc), _p(z), _p(bias), _lib.DTYPE_BF16,
+                                    _p(want), 1, n, k, _p(ws), ws.numel(), _stream()))
+    torch.cuda.synchronize()
+    assert torch.equal(out_sum, x + delta.to(torch.bfloat16)) and torch.equal(out_sum, ref_sum)
+    got = y.float().sum(0) if planes else y.float()
+    ref = want.float().sum(0) if planes else want.float()
+    assert bool(torch.isfinite(got).all())
+    assert _normwise(got, ref) <= 1e-2
+    assert (got == ref).float().mean().item() >= 0.9
+
+
 def _torch_attention(qkv, cos, sin, k_cache, v_cache, pos, heads, kv_heads):
     """The module path of one cached token: rotary in bf16, cache write,
     fp32 attention over positions 0..pos (qwen_int4_hip.model, which restates
