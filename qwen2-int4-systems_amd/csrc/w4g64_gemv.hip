@@ -525,24 +525,26 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
         }
     }
     const int col0 = nb * kBlockCols;
-    if (a.paired && a.splits == 1) {
-        // gate and up of the same i are in this wave: h straight to the planes
-        for (int idx = lane; idx < a.M * (R / 2); idx += 64) {
-            const int m = idx / (R / 2);
-            const int c = idx - m * (R / 2);
-            int i;
-            slot_feature(wave * R + c, i);
-            if (i >= half_n) continue;
-            float g = 0.0f, up = 0.0f;
+    if constexpr (R >= 2) {  // paired plans keep at most 8 segments (R >= 2)
+        if (a.paired && a.splits == 1) {
+            // gate and up of the same i are in this wave: h straight to the planes
+            for (int idx = lane; idx < a.M * (R / 2); idx += 64) {
+                const int m = idx / (R / 2);
+                const int c = idx - m * (R / 2);
+                int i;
+                slot_feature(wave * R + c, i);
+                if (i >= half_n) continue;
+                float g = 0.0f, up = 0.0f;
 #pragma unroll
-            for (int s = 0; s < SW; ++s) {
-                g += red[(m * kBlockCols + wave * R + c) * SW + s];
-                up += red[(m * kBlockCols + wave * R + R / 2 + c) * SW + s];
+                for (int s = 0; s < SW; ++s) {
+                    g += red[(m * kBlockCols + wave * R + c) * SW + s];
+                    up += red[(m * kBlockCols + wave * R + R / 2 + c) * SW + s];
+                }
+                store_silu_planes(a.y, m, i, a.M, half_n, g + load_bias(a.bias, a.bias_kind, i),
+                                  up + load_bias(a.bias, a.bias_kind, half_n + i));
             }
-            store_silu_planes(a.y, m, i, a.M, half_n, g + load_bias(a.bias, a.bias_kind, i),
-                              up + load_bias(a.bias, a.bias_kind, half_n + i));
+            return;
         }
-        return;
     }
     for (int idx = lane; idx < a.M * R; idx += 64) {
         const int m = idx / R;
@@ -587,12 +589,13 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
                                    __HIP_MEMORY_SCOPE_AGENT);
         return v + load_bias(a.bias, a.bias_kind, nn);
     };
-    if (a.paired) {
+    if (a.paired && R >= 2) {
         for (int idx = tid; idx < a.M * (kBlockCols / 2); idx += kThreads) {
             const int m = idx / (kBlockCols / 2);
             const int pc = idx - m * (kBlockCols / 2);  // pair: wave pc / (R/2), offset pc % (R/2)
+            constexpr int kHalf = R >= 2 ? R / 2 : 1;
             int i;
-            slot_feature((pc / (R / 2)) * R + pc % (R / 2), i);
+            slot_feature((pc / kHalf) * R + pc % kHalf, i);
             if (i >= half_n) continue;
             store_silu_planes(a.y, m, i, a.M, half_n, reduce_partials(m, i), reduce_partials(m, half_n + i));
         }
