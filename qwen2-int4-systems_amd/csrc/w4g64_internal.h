@@ -63,7 +63,7 @@ const char* gemv_kernel_name(const GemvPlan& plan, int x_kind);
 // Plan of the paired gate|up GEMV (bf16, out_features = 2 I rows: gate then
 // up): the segmented kernel with at most 8 segments, so that every wave holds
 // whole (gate, up) pairs.
-GemvPlan plan_gemv_paired(int64_t rows, int64_t out_features, int64_t in_features, int x_kind = kBF16);
+GemvPlan plan_gemv_paired(int64_t rows, int64_t out_features, int64_t in_features, int x_kind = 2 /* bf16 */);
 // The 9..16-row kernel's plan with its shape forced (> 0: feature blocks per
 // workgroup, waves per block, K splits) -- for tuning sweeps.  false if the
 // rows or the shape do not fit it.
