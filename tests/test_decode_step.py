@@ -140,6 +140,8 @@ def _torch_attention(qkv, cos, sin, k_cache, v_cache, pos, heads, kv_heads):
     (3, 12, 2, 130, (0, 64, 127, 129)),
     (2, 8, 1, 64, (0, 31, 63)),
     (1, 4, 4, 700, (5, 699)),
+    (1, 12, 2, 2048, (1000, 2047)),  # 32 chunks merged
+    (1, 12, 2, 2200, (0, 64, 2199)),  # a partial last chunk; early positions leave most chunks empty
 ])
 def test_decode_attention_matches_torch(batch, heads, kv_heads, max_length, positions):
     lib = _lib.load()
