@@ -648,15 +648,20 @@ hipError_t launch_sw(const GemvArgs& args, const GemvPlan& plan, hipStream_t str
 }  // namespace
 
 constexpr int kRows16Buckets[] = {2, 3, 6, 9, 12, 18};  // steps of the 9..16-row kernel
+constexpr int64_t kDeviceCUs = 256;                        // MI355X compute units
 
 // 9..16 fp16/bf16 rows: fblocks 16-feature blocks per workgroup, `waves`
 // waves per block taking its K range's groups round robin; the range's
 // activations are staged in LDS (at most ~60 KB: 28 groups at 16 rows).
-// Measured at 16 rows (fp16, cold weights): K = 1536 runs best as one block
-// of 8 waves (3 steps; gate 8960x1536 8.4 us, q 1536x1536 4.2 us); K = 8960
-// as two blocks of 4 waves over the 5 K splits the LDS budget needs (down
-// 1536x8960 11.2 us).  More splits, or 8 waves over 6+ steps (133 VGPRs: one
-// such workgroup per CU, two dispatch rounds), measured slower.
+// Measured at 16 rows (fp16, cold weights, eager events): K = 1536 runs best
+// as one block of 8 waves (3 steps; q 1536x1536 4.2 us) while that leaves at
+// most two workgroups per CU; with more 16-feature blocks (gate 8960x1536:
+// 560) as three blocks of 4 waves, one 48-feature workgroup per CU that
+// stages the activations once (8.8 -> 8.0 us fp16, 9.2 -> 8.3 us bf16, 8.2 ->
+// 8.0 us at 12 rows).  K = 8960 runs as two blocks of 4 waves over the 5 K
+// splits the LDS budget needs (down 1536x8960 11.2 us).  More splits, or 8
+// waves over 6+ steps (133 VGPRs: one such workgroup per CU, two dispatch
+// rounds), measured slower.
 bool plan_rows16(int64_t rows, int64_t out_features, int64_t in_features, GemvPlan& plan, int force_fblocks,
                  int force_waves, int force_splits) {
     if (rows < 9 || rows > 16) return false;
@@ -666,10 +671,12 @@ bool plan_rows16(int64_t rows, int64_t out_features, int64_t in_features, GemvPl
     plan.segments = 1;
     plan.tiles = 1;
     const bool short_k = groups <= 48;
-    plan.fblocks = force_fblocks > 0 ? force_fblocks : (short_k ? 1 : 2);
+    const bool wide = (out_features + 15) / 16 > 2 * kDeviceCUs;  // more than two 16-feature blocks per CU
+    plan.fblocks = force_fblocks > 0 ? force_fblocks : (short_k ? (wide ? 3 : 1) : 2);
     plan.waves = force_waves > 0 ? force_waves : (plan.fblocks == 1 ? (short_k ? 8 : 4) : 4);
     const int fb = plan.fblocks, kw = plan.waves;
-    if (!((fb == 1 && (kw == 4 || kw == 8)) || (fb == 2 && (kw == 2 || kw == 4)) || (fb == 4 && (kw == 1 || kw == 2))))
+    if (!((fb == 1 && (kw == 4 || kw == 8)) || (fb == 2 && (kw == 2 || kw == 4)) || (fb == 3 && kw == 4) ||
+          (fb == 4 && (kw == 1 || kw == 2))))
         return false;
     plan.n_blocks = (int)((out_features + 16 * fb - 1) / (16 * fb));
     auto lds_for = [&](int64_t g) { return rows * (g * 64 + 8) * 2 + rows * g * 4; };
@@ -697,7 +704,6 @@ bool plan_rows16(int64_t rows, int64_t out_features, int64_t in_features, GemvPl
 }
 
 namespace {
-constexpr int64_t kDeviceCUs = 256;  // MI355X compute units
 
 // The segmented kernel's plan for `sw` segments and at least `min_splits` K
 // splits (more when a lane would need more than kMaxSteps group steps or

@@ -282,6 +282,7 @@ hipError_t launch_shape16(const Gemv16Args& args, const GemvPlan& plan, hipStrea
     if (plan.fblocks == 1 && plan.waves == 8) return launch_steps16<XK, 8, 1>(args, plan, stream, start, stop);
     if (plan.fblocks == 2 && plan.waves == 2) return launch_steps16<XK, 2, 2>(args, plan, stream, start, stop);
     if (plan.fblocks == 2 && plan.waves == 4) return launch_steps16<XK, 4, 2>(args, plan, stream, start, stop);
+    if (plan.fblocks == 3 && plan.waves == 4) return launch_steps16<XK, 4, 3>(args, plan, stream, start, stop);
     if (plan.fblocks == 4 && plan.waves == 1) return launch_steps16<XK, 1, 4>(args, plan, stream, start, stop);
     if (plan.fblocks == 4 && plan.waves == 2) return launch_steps16<XK, 2, 4>(args, plan, stream, start, stop);
     return hipErrorInvalidValue;

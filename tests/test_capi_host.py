@@ -222,7 +222,8 @@ def test_workspace_and_kernel_plan_queries():
     assert lib.w4g64_linear_workspace_bytes(1, 1536, 100, _lib.DTYPE_F16) == 0
     assert lib.w4g64_linear_kernel_name(1, 8960, 1536, _lib.DTYPE_F16).startswith(b"gemv_kernel<f16")
     assert lib.w4g64_linear_kernel_name(16, 1536, 8960, _lib.DTYPE_BF16) == b"gemv16_kernel<bf16,9,4,2>"
-    assert lib.w4g64_linear_kernel_name(16, 8960, 1536, _lib.DTYPE_F16) == b"gemv16_kernel<f16,3,8,1>"
+    assert lib.w4g64_linear_kernel_name(16, 8960, 1536, _lib.DTYPE_F16) == b"gemv16_kernel<f16,6,4,3>"
+    assert lib.w4g64_linear_kernel_name(16, 1536, 1536, _lib.DTYPE_F16) == b"gemv16_kernel<f16,3,8,1>"
     assert lib.w4g64_linear_kernel_name(16, 1536, 8960, _lib.DTYPE_F32).startswith(b"gemv_kernel<f32")
     assert lib.w4g64_linear_kernel_name(2048, 8960, 1536, _lib.DTYPE_BF16).startswith(b"gemm2_kernel<bf16")
     assert lib.w4g64_linear_kernel_name(1, 8960, 1536, 8) == b"none"

@@ -293,14 +293,16 @@ def test_ragged_shapes(rows, n, k, dtype):
 @pytest.mark.parametrize(
     ("rows", "n", "k"),
     [(9, 1536, 1536), (12, 256, 1536), (16, 8960, 1536), (16, 1536, 8960), (13, 72, 3072), (16, 40, 9280),
-     (10, 96, 64)],
+     (10, 96, 64), (9, 8200, 512)],
 )
 @pytest.mark.parametrize("dtype", ["fp16", "bf16"])
 def test_decode_nine_to_sixteen_rows(rows, n, k, dtype):
     """Rows 9..16 run the kernel that stages the activations in LDS and splits
     K across the waves of each 16-feature block; long K (8960, 9280, and 3072
     at 13 rows) also splits K across workgroups, and long K puts two feature
-    blocks in a workgroup (n = 40: the second block is partly past N)."""
+    blocks in a workgroup (n = 40: the second block is partly past N).  Short
+    K with more than 512 16-feature blocks (n = 8960, 8200) puts three blocks
+    in a workgroup, the last workgroup partly past N."""
     from qwen_int4_hip import linear_kernel_name
 
     assert linear_kernel_name(rows, n, k, torch.float16 if dtype == "fp16" else torch.bfloat16).startswith(
