@@ -858,6 +858,7 @@ hipError_t launch_gemv(const LinearProblem& p, const GemvPlan& plan, void* works
         case kPlanes:
             // 3 rows x rows: more than 16 virtual rows only with one segment per wave
             if (plan.tiles == 1) return launch_sw<kPlanes, 1>(args, plan, stream, start, stop);
+            if (plan.segments != 1 || plan.tiles > 3) return hipErrorInvalidValue;
             if (plan.tiles == 2) return launch_steps<kPlanes, 1, 2>(args, plan, stream, start, stop);
             return launch_steps<kPlanes, 1, 3>(args, plan, stream, start, stop);
         default:
