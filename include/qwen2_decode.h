@@ -63,6 +63,31 @@ int qwen2_decode_attention(const void* qkv, const void* cos, const void* sin, vo
                            int64_t num_kv_heads, int64_t head_dim, int64_t max_length, float scale,
                            void* workspace, int64_t workspace_bytes, void* stream);
 
+/* Bytes of workspace qwen2_prefill_attention needs: the rotated queries,
+ * bf16 [batch, num_heads, length, head_dim]. */
+int64_t qwen2_prefill_attention_workspace_bytes(int64_t batch, int64_t num_heads, int64_t length);
+
+/* Attention over a prompt of `length` positions per sequence.
+ *   qkv bf16 [batch * length, (num_heads + 2 num_kv_heads) * head_dim] (q | k | v
+ *     projections of every position, row b * length + i);
+ *   cos, sin bf16 [batch * length, head_dim]: the rotary factors of position i;
+ *   k_cache, v_cache bf16 [batch, num_kv_heads, max_length, head_dim].
+ * Rotates q and k as qwen2_decode_attention does, writes the rotated keys and
+ * the values at positions 0..length-1 of the caches (later positions are left
+ * alone), and writes
+ *   out[b * length + i, h * head_dim + d] =
+ *       bf16( softmax_{t <= i}(q_{h,i} . k_t * scale) . v_t[d] )
+ * with fp32 scores, softmax and sums (causal mask).  head_dim == 128,
+ * num_heads / num_kv_heads <= 8, length <= max_length; qkv, the caches and
+ * the workspace 16-byte aligned.
+ * Replaces: the rotary step, cache update and attention of
+ *           QwenAttention.forward over a prompt (src/qwen_int4/model.py:17-31,
+ *           :61-122, the causal mask of :94-120). */
+int qwen2_prefill_attention(const void* qkv, const void* cos, const void* sin, void* k_cache, void* v_cache,
+                            void* out, int64_t batch, int64_t length, int64_t num_heads, int64_t num_kv_heads,
+                            int64_t head_dim, int64_t max_length, float scale, void* workspace,
+                            int64_t workspace_bytes, void* stream);
+
 /* out[r, i] = silu(gate) * up in fp32, gate = gate_up[r, i], up = gate_up[r, I + i]
  * (bf16 inputs, the fused gate|up projection), silu(x) = x / (1 + exp(-x)).
  * Replaces: the SwiGLU product of QwenMLP.forward (src/qwen_int4/model.py:133-136). */

@@ -17,6 +17,12 @@
 //                       of a (sequence, head) to arrive merges the chunks
 //                       (rescaled by exp(m_chunk - m)) and writes bf16
 //                       (model.py:61-122).
+//   prefill_rope_kernel, prefill_attention_kernel
+//                       a prompt: rotary of every position (queries to a
+//                       workspace, keys and values into the caches), then
+//                       causal GQA attention, one workgroup per (sequence,
+//                       head, 64 query rows) over 64-key blocks staged in LDS,
+//                       online softmax (model.py:17-31, :61-122).
 //   silu_mul_kernel     silu(gate) * up in fp32 (model.py:133-136).
 //
 // The new key at position p is read by the chunk that holds p from LDS, never
@@ -436,6 +442,216 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
     if (tid == 0) __hip_atomic_store(a.counters + slot, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Reduction over the 16 lanes of a row (quad swaps, half-row and row
+// mirrors): every lane of the row ends with the row's result.
+__device__ __forceinline__ float row16_max(float v) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) v = fmaxf(v, dpp_step(v, k));
+    return v;
+}
+__device__ __forceinline__ float row16_sum(float v) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) v += dpp_step(v, k);
+    return v;
+}
+// ---- prefill: rotary + cache write, then causal GQA attention over the prompt ----
+
+struct PrefillArgs {
+    const uint16_t* qkv;  // [batch * length][(heads + 2 kv_heads) * 128]
+    const uint16_t* cos;  // [batch * length][128]
+    const uint16_t* sin;
+    uint16_t* k_cache;    // [batch][kv_heads][max_len][128]
+    uint16_t* v_cache;
+    uint16_t* qrot;       // [batch][heads][length][128] rotated queries (workspace)
+    uint16_t* out;        // [batch * length][heads * 128]
+    int length;
+    int heads;
+    int kv_heads;
+    int max_len;
+    float scale2;         // scale * log2(e): the softmax runs in base 2
+};
+
+constexpr int kPrefillBlock = 64;  // query rows per workgroup and keys per staged block
+
+// One workgroup per (sequence, position): rotated query heads into qrot, the
+// rotated key heads and the values into the caches (model.py:17-31, :76-77).
+__global__ __launch_bounds__(256) void prefill_rope_kernel(PrefillArgs a) {
+    const int row = blockIdx.x;  // b * length + i
+    const int b = row / a.length;
+    const int i = row - b * a.length;
+    const int width = (a.heads + 2 * a.kv_heads) * kHeadDim;
+    const uint16_t* src = a.qkv + (int64_t)row * width;
+    const uint16_t* cs = a.cos + (int64_t)row * kHeadDim;
+    const uint16_t* sn = a.sin + (int64_t)row * kHeadDim;
+    for (int e = threadIdx.x; e < width; e += blockDim.x) {
+        const int head = e / kHeadDim;  // query heads, then key heads, then value heads
+        const int d = e % kHeadDim;
+        if (head < a.heads) {
+            const uint16_t* vec = src + head * kHeadDim;
+            a.qrot[(((int64_t)b * a.heads + head) * a.length + i) * kHeadDim + d] =
+                float_to_bf16_bits(rope_elem(vec[d], vec[d ^ (kHeadDim / 2)], cs[d], sn[d], d));
+        } else if (head < a.heads + a.kv_heads) {
+            const uint16_t* vec = src + head * kHeadDim;
+            const int kvh = head - a.heads;
+            a.k_cache[(((int64_t)b * a.kv_heads + kvh) * a.max_len + i) * kHeadDim + d] =
+                float_to_bf16_bits(rope_elem(vec[d], vec[d ^ (kHeadDim / 2)], cs[d], sn[d], d));
+        } else {
+            const int kvh = head - a.heads - a.kv_heads;
+            a.v_cache[(((int64_t)b * a.kv_heads + kvh) * a.max_len + i) * kHeadDim + d] = src[e];
+        }
+    }
+}
+
+// One workgroup of 4 waves per (sequence, query head, block of 64 query
+// rows); wave w owns rows 16 w .. 16 w + 15 of the block.  For each key block
+// kb <= the query block (causal):
+//   staging: the 64 keys as rows [key][dim] and the values transposed
+//            [dim][key] in LDS (shared by the 4 waves);
+//   scores:  MFMA, A = the wave's rotated query rows (registers), B = keys;
+//            D[row 4 q + r][key 16 cb + j], times scale * log2(e), masked
+//            past the row's position;
+//   softmax: online per row in base 2 (running max m and sum l, earlier
+//            sums rescaled by 2^(m_old - m_new));
+//   values:  MFMA, A = probabilities (bf16 hi + lo, through LDS), B = the
+//            transposed values; D[row 4 q + r][dimension 16 cb + j].
+// Every row sees key 0 in the first block, so its running max is finite.
+__global__ __launch_bounds__(256) void prefill_attention_kernel(PrefillArgs a) {
+    __shared__ __attribute__((aligned(16))) uint16_t ks[kPrefillBlock][kRowStride];          // keys
+    __shared__ __attribute__((aligned(16))) uint16_t vt[kHeadDim][kPrefillBlock + 8];       // values^T
+    __shared__ __attribute__((aligned(16))) float pw[4][16][kPrefillBlock + 4];             // probabilities
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int mj = lane & 15;
+    const int mq = lane >> 4;
+    const int qblocks = (a.length + kPrefillBlock - 1) / kPrefillBlock;
+    const int qb = blockIdx.x % qblocks;
+    const int head = (blockIdx.x / qblocks) % a.heads;
+    const int b = blockIdx.x / (qblocks * a.heads);
+    const int kvh = head / (a.heads / a.kv_heads);
+    const int q0 = qb * kPrefillBlock + 16 * wave;  // this wave's first query row
+    const uint16_t* kc = a.k_cache + ((int64_t)b * a.kv_heads + kvh) * a.max_len * kHeadDim;
+    const uint16_t* vc = a.v_cache + ((int64_t)b * a.kv_heads + kvh) * a.max_len * kHeadDim;
+
+    // A operands: query row q0 + mj (clamped), dimensions 32 sl + 8 mq .. + 7
+    u32x4 qa[kHeadDim / 32];
+    {
+        const int qi = min(q0 + mj, a.length - 1);
+        const uint16_t* qrow = a.qrot + (((int64_t)b * a.heads + head) * a.length + qi) * kHeadDim;
+#pragma unroll
+        for (int sl = 0; sl < kHeadDim / 32; ++sl) qa[sl] = *(const u32x4*)(qrow + 32 * sl + 8 * mq);
+    }
+    float m_run[4], l_run[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        m_run[r] = -INFINITY;
+        l_run[r] = 0.0f;
+    }
+    float4v oacc[kHeadDim / 16];
+#pragma unroll
+    for (int cb = 0; cb < kHeadDim / 16; ++cb) oacc[cb] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+
+    for (int kb = 0; kb <= qb; ++kb) {
+        const int t0 = kb * kPrefillBlock;
+        // ---- stage keys and transposed values: piece e -> key e / 16, 8 dimensions 8 (e % 16) ----
+        {
+            u32x4 kr[4], vr[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int e = tid + 256 * u;
+                const int key = min(t0 + e / 16, a.length - 1);
+                kr[u] = *(const u32x4*)(kc + (int64_t)key * kHeadDim + 8 * (e % 16));
+                vr[u] = *(const u32x4*)(vc + (int64_t)key * kHeadDim + 8 * (e % 16));
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int e = tid + 256 * u;
+                const int r = e / 16, c = e % 16;
+                *(u32x4*)&ks[r][8 * c] = kr[u];
+#pragma unroll
+                for (int h = 0; h < 8; ++h) vt[8 * c + h][r] = (uint16_t)(vr[u][h / 2] >> (16 * (h & 1)));
+            }
+        }
+        __syncthreads();
+        // ---- scores ----
+        float s[4][4];
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb) {
+            float4v sacc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int sl = 0; sl < kHeadDim / 32; ++sl) {
+                const u32x4 bv = *(const u32x4*)&ks[16 * cb + mj][32 * sl + 8 * mq];
+                sacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, qa[sl]),
+                                                               __builtin_bit_cast(bf16x8, bv), sacc, 0, 0, 0);
+            }
+            const int t = t0 + 16 * cb + mj;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) s[cb][r] = t <= q0 + 4 * mq + r ? sacc[r] * a.scale2 : -INFINITY;
+        }
+        // ---- online softmax per row 4 mq + r ----
+        float alpha[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float bm = row16_max(fmaxf(fmaxf(s[0][r], s[1][r]), fmaxf(s[2][r], s[3][r])));
+            const float mn = fmaxf(m_run[r], bm);
+            alpha[r] = __builtin_amdgcn_exp2f(m_run[r] - mn);  // 2^-inf = 0 on the first block
+            float ps = 0.0f;
+#pragma unroll
+            for (int cb = 0; cb < 4; ++cb) {
+                const float p = __builtin_amdgcn_exp2f(s[cb][r] - mn);  // masked: 2^-inf = 0
+                pw[wave][4 * mq + r][16 * cb + mj] = p;
+                ps += p;
+            }
+            l_run[r] = fmaf(l_run[r], alpha[r], row16_sum(ps));
+            m_run[r] = mn;
+        }
+        // LDS operations of one wave complete in order; the fences keep the
+        // compiler from moving the reads above the writes
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+#pragma unroll
+        for (int cb = 0; cb < kHeadDim / 16; ++cb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) oacc[cb][r] *= alpha[r];
+#pragma unroll
+        for (int kh = 0; kh < kPrefillBlock / 32; ++kh) {
+            // A = probabilities of row mj, keys 32 kh + 8 mq .. + 7, as bf16 hi + lo
+            const float4v p0 = *(const float4v*)&pw[wave][mj][32 * kh + 8 * mq];
+            const float4v p1 = *(const float4v*)&pw[wave][mj][32 * kh + 8 * mq + 4];
+            u32x4 phi, plo;
+#pragma unroll
+            for (int h = 0; h < 4; ++h) {
+                const float x0 = h < 2 ? p0[2 * h] : p1[2 * h - 4];
+                const float x1 = h < 2 ? p0[2 * h + 1] : p1[2 * h - 3];
+                const uint16_t h0 = float_to_bf16_bits(x0), h1 = float_to_bf16_bits(x1);
+                const uint16_t l0 = float_to_bf16_bits(x0 - bf16_bits_to_float(h0));
+                const uint16_t l1 = float_to_bf16_bits(x1 - bf16_bits_to_float(h1));
+                phi[h] = (uint32_t)h0 | ((uint32_t)h1 << 16);
+                plo[h] = (uint32_t)l0 | ((uint32_t)l1 << 16);
+            }
+#pragma unroll
+            for (int cb = 0; cb < kHeadDim / 16; ++cb) {
+                const u32x4 bv = *(const u32x4*)&vt[16 * cb + mj][32 * kh + 8 * mq];
+                oacc[cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, phi),
+                                                                   __builtin_bit_cast(bf16x8, bv), oacc[cb], 0, 0, 0);
+                oacc[cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, plo),
+                                                                   __builtin_bit_cast(bf16x8, bv), oacc[cb], 0, 0, 0);
+            }
+        }
+        __syncthreads();  // the next block's staging overwrites ks and vt
+    }
+    // ---- out[b * length + i][head * 128 + d] = bf16(o / l) ----
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int i = q0 + 4 * mq + r;
+        if (i >= a.length) continue;
+        uint16_t* orow = a.out + ((int64_t)b * a.length + i) * a.heads * kHeadDim + head * kHeadDim;
+        const float inv = 1.0f / l_run[r];
+#pragma unroll
+        for (int cb = 0; cb < kHeadDim / 16; ++cb) orow[16 * cb + mj] = float_to_bf16_bits(oacc[cb][r] * inv);
+    }
+}
+
 __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* gate_up, float* out, int64_t total,
                                                        int inter) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -538,6 +754,59 @@ int qwen2_decode_attention(const void* qkv, const void* cos, const void* sin, vo
     args.partials = (float*)((char*)workspace + attention_counter_bytes(batch, num_kv_heads));
     hipLaunchKernelGGL(attention_kernel, dim3((unsigned)blocks), dim3(kAttnThreads), 0, (hipStream_t)stream, args);
     return launch_status(hipGetLastError(), "decode_attention");
+}
+
+int64_t qwen2_prefill_attention_workspace_bytes(int64_t batch, int64_t num_heads, int64_t length) {
+    if (batch <= 0 || num_heads <= 0 || length <= 0) return 0;
+    return batch * num_heads * length * kHeadDim * (int64_t)sizeof(uint16_t);
+}
+
+int qwen2_prefill_attention(const void* qkv, const void* cos, const void* sin, void* k_cache, void* v_cache,
+                            void* out, int64_t batch, int64_t length, int64_t num_heads, int64_t num_kv_heads,
+                            int64_t head_dim, int64_t max_length, float scale, void* workspace,
+                            int64_t workspace_bytes, void* stream) {
+    if (batch < 0 || length < 0) return set_error(W4G64_STATUS_INVALID_VALUE, "batch and length must be non-negative");
+    if (head_dim != kHeadDim)
+        return set_error(W4G64_STATUS_UNSUPPORTED, "head_dim must be %d, got %lld", kHeadDim, (long long)head_dim);
+    if (num_kv_heads <= 0 || num_heads <= 0 || num_heads % num_kv_heads != 0 ||
+        num_heads / num_kv_heads > kMaxGroup)
+        return set_error(W4G64_STATUS_INVALID_VALUE,
+                         "num_heads (%lld) must be a positive multiple of num_kv_heads (%lld), at most %d times",
+                         (long long)num_heads, (long long)num_kv_heads, kMaxGroup);
+    if (length > max_length || max_length > 0x7FFFFFFF)
+        return set_error(W4G64_STATUS_INVALID_VALUE, "length (%lld) must be at most max_length (%lld)",
+                         (long long)length, (long long)max_length);
+    if (batch == 0 || length == 0) return clear_error();
+    if (!qkv || !cos || !sin || !k_cache || !v_cache || !out)
+        return set_error(W4G64_STATUS_INVALID_VALUE, "all tensors must be non-null device pointers");
+    if (!aligned16(qkv) || !aligned16(k_cache) || !aligned16(v_cache))
+        return set_error(W4G64_STATUS_INVALID_VALUE, "qkv, k_cache and v_cache must be 16-byte aligned");
+    const int64_t need = qwen2_prefill_attention_workspace_bytes(batch, num_heads, length);
+    if (!workspace || workspace_bytes < need || !aligned16(workspace))
+        return set_error(W4G64_STATUS_WORKSPACE, "prefill attention workspace of %lld bytes (16-byte aligned) required, got %lld",
+                         (long long)need, (long long)(workspace ? workspace_bytes : 0));
+    const int64_t qblocks = (length + kPrefillBlock - 1) / kPrefillBlock;
+    if (batch * length > 0x7FFFFFFF || batch * num_heads * qblocks > 0x7FFFFFFF)
+        return set_error(W4G64_STATUS_INVALID_VALUE, "problem too large");
+    PrefillArgs args;
+    args.qkv = (const uint16_t*)qkv;
+    args.cos = (const uint16_t*)cos;
+    args.sin = (const uint16_t*)sin;
+    args.k_cache = (uint16_t*)k_cache;
+    args.v_cache = (uint16_t*)v_cache;
+    args.qrot = (uint16_t*)workspace;
+    args.out = (uint16_t*)out;
+    args.length = (int)length;
+    args.heads = (int)num_heads;
+    args.kv_heads = (int)num_kv_heads;
+    args.max_len = (int)max_length;
+    args.scale2 = scale * 1.4426950408889634f;
+    hipLaunchKernelGGL(prefill_rope_kernel, dim3((unsigned)(batch * length)), dim3(256), 0, (hipStream_t)stream, args);
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return launch_status(err, "prefill_rope");
+    hipLaunchKernelGGL(prefill_attention_kernel, dim3((unsigned)(batch * num_heads * qblocks)), dim3(256), 0,
+                       (hipStream_t)stream, args);
+    return launch_status(hipGetLastError(), "prefill_attention");
 }
 
 int qwen2_silu_mul(const void* gate_up, float* out, int64_t rows, int64_t intermediate, void* stream) {

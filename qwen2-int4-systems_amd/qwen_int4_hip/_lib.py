@@ -48,6 +48,8 @@ SIGNATURES = {
     "qwen2_add_rmsnorm": (_int, [_p, _p, _int, _p, ctypes.c_float, _p, _p, _i64, _i64, _p]),
     "qwen2_decode_attention_workspace_bytes": (_i64, [_i64, _i64, _i64]),
     "qwen2_decode_attention": (_int, [_p] * 7 + [_i64] * 5 + [ctypes.c_float, _p, _i64, _p]),
+    "qwen2_prefill_attention_workspace_bytes": (_i64, [_i64, _i64, _i64]),
+    "qwen2_prefill_attention": (_int, [_p] * 6 + [_i64] * 6 + [ctypes.c_float, _p, _i64, _p]),
     "qwen2_silu_mul": (_int, [_p, _p, _i64, _i64, _p]),
     "qwen2_lm_head_workspace_bytes": (_i64, [_i64, _i64, _i64]),
     "qwen2_lm_head": (_int, [_p, _p, _p, _p, _i64, _i64, _i64, _p, _i64, _p]),

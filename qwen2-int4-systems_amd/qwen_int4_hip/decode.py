@@ -277,8 +277,6 @@ class FusedPrefill:
         return self._workspace
 
     def __call__(self, input_ids: torch.Tensor, caches) -> torch.Tensor:
-        from .model import attend, rotate_half
-
         model, lib = self.model, self.lib
         batch, length = input_ids.shape
         rows = batch * length
@@ -298,9 +296,11 @@ class FusedPrefill:
         down = torch.empty((rows, self.hidden), dtype=torch.float32, device=device)
         positions = torch.arange(length, device=device).view(1, -1).expand(batch, length)
         cos, sin = model.model.rotary_emb(positions, bf16)
-        cos, sin = cos.unsqueeze(1), sin.unsqueeze(1)
-        allowed = torch.ones((length, length), dtype=torch.bool, device=device).tril().view(1, 1, length, length)
+        cos, sin = cos.reshape(rows, -1).contiguous(), sin.reshape(rows, -1).contiguous()
         h, kvh, d = self.heads, self.kv_heads, self.head_dim
+        attended = torch.empty((rows, h * d), dtype=bf16, device=device)
+        qrot = torch.empty(lib.qwen2_prefill_attention_workspace_bytes(batch, h, length) // 2, dtype=bf16,
+                           device=device)
 
         def linear(inp, code, w, out):
             bias = w["bias"]
@@ -318,17 +318,10 @@ class FusedPrefill:
             for layer, fused, (k_cache, v_cache) in zip(model.model.layers, self.fused, caches):
                 norm(delta, delta_code, layer.input_layernorm.weight)
                 linear(normed, _lib.DTYPE_BF16, fused["qkv"], qkv)
-                q = qkv[:, : h * d].view(batch, length, h, d).transpose(1, 2)
-                k = qkv[:, h * d:(h + kvh) * d].view(batch, length, kvh, d).transpose(1, 2)
-                v = qkv[:, (h + kvh) * d:].view(batch, length, kvh, d).transpose(1, 2)
-                q = q * cos + rotate_half(q) * sin
-                k = k * cos + rotate_half(k) * sin
-                k_cache[:, :, :length].copy_(k)
-                v_cache[:, :, :length].copy_(v)
-                group = h // kvh
-                attended = attend(q, k.repeat_interleave(group, dim=1), v.repeat_interleave(group, dim=1), allowed,
-                                  d ** -0.5)
-                attended = attended.transpose(1, 2).reshape(rows, h * d)
+                # rotary, cache update and causal attention in one call
+                _lib.check(lib.qwen2_prefill_attention(
+                    _ptr(qkv), _ptr(cos), _ptr(sin), _ptr(k_cache), _ptr(v_cache), _ptr(attended), batch, length,
+                    h, kvh, d, k_cache.shape[2], ctypes.c_float(d ** -0.5), _ptr(qrot), qrot.numel() * 2, stream))
                 op = layer.self_attn.o_proj
                 linear(attended, _lib.DTYPE_BF16, {"qweight": op.qweight, "scales": op.scales, "zeros": op.zeros,
                                                    "bias": None}, o)

@@ -102,6 +102,21 @@ def test_decode_step_entry_points_reject_before_launch():
     assert lib.qwen2_decode_attention(p, p, p, odd, p, p, p, 1, 12, 2, 128, 640, f(0.1), p, ws,
                                       null) == _lib.STATUS_INVALID_VALUE
     assert b"aligned" in lib.w4g64_last_error()
+    # prefill attention: head_dim, grouping, length vs cache, workspace, alignment
+    pws = lib.qwen2_prefill_attention_workspace_bytes(1, 12, 512)
+    assert pws == 12 * 512 * 128 * 2
+    assert lib.qwen2_prefill_attention_workspace_bytes(1, 12, 0) == 0
+    pargs = [p] * 6
+    assert lib.qwen2_prefill_attention(*pargs, 1, 512, 12, 2, 64, 640, f(0.1), p, pws, null) == _lib.STATUS_UNSUPPORTED
+    assert lib.qwen2_prefill_attention(*pargs, 1, 512, 12, 5, 128, 640, f(0.1), p, pws,
+                                       null) == _lib.STATUS_INVALID_VALUE
+    assert lib.qwen2_prefill_attention(*pargs, 1, 641, 12, 2, 128, 640, f(0.1), p, 1 << 30,
+                                       null) == _lib.STATUS_INVALID_VALUE
+    assert lib.qwen2_prefill_attention(*pargs, 1, 512, 12, 2, 128, 640, f(0.1), p, pws - 2,
+                                       null) == _lib.STATUS_WORKSPACE
+    assert lib.qwen2_prefill_attention(p, p, p, odd, p, p, 1, 512, 12, 2, 128, 640, f(0.1), p, pws,
+                                       null) == _lib.STATUS_INVALID_VALUE
+    assert lib.qwen2_prefill_attention(*pargs, 0, 512, 12, 2, 128, 640, f(0.1), null, 0, null) == _lib.STATUS_OK
     # silu_mul
     assert lib.qwen2_silu_mul(p, p, 1, 0, null) == _lib.STATUS_INVALID_VALUE
     assert lib.qwen2_silu_mul(null, p, 1, 64, null) == _lib.STATUS_INVALID_VALUE

@@ -171,6 +171,52 @@ def test_decode_attention_matches_torch(batch, heads, kv_heads, max_length, posi
             assert cos_sim.item() >= 0.99999, (pos, cos_sim.item())
 
 
+@pytest.mark.parametrize("batch,heads,kv_heads,length,max_length", [
+    (1, 12, 2, 512, 640),  # the prefill of the model's workload
+    (2, 8, 1, 100, 128),   # a partial last block; group 8
+    (3, 4, 4, 65, 70),     # one query row past a block boundary; no grouping
+    (1, 12, 2, 1, 8),      # a single position
+])
+def test_prefill_attention_matches_torch(batch, heads, kv_heads, length, max_length):
+    """Rotary, cache update and causal attention over a prompt against the
+    module path's torch restatement (rotary in bf16, fp32 attention)."""
+    lib = _lib.load()
+    g = _gen(batch * 100 + length)
+    d = 128
+    rows = batch * length
+    qkv = (torch.randn((rows, (heads + 2 * kv_heads) * d), generator=g, device="cuda") * 2).to(torch.bfloat16)
+    k_cache = torch.randn((batch, kv_heads, max_length, d), generator=g, device="cuda").to(torch.bfloat16)
+    v_cache = torch.randn((batch, kv_heads, max_length, d), generator=g, device="cuda").to(torch.bfloat16)
+    positions = torch.arange(length, device="cuda").view(1, -1).expand(batch, length)
+    cos, sin = RotaryEmbedding(d, 1_000_000.0).cuda()(positions, torch.bfloat16)
+    q = qkv[:, : heads * d].view(batch, length, heads, d).transpose(1, 2)
+    k = qkv[:, heads * d:(heads + kv_heads) * d].view(batch, length, kv_heads, d).transpose(1, 2)
+    v = qkv[:, (heads + kv_heads) * d:].view(batch, length, kv_heads, d).transpose(1, 2)
+    c, s = cos.unsqueeze(1), sin.unsqueeze(1)
+    q = q * c + rotate_half(q) * s
+    k = k * c + rotate_half(k) * s
+    want_k, want_v = k_cache.clone(), v_cache.clone()
+    want_k[:, :, :length] = k
+    want_v[:, :, :length] = v
+    allowed = torch.ones((length, length), dtype=torch.bool, device="cuda").tril().view(1, 1, length, length)
+    group = heads // kv_heads
+    want = attend(q, k.repeat_interleave(group, dim=1), v.repeat_interleave(group, dim=1), allowed, d ** -0.5)
+    want = want.transpose(1, 2).reshape(rows, heads * d)
+    out = torch.empty((rows, heads * d), dtype=torch.bfloat16, device="cuda")
+    ws = torch.empty(lib.qwen2_prefill_attention_workspace_bytes(batch, heads, length), dtype=torch.uint8,
+                     device="cuda")
+    _lib.check(lib.qwen2_prefill_attention(
+        _p(qkv), _p(cos.reshape(rows, d).contiguous()), _p(sin.reshape(rows, d).contiguous()), _p(k_cache),
+        _p(v_cache), _p(out), batch, length, heads, kv_heads, d, max_length, ctypes.c_float(d ** -0.5), _p(ws),
+        ws.numel(), _stream()))
+    torch.cuda.synchronize()
+    assert torch.equal(k_cache, want_k) and torch.equal(v_cache, want_v)  # rows past the prompt untouched
+    err = (out.float() - want.float()).abs().max().item()
+    cos_sim = torch.nn.functional.cosine_similarity(out.double().flatten(), want.double().flatten(), dim=0)
+    assert err <= 1e-2 * want.float().abs().max().item(), err
+    assert cos_sim.item() >= 0.99999, cos_sim.item()
+
+
 @pytest.mark.parametrize("rows,inter", [(1, 8960), (4, 8960), (16, 100)])
 def test_silu_mul_matches_torch(rows, inter):
     lib = _lib.load()
