@@ -247,15 +247,24 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
         // rows past `cached` re-read a valid row of this chunk and are not used
         const int cached = min(nk, pos - t0);
         constexpr int kPieces = kChunk * (kHeadDim / 8) / kAttnThreads;
+        static_assert(kPieces == 4 && kAttnThreads == 16 * (kHeadDim / 8), "value staging: 16 columns x 4 rows");
+        // keys: piece e -> row e / 16, 16-byte column e % 16 (row-major LDS
+        // stores); values: thread t takes column vc = t / 16 of the four rows
+        // 4 (t % 16) + i, so that it holds four consecutive positions of
+        // 8 dimensions for the transposed stores
+        const int vcol = tid / (kHeadDim / 8);
+        const int vrow0 = kPieces * (tid % (kHeadDim / 8));
         u32x4 kr[kPieces], vr[kPieces];
 #pragma unroll
         for (int i = 0; i < kPieces; ++i) {
             const int e = tid + kAttnThreads * i;
             const int r = min(e / (kHeadDim / 8), max(cached - 1, 0));
-            const int64_t off = cache_base + (int64_t)(t0 + r) * kHeadDim + 8 * (e % (kHeadDim / 8));
-            kr[i] = *(const u32x4*)(a.k_cache + off);
-            vr[i] = *(const u32x4*)(a.v_cache + off);
+            kr[i] = *(const u32x4*)(a.k_cache + cache_base + (int64_t)(t0 + r) * kHeadDim + 8 * (e % (kHeadDim / 8)));
+            const int rv = min(vrow0 + i, max(cached - 1, 0));
+            vr[i] = *(const u32x4*)(a.v_cache + cache_base + (int64_t)(t0 + rv) * kHeadDim + 8 * vcol);
         }
+        // the new value's 8 dimensions of column vcol (used when pos is in this chunk)
+        const u32x4 vnew8 = *(const u32x4*)(qkv + (a.heads + a.kv_heads + kvh) * kHeadDim + 8 * vcol);
 #pragma unroll
         for (int i = 0; i < kQItems; ++i) {
             const int e = tid + kAttnThreads * i;
@@ -268,20 +277,30 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
             a.k_cache[cache_base + (int64_t)pos * kHeadDim + tid] = kb;
             a.v_cache[cache_base + (int64_t)pos * kHeadDim + tid] = vx;
             ks[pos - t0][tid] = kb;
-            vt[tid][pos - t0] = vx;
         }
 #pragma unroll
         for (int i = 0; i < kPieces; ++i) {
             const int e = tid + kAttnThreads * i;
             const int r = e / (kHeadDim / 8);
             const int c = e % (kHeadDim / 8);
-            if (r < cached) {
-                *(u32x4*)&ks[r][8 * c] = kr[i];
+            if (r < cached) *(u32x4*)&ks[r][8 * c] = kr[i];
+        }
+        // values transposed, four positions per 8-byte store: cached rows,
+        // the new value at pos, zeros past pos (their probability is 0)
+        {
+            u32x4 v4[kPieces];
 #pragma unroll
-                for (int h = 0; h < 8; ++h) vt[8 * c + h][r] = (uint16_t)(vr[i][h / 2] >> (16 * (h & 1)));
-            } else if (r >= nk) {  // unattended positions: zero values (their probability is 0)
+            for (int i = 0; i < kPieces; ++i) {
+                const int r = vrow0 + i;
+                const u32x4 zero = {0u, 0u, 0u, 0u};
+                v4[i] = r < cached ? vr[i] : (t0 + r == pos ? vnew8 : zero);
+            }
 #pragma unroll
-                for (int h = 0; h < 8; ++h) vt[8 * c + h][r] = 0;
+            for (int h = 0; h < 8; ++h) {
+                const uint32_t sel = (h & 1) ? 0x07060302u : 0x05040100u;  // high or low halves
+                const uint32_t p01 = __builtin_amdgcn_perm(v4[1][h / 2], v4[0][h / 2], sel);
+                const uint32_t p23 = __builtin_amdgcn_perm(v4[3][h / 2], v4[2][h / 2], sel);
+                *(u32x2*)&vt[8 * vcol + h][vrow0] = u32x2{p01, p23};
             }
         }
         __syncthreads();
@@ -728,8 +747,8 @@ int qwen2_decode_attention(const void* qkv, const void* cos, const void* sin, vo
     if (batch == 0) return clear_error();
     if (!qkv || !cos || !sin || !k_cache || !v_cache || !position || !out)
         return set_error(W4G64_STATUS_INVALID_VALUE, "all tensors must be non-null device pointers");
-    if (!aligned16(k_cache) || !aligned16(v_cache))
-        return set_error(W4G64_STATUS_INVALID_VALUE, "k_cache and v_cache must be 16-byte aligned");
+    if (!aligned16(qkv) || !aligned16(k_cache) || !aligned16(v_cache))
+        return set_error(W4G64_STATUS_INVALID_VALUE, "qkv, k_cache and v_cache must be 16-byte aligned");
     const int64_t need = qwen2_decode_attention_workspace_bytes(batch, num_kv_heads, max_length);
     if (!workspace || workspace_bytes < need)
         return set_error(W4G64_STATUS_WORKSPACE, "attention workspace of %lld bytes required, got %lld",
