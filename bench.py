@@ -34,12 +34,17 @@ greedy tokens with a static KV cache, each decode step one HIP graph replay:
 prefill and decode tokens/s.
 
 Weights and activations are generated on the GPU with the package's own
-quantizer (the mirror of src/qwen_int4/quantization.py).  The cpu_baseline
-leg runs the CPU restatement of the reference's torch backend on the host
-cores over a bounded sample of the decode steps, and checks every decode
-output and the rows-2048 GEMM outputs of this run against it (normwise
-relative error <= 1e-2, as the reference harness checks parity:
-scripts/autotune_phase_e_triton_v6.py:96-113).
+quantizer (the mirror of src/qwen_int4/quantization.py).  Protocol (the
+reference harness's: scripts/autotune_phase_e_triton_v6.py:41-56, :96-113;
+scripts/benchmark_phase_f_model.py:33-50): parity first -- every decode output
+and the rows-2048 GEMM outputs of this run are checked against the CPU
+restatement of the reference's torch backend (normwise relative error <=
+1e-2) before anything is timed, on every run; then warm-up, the timed steps,
+and medians and 95th percentiles over >= 100 samples per decode shape, per
+decode step, per GEMM shape, and p50/p95 for the end-to-end prefill and
+decode tokens.  The cpu_baseline leg times the same CPU restatement on the
+host cores over a bounded sample of the decode steps, and the single
+q_proj 1536x1536 call at M = 1 on its own.
 
 HBM traffic (roofline "traffic"): `--profile-pass` runs, untimed, a
 calibration kernel of exactly known traffic (the unpack kernel: reads P bytes,
@@ -249,6 +254,23 @@ def graph_kernel_durations(cases, reps, hip, torch, launches: int = 32):
     return durations
 
 
+def replay_samples(run, reps: int, hip, torch):
+    """Durations (ms) of `reps` calls of run(i), each between two HIP events
+    recorded on the current stream (where graph replays launch)."""
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    events = [(hip.event(), hip.event()) for _ in range(reps)]
+    for i, (a, b) in enumerate(events):
+        hip.record(a, stream)
+        run(i)
+        hip.record(b, stream)
+    torch.cuda.synchronize()
+    out = [hip.elapsed_ms(a, b) for a, b in events]
+    for a, b in events:
+        hip.lib.hipEventDestroy(a)
+        hip.lib.hipEventDestroy(b)
+    return out
+
+
 def dense_library_gemm_ms(cases, torch, reps: int = 12):
     """Median time (ms) of torch.matmul on each case's bf16 activations with a
     dense bf16 [K, N] weight of the same shape: the vendor GEMM library's rate
@@ -274,21 +296,38 @@ def dense_library_gemm_ms(cases, torch, reps: int = 12):
 # CPU baseline (and the parity check against it)
 # ---------------------------------------------------------------------------
 
-def cpu_baseline(decode, gemm, torch, budget_s: float = 12.0):
-    """The reference's torch backend restated on CPU (the oracle's port), timed
-    on host cores over a bounded sample of decode steps; every decode output
-    and the rows-2048 GEMM outputs of this run are checked against it."""
+def host_threads() -> int:
+    """CPUs this process may run on (os.cpu_count() counts the whole machine,
+    which on a shared host can exceed the process's CPU set)."""
+    try:
+        return len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        return os.cpu_count() or 1
+
+
+def cpu_model_name() -> str:
+    name = platform.processor() or "unknown"
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return name
+
+
+def cpu_parity(decode, gemm, torch):
+    """The cpu_baseline leg's checker, run before any timed region: every
+    decode output and the rows-2048 GEMM outputs of this run against the
+    CPU restatement of the reference's torch backend (backends.py:73-98),
+    normwise relative error <= 1e-2 -- the reference harness checks parity
+    before it times (scripts/autotune_phase_e_triton_v6.py:96-101)."""
     from oracle import oracle as O
 
-    threads = max(1, min(16, os.cpu_count() or 1))
-    torch.set_num_threads(threads)
-
-    def host(case):
-        return (case["x"].cpu(), *(t.cpu() for t in case["w"]))
-
+    torch.set_num_threads(host_threads())
     worst = 0.0
     for case in list(decode) + list(gemm):
-        x, q, s, z = host(case)
+        x, q, s, z = case["x"].cpu(), *(t.cpu() for t in case["w"])
         ref = O.reference_linear_torch(x, q, s, z, None, out_features=case["n"], in_features=case["k"],
                                        return_f32=True)
         got = case["out"].float().cpu()
@@ -298,30 +337,48 @@ def cpu_baseline(decode, gemm, torch, budget_s: float = 12.0):
                              f"{rel:.3e}")
         worst = max(worst, rel)
     log(f"parity vs CPU reference: worst normwise relative error {worst:.2e} over {len(decode) + len(gemm)} calls")
+    return {"calls": len(decode) + len(gemm), "worst_normwise_rel_err": worst, "bar": 1e-2}
 
-    tensors = [(*host(case), case["n"], case["k"]) for case in decode]
+
+def _cpu_samples(fn, warmup: int, reps: int, budget_s: float):
+    """perf_counter_ns samples (s) of fn: warm-up, then up to `reps` calls
+    within `budget_s` (scripts/autotune_phase_e_triton_v6.py:41-56 times
+    warm-up 20 + 100 iterations; the CPU leg is bounded by time instead)."""
+    for _ in range(warmup):
+        fn()
+    times = []
+    start = time.perf_counter()
+    while len(times) < reps and (time.perf_counter() - start) < budget_s:
+        t0 = time.perf_counter_ns()
+        fn()
+        times.append((time.perf_counter_ns() - t0) * 1e-9)
+    return times
+
+
+def cpu_baseline(decode, torch, budget_s: float = 12.0):
+    """The reference's torch backend restated on CPU (the oracle's port),
+    timed on the host cores: the decode step (all 21 calls) over a bounded
+    sample, and the single q_proj 1536x1536 call at M = 1 of the CPU
+    configuration on its own."""
+    from oracle import oracle as O
+
+    threads = host_threads()
+    torch.set_num_threads(threads)
+    tensors = [(c["x"].cpu(), *(t.cpu() for t in c["w"]), c["n"], c["k"]) for c in decode]
     step_bytes = sum(case["bytes"] for case in decode)
 
     def one_step():
         for x, q, s, z, n, k in tensors:
             O.reference_linear_torch(x, q, s, z, None, out_features=n, in_features=k)
 
-    one_step()  # warm-up
-    times = []
-    start = time.perf_counter()
-    while len(times) < 30 and (time.perf_counter() - start) < budget_s:
-        t0 = time.perf_counter()
-        one_step()
-        times.append(time.perf_counter() - t0)
+    times = _cpu_samples(one_step, 1, 30, budget_s)
     step_s = statistics.median(times)
-    cpu_model = platform.processor() or "unknown"
-    try:
-        for line in Path("/proc/cpuinfo").read_text().splitlines():
-            if line.startswith("model name"):
-                cpu_model = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
+    # the CPU configuration: symmetric RTN q_proj 1536x1536, M = 1, fp16 activations
+    q_case = next(c for c in decode if c["name"] == "q_proj" and c["rows"] == 1)
+    qx, qq, qs, qz = q_case["x"].cpu(), *(t.cpu() for t in q_case["w"])
+    q_times = _cpu_samples(lambda: O.reference_linear_torch(qx, qq, qs, qz, None, out_features=1536,
+                                                            in_features=1536), 5, 100, 5.0)
+    q_s = statistics.median(q_times)
     return {
         "value": step_bytes / step_s / 1e9,
         "unit": "GB/s",
@@ -329,9 +386,25 @@ def cpu_baseline(decode, gemm, torch, budget_s: float = 12.0):
         "kind": "port",
         "sample": (f"{len(times)} decode steps (21 calls each: 7 shapes x rows 1/4/16, fp16) of the torch CPU "
                    f"restatement of the reference's torch backend; median {step_s * 1e3:.1f} ms/step; "
-                   f"host {cpu_model}, os.cpu_count()={os.cpu_count()}"),
-        "parity_worst_normwise_rel_err": worst,
+                   f"host {cpu_model_name()}, os.cpu_count()={os.cpu_count()}, threads = CPUs in this process's "
+                   f"affinity set"),
+        "step_ms_p50": round(step_s * 1e3, 3),
+        "step_ms_p95": round(percentile(times, 95) * 1e3, 3),
+        "q_proj_m1": {
+            "workload": "q_proj 1536x1536, M=1, symmetric RTN W4G64, fp16 activations, CPU torch backend",
+            "calls": len(q_times), "us_p50": round(q_s * 1e6, 1), "us_p95": round(percentile(q_times, 95) * 1e6, 1),
+            "GBps": round(q_case["bytes"] / q_s / 1e9, 3),
+        },
     }
+
+
+def percentile(values, p: float) -> float:
+    """Nearest-rank percentile."""
+    ordered = sorted(values)
+    if not ordered:
+        return float("nan")
+    rank = max(1, int(-(-len(ordered) * p // 100)))
+    return ordered[min(rank, len(ordered)) - 1]
 
 
 # ---------------------------------------------------------------------------
@@ -522,7 +595,7 @@ def build_model(torch, seed: int):
     from qwen_int4_hip.model import QwenInt4ForCausalLM
 
     gen = torch.Generator(device="cuda").manual_seed(seed)
-    model = QwenInt4ForCausalLM(SimpleNamespace(**QWEN2_1_5B)).to("cuda")
+    model = QwenInt4ForCausalLM(SimpleNamespace(**QWEN2_1_5B), packing="canonical", group_size=64).to("cuda")
     with torch.no_grad():
         emb = model.model.embed_tokens.weight
         emb.copy_(torch.randn(emb.shape, generator=gen, device="cuda") * 0.02)
@@ -537,20 +610,49 @@ def build_model(torch, seed: int):
     return model.eval()
 
 
-def end_to_end(torch, prompt_len: int = 512, new_tokens: int = 128):
+def end_to_end(torch, hip, prompt_len: int = 512, new_tokens: int = 128, prefill_reps: int = 10,
+               check_steps: int = 8):
+    """Prefill and greedy decode of the full workload on the serving path
+    (FusedPrefill + one graph replay of FusedDecodeStep per token), with the
+    reference harness's statistics (p50/p95: scripts/benchmark_phase_f_model.py
+    :33-50) and, before timing, a check of the served logits against the
+    module path (growing cache, same HIP linears, unfused glue) under teacher
+    forcing."""
     from qwen_int4_hip.generation import StaticGreedyDecoder
 
     model = build_model(torch, BASE_SEED)
     gen = torch.Generator().manual_seed(BASE_SEED + 4)
     prompt = torch.randint(0, QWEN2_1_5B["vocab_size"], (1, prompt_len), generator=gen).cuda()
     decoder = StaticGreedyDecoder(model, 1, prompt_len + new_tokens)
-    decoder.generate(prompt, 4)  # warm-up: kernels, workspaces, the decode-step graph
+
+    def cos(a, b):
+        a, b = a.double().flatten(), b.double().flatten()
+        return float(a @ b / (a.norm() * b.norm()))
+
+    with torch.inference_mode():
+        served = [decoder.prefill(prompt).clone()]
+        want, cache = model(prompt, use_cache=True)
+        checks = [cos(served[0], want)]
+        token = want[:, -1:].argmax(dim=-1)
+        for _ in range(check_steps):
+            got = decoder.step(token).clone()
+            want, cache = model(token, past_key_values=cache, use_cache=True)
+            checks.append(cos(got, want))
+            if not bool(torch.isfinite(got).all()):
+                raise SystemExit("e2e: non-finite logits on the serving path")
+            token = want[:, -1:].argmax(dim=-1)
+        del cache, want
+    if min(checks) < 0.999:
+        raise SystemExit(f"e2e: served logits differ from the module path (min cosine {min(checks):.6f})")
     torch.cuda.synchronize()
-    decoder.length = 0
-    t0 = time.perf_counter()
-    decoder.prefill(prompt)
-    torch.cuda.synchronize()
-    prefill_s = time.perf_counter() - t0
+
+    prefill_ms = []
+    for _ in range(prefill_reps):
+        decoder.length = 0
+        t0 = time.perf_counter()
+        decoder.prefill(prompt)
+        torch.cuda.synchronize()
+        prefill_ms.append((time.perf_counter() - t0) * 1e3)
     tokens = [decoder.token.clone()]
     t0 = time.perf_counter()
     for _ in range(new_tokens - 1):
@@ -558,29 +660,40 @@ def end_to_end(torch, prompt_len: int = 512, new_tokens: int = 128):
         tokens.append(decoder.token.clone())
     torch.cuda.synchronize()
     decode_s = time.perf_counter() - t0
+    # per-token distribution: the same decode again, each step between two events
+    decoder.length = 0
+    decoder.prefill(prompt)
+    step_ms = replay_samples(lambda i: decoder.step(), new_tokens - 1, hip, torch)
     linear_bytes = 28 * sum(algorithmic_bytes(1, n, k) for n, k in QWEN2_SHAPES.values())
     head_bytes = QWEN2_1_5B["vocab_size"] * QWEN2_1_5B["hidden_size"] * 2
     per_token = decode_s / (new_tokens - 1)
+    prefill_p50 = statistics.median(prefill_ms)
     head = lm_head_rate(torch, decoder, head_bytes)
     return {
         "workload": (f"Qwen2-1.5B architecture (28 layers, hidden 1536, GQA 12/2 x 128, SwiGLU 8960, vocab 151936), "
                      f"random-init N(0,0.02) weights, 196 symmetric RTN W4G64 linears, tied bf16 LM head; batch 1, "
                      f"{prompt_len}-token random prompt then {new_tokens} greedy tokens, static KV cache, one HIP graph "
                      f"replay per decode step"),
-        "prefill_ms": round(prefill_s * 1e3, 3),
-        "prefill_tokens_per_s": round(prompt_len / prefill_s, 1),
+        "prefill_ms": round(prefill_p50, 3),
+        "prefill_ms_p95": round(percentile(prefill_ms, 95), 3),
+        "prefill_samples": len(prefill_ms),
+        "prefill_tokens_per_s": round(prompt_len / (prefill_p50 * 1e-3), 1),
         "decode_ms_per_token": round(per_token * 1e3, 4),
+        "decode_ms_p50": round(statistics.median(step_ms), 4),
+        "decode_ms_p95": round(percentile(step_ms, 95), 4),
         "decode_tokens_per_s": round(1.0 / per_token, 1),
         "decode_weight_bytes_per_token": linear_bytes + head_bytes,
         "decode_weight_GBps": round((linear_bytes + head_bytes) / per_token / 1e9, 1),
         "generated_tokens": int(torch.cat(tokens, dim=1).numel()),
+        "served_vs_module_path_min_cosine": round(min(checks), 7),
         "lm_head": head,
     }
 
 
 def log_e2e(e2e) -> None:
-    log(f"e2e: prefill {e2e['prefill_ms']:.1f} ms ({e2e['prefill_tokens_per_s']:.0f} tok/s), "
-        f"decode {e2e['decode_ms_per_token']:.3f} ms/token ({e2e['decode_tokens_per_s']:.0f} tok/s)")
+    log(f"e2e: prefill p50 {e2e['prefill_ms']:.2f} ms p95 {e2e['prefill_ms_p95']:.2f} ms "
+        f"({e2e['prefill_tokens_per_s']:.0f} tok/s), decode {e2e['decode_ms_per_token']:.3f} ms/token "
+        f"(p50 {e2e['decode_ms_p50']:.3f}, p95 {e2e['decode_ms_p95']:.3f}; {e2e['decode_tokens_per_s']:.0f} tok/s)")
     if e2e.get("lm_head"):
         h = e2e["lm_head"]
         log(f"e2e LM head: {h['us_per_call']:.1f} us per call, {h['GBps']:.0f} GB/s ({100 * h['frac']:.1f}% of 8 TB/s)")
@@ -626,9 +739,10 @@ def main() -> int:
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=512)
     parser.add_argument("--warmup", type=int, default=64)
-    parser.add_argument("--kernel-reps", type=int, default=32, help="timed graph replays per decode case (32 launches each); event-timed calls per GEMM case")
+    parser.add_argument("--kernel-reps", type=int, default=32, help="timed graph replays per decode case (32 launches each) and event-timed calls per GEMM case "
+                             "(at least 100)")
     parser.add_argument("--no-cpu-baseline", action="store_true",
-                        help="skip the CPU baseline leg (and with it the parity check against the CPU reference)")
+                        help="skip the CPU timing of the baseline leg (its parity check always runs)")
     parser.add_argument("--no-gemm", action="store_true")
     parser.add_argument("--no-e2e", action="store_true", help="skip the end-to-end Qwen2-1.5B generation")
     parser.add_argument("--e2e-only", action="store_true",
@@ -668,18 +782,30 @@ def main() -> int:
     props = torch.cuda.get_device_properties(0)
     log(f"device: {props.name} CUs={props.multi_processor_count}")
     if args.e2e_only:
-        e2e = end_to_end(torch)
+        e2e = end_to_end(torch, hip)
         log_e2e(e2e)
         print(json.dumps({"e2e": e2e}), flush=True)
         return 0
 
-    # ---------------- decode workload ----------------
+    # ---------------- workloads and parity (before any timing) ----------------
     base, copies, cases = decode_cases(torch, COPIES)
     distinct_mb = sum(sum(t.numel() * t.element_size() for t in c[0]) for c in copies.values()) * COPIES / 1e6
     step_bytes = sum(c["bytes"] for c in cases)
-    for c in cases:  # checked against the CPU reference in the cpu_baseline leg
+    for c in cases:
         c["out"] = linear_canonical_w4g64_hip(c["x"], *c["w"])
+    gemm_cases = []
+    if not args.no_gemm:
+        for name in PREFILL_SHAPES:
+            n, k = QWEN2_SHAPES[name]
+            for rows in PREFILL_ROWS:
+                x = gen_activations(rows, k, BASE_SEED + 7 * rows + n, torch.bfloat16, torch)
+                gemm_cases.append({"name": name, "rows": rows, "n": n, "k": k, "x": x, "w": base[name],
+                                   "copies": copies[name][:4], "copy0": 0})
+        for c in gemm_cases:
+            c["out"] = linear_canonical_w4g64_hip(c["x"], *c["w"])
+    parity = cpu_parity(cases, [c for c in gemm_cases if c["rows"] == 2048], torch)
 
+    # ---------------- decode workload ----------------
     # HIP graphs: graph p runs the 21 calls of a step on copies (3p + rows_index) % COPIES
     side = torch.cuda.Stream()
     phases = COPIES
@@ -706,9 +832,13 @@ def main() -> int:
     ms_per_step = wall * 1e3 / args.steps
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
     log(f"decode: {ms_per_step * 1e3:.1f} us/step, {value:.1f} GB/s whole-step ({step_bytes / 1e6:.1f} MB/step)")
+    # distribution of single steps: each replay between two events on the replay stream
+    step_samples = replay_samples(lambda i: graphs[i % phases].replay(), max(100, args.kernel_reps), hip, torch)
+    step_p50, step_p95 = statistics.median(step_samples), percentile(step_samples, 95)
+    log(f"decode step: p50 {step_p50 * 1e3:.1f} us, p95 {step_p95 * 1e3:.1f} us over {len(step_samples)} replays")
 
     # live per-kernel durations: HIP events around graph replays of each shape
-    durations = graph_kernel_durations(cases, args.kernel_reps, hip, torch)
+    durations = graph_kernel_durations(cases, max(100, args.kernel_reps), hip, torch)
     per_case = []
     kernel_ms_total = 0.0
     for c, d in zip(cases, durations):
@@ -718,6 +848,7 @@ def main() -> int:
             "name": c["name"], "rows": c["rows"], "n": c["n"], "k": c["k"], "bytes": c["bytes"],
             "kernel": linear_kernel_name(c["rows"], c["n"], c["k"], torch.float16),
             "kernel_us_mean": mean_ms * 1e3, "kernel_us_median": statistics.median(d) * 1e3,
+            "kernel_us_p95": percentile(d, 95) * 1e3, "samples": len(d),
             "GBps": c["bytes"] / (mean_ms * 1e-3) / 1e9,
         })
     achieved = step_bytes / (kernel_ms_total * 1e-3) / 1e9
@@ -725,8 +856,10 @@ def main() -> int:
     m1_mlp_gbs = sum(p["bytes"] for p in m1_mlp) / (sum(p["kernel_us_mean"] for p in m1_mlp) * 1e-6) / 1e9
     m1 = [p for p in per_case if p["rows"] == 1]
     m1_gbs = sum(p["bytes"] for p in m1) / (sum(p["kernel_us_mean"] for p in m1) * 1e-6) / 1e9
+    dominant = max(per_case, key=lambda p: p["kernel_us_mean"])
     for p in per_case:
-        log(f"  {p['name']:9s} rows={p['rows']:2d}  {p['kernel_us_mean']:7.2f} us  {p['GBps']:8.1f} GB/s")
+        log(f"  {p['name']:9s} rows={p['rows']:2d}  {p['kernel_us_mean']:7.2f} us (p50 {p['kernel_us_median']:6.2f}, "
+            f"p95 {p['kernel_us_p95']:6.2f})  {p['GBps']:8.1f} GB/s")
     log(f"decode kernels: {achieved:.1f} GB/s over all calls; M=1: {m1_gbs:.1f} GB/s; M=1 MLP shapes "
         f"{m1_mlp_gbs:.1f} GB/s")
 
@@ -751,6 +884,9 @@ def main() -> int:
             "distinct_weight_MB": round(distinct_mb, 1),
             "bytes_per_step": step_bytes,
         },
+        "step_us_p50": round(step_p50 * 1e3, 2),
+        "step_us_p95": round(step_p95 * 1e3, 2),
+        "parity": parity,
         "roofline": {
             "bound": "hbm",
             "kernel": "gemv_kernel / gemv16_kernel (all 21 calls of a step)",
@@ -763,6 +899,10 @@ def main() -> int:
             "m1_GBps": round(m1_gbs, 2),
             "m1_mlp_GBps": round(m1_mlp_gbs, 2),
             "m1_mlp_frac": round(m1_mlp_gbs / HBM_PEAK_GBS, 4),
+            "dominant_kernel": {"call": f"{dominant['name']} rows={dominant['rows']}", "kernel": dominant["kernel"],
+                                "us_mean": round(dominant["kernel_us_mean"], 3),
+                                "achieved_GBps": round(dominant["GBps"], 1),
+                                "frac": round(dominant["GBps"] / HBM_PEAK_GBS, 4)},
         },
     }
     traffic = committed_traffic()
@@ -773,17 +913,8 @@ def main() -> int:
                                                 f"{traffic['decode']['algorithmic_bytes_per_launch']:.0f} B/launch")
 
     # ---------------- prefill GEMM ----------------
-    gemm_cases = []
-    if not args.no_gemm:
-        for name in PREFILL_SHAPES:
-            n, k = QWEN2_SHAPES[name]
-            for rows in PREFILL_ROWS:
-                x = gen_activations(rows, k, BASE_SEED + 7 * rows + n, torch.bfloat16, torch)
-                gemm_cases.append({"name": name, "rows": rows, "n": n, "k": k, "x": x, "w": base[name],
-                                   "copies": copies[name][:4], "copy0": 0})
-        for c in gemm_cases:
-            c["out"] = linear_canonical_w4g64_hip(c["x"], *c["w"])
-        gd = kernel_durations(gemm_cases, 8, hip, torch)
+    if gemm_cases:
+        gd = kernel_durations(gemm_cases, max(100, args.kernel_reps), hip, torch)
         dense = dense_library_gemm_ms(gemm_cases, torch)
         gemm_rows = []
         flops_2048 = 0.0
@@ -794,11 +925,12 @@ def main() -> int:
             flops = 2.0 * c["rows"] * c["n"] * c["k"]
             tflops = flops / (mean_ms * 1e-3) / 1e12
             gemm_rows.append({"name": c["name"], "rows": c["rows"], "n": c["n"], "k": c["k"],
-                              "kernel_us_mean": mean_ms * 1e3, "TFLOPs": tflops,
+                              "kernel_us_mean": mean_ms * 1e3, "kernel_us_p50": statistics.median(d) * 1e3,
+                              "kernel_us_p95": percentile(d, 95) * 1e3, "samples": len(d), "TFLOPs": tflops,
                               "dense_bf16_library_us": dense_ms * 1e3,
                               "dense_bf16_library_TFLOPs": flops / (dense_ms * 1e-3) / 1e12})
-            log(f"  gemm {c['name']:9s} rows={c['rows']:4d}  {mean_ms * 1e3:8.2f} us  {tflops:7.1f} TFLOP/s   "
-                f"(dense bf16 torch.matmul {dense_ms * 1e3:8.2f} us)")
+            log(f"  gemm {c['name']:9s} rows={c['rows']:4d}  {mean_ms * 1e3:8.2f} us (p95 {percentile(d, 95) * 1e3:8.2f})"
+                f"  {tflops:7.1f} TFLOP/s   (dense bf16 torch.matmul {dense_ms * 1e3:8.2f} us)")
             if c["rows"] == 2048:
                 flops_2048 += flops
                 ms_2048 += mean_ms
@@ -822,12 +954,13 @@ def main() -> int:
         }
 
     if not args.no_e2e:
-        result["e2e"] = end_to_end(torch)
+        result["e2e"] = end_to_end(torch, hip)
         log_e2e(result["e2e"])
 
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(cases, [c for c in gemm_cases if c["rows"] == 2048], torch)
-        log(f"cpu baseline: {result['cpu_baseline']['value']:.3f} GB/s on {result['cpu_baseline']['cores']} threads")
+        result["cpu_baseline"] = cpu_baseline(cases, torch)
+        log(f"cpu baseline: {result['cpu_baseline']['value']:.3f} GB/s on {result['cpu_baseline']['cores']} threads; "
+            f"q_proj M=1 {result['cpu_baseline']['q_proj_m1']['us_p50']:.0f} us")
     result["decode_per_shape"] = per_case
     if args.report:
         Path(args.report).parent.mkdir(parents=True, exist_ok=True)

@@ -384,18 +384,9 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
     }
 
     // ---- arrival: the last workgroup of this (sequence, head) merges ----
-    // The wait completes this workgroup's partial stores before its arrival
-    // is counted; the merger loads only after its counter update returned.
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (tid == 0) {
-        const unsigned prev = __hip_atomic_fetch_add(a.counters + slot, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        s_last = prev == (unsigned)a.chunks - 1u;
-    }
-    __syncthreads();
-    if (!s_last) return;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    // The partial stores are published by the arrival's agent-scope release
+    // and acquired by the last arriver (arrive_last).
+    if (!arrive_last(a.counters + slot, (unsigned)a.chunks, &s_last)) return;
     // Every device-coherent load travels to memory, so the merge issues all of
     // them at once: the statistics into LDS and, per thread (dimension d,
     // heads g0, g0 + 2, ...), the weighted sums of up to kMergeBatch chunks.

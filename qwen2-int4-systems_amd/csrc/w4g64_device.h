@@ -147,4 +147,25 @@ __device__ __forceinline__ void store_out(void* y, int64_t idx, float v) {
 
 __device__ __forceinline__ float bf16_round(float v) { return bf16_bits_to_float(float_to_bf16_bits(v)); }
 
+// Arrival of a workgroup at a cross-workgroup merge: true in the last of
+// `expected` workgroups to arrive on `counter`.  The workgroup barrier orders
+// every thread's partial-sum stores before thread 0's agent-scope release
+// (the fetch_add), and the last arriver's agent-scope acquire fence before
+// the barrier that releases its threads to read the partial sums, so the
+// merge sees every other workgroup's stores under the HIP memory model
+// (happens-before is transitive across the workgroup and agent scopes).
+// `flag` is a __shared__ int of the caller.  Every thread must call this.
+__device__ __forceinline__ bool arrive_last(unsigned* counter, unsigned expected, int* flag) {
+    __builtin_amdgcn_s_waitcnt(0);  // this thread's stores have completed
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const unsigned prev = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+        const bool last = prev == expected - 1u;
+        if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        *flag = last;
+    }
+    __syncthreads();
+    return *flag != 0;
+}
+
 }  // namespace w4g64

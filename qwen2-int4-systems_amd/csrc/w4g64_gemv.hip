@@ -568,20 +568,10 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
     if (a.splits == 1) return;
 
     // ---- K split across workgroups: the last arrival of the block reduces ----
-    // Partials travel through device-coherent (sc1) atomic stores and loads.
-    // The wait makes every partial store of this workgroup complete before the
-    // arrival is counted; the reducer loads only after its counter update
-    // returned.  No cache write-back or invalidation is needed.
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (tid == 0) {
-        const unsigned prev = __hip_atomic_fetch_add(a.counters + nb, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        s_last = (prev == (unsigned)a.splits - 1u);
-    }
-    __syncthreads();
-    if (!s_last) return;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    // Partials travel through device-coherent (sc1) atomic stores and loads,
+    // published by the arrival's agent-scope release and acquired by the last
+    // arriver (arrive_last).
+    if (!arrive_last(a.counters + nb, (unsigned)a.splits, &s_last)) return;
     auto reduce_partials = [&](int m, int nn) {
         float v = 0.0f;
         for (int s = 0; s < a.splits; ++s)

@@ -224,19 +224,10 @@ __global__ __launch_bounds__(KW * FB * 64) void gemv16_kernel(Gemv16Args a) {
     if (a.splits == 1) return;
 
     // ---- K split across workgroups: the last arrival of the block reduces ----
-    // Partials travel through device-coherent (sc1) atomic stores and loads;
-    // the wait completes this workgroup's partial stores before its arrival is
-    // counted, and the reducer loads only after its counter update returned.
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (tid == 0) {
-        const unsigned prev = __hip_atomic_fetch_add(a.counters + nb, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        s_last = (prev == (unsigned)a.splits - 1u);
-    }
-    __syncthreads();
-    if (!s_last) return;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    // Partials travel through device-coherent (sc1) atomic stores and loads,
+    // published by the arrival's agent-scope release and acquired by the last
+    // arriver (arrive_last).
+    if (!arrive_last(a.counters + nb, (unsigned)a.splits, &s_last)) return;
     for (int idx = tid; idx < a.M * kCols; idx += kThreads16) {
         const int m = idx / kCols;
         const int c = idx - m * kCols;

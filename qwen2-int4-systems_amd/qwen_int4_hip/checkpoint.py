@@ -5,14 +5,16 @@ safetensors files load drop-in into ``QwenInt4ForCausalLM``:
 
   * metadata of the symmetric RTN export (scripts/quantize_model.py:148-162)
     and of the canonical asymmetric AWQ export (src/qwen_int4/export.py:38-57);
-  * ``load_quantized_checkpoint`` (src/qwen_int4/checkpoint.py:51-118): the
-    quantized tensors must match the model's buffers name for name and shape
-    for shape, AWQ files also carry their transformed norms and v_proj bias,
-    and non-zero zero points require an asymmetric contract -- with the same
-    checks and messages.  The tensors are read straight into the device of
-    the model's buffers (safetensors loads to that device; no host copy of
-    the whole file), and buffers that ``decode.fuse_projections`` turned into
-    views of fused q|k|v and gate|up buffers are written through;
+  * ``load_quantized_checkpoint`` (the contract of src/qwen_int4/
+    checkpoint.py:51-118): the quantized tensors must match the model's
+    buffers name for name and shape for shape, AWQ files also carry their
+    transformed norms and v_proj bias, and non-zero zero points require an
+    asymmetric contract, with the reference's error messages.  Everything is
+    checked from the file header before any tensor is read, and the tensors
+    are then streamed one at a time onto the device of the model's buffers
+    (no host copy of the whole file); buffers that
+    ``decode.fuse_projections`` turned into views of fused q|k|v and gate|up
+    buffers are written through;
   * the frozen canonical AWQ v6 manifest and the checks on a v6 file's bytes
     and metadata before it loads (src/qwen_int4/artifact_contract.py:52-167,
     src/qwen_int4/checkpoint.py:121-140);
@@ -32,7 +34,7 @@ from pathlib import Path
 
 import torch
 from safetensors import safe_open
-from safetensors.torch import load_file, save_file
+from safetensors.torch import save_file
 
 from .quantization import (
     CANONICAL_PACKING_METADATA,
@@ -138,66 +140,69 @@ def _buffer_device(model: torch.nn.Module) -> torch.device:
     return torch.device("cpu")
 
 
+def _file_header(path: Path) -> tuple[dict[str, tuple[int, ...]], dict[str, str]]:
+    """Tensor shapes and metadata from the safetensors header alone."""
+    with safe_open(str(path), framework="pt", device="cpu") as handle:
+        shapes = {key: tuple(handle.get_slice(key).get_shape()) for key in handle.keys()}
+        return shapes, handle.metadata() or {}
+
+
+def _key_set_problems(want: dict[str, tuple], have: dict[str, tuple]) -> tuple[list, list, dict]:
+    """(missing, unexpected, shape mismatches) of a file's keys against a model's."""
+    missing = sorted(set(want) - set(have))
+    unexpected = sorted(set(have) - set(want))
+    shapes = {key: (want[key], have[key]) for key in sorted(set(want) & set(have)) if want[key] != have[key]}
+    return missing, unexpected, shapes
+
+
 def load_quantized_checkpoint(model: torch.nn.Module, path: str | Path, *,
                               device: torch.device | str | None = None) -> LoadReport:
-    """Strictly load the quantized tensors (and an AWQ file's transformed
-    state) into ``model`` (src/qwen_int4/checkpoint.py:51-118).  Tensors are
-    read directly onto ``device`` (default: where the model's quantized
-    buffers live)."""
+    """Load a W4G64 checkpoint's quantized tensors -- and, for the AWQ format,
+    its transformed norms and v_proj biases -- into ``model``, strictly
+    (the contract of src/qwen_int4/checkpoint.py:51-118).
+
+    Three phases, so that a rejected file leaves the model untouched:
+      1. the file's header alone (names and shapes, no tensor data) is
+         checked against the model: the quantized key sets must be equal
+         with equal shapes, and an AWQ file must carry exactly the model's
+         transformed-state keys;
+      2. unless the metadata names an asymmetric zero-point contract, every
+         ``.zeros`` tensor of the file must be all zero;
+      3. each tensor is read onto ``device`` (default: where the model's
+         quantized buffers live) and copied into its buffer -- buffers that
+         are views of fused projection buffers receive the data in place.
+    Returns the count of loaded keys and of file keys left unused."""
     path = Path(path)
     if not path.is_file():
         raise FileNotFoundError(path)
-    target = torch.device(device) if device is not None else _buffer_device(model)
-    checkpoint = load_file(str(path), device=str(target))
-    expected = model.state_dict()
-    expected_quantized = {key for key in expected if is_quantized_key(key)}
-    checkpoint_quantized = {key for key in checkpoint if is_quantized_key(key)}
-    missing = expected_quantized - checkpoint_quantized
-    unexpected = checkpoint_quantized - expected_quantized
-    mismatched = {
-        key: (tuple(expected[key].shape), tuple(checkpoint[key].shape))
-        for key in expected_quantized & checkpoint_quantized
-        if expected[key].shape != checkpoint[key].shape
-    }
+    shapes, metadata = _file_header(path)
+    targets = model.state_dict()
+    want = {key: tuple(t.shape) for key, t in targets.items() if is_quantized_key(key)}
+    have = {key: shape for key, shape in shapes.items() if is_quantized_key(key)}
+    missing, unexpected, mismatched = _key_set_problems(want, have)
     if missing or unexpected or mismatched:
-        raise RuntimeError(
-            "checkpoint contract mismatch:\n"
-            f"  missing={sorted(missing)}\n"
-            f"  unexpected={sorted(unexpected)}\n"
-            f"  shape_mismatches={mismatched}"
-        )
-
-    metadata = checkpoint_metadata(path)
-    transformed: dict[str, torch.Tensor] = {}
+        raise RuntimeError(f"checkpoint contract mismatch:\n  missing={missing}\n  unexpected={unexpected}\n"
+                           f"  shape_mismatches={mismatched}")
+    keys = sorted(want)
     if metadata.get("format_version") == AWQ_FORMAT_VERSION:
-        expected_transformed = {key for key in expected if key.endswith(AWQ_TRANSFORMED_SUFFIXES)}
-        checkpoint_transformed = {key for key in checkpoint if key.endswith(AWQ_TRANSFORMED_SUFFIXES)}
-        missing_t = expected_transformed - checkpoint_transformed
-        unexpected_t = checkpoint_transformed - expected_transformed
-        if missing_t or unexpected_t:
-            raise RuntimeError(
-                "AWQ transformed-state contract mismatch:\n"
-                f"  missing={sorted(missing_t)}\n"
-                f"  unexpected={sorted(unexpected_t)}"
-            )
-        transformed = {key: checkpoint[key] for key in checkpoint_transformed}
-
-    load_tensors = {**{key: checkpoint[key] for key in checkpoint_quantized}, **transformed}
-    # copy_ into the existing buffers (load_state_dict's default): views of
-    # fused projection buffers stay views and receive the data
-    incompatible = model.load_state_dict(load_tensors, strict=False)
-    if incompatible.unexpected_keys:
-        raise RuntimeError(f"quantized state_dict load failed: unexpected={sorted(incompatible.unexpected_keys)}")
-
-    nonzero_zero_points = [
-        name for name, tensor in model.named_buffers()
-        if name.endswith(".zeros") and torch.count_nonzero(tensor).item()
-    ]
-    if nonzero_zero_points and metadata.get("zero_point", "") not in ASYMMETRIC_ZERO_POINT_CONTRACTS:
-        raise RuntimeError(
-            "non-zero zero-points found without an asymmetric checkpoint contract: " + ", ".join(nonzero_zero_points)
-        )
-    return LoadReport(len(load_tensors), len(checkpoint) - len(load_tensors))
+        t_want = {key: () for key in targets if key.endswith(AWQ_TRANSFORMED_SUFFIXES)}
+        t_have = {key: () for key in shapes if key.endswith(AWQ_TRANSFORMED_SUFFIXES)}
+        t_missing, t_unexpected, _ = _key_set_problems(t_want, t_have)
+        if t_missing or t_unexpected:
+            raise RuntimeError(f"AWQ transformed-state contract mismatch:\n  missing={t_missing}\n"
+                               f"  unexpected={t_unexpected}")
+        keys += sorted(t_want)
+    target = torch.device(device) if device is not None else _buffer_device(model)
+    with safe_open(str(path), framework="pt", device=str(target)) as handle:
+        if metadata.get("zero_point", "") not in ASYMMETRIC_ZERO_POINT_CONTRACTS:
+            nonzero = [key for key in keys if key.endswith(".zeros") and bool(handle.get_tensor(key).any())]
+            if nonzero:
+                raise RuntimeError("non-zero zero-points found without an asymmetric checkpoint contract: "
+                                   + ", ".join(nonzero))
+        with torch.no_grad():
+            for key in keys:
+                targets[key].copy_(handle.get_tensor(key))
+    return LoadReport(len(keys), len(shapes) - len(keys))
 
 
 # Non-quantized tensors every model needs from its base model (the checkpoint
@@ -372,17 +377,20 @@ def validate_canonical_awq_v6_checkpoint(path: str | Path, contract: CanonicalAW
     return metadata
 
 
+def _layers_outside(model: torch.nn.Module, group_size: int) -> list[str]:
+    """Quantized layers of ``model`` that are not canonical W4G``group_size``."""
+    return [name for name, module in model.named_modules()
+            if hasattr(module, "qweight") and not (getattr(module, "group_size", None) == group_size
+                                                   and getattr(module, "packing", None) is PackingFormat.CANONICAL)]
+
+
 def load_canonical_awq_v6_checkpoint(model: torch.nn.Module, path: str | Path, contract: CanonicalAWQV6Contract, *,
                                      device: torch.device | str | None = None) -> LoadReport:
-    """Check the file against the v6 contract and every quantized layer of
-    ``model`` for W4G64 canonical packing, then load
-    (src/qwen_int4/checkpoint.py:121-140)."""
+    """The frozen v6 file into a W4G64 canonical model: the file's bytes and
+    metadata against the manifest's contract first, then the model's layers,
+    then the strict load (src/qwen_int4/checkpoint.py:121-140)."""
     validate_canonical_awq_v6_checkpoint(path, contract)
-    wrong = [
-        name for name, module in model.named_modules()
-        if hasattr(module, "qweight") and (getattr(module, "group_size", None) != contract.group_size
-                                           or getattr(module, "packing", None) is not PackingFormat.CANONICAL)
-    ]
-    if wrong:
-        raise RuntimeError("model does not satisfy canonical AWQ v6 W4G64 packing: " + ", ".join(wrong))
+    outside = _layers_outside(model, contract.group_size)
+    if outside:
+        raise RuntimeError("model does not satisfy canonical AWQ v6 W4G64 packing: " + ", ".join(outside))
     return load_quantized_checkpoint(model, path, device=device)

@@ -44,6 +44,44 @@ def _ptr(tensor: torch.Tensor | None) -> ctypes.c_void_p | None:
     return None if tensor is None else ctypes.c_void_p(tensor.data_ptr())
 
 
+def check_static_caches(caches, *, layers: int, batch: int, kv_heads: int, head_dim: int, min_length: int,
+                        device) -> int:
+    """Validate per-layer (key, value) static caches before any kernel writes
+    them: each [batch, kv_heads, L, head_dim], bf16, contiguous, on
+    ``device``, one common L >= ``min_length``.  Returns L.  The shape and
+    device messages are those of the reference's attention (model.py:80-86)."""
+    if len(caches) != layers:
+        raise ValueError("past_key_values must contain one entry per decoder layer")
+    length = None
+    for pair in caches:
+        if not isinstance(pair, (tuple, list)) or len(pair) != 2:
+            raise ValueError("past key/value cache shape does not match this attention layer")
+        for t in pair:
+            if not isinstance(t, torch.Tensor) or t.ndim != 4 or tuple(t.shape[:2]) != (batch, kv_heads) \
+                    or t.shape[3] != head_dim or (length is not None and t.shape[2] != length):
+                raise ValueError("past key/value cache shape does not match this attention layer")
+            length = t.shape[2]
+            if t.device != torch.device(device):
+                raise ValueError("past key/value cache must be on the attention device")
+            if t.dtype != torch.bfloat16:
+                raise ValueError("static key/value caches must have dtype torch.bfloat16")
+            if not t.is_contiguous():
+                raise ValueError("static key/value caches must be contiguous")
+    if length < min_length:
+        raise ValueError(f"static key/value caches hold {length} positions; {min_length} are needed")
+    return length
+
+
+def check_token_ids(token_ids, *, batch: int, length: int | None, device, name: str = "input_ids") -> None:
+    """[batch, length] (``length`` None: any positive) int64 ids on ``device``."""
+    if not isinstance(token_ids, torch.Tensor) or token_ids.ndim != 2 or token_ids.shape[0] != batch \
+            or token_ids.shape[1] == 0 or (length is not None and token_ids.shape[1] != length):
+        want = f"[{batch}, {length if length is not None else 'sequence'}]"
+        raise ValueError(f"{name} must have shape {want}")
+    if token_ids.dtype != torch.int64 or token_ids.device != torch.device(device):
+        raise ValueError(f"{name} must be an int64 tensor on {device}")
+
+
 def _fuse(modules: list[QuantLinear]) -> dict:
     """Concatenate the packed buffers of linears that share their input along
     the output dimension and re-point each module's buffers at its slice."""
@@ -184,6 +222,12 @@ class FusedDecodeStep:
         ``next_token`` (int64 [batch, 1], may be ``token_ids`` itself), the
         greedy choice logits.argmax(-1) is written there."""
         model = self.model
+        check_token_ids(token_ids, batch=self.batch, length=1, device=self.device, name="token_ids")
+        if not isinstance(position, torch.Tensor) or position.numel() != 1 or position.dtype != torch.int64 \
+                or position.device != self.device:
+            raise ValueError(f"position must be a 1-element int64 tensor on {self.device}")
+        check_static_caches(caches, layers=len(model.model.layers), batch=self.batch, kv_heads=self.kv_heads,
+                            head_dim=self.head_dim, min_length=1, device=self.device)
         stream = ctypes.c_void_p(torch.cuda.current_stream(self.device).cuda_stream)
         torch.index_select(model.model.embed_tokens.weight, 0, token_ids.reshape(-1), out=self.x)
         cos, sin = model.model.rotary_emb(position.view(1, 1).expand(self.batch, 1), torch.bfloat16)
@@ -278,9 +322,14 @@ class FusedPrefill:
 
     def __call__(self, input_ids: torch.Tensor, caches) -> torch.Tensor:
         model, lib = self.model, self.lib
+        device = model.lm_head.weight.device
+        if not isinstance(input_ids, torch.Tensor) or input_ids.ndim != 2:
+            raise ValueError("input_ids must have shape [batch, sequence]")
         batch, length = input_ids.shape
+        check_token_ids(input_ids, batch=batch, length=None, device=device)
+        check_static_caches(caches, layers=len(model.model.layers), batch=batch, kv_heads=self.kv_heads,
+                            head_dim=self.head_dim, min_length=length, device=device)
         rows = batch * length
-        device = input_ids.device
         stream = ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
         bf16 = torch.bfloat16
         shapes = [(self.heads * self.head_dim + 2 * self.kv_heads * self.head_dim, self.hidden, _lib.DTYPE_BF16),

@@ -1,93 +1,111 @@
 """Cached greedy generation over the HIP W4G64 model.
 
-``CachedGenerationState`` and ``greedy_generate_cached`` restate
-src/qwen_int4/generation.py:10-111 (prefill, greedy decode with the growing
-per-layer cache, request selection, close).  ``StaticGreedyDecoder`` is the
-serving form of the same loop for a batch of unpadded prompts of one length:
-the cache is preallocated, each decode step has fixed shapes and runs as one
-replay of a HIP graph captured after a warm-up step.
+``CachedGenerationState`` and ``greedy_generate_cached`` provide the
+reference's cached-generation interface (src/qwen_int4/generation.py:10-115:
+the same names, attributes, arguments, exception types and the message
+fragments its tests match): one prefill of a left-padded batch, then one
+cached greedy step at a time, with request selection and an explicit close.
+``StaticGreedyDecoder`` is the serving form of the same loop for a batch of
+unpadded prompts of one length: the cache is preallocated, each decode step
+has fixed shapes and runs as one replay of a HIP graph captured after a
+warm-up step.
 """
 
 from __future__ import annotations
-
-from dataclasses import dataclass
 
 import torch
 
 from .decode import FusedDecodeStep, FusedPrefill
 
 
-@dataclass
+def _is_left_padded(mask: torch.Tensor) -> bool:
+    """Every row is zero or more padding positions followed by a non-empty run
+    of valid ones: along a row the mask never falls from valid to padding,
+    and its last position is valid."""
+    m = mask.to(torch.int8)
+    never_falls = bool((m[:, 1:] >= m[:, :-1]).all()) if m.shape[1] > 1 else True
+    return never_falls and bool(m[:, -1].all())
+
+
 class CachedGenerationState:
-    """Owned KV cache and mask state for one left-padded generation batch."""
+    """A left-padded batch under cached greedy decoding.
 
-    model: torch.nn.Module
-    generated_ids: torch.Tensor
-    attention_mask: torch.Tensor
-    logits: torch.Tensor
-    past_key_values: tuple
-    active: bool = True
+    Holds the model, every token so far (``generated_ids``), the attention
+    mask over them, the logits of the last forward and the per-layer
+    key/value caches, which it owns: ``select_requests`` reorders or drops
+    rows of all of them together, and ``close`` releases the caches, after
+    which every use raises."""
 
-    def _require_active(self) -> None:
-        if not self.active:
-            raise RuntimeError("cached generation state is closed")
+    def __init__(self, model, generated_ids: torch.Tensor, attention_mask: torch.Tensor, logits: torch.Tensor,
+                 past_key_values: tuple, active: bool = True) -> None:
+        self.model = model
+        self.generated_ids = generated_ids
+        self.attention_mask = attention_mask
+        self.logits = logits
+        self.past_key_values = past_key_values
+        self.active = active
 
     @classmethod
     def prefill(cls, model, input_ids: torch.Tensor, attention_mask: torch.Tensor | None = None):
+        """Run the prompt batch once with the cache enabled."""
         if input_ids.ndim != 2 or input_ids.shape[1] == 0:
             raise ValueError("input_ids must have shape [batch, non_empty_sequence]")
-        if attention_mask is None:
-            attention_mask = torch.ones_like(input_ids, dtype=torch.bool)
-        if attention_mask.shape != input_ids.shape:
+        mask = torch.ones_like(input_ids, dtype=torch.bool) if attention_mask is None else attention_mask
+        if mask.shape != input_ids.shape:
             raise ValueError("attention_mask must have the same shape as input_ids")
-        mask = attention_mask.to(dtype=torch.bool)
-        # left padding only: every row is some padding followed by a non-empty valid run
-        valid = mask.long()
-        first = torch.where(mask.any(dim=1), valid.argmax(dim=1), torch.full_like(valid[:, 0], mask.shape[1]))
-        tail_valid = torch.arange(mask.shape[1], device=mask.device).view(1, -1) >= first.view(-1, 1)
-        if bool((first >= mask.shape[1]).any()) or not bool(torch.equal(tail_valid, mask)):
+        mask = mask.to(dtype=torch.bool)
+        if not _is_left_padded(mask):
             raise ValueError("cached batching supports only non-empty left-padded attention masks")
         with torch.inference_mode():
-            logits, cache = model(input_ids, attention_mask=mask, use_cache=True)
-        if not isinstance(cache, tuple):
+            logits, caches = model(input_ids, attention_mask=mask, use_cache=True)
+        if not isinstance(caches, tuple):
             raise RuntimeError("cache-enabled model did not return per-layer key/value tensors")
-        return cls(model, input_ids, mask, logits, cache)
+        return cls(model, input_ids, mask, logits, caches)
+
+    def _check_open(self) -> None:
+        if not self.active:
+            raise RuntimeError("cached generation state is closed")
 
     def next_greedy_tokens(self) -> torch.Tensor:
-        self._require_active()
+        """[batch, 1]: the argmax of each row's last logits."""
+        self._check_open()
         return self.logits[:, -1].argmax(dim=-1, keepdim=True)
 
     def decode(self, next_tokens: torch.Tensor) -> torch.Tensor:
-        self._require_active()
+        """Append one token per row and run it against the cache; returns the
+        new logits [batch, 1, vocab]."""
+        self._check_open()
         if next_tokens.ndim != 2 or next_tokens.shape != (self.generated_ids.shape[0], 1):
             raise ValueError("next_tokens must have shape [batch, 1]")
+        grown = torch.cat((self.attention_mask, torch.ones_like(next_tokens, dtype=torch.bool)), dim=1)
         with torch.inference_mode():
-            self.generated_ids = torch.cat((self.generated_ids, next_tokens), dim=1)
-            self.attention_mask = torch.cat((self.attention_mask, torch.ones_like(next_tokens, dtype=torch.bool)),
-                                            dim=1)
-            self.logits, self.past_key_values = self.model(next_tokens, attention_mask=self.attention_mask,
-                                                           past_key_values=self.past_key_values, use_cache=True)
+            logits, caches = self.model(next_tokens, attention_mask=grown, past_key_values=self.past_key_values,
+                                        use_cache=True)
+        self.generated_ids = torch.cat((self.generated_ids, next_tokens), dim=1)
+        self.attention_mask, self.logits, self.past_key_values = grown, logits, caches
         return self.logits
 
     def select_requests(self, indices) -> None:
-        """Reorder or remove requests while preserving cache ownership."""
-        self._require_active()
-        selected = torch.as_tensor(indices, dtype=torch.long, device=self.generated_ids.device)
-        if selected.ndim != 1 or selected.numel() == 0:
+        """Keep only the rows ``indices`` (in that order), in every owned tensor."""
+        self._check_open()
+        rows = torch.as_tensor(indices, dtype=torch.long, device=self.generated_ids.device)
+        if rows.ndim != 1 or rows.numel() == 0:
             raise ValueError("request indices must be a non-empty one-dimensional sequence")
-        batch = self.generated_ids.shape[0]
-        if int(selected.min()) < 0 or int(selected.max()) >= batch:
+        lo, hi = int(rows.min()), int(rows.max())
+        if lo < 0 or hi >= self.generated_ids.shape[0]:
             raise IndexError("request index is outside the cached batch")
-        if selected.unique().numel() != selected.numel():
+        if rows.unique().numel() != rows.numel():
             raise ValueError("duplicate request indices require explicit beam-cache semantics")
-        self.generated_ids = self.generated_ids.index_select(0, selected)
-        self.attention_mask = self.attention_mask.index_select(0, selected)
-        self.logits = self.logits.index_select(0, selected)
-        self.past_key_values = tuple((k.index_select(0, selected), v.index_select(0, selected))
-                                     for k, v in self.past_key_values)
+
+        def pick(t: torch.Tensor) -> torch.Tensor:
+            return t.index_select(0, rows)
+
+        self.generated_ids, self.attention_mask, self.logits = map(pick, (self.generated_ids, self.attention_mask,
+                                                                          self.logits))
+        self.past_key_values = tuple(tuple(map(pick, pair)) for pair in self.past_key_values)
 
     def close(self) -> None:
-        """Release owned cache tensors and make further use fail closed."""
+        """Drop the caches and logits; later calls raise RuntimeError."""
         self.past_key_values = ()
         self.logits = torch.empty(0, device=self.generated_ids.device)
         self.active = False
@@ -95,7 +113,7 @@ class CachedGenerationState:
 
 def greedy_generate_cached(model, input_ids: torch.Tensor, *, max_new_tokens: int,
                            attention_mask: torch.Tensor | None = None) -> torch.Tensor:
-    """One prefill, then ``max_new_tokens`` cached greedy decode steps."""
+    """Prompt plus ``max_new_tokens`` greedy tokens per row, [batch, T + max_new_tokens]."""
     if max_new_tokens < 0:
         raise ValueError("max_new_tokens must be non-negative")
     state = CachedGenerationState.prefill(model, input_ids, attention_mask)

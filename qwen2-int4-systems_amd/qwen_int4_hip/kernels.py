@@ -51,27 +51,47 @@ def _aligned(tensor: torch.Tensor, bytes_: int) -> torch.Tensor:
 
 
 # ---------------------------------------------------------------------------
-# Workspace: split-K partials and arrival counters of the decode GEMV.  One
-# zero-filled buffer per (device, stream), grown on demand; the kernels leave
-# the counters at zero, so it is cleared only when (re)allocated.
+# Workspace: split-K partials and arrival counters of the decode GEMV and the
+# GEMM.  One zero-filled buffer per (device, stream), grown on demand; the
+# kernels leave the counters at zero, so it is cleared only when allocated.
+# A HIP graph captured on a stream keeps the raw address of the buffer it was
+# captured with, so a buffer is never freed once replaced: it moves to
+# ``_retired`` and lives as long as the process.  Growing (or creating) a
+# buffer while the stream is being captured is refused -- run the same call
+# once before the capture, as the warm-up of every capture in this package
+# does.
 # ---------------------------------------------------------------------------
 
 _workspaces: dict[tuple[int, int], torch.Tensor] = {}
+_retired: list[torch.Tensor] = []
 _workspace_lock = threading.Lock()
+
+
+def _grow_workspace(key, nbytes: int, device, capturing: bool) -> torch.Tensor:
+    """The buffer for ``key`` with at least ``nbytes`` bytes (the dict logic
+    of ``_workspace``; device-independent, so it is testable on the CPU)."""
+    with _workspace_lock:
+        buffer = _workspaces.get(key)
+        if buffer is not None and buffer.numel() >= nbytes:
+            return buffer
+        if capturing:
+            raise RuntimeError(
+                f"W4G64 workspace of {nbytes} bytes is not allocated for this stream; HIP graph capture cannot "
+                "allocate it -- run the same call on the capture stream once before capturing")
+        size = max(nbytes, 2 * (0 if buffer is None else buffer.numel()), 1 << 20)
+        if buffer is not None:
+            _retired.append(buffer)  # a captured graph may still point at it
+        buffer = torch.zeros(size, dtype=torch.uint8, device=device)
+        _workspaces[key] = buffer
+        return buffer
 
 
 def _workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
     if nbytes <= 0:
         return None
     index = device.index if device.index is not None else torch.cuda.current_device()
-    key = (index, torch.cuda.current_stream(device).cuda_stream)
-    with _workspace_lock:
-        buffer = _workspaces.get(key)
-        if buffer is None or buffer.numel() < nbytes:
-            size = max(nbytes, 2 * (0 if buffer is None else buffer.numel()), 1 << 20)
-            buffer = torch.zeros(size, dtype=torch.uint8, device=device)
-            _workspaces[key] = buffer
-    return buffer
+    stream = torch.cuda.current_stream(device)
+    return _grow_workspace((index, stream.cuda_stream), nbytes, device, torch.cuda.is_current_stream_capturing())
 
 
 # ---------------------------------------------------------------------------

@@ -33,7 +33,7 @@ class QuantLinear(nn.Module):
         self.num_groups = in_features // group_size
         self.backend = "hip"
         self.packing = PackingFormat(packing)
-        # Zero initialization makes an accidental partial load deterministic.
+        # Buffers start as zeros, so a load that skips some of them leaves known values.
         self.register_buffer("qweight", torch.zeros(out_features * in_features // 2, 1, dtype=torch.uint8))
         self.register_buffer("scales", torch.zeros(out_features, self.num_groups, dtype=torch.float16))
         self.register_buffer(

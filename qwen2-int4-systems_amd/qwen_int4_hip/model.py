@@ -210,8 +210,12 @@ class QwenModel(nn.Module):
 
 
 class QwenInt4ForCausalLM(nn.Module):
-    def __init__(self, config, *, backend: str = "hip", packing: PackingFormat | str = PackingFormat.CANONICAL,
-                 group_size: int = 64) -> None:
+    # The reference's defaults (LEGACY packing, group 128, model.py:207-209);
+    # the HIP backend rejects them at the first forward, so a W4G64 model is
+    # built with packing="canonical", group_size=64, as the reference's own
+    # scripts do.
+    def __init__(self, config, *, backend: str = "hip", packing: PackingFormat | str = PackingFormat.LEGACY_SIGNED_ADD,
+                 group_size: int = 128) -> None:
         super().__init__()
         packing = PackingFormat(packing)
         self.config = config

@@ -341,3 +341,66 @@ def test_hip_backend_fails_loudly_without_gpu():
     layer = QuantLinear(128, 64, group_size=64, packing=PackingFormat.CANONICAL)
     with pytest.raises(RuntimeError, match="HIP backend requires"):
         layer(torch.zeros(1, 128, dtype=torch.float16))
+
+
+def test_workspace_growth_keeps_replaced_buffers_and_refuses_capture():
+    """A captured HIP graph holds the raw address of the workspace it was
+    captured with: growing the (device, stream) buffer must keep the old one
+    alive, and growing during a capture must be refused."""
+    from qwen_int4_hip import kernels
+
+    key = ("cpu-test", 1)
+    try:
+        first = kernels._grow_workspace(key, 100, "cpu", capturing=False)
+        assert first.numel() >= 100 and not bool(first.any())
+        assert kernels._grow_workspace(key, 50, "cpu", capturing=True) is first  # fits: no allocation
+        retired = len(kernels._retired)
+        second = kernels._grow_workspace(key, first.numel() + 1, "cpu", capturing=False)
+        assert second.numel() > first.numel() and second is not first
+        assert kernels._retired[-1] is first and len(kernels._retired) == retired + 1
+        with pytest.raises(RuntimeError, match="capture"):
+            kernels._grow_workspace(key, second.numel() + 1, "cpu", capturing=True)
+        with pytest.raises(RuntimeError, match="capture"):
+            kernels._grow_workspace(("cpu-test", 2), 10, "cpu", capturing=True)
+        assert kernels._workspaces[key] is second
+    finally:
+        kernels._workspaces.pop(key, None)
+        kernels._workspaces.pop(("cpu-test", 2), None)
+
+
+def test_fused_paths_reject_mismatched_caches_and_ids_on_the_host():
+    """The fused decode step and prefill validate the caches they write, and
+    the token ids, before any launch (the reference's attention rejects
+    mismatched caches, src/qwen_int4/model.py:80-86)."""
+    from qwen_int4_hip.decode import check_static_caches, check_token_ids
+
+    def caches(n=2, shape=(1, 2, 16, 128), dtype=torch.bfloat16):
+        return [(torch.zeros(shape, dtype=dtype), torch.zeros(shape, dtype=dtype)) for _ in range(n)]
+
+    ok = dict(layers=2, batch=1, kv_heads=2, head_dim=128, min_length=4, device="cpu")
+    assert check_static_caches(caches(), **ok) == 16
+    with pytest.raises(ValueError, match="one entry per decoder layer"):
+        check_static_caches(caches(3), **ok)
+    for bad in [(2, 2, 16, 128), (1, 1, 16, 128), (1, 2, 16, 64), (1, 2, 16)]:
+        with pytest.raises(ValueError, match="cache shape does not match"):
+            check_static_caches(caches(shape=bad), **ok)
+    mixed = caches()
+    mixed[1] = (mixed[1][0], torch.zeros((1, 2, 8, 128), dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="cache shape does not match"):
+        check_static_caches(mixed, **ok)
+    with pytest.raises(ValueError, match="bfloat16"):
+        check_static_caches(caches(dtype=torch.float16), **ok)
+    strided = [(k.transpose(2, 3).contiguous().transpose(2, 3), v) for k, v in caches()]
+    with pytest.raises(ValueError, match="contiguous"):
+        check_static_caches(strided, **ok)
+    with pytest.raises(ValueError, match="positions"):
+        check_static_caches(caches(), **dict(ok, min_length=17))
+    with pytest.raises(ValueError, match="attention device"):
+        check_static_caches(caches(), **dict(ok, device="meta"))
+    check_token_ids(torch.zeros((2, 5), dtype=torch.int64), batch=2, length=None, device="cpu")
+    with pytest.raises(ValueError, match="shape"):
+        check_token_ids(torch.zeros((1, 5), dtype=torch.int64), batch=2, length=None, device="cpu")
+    with pytest.raises(ValueError, match="shape"):
+        check_token_ids(torch.zeros((2, 2), dtype=torch.int64), batch=2, length=1, device="cpu", name="token_ids")
+    with pytest.raises(ValueError, match="int64"):
+        check_token_ids(torch.zeros((2, 1), dtype=torch.int32), batch=2, length=1, device="cpu")

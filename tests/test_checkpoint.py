@@ -125,7 +125,7 @@ def test_quantized_key_suffixes():
 def test_model_quantized_tensors_match_the_reference_v4_inventory():
     config = SimpleNamespace(num_hidden_layers=28, **QWEN2_1_5B)
     with torch.device("meta"):
-        model = QwenInt4ForCausalLM(config)
+        model = QwenInt4ForCausalLM(config, packing="canonical", group_size=64)
     state = model.state_dict()
     quantized = {key: tuple(value.shape) for key, value in state.items() if is_quantized_key(key)}
     inventory = RTN_V4["tensor_inventory"]
@@ -237,9 +237,9 @@ def test_load_writes_through_fused_projection_views(tmp_path: Path):
     config = SimpleNamespace(num_hidden_layers=2, **dict(QWEN2_1_5B, hidden_size=128, num_attention_heads=2,
                                                          num_key_value_heads=1, head_dim=64, intermediate_size=256,
                                                          vocab_size=64))
-    source = _fill(QwenInt4ForCausalLM(config), 17)
+    source = _fill(QwenInt4ForCausalLM(config, packing="canonical", group_size=64), 17)
     path = save_quantized_checkpoint(source, tmp_path / "awq.safetensors", canonical_awq_metadata(group_size=64))
-    target = QwenInt4ForCausalLM(config)
+    target = QwenInt4ForCausalLM(config, packing="canonical", group_size=64)
     fused = fuse_projections(target)
     report = load_quantized_checkpoint(target, path)
     expected_keys = [k for k in source.state_dict() if is_quantized_key(k) or k.endswith(
@@ -261,8 +261,8 @@ def test_non_quantized_state_is_taken_from_the_base_model():
     config = SimpleNamespace(num_hidden_layers=2, **dict(QWEN2_1_5B, hidden_size=128, num_attention_heads=2,
                                                          num_key_value_heads=1, head_dim=64, intermediate_size=256,
                                                          vocab_size=64))
-    base = _fill(QwenInt4ForCausalLM(config), 31)
-    target = QwenInt4ForCausalLM(config)
+    base = _fill(QwenInt4ForCausalLM(config, packing="canonical", group_size=64), 31)
+    target = QwenInt4ForCausalLM(config, packing="canonical", group_size=64)
     state = extract_non_quantized_state(base, target)
     assert not any(is_quantized_key(k) for k in state)
     assert {"model.embed_tokens.weight", "model.norm.weight", "lm_head.weight",
@@ -380,17 +380,17 @@ def test_load_straight_to_the_gpu_matches_a_host_load(tmp_path: Path):
     decode) gives the same model, and the same logits, as a host load moved
     to the GPU afterwards."""
     config = SimpleNamespace(num_hidden_layers=2, **QWEN2_1_5B)
-    source = _fill(QwenInt4ForCausalLM(config), 19)
+    source = _fill(QwenInt4ForCausalLM(config, packing="canonical", group_size=64), 19)
     with torch.no_grad():
         for module in source.modules():
             if isinstance(module, QuantLinear):
                 module.scales.mul_(0.01)  # keep activations in range over two layers
     path = save_quantized_checkpoint(source, tmp_path / "awq.safetensors", canonical_awq_metadata(group_size=64))
-    host = QwenInt4ForCausalLM(config)
+    host = QwenInt4ForCausalLM(config, packing="canonical", group_size=64)
     load_quantized_checkpoint(host, path)
     host.model.embed_tokens.weight.data.copy_(source.model.embed_tokens.weight)
     host = host.cuda()
-    device = QwenInt4ForCausalLM(config).cuda()
+    device = QwenInt4ForCausalLM(config, packing="canonical", group_size=64).cuda()
     device.model.embed_tokens.weight.data.copy_(source.model.embed_tokens.weight)
     fuse_projections(device)
     report = load_quantized_checkpoint(device, path)
@@ -412,7 +412,7 @@ def test_exported_awq_checkpoint_round_trips_through_the_fused_decoder(tmp_path:
 
     config = SimpleNamespace(num_hidden_layers=2, **QWEN2_1_5B)
     gen = torch.Generator(device="cuda").manual_seed(23)
-    source = QwenInt4ForCausalLM(config).cuda()
+    source = QwenInt4ForCausalLM(config, packing="canonical", group_size=64).cuda()
     with torch.no_grad():
         source.model.embed_tokens.weight.copy_(torch.randn(source.model.embed_tokens.weight.shape, generator=gen,
                                                            device="cuda") * 0.02)
@@ -429,7 +429,7 @@ def test_exported_awq_checkpoint_round_trips_through_the_fused_decoder(tmp_path:
             if name.endswith("layernorm.weight"):
                 p.copy_(torch.rand(p.shape, generator=gen, device="cuda") + 0.5)
     path = save_quantized_checkpoint(source, tmp_path / "awq" / "model.safetensors", canonical_awq_metadata(group_size=64))
-    target = QwenInt4ForCausalLM(config).cuda()
+    target = QwenInt4ForCausalLM(config, packing="canonical", group_size=64).cuda()
     fuse_projections(target)
     # the reference's load order (src/qwen_int4/cli.py:92-95): base-model tensors, then the checkpoint
     load_non_quantized_state(target, extract_non_quantized_state(source, target))

@@ -449,7 +449,7 @@ def _build(config, seed):
     from qwen_int4_hip import QuantLinear, quantize_symmetric_rtn
 
     gen = _gen(seed)
-    model = QwenInt4ForCausalLM(config).cuda()
+    model = QwenInt4ForCausalLM(config, packing="canonical", group_size=64).cuda()
     with torch.no_grad():
         emb = model.model.embed_tokens.weight
         emb.copy_(torch.randn(emb.shape, generator=gen, device="cuda") * 0.02)

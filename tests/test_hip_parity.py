@@ -422,3 +422,38 @@ def test_hip_graph_capture_replays_match_eager():
         torch.cuda.synchronize()
         for got, ref in zip(again, eager):
             assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+
+
+def test_graphs_captured_before_and_after_workspace_growth_both_replay():
+    """A small-row graph captured on a stream, then (after an eager call grows
+    that stream's workspace) a large-row graph on the same stream: both keep
+    replaying correctly, interleaved -- the first graph's workspace was not
+    freed when the buffer grew."""
+    n, k = SHAPES["down_proj"]
+    q, s, z = weights("sym", n, k, O.BASE_SEED + n + k)
+    w = dev_weights(q, s, z)
+    small = to_dev(O.activations(4, k, seed=31, dtype="fp16"), "fp16")  # split-K GEMV: counters + partials
+    large = to_dev(O.activations(200, k, seed=32, dtype="bf16"), "bf16")  # split-K GEMM: tens of MB of partials
+    want_small = linear_canonical_w4g64_hip(small, *w)
+    want_large = linear_canonical_w4g64_hip(large, *w)
+    from qwen_int4_hip import kernels
+
+    side = torch.cuda.Stream()
+    graphs, outs, buffers = [], [], []
+    for x in (small, large):
+        with torch.cuda.stream(side):
+            linear_canonical_w4g64_hip(x, *w)  # warm-up: grows this stream's workspace outside capture
+        torch.cuda.synchronize()
+        buffers.append(kernels._workspaces[(torch.cuda.current_device(), side.cuda_stream)])
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=side):
+            outs.append(linear_canonical_w4g64_hip(x, *w))
+        graphs.append(graph)
+    assert buffers[1] is not buffers[0] and any(b is buffers[0] for b in kernels._retired)  # the buffer grew in between
+    for replay in range(3):
+        for graph in (graphs[1], graphs[0]):
+            graph.replay()
+            torch.cuda.synchronize()
+            linear_canonical_w4g64_hip(large, *w)  # eager work on the default stream between replays
+        assert torch.equal(outs[0].view(torch.int16), want_small.view(torch.int16)), f"replay {replay}"
+        assert torch.equal(outs[1].view(torch.int16), want_large.view(torch.int16)), f"replay {replay}"
