@@ -118,6 +118,25 @@ int w4g64_linear_timed(const void* x, int x_dtype, const uint8_t* qweight, const
                        int64_t out_features, int64_t in_features, void* workspace, int64_t workspace_bytes,
                        void* stream, void* start_event, void* stop_event);
 
+/* w4g64_linear without a workspace argument and without any allocation:
+ * its split-K partial sums and arrival counters live in a file-scope device
+ * array of the library (w4g64_static_scratch_bytes() bytes, 4 MiB, one per
+ * GPU, held until the process ends), whose address is looked up once per
+ * device on the first call there.  Problems that need more scratch than that
+ * (the split-K prefill GEMM; every decode call of 1..16 rows of the
+ * Qwen2-1.5B shapes fits) are rejected with W4G64_STATUS_UNSUPPORTED.  Calls
+ * on one GPU share the array: calls that overlap on one GPU (on different
+ * streams) race; calls in one stream order are safe, since every kernel
+ * leaves the counters at zero.  Same arguments, checks and results as
+ * w4g64_linear otherwise.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * (code under HIP graph capture, serving loops that forbid hipMalloc). */
+int w4g64_linear_static_scratch(const void* x, int x_dtype, const uint8_t* qweight, const uint16_t* scales,
+                                 const uint8_t* zeros, const void* bias, int bias_dtype, void* y, int64_t rows,
+                                 int64_t out_features, int64_t in_features, void* stream);
+/* Size in bytes of w4g64_linear_static_scratch's per-GPU array. */
+int64_t w4g64_static_scratch_bytes(void);
+
 /* Fusion of the SwiGLU product into the down projection: gate_up is
  * [rows, 2 * in_features] bf16 (gate | up), the activation is
  * h = silu(gate) * up in fp32 (silu(g) = g / (1 + exp(-g))), and

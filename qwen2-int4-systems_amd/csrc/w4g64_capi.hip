@@ -10,9 +10,15 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <mutex>
+
 #include "../../include/w4g64.h"
 #include "w4g64_device.h"
 #include "w4g64_internal.h"
+
+// The allocation-free entry point's scratch (w4g64_linear_static_scratch).
+constexpr int64_t kScratchBytes = 4ll << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
 namespace {
 
@@ -38,6 +44,49 @@ int element_bytes(int dtype) { return dtype == W4G64_DTYPE_F32 ? 4 : 2; }
 int hip_status(hipError_t err, const char* what) {
     if (err != hipSuccess) return fail(W4G64_STATUS_HIP_ERROR, "%s launch failed: %s", what, hipGetErrorString(err));
     return ok();
+}
+
+// ---- the allocation-free entry point's scratch ----
+// One file-scope device array per GPU, the workspace of
+// w4g64_linear_static_scratch: [64 KiB arrival counters][fp32 partial sums].
+// Every decode call (1..16 rows) of the Qwen2-1.5B shapes fits (at most
+// 3.34 MiB, fp32 gate|up at 16 rows); larger needs are rejected.  In host
+// code `scratch` names a host-side stand-in, never the device memory: the
+// device address comes from hipGetSymbolAddress, once per device, and only
+// that address is used.
+constexpr int kMaxScratchDevices = 64;
+
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+__global__ void zero_words_kernel(uint32_t* p, int64_t words) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < words) p[i] = 0u;
+}
+
+// The current device's scratch address, set up on the first call on that
+// device: the symbol's device address, and the counter area cleared by a
+// fill kernel on `stream` (no memset node: the caller may be capturing).
+int device_scratch(hipStream_t stream, void** out) {
+    int device = -1;
+    if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= kMaxScratchDevices)
+        return fail(W4G64_STATUS_HIP_ERROR, "no usable current HIP device (got %d)", device);
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (!g_scratch_ptr[device]) {
+        void* ptr = nullptr;
+        const hipError_t err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (err != hipSuccess || !ptr)
+            return fail(W4G64_STATUS_HIP_ERROR, "hipGetSymbolAddress(scratch) failed on device %d: %s", device,
+                        hipGetErrorString(err));
+        const int64_t words = w4g64::kGemvCounterBytes / 4;
+        hipLaunchKernelGGL(zero_words_kernel, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, stream,
+                           (uint32_t*)ptr, words);
+        if (hipGetLastError() != hipSuccess)
+            return fail(W4G64_STATUS_HIP_ERROR, "clearing the scratch counters failed on device %d", device);
+        g_scratch_ptr[device] = ptr;
+    }
+    *out = g_scratch_ptr[device];
+    return W4G64_STATUS_OK;
 }
 
 }  // namespace
@@ -205,6 +254,29 @@ int w4g64_linear_timed(const void* x, int x_dtype, const uint8_t* qweight, const
     return linear_impl(x, x_dtype, qweight, scales, zeros, bias, bias_dtype, y, rows, out_features, in_features,
                        workspace, workspace_bytes, stream, start_event, stop_event);
 }
+
+int w4g64_linear_static_scratch(const void* x, int x_dtype, const uint8_t* qweight, const uint16_t* scales,
+                                 const uint8_t* zeros, const void* bias, int bias_dtype, void* y, int64_t rows,
+                                 int64_t out_features, int64_t in_features, void* stream) {
+    // the problem's own checks first, then the scratch bound (its planner
+    // needs sane sizes), then the set-up, and nothing that allocates
+    if (rows <= 0 || in_features <= 0 || in_features % 64 || out_features <= 0 || rows > (1ll << 30) ||
+        in_features > (1ll << 30) || out_features > (1ll << 30))
+        return linear_impl(x, x_dtype, qweight, scales, zeros, bias, bias_dtype, y, rows, out_features, in_features,
+                           nullptr, 0, stream, nullptr, nullptr);
+    const int64_t need = w4g64_linear_workspace_bytes(rows, out_features, in_features, x_dtype);
+    if (need > kScratchBytes)
+        return fail(W4G64_STATUS_UNSUPPORTED,
+                    "this problem needs %lld bytes of scratch; the allocation-free entry point holds at most %lld "
+                    "(use w4g64_linear with a caller-owned workspace)",
+                    (long long)need, (long long)kScratchBytes);
+    void* ptr = nullptr;
+    if (int st = device_scratch((hipStream_t)stream, &ptr)) return st;
+    return linear_impl(x, x_dtype, qweight, scales, zeros, bias, bias_dtype, y, rows, out_features, in_features, ptr,
+                       kScratchBytes, stream, nullptr, nullptr);
+}
+
+int64_t w4g64_static_scratch_bytes(void) { return kScratchBytes; }
 
 // Shared checks of the fused decode entry points (weights, bias, sizes).
 static int fused_common_checks(const uint8_t* qweight, const uint16_t* scales, const uint8_t* zeros,
