@@ -178,8 +178,12 @@ const char* w4g64_linear_kernel_name(int64_t rows, int64_t out_features, int64_t
                    ? w4g64::gemv_kernel_name(w4g64::plan_gemv(rows, out_features, in_features, x_dtype), x_dtype)
                    : w4g64::gemm_kernel_name(rows, out_features, in_features, x_dtype);
     if (x_dtype != W4G64_DTYPE_F16 && x_dtype != W4G64_DTYPE_BF16 && x_dtype != W4G64_DTYPE_F32) return "none";
-    if (rows <= w4g64::kGemvMaxRows)
+    if (rows <= w4g64::kGemvMaxRows) {
+        w4g64::GemvPlan lean;
+        if (w4g64::plan_seg(rows, out_features, in_features, x_dtype, lean))
+            return w4g64::gemv_kernel_name(lean, x_dtype);  // with 16-byte aligned operands
         return w4g64::gemv_kernel_name(w4g64::plan_gemv(rows, out_features, in_features, x_dtype), x_dtype);
+    }
     return w4g64::gemm_kernel_name(rows, out_features, in_features, x_dtype);
 }
 
@@ -230,6 +234,10 @@ static int linear_impl(const void* x, int x_dtype, const uint8_t* qweight, const
         if (out_features > w4g64::kGemvMaxColumnBlocks * 64)
             return fail(W4G64_STATUS_UNSUPPORTED, "decode path supports at most %lld output features",
                         (long long)(w4g64::kGemvMaxColumnBlocks * 64));
+        w4g64::GemvPlan lean;
+        if (w4g64::plan_seg(rows, out_features, in_features, p.x_kind, lean) && w4g64::seg_supported(p))
+            return hip_status(w4g64::launch_gemv_seg(p, lean, s, (hipEvent_t)start_event, (hipEvent_t)stop_event),
+                              "gemv");
         const w4g64::GemvPlan plan = w4g64::plan_gemv(rows, out_features, in_features, p.x_kind);
         if (int st = check_workspace(workspace, workspace_bytes, plan.workspace_bytes)) return st;
         return hip_status(w4g64::launch_gemv(p, plan, workspace, s, (hipEvent_t)start_event, (hipEvent_t)stop_event),

@@ -49,6 +49,8 @@ struct GemvPlan {
     int splits;            // K splits across workgroups
     int groups_per_split;  // 64-wide K groups per split
     int tiles;             // 16-row MFMA A tiles (fp32 input uses 3 bf16 parts per row)
+    int kparts = 1;        // kind 2: K parts per workgroup (its waves split K)
+    int stage = 1;         // kind 2: staging loads per lane
     int64_t lds_bytes;     // dynamic LDS per workgroup
     int64_t workspace_bytes;
     int64_t counter_bytes;
@@ -71,6 +73,16 @@ bool plan_rows16(int64_t rows, int64_t out_features, int64_t in_features, GemvPl
                  int force_waves, int force_splits);
 hipError_t launch_gemv16(const LinearProblem& p, const GemvPlan& plan, void* workspace, hipStream_t stream,
                          hipEvent_t start, hipEvent_t stop);
+
+// Lean decode GEMV (one fp16/bf16 row, even group count, N G 2 and N P
+// multiples of 16, at most three 16-byte weight loads per lane): whole rows
+// per workgroup, no workspace.  plan.kind = 2; segments, fblocks (row blocks)
+// and kparts (K parts) select the shape, stage the staging loads per lane.
+bool plan_seg(int64_t rows, int64_t out_features, int64_t in_features, int x_kind, GemvPlan& plan);
+// Pointer alignment and forms the lean kernel takes (plain linear only).
+bool seg_supported(const LinearProblem& p);
+hipError_t launch_gemv_seg(const LinearProblem& p, const GemvPlan& plan, hipStream_t stream, hipEvent_t start,
+                           hipEvent_t stop);
 
 // Prefill GEMM v2 (pipelined, fp16/bf16 activations).  Tiles of a last,
 // mostly empty round of workgroups (or all tiles, when there are fewer than

@@ -235,7 +235,16 @@ def test_workspace_and_kernel_plan_queries():
     assert 64 * 1024 + 512 * 8960 * 4 <= ws32 <= 64 * 1024 + (64 << 20) + 512 * 8960 * 4 + 256
     assert lib.w4g64_linear_kernel_name(512, 1536, 8960, _lib.DTYPE_F32).startswith(b"gemm2_kernel<bf16 hi|lo")
     assert lib.w4g64_linear_workspace_bytes(1, 1536, 100, _lib.DTYPE_F16) == 0
-    assert lib.w4g64_linear_kernel_name(1, 8960, 1536, _lib.DTYPE_F16).startswith(b"gemv_kernel<f16")
+    # one row of even-group shapes with at most three 16-byte weight loads per
+    # lane: the lean kernel (no workspace)
+    assert lib.w4g64_linear_kernel_name(1, 8960, 1536, _lib.DTYPE_F16) == b"gemv_seg_kernel<f16,4,4,1,3>"
+    assert lib.w4g64_linear_kernel_name(1, 1536, 1536, _lib.DTYPE_BF16) == b"gemv_seg_kernel<bf16,4,1,4,1>"
+    assert lib.w4g64_linear_workspace_bytes(1, 8960, 1536, _lib.DTYPE_F16) == 0
+    # odd group counts, the long-K down projection and several rows keep the segmented kernel
+    assert lib.w4g64_linear_kernel_name(1, 64, 192, _lib.DTYPE_F16).startswith(b"gemv_kernel<f16")
+    assert lib.w4g64_linear_kernel_name(1, 1536, 8960, _lib.DTYPE_F16).startswith(b"gemv_kernel<f16")
+    assert lib.w4g64_linear_kernel_name(4, 1536, 1536, _lib.DTYPE_BF16).startswith(b"gemv_kernel<bf16")
+    assert lib.w4g64_linear_kernel_name(8, 1536, 8960, _lib.DTYPE_F16).startswith(b"gemv_kernel<f16")
     assert lib.w4g64_linear_kernel_name(16, 1536, 8960, _lib.DTYPE_BF16) == b"gemv16_kernel<bf16,9,4,2>"
     assert lib.w4g64_linear_kernel_name(16, 8960, 1536, _lib.DTYPE_F16) == b"gemv16_kernel<f16,6,4,3>"
     assert lib.w4g64_linear_kernel_name(16, 1536, 1536, _lib.DTYPE_F16) == b"gemv16_kernel<f16,3,8,1>"

@@ -181,6 +181,57 @@ def test_decode_all_qwen2_shapes_fp16(name, rows):
     assert np.mean(np.abs(out - ref) <= ulp) > 0.99
 
 
+LEAN_SHAPES = [(2048, 1536, "sym"), (17920, 1536, "asym"), (1536, 8960, "awq"), (200, 256, "asym"),
+                  (256, 1536, "sym")]
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+@pytest.mark.parametrize("rows", [1, 2, 3, 5, 8])
+@pytest.mark.parametrize("n,k,kind", LEAN_SHAPES)
+def test_lean_decode_kernel(n, k, kind, rows, dtype):
+    """Decode shapes through the GEMV kernels: one row of the fused q|k|v and
+    gate|up widths, of a partial last row block (200 features) and of a
+    256-wide projection takes the lean kernel (16-byte weight loads, whole
+    rows per workgroup); the long-K down projection and several rows take the
+    segmented kernel.  Bias, asymmetric and AWQ-folded codes."""
+    from qwen_int4_hip import linear_kernel_name
+
+    torch_dtype = torch.float16 if dtype == "fp16" else torch.bfloat16
+    lean = rows == 1 and k <= 1536
+    assert linear_kernel_name(rows, n, k, torch_dtype).startswith("gemv_seg_kernel" if lean else "gemv_kernel")
+    q, s, z = weights(kind, n, k, O.BASE_SEED + n + k + rows)
+    x = O.activations(rows, k, seed=O.BASE_SEED + 13 * rows + n, dtype=dtype, outliers=kind != "sym")
+    bias = O.f32_to_bf16_bits(np.random.default_rng(n + rows).standard_normal(n).astype(np.float32) * np.float32(0.1))
+    out, ref = check_linear(x, q, s, z, bias, n, k, dtype)
+    if dtype == "fp16":  # exact (code - zero) in fp16: within one fp16 ulp almost everywhere
+        ulp = np.spacing(np.abs(ref).astype(np.float16)).astype(np.float32)
+        assert np.mean(np.abs(out - ref) <= ulp) > 0.99
+
+
+@pytest.mark.parametrize("name", ["gate_proj", "q_proj"])
+def test_lean_and_segmented_kernels_agree(name):
+    """The same problem through the lean kernel and, with a scales view that
+    is only 2-byte aligned (which the lean kernel does not take), through the
+    segmented kernel: both round fp32 values that differ only by summation
+    order (the lean kernel applies zero points after the MFMA), so they agree
+    within two fp16 ulps."""
+    from qwen_int4_hip import linear_kernel_name
+
+    n, k = SHAPES[name]
+    assert linear_kernel_name(1, n, k, torch.float16).startswith("gemv_seg_kernel")
+    q, s, z = weights("asym", n, k, O.BASE_SEED + 5)
+    xt = to_dev(O.activations(1, k, seed=O.BASE_SEED + 6, dtype="fp16"), "fp16")
+    qd, sd, zd = dev_weights(q, s, z)
+    fast = linear_canonical_w4g64_hip(xt, qd, sd, zd)
+    shifted = torch.empty(sd.numel() + 1, dtype=torch.float16, device=DEV)
+    shifted[1:].copy_(sd.reshape(-1))
+    slow = linear_canonical_w4g64_hip(xt, qd, shifted[1:].view(sd.shape), zd)
+    diff = (fast.float() - slow.float()).abs().cpu()
+    big = torch.maximum(fast.float().abs(), slow.float().abs()).cpu().numpy().astype(np.float16)
+    ulp = torch.from_numpy(np.spacing(big).astype(np.float32))
+    assert bool((diff <= 2 * ulp).all()), float((diff / ulp).max())
+
+
 @pytest.mark.parametrize("rows", [128, 512, 2048])
 @pytest.mark.parametrize("name", ["gate_proj", "down_proj"])
 def test_prefill_mlp_shapes_bf16(name, rows):
