@@ -18,11 +18,16 @@
 //     distinct 16-byte bank groups, so fragment reads are conflict-free.
 //   * Weights (B): each wave reads back its own packed columns (16 B = 32
 //     consecutive K values per lane and column block) and dequantizes only
-//     its own columns:
-//     (code - zero) built exactly in fp16 with the magic-number trick in
-//     natural K order (v_perm + v_bitop3), then times the scale: fp16 weights
-//     are RNE((code - zero) * scale) in fp16; bf16 weights are
-//     RNE(fp32((code - zero) * scale)).
+//     its own columns, one MFMA sub-step ahead of their use, into exact
+//     weights: w = (code - zero) * scale has at most 15 significant bits, so
+//     it is exact in fp32, and it is split into hi = RNE(w) in the MFMA type
+//     and lo = w - hi, which that type also holds exactly (bf16: at most 8
+//     bits remain; fp16: lo is a multiple of the scale's last bit, itself a
+//     multiple of 2^-24, with at most 5 significant bits).  Every B fragment
+//     is multiplied twice, x * hi + x * lo == x * w: the products are those
+//     of the exact fp32 weights, as in a dequantize-then-fp32-matmul, and
+//     only the fp32 accumulation order differs.  (fp16 weights with |w| >
+//     65504 overflow hi; fp16 outputs of such a product would overflow too.)
 //   * MFMA K slots: lane group q (of 2) takes K values [32q, 32q + 32) of the
 //     group, sub-step kk uses [32q + 8kk, 32q + 8kk + 8); A and B fragments
 //     use the same slots, so the contraction is unchanged.
@@ -36,10 +41,9 @@
 //     activation band in their L2.
 //   * fp32 activations: a first kernel splits each row into two bf16 planes,
 //     hi = RNE(x) and lo = RNE(x - hi) (16 significant bits, |x - hi - lo| <=
-//     2^-17 |x|, below the bf16-rounded dequantized weight's own 2^-9), laid
-//     out as one row [hi | lo] of 2K values in the workspace; the GEMM then
-//     runs over K' = 2K with weight group g mod G, so both planes meet the
-//     same dequantized weights, and stores fp32 outputs.
+//     2^-17 |x|), laid out as one row [hi | lo] of 2K values in the
+//     workspace; the GEMM then runs over K' = 2K with weight group g mod G,
+//     so both planes meet the same exact weights, and stores fp32 outputs.
 #include <type_traits>
 
 #include "w4g64_device.h"
@@ -90,18 +94,19 @@ __device__ __forceinline__ void wait_vmcnt() {
 // the 8 rows of either parity among 16 consecutive rows.
 __device__ __forceinline__ int a_swizzle(int r) { return ((r >> 1) & 7) ^ ((r & 1) << 2); }
 
-// Scheduling shape of one sub-step: each of the MB A-fragment reads is paired
-// with two MFMAs, with up to V other VALU instructions after each MFMA, and
-// no instruction crosses the end of the sub-step.
-template <int MB, int V>
+// Scheduling shape of one sub-step: each of the MB A-fragment reads is
+// followed by 2 P MFMAs, with up to V other VALU instructions after each
+// MFMA, and no instruction crosses the end of the sub-step.
+template <int MB, int P, int V>
 __device__ __forceinline__ void sched_interleave() {
 #pragma unroll
     for (int i = 0; i < MB; ++i) {
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-        if constexpr (V > 0) __builtin_amdgcn_sched_group_barrier(0x002, V, 0);  // VALU
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-        if constexpr (V > 0) __builtin_amdgcn_sched_group_barrier(0x002, V, 0);  // VALU
+#pragma unroll
+        for (int p = 0; p < 2 * P; ++p) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+            if constexpr (V > 0) __builtin_amdgcn_sched_group_barrier(0x002, V, 0);  // VALU
+        }
     }
     __builtin_amdgcn_sched_barrier(0);
 }
@@ -127,34 +132,52 @@ __device__ __forceinline__ uint32_t nib_pair_natural(uint32_t w, int b) {
     return ((rep ^ kSel) & kMask) | (kSel & ~kMask);
 }
 
-// Dequantized weights of one packed dword (8 consecutive K values of one
-// column) as 4 natural-order fp16 / bf16 pairs.
-//   fp16: (m - c) is exact in fp16 (m = magic value, c = magic offset + zero),
-//         then one fp16 multiply by the scale: RNE(d * scale).
-//   bf16: d * s = m * s - c * s, and both products fit in 22 bits, so one fp32
-//         FMA against the precomputed exact c * s yields d * s exactly;
-//         then RNE to bf16.
+// Per-group constants of one column's dequantization.
+struct BConst {
+    uint32_t zc;  // fp16: bits of (1032 + z, 72 + z)
+    uint32_t s2;  // fp16: bits of (scale, scale)
+    float s;      // bf16: the scale
+    float cs_lo;  // bf16: (1032 + z) * scale, exact (11-bit by 11-bit product)
+    float cs_hi;  // bf16: (72 + z) * scale, exact
+};
+
+// Exact weights of one packed dword (8 consecutive K values of one column)
+// as the hi and lo B fragments (4 natural-order pairs each).
+//   fp16: d = (m - c) is exact in fp16 (m = magic value, c = magic offset +
+//         zero); hi = RNE(d * scale) by one packed fp16 multiply; lo = d *
+//         scale - hi by an fp32 FMA of the fp16 operands (exact product,
+//         exact difference), exact in fp16.
+//   bf16: w = d * s = m * s - c * s, and both products fit in 22 bits, so
+//         one fp32 FMA against the precomputed exact c * s yields w exactly;
+//         hi = RNE(w) in bf16 and lo = RNE(w - hi) = w - hi.
 template <int XK>
-__device__ __forceinline__ u32x4 dequant_natural(uint32_t w, uint32_t zc_bits, uint32_t s2_bits, float s,
-                                                 float cs_lo, float cs_hi) {
-    u32x4 out;
+__device__ __forceinline__ void dequant_hl(uint32_t w, const BConst& c, u32x4& hi, u32x4& lo) {
     if constexpr (XK == kF16) {
-        const half2v zc = __builtin_bit_cast(half2v, zc_bits);   // (1032 + z, 72 + z)
-        const half2v s2 = __builtin_bit_cast(half2v, s2_bits);   // (scale, scale)
+        const half2v zc = __builtin_bit_cast(half2v, c.zc);
+        const half2v s2 = __builtin_bit_cast(half2v, c.s2);
+        const float s = (float)s2[0];
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
-            const half2v v = (__builtin_bit_cast(half2v, nib_pair_natural(w, b)) - zc) * s2;
-            out[b] = __builtin_bit_cast(uint32_t, v);
+            const half2v d = __builtin_bit_cast(half2v, nib_pair_natural(w, b)) - zc;
+            const half2v h = d * s2;
+            const half2v l = {(_Float16)__builtin_fmaf((float)d[0], s, -(float)h[0]),
+                              (_Float16)__builtin_fmaf((float)d[1], s, -(float)h[1])};
+            hi[b] = __builtin_bit_cast(uint32_t, h);
+            lo[b] = __builtin_bit_cast(uint32_t, l);
         }
     } else {
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
             const half2v m = __builtin_bit_cast(half2v, nib_pair_natural(w, b));  // (1024 + n', 64 + n')
-            const float2v f = {__builtin_fmaf((float)m[0], s, -cs_lo), __builtin_fmaf((float)m[1], s, -cs_hi)};
-            out[b] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2v));  // one RNE pair conversion
+            const float w0 = __builtin_fmaf((float)m[0], c.s, -c.cs_lo);
+            const float w1 = __builtin_fmaf((float)m[1], c.s, -c.cs_hi);
+            const uint32_t hb = __builtin_bit_cast(uint32_t, __builtin_convertvector(float2v{w0, w1}, bf16x2v));
+            const float h0 = __builtin_bit_cast(float, hb << 16);
+            const float h1 = __builtin_bit_cast(float, hb & 0xFFFF0000u);
+            hi[b] = hb;
+            lo[b] = __builtin_bit_cast(uint32_t, __builtin_convertvector(float2v{w0 - h0, w1 - h1}, bf16x2v));
         }
     }
-    return out;
 }
 
 template <int XK, int BM, int OUTK>
@@ -263,8 +286,8 @@ __global__ __launch_bounds__(256, 2) void gemm2_kernel(Gemm2Args a) {
         zpar[bj] = (int)(((n < a.N ? n : a.N - 1) * a.wg) & 1);
     }
 
-    // B fragments of step g, column block bj: this wave's packed columns,
-    // read back from the stage and dequantized in natural K order.
+    // Packed weights of step g, column block bj, read back from the stage:
+    // dword kk holds K values [32q + 8kk, +8) of column nw + 32 bj + j.
     struct BRaw {
         u32x4 w;
         uint32_t sbits;
@@ -279,18 +302,18 @@ __global__ __launch_bounds__(256, 2) void gemm2_kernel(Gemm2Args a) {
         r.zb = st[kABytes + kWBytes + kSBytes + 256 * wave + 4 * c];
         return r;
     };
-    auto dequant_b = [&](int g, int bj, const BRaw& r, u32x4 (&bf)[2][4]) {
+    auto group_const = [&](int g, int bj, const BRaw& r) {
         int zn = (int)(((zpar[bj] ^ wgroup(g)) & 1) ? (r.zb >> 4) : (r.zb & 0xF));
         zn -= (zn & 8) << 1;
+        BConst c;
         const uint32_t zlo = 0x6408u + (uint32_t)zn;       // fp16 bits of 1032 + z
         const uint32_t zhi = 0x5480u + 16u * (uint32_t)zn;  // fp16 bits of 72 + z
-        const uint32_t zc = (zlo & 0xFFFFu) | ((zhi & 0xFFFFu) << 16);
-        const float s = half_bits_to_float((uint16_t)r.sbits);
-        const uint32_t s2 = (r.sbits & 0xFFFFu) * 0x00010001u;
-        const float cs_lo = (float)(1032 + zn) * s;  // exact: 11-bit by 11-bit product
-        const float cs_hi = (float)(72 + zn) * s;
-#pragma unroll
-        for (int kk = 0; kk < 4; ++kk) bf[bj][kk] = dequant_natural<XK>(r.w[kk], zc, s2, s, cs_lo, cs_hi);
+        c.zc = (zlo & 0xFFFFu) | ((zhi & 0xFFFFu) << 16);
+        c.s2 = (r.sbits & 0xFFFFu) * 0x00010001u;
+        c.s = half_bits_to_float((uint16_t)r.sbits);
+        c.cs_lo = (float)(1032 + zn) * c.s;
+        c.cs_hi = (float)(72 + zn) * c.s;
+        return c;
     };
     // A fragments of sub-step kk from the swizzled stage.
     const int fr = lane & 31;
@@ -302,32 +325,49 @@ __global__ __launch_bounds__(256, 2) void gemm2_kernel(Gemm2Args a) {
             af[bi] = *(const u32x4*)(st + r * 128 + chunk * 16);
         }
     };
-    auto mma = [&](const u32x4 (&af)[MB], const u32x4 (&bf)[2][4], int kk) {
-#pragma unroll
-        for (int bi = 0; bi < MB; ++bi) {
-#pragma unroll
-            for (int bj = 0; bj < 2; ++bj) {
-                if constexpr (XK == kF16) {
-                    acc[bi][bj] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-                        __builtin_bit_cast(half8, af[bi]), __builtin_bit_cast(half8, bf[bj][kk]), acc[bi][bj], 0, 0, 0);
-                } else {
-                    acc[bi][bj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                        __builtin_bit_cast(bf16x8, af[bi]), __builtin_bit_cast(bf16x8, bf[bj][kk]), acc[bi][bj], 0,
-                        0, 0);
-                }
-            }
-        }
+    // B fragments of one sub-step: [column block][hi, lo]
+    struct BFrag {
+        u32x4 v[2][2];
     };
+    auto dequant = [&](const u32x4 (&w)[2], const BConst (&c)[2], int kk) {
+        BFrag f;
+#pragma unroll
+        for (int bj = 0; bj < 2; ++bj) dequant_hl<XK>(w[bj][kk], c[bj], f.v[bj][0], f.v[bj][1]);
+        return f;
+    };
+    // every hi product, then every lo product: 2 MB independent MFMAs
+    // separate the two that update one accumulator
+    auto mma = [&](const u32x4 (&af)[MB], const BFrag& bf) {
+#pragma unroll
+        for (int hl = 0; hl < 2; ++hl)
+#pragma unroll
+            for (int bi = 0; bi < MB; ++bi)
+#pragma unroll
+                for (int bj = 0; bj < 2; ++bj) {
+                    if constexpr (XK == kF16) {
+                        acc[bi][bj] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                            __builtin_bit_cast(half8, af[bi]), __builtin_bit_cast(half8, bf.v[bj][hl]), acc[bi][bj],
+                            0, 0, 0);
+                    } else {
+                        acc[bi][bj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                            __builtin_bit_cast(bf16x8, af[bi]), __builtin_bit_cast(bf16x8, bf.v[bj][hl]),
+                            acc[bi][bj], 0, 0, 0);
+                    }
+                }
+    };
+    constexpr int kV = XK == kF16 ? 4 : 6;  // dequant VALU instructions placed after each MFMA
 
     // ---- rotated software pipeline ----
-    // Step g, four sub-steps of 2 * MB MFMAs each:
-    //   kk = 0: read this wave's B data of step g + 1 and the A fragments of
-    //           kk = 1;
-    //   kk = 1, 2: read the A fragments of kk + 1; dequantize B of step g + 1
-    //           (column block kk - 1) between the MFMAs;
+    // Step g, four sub-steps of 4 MB MFMAs each (hi and lo weights):
+    //   kk = 0: read this wave's packed B data of step g + 1 and the A
+    //           fragments of kk = 1; dequantize B of step g, kk = 1;
+    //   kk = 1: read the A fragments of kk = 2; dequantize B of kk = 2;
+    //   kk = 2: read the A fragments of kk = 3; dequantize B of kk = 3 and
+    //           form step g + 1's scale and zero constants;
     //   kk = 3: workgroup barrier (every wave has finished reading stage g and
     //           all of step g + 1 has landed), refill stage g with step g + 3,
-    //           read the A fragments of step g + 1, kk = 0.
+    //           read the A fragments of step g + 1, kk = 0, and dequantize
+    //           its B of kk = 0.
     // "Step s has landed" for this wave = its vector memory counter is at most
     // the number of operations issued after step s's (in-order completion).
     // Steps g + 3 < G run the branch-free body; the last (up to) three steps
@@ -341,13 +381,15 @@ __global__ __launch_bounds__(256, 2) void gemm2_kernel(Gemm2Args a) {
     else wait_vmcnt<0>();
     block_barrier();
 
-    u32x4 bcur[2][4];
-    {
-        const BRaw r0 = read_b(0, 0);
-        const BRaw r1 = read_b(0, 1);
-        dequant_b(0, 0, r0, bcur);
-        dequant_b(0, 1, r1, bcur);
+    u32x4 wcur[2];
+    BConst ccur[2];
+#pragma unroll
+    for (int bj = 0; bj < 2; ++bj) {
+        const BRaw r = read_b(0, bj);
+        wcur[bj] = r.w;
+        ccur[bj] = group_const(0, bj, r);
     }
+    BFrag bcur = dequant(wcur, ccur, 0);
     u32x4 a0[MB], a1[MB];
     read_a(smem[0], 0, a0);
 
@@ -358,22 +400,24 @@ __global__ __launch_bounds__(256, 2) void gemm2_kernel(Gemm2Args a) {
         // ---- kk = 0 ----
         if constexpr (kTail) wait_vmcnt<0>();
         else wait_vmcnt<kOpsPerStep>();  // this wave's loads of step g + 1
-        const BRaw r0 = read_b(gn, 0);
-        const BRaw r1 = read_b(gn, 1);
+        const BRaw rn0 = read_b(gn, 0);
+        const BRaw rn1 = read_b(gn, 1);
         read_a(st, 1, a1);
-        mma(a0, bcur, 0);
-        sched_interleave<MB, 0>();
+        const BFrag b1 = dequant(wcur, ccur, 1);
+        mma(a0, bcur);
+        sched_interleave<MB, 2, kV>();
         // ---- kk = 1 ----
-        u32x4 bnext[2][4];
         read_a(st, 2, a0);
-        dequant_b(gn, 0, r0, bnext);
-        mma(a1, bcur, 1);
-        sched_interleave<MB, XK == kF16 ? 5 : 6>();
+        const BFrag b2 = dequant(wcur, ccur, 2);
+        mma(a1, b1);
+        sched_interleave<MB, 2, kV>();
         // ---- kk = 2 ----
         read_a(st, 3, a1);
-        dequant_b(gn, 1, r1, bnext);
-        mma(a0, bcur, 2);
-        sched_interleave<MB, XK == kF16 ? 5 : 6>();
+        const BFrag b3 = dequant(wcur, ccur, 3);
+        const u32x4 wnext[2] = {rn0.w, rn1.w};
+        const BConst cnext[2] = {group_const(gn, 0, rn0), group_const(gn, 1, rn1)};
+        mma(a0, b2);
+        sched_interleave<MB, 2, kV>();
         // ---- kk = 3 ----
         if (!kTail || g + 1 < G) {
             wait_lgkmcnt0();
@@ -381,12 +425,14 @@ __global__ __launch_bounds__(256, 2) void gemm2_kernel(Gemm2Args a) {
             if (!kTail) issue(g + 3);
         }
         read_a(smem[(g + 1) % kStages], 0, a0);
-        mma(a1, bcur, 3);
-        sched_interleave<MB, 1>();
+        bcur = dequant(wnext, cnext, 0);
+        mma(a1, b3);
+        sched_interleave<MB, 2, kV>();
 #pragma unroll
-        for (int bj = 0; bj < 2; ++bj)
-#pragma unroll
-            for (int kk = 0; kk < 4; ++kk) bcur[bj][kk] = bnext[bj][kk];
+        for (int bj = 0; bj < 2; ++bj) {
+            wcur[bj] = wnext[bj];
+            ccur[bj] = cnext[bj];
+        }
     };
     int g = 0;
     for (; g + 3 < G; ++g) step(g, std::false_type{});

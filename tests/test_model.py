@@ -143,8 +143,9 @@ def test_static_graph_decoder_matches_growing_cache_generation():
 
 # Allowed distance to the reference backend, as a multiple of the distance of
 # an exact-weight fp64-accumulation model (the model's own sensitivity to
-# summation order at this depth).
-FLOOR_FACTOR = 2.5
+# summation order at this depth).  Every HIP linear multiplies the exact fp32
+# weights, as the reference does, so only summation order separates them.
+FLOOR_FACTOR = 1.2
 
 QWEN2_1_5B = dict(hidden_size=1536, num_attention_heads=12, num_key_value_heads=2, head_dim=128,
                   intermediate_size=8960, vocab_size=151936, rms_norm_eps=1e-6, rope_theta=1_000_000.0)
@@ -198,9 +199,9 @@ def test_full_size_qwen2_logits_against_model_sensitivity():
     exact-weight fp64-accumulation model lands at cosine ~0.99965 of the
     reference backend (1 - cosine grows ~1.2e-5 per layer), so the 0.9999 gate
     cannot be met at this depth by any implementation that does not repeat the
-    reference's own fp32 summation order.  The HIP model must stay within
-    2.5x that intrinsic distance (measured: 2x, from the prefill GEMM's
-    bf16-rounded dequantized weights) and at cosine >= 0.999."""
+    reference's own fp32 summation order.  The HIP model, whose linears
+    multiply the exact fp32 weights, must stay within 1.2x that intrinsic
+    distance and at cosine >= 0.999."""
     config = SimpleNamespace(num_hidden_layers=28, **QWEN2_1_5B)
     model = build(config, 20260831, "cuda")
     prompt = torch.randint(0, config.vocab_size, (1, 64), generator=torch.Generator().manual_seed(4)).cuda()
@@ -211,6 +212,7 @@ def test_full_size_qwen2_logits_against_model_sensitivity():
         del ref
         floor = 1.0 - cosine(with_f64_linears(model)(prompt), want)
     distance = 1.0 - cosine(got, want)
+    print(f"28 layers, 64-token prompt: 1-cos {distance:.3e} (floor {floor:.3e})")
     assert distance <= max(FLOOR_FACTOR * floor, 1e-4), f"1 - cosine = {distance:.3e}, model sensitivity {floor:.3e}"
     assert distance <= 1e-3
 
