@@ -81,14 +81,14 @@ int w4g64_dequantize_canonical(const uint8_t* qweight, const uint16_t* scales, c
                                float* out, int64_t out_features, int64_t in_features, void* stream);
 
 /* Bytes of workspace w4g64_linear needs for this problem (0 = none).
- * Layout: a fixed 64 KiB area of per-column-block arrival counters, then the
- * fp32 split-K partial sums (decode shapes that split K across workgroups;
- * prefill shapes whose tiles do not fill whole rounds of the device's
- * workgroup slots, up to 64 MiB of partials).  The counter area must be zero
- * before the first call and every call leaves it zero, so a caller allocates
- * and clears one workspace once (sized for its largest problem) and reuses it
- * for every shape.  Calls sharing a workspace must be ordered on one stream.
- * The prefill plan depends on the current device's CU count. */
+ * It holds fp32 split-K partial sums (decode shapes that split K across
+ * workgroups; prefill shapes whose tiles do not fill whole rounds of the
+ * device's workgroup slots, up to 64 MiB) -- and, for fp32 activations of the
+ * prefill GEMM, their two bf16 planes.  Every call writes what it reads, so a
+ * workspace needs no initial contents: a caller allocates one (sized for its
+ * largest problem) and reuses it for every shape.  Calls sharing a workspace
+ * must be ordered on one stream.  The prefill plan depends on the current
+ * device's CU count. */
 int64_t w4g64_linear_workspace_bytes(int64_t rows, int64_t out_features, int64_t in_features,
                                      int x_dtype);
 
@@ -119,15 +119,15 @@ int w4g64_linear_timed(const void* x, int x_dtype, const uint8_t* qweight, const
                        void* stream, void* start_event, void* stop_event);
 
 /* w4g64_linear without a workspace argument and without any allocation:
- * its split-K partial sums and arrival counters live in a file-scope device
+ * its split-K partial sums live in a file-scope device
  * array of the library (w4g64_static_scratch_bytes() bytes, 4 MiB, one per
  * GPU, held until the process ends), whose address is looked up once per
  * device on the first call there.  Problems that need more scratch than that
  * (the split-K prefill GEMM; every decode call of 1..16 rows of the
  * Qwen2-1.5B shapes fits) are rejected with W4G64_STATUS_UNSUPPORTED.  Calls
  * on one GPU share the array: calls that overlap on one GPU (on different
- * streams) race; calls in one stream order are safe, since every kernel
- * leaves the counters at zero.  Same arguments, checks and results as
+ * streams) race; calls in one stream order are safe, since every call
+ * writes the partials it reads.  Same arguments, checks and results as
  * w4g64_linear otherwise.
  * No counterpart in the reference: it is for callers that cannot allocate
  * (code under HIP graph capture, serving loops that forbid hipMalloc). */

@@ -48,9 +48,10 @@ int hip_status(hipError_t err, const char* what) {
 
 // ---- the allocation-free entry point's scratch ----
 // One file-scope device array per GPU, the workspace of
-// w4g64_linear_static_scratch: [64 KiB arrival counters][fp32 partial sums].
-// Every decode call (1..16 rows) of the Qwen2-1.5B shapes fits (at most
-// 3.34 MiB, fp32 gate|up at 16 rows); larger needs are rejected.  In host
+// w4g64_linear_static_scratch: the split-K partial sums (fp32), written in
+// full by every call that uses them, so nothing in it needs clearing.  Every
+// decode call (1..16 rows) of the Qwen2-1.5B shapes fits (at most 3.28 MiB,
+// fp32 gate|up at 16 rows); larger needs are rejected.  In host
 // code `scratch` names a host-side stand-in, never the device memory: the
 // device address comes from hipGetSymbolAddress, once per device, and only
 // that address is used.
@@ -59,15 +60,9 @@ constexpr int kMaxScratchDevices = 64;
 std::mutex g_scratch_mutex;
 void* g_scratch_ptr[kMaxScratchDevices] = {};
 
-__global__ void zero_words_kernel(uint32_t* p, int64_t words) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < words) p[i] = 0u;
-}
-
-// The current device's scratch address, set up on the first call on that
-// device: the symbol's device address, and the counter area cleared by a
-// fill kernel on `stream` (no memset node: the caller may be capturing).
-int device_scratch(hipStream_t stream, void** out) {
+// The current device's scratch address: the symbol's device address, looked
+// up on the first call on that device.
+int device_scratch(void** out) {
     int device = -1;
     if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= kMaxScratchDevices)
         return fail(W4G64_STATUS_HIP_ERROR, "no usable current HIP device (got %d)", device);
@@ -78,11 +73,6 @@ int device_scratch(hipStream_t stream, void** out) {
         if (err != hipSuccess || !ptr)
             return fail(W4G64_STATUS_HIP_ERROR, "hipGetSymbolAddress(scratch) failed on device %d: %s", device,
                         hipGetErrorString(err));
-        const int64_t words = w4g64::kGemvCounterBytes / 4;
-        hipLaunchKernelGGL(zero_words_kernel, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, stream,
-                           (uint32_t*)ptr, words);
-        if (hipGetLastError() != hipSuccess)
-            return fail(W4G64_STATUS_HIP_ERROR, "clearing the scratch counters failed on device %d", device);
         g_scratch_ptr[device] = ptr;
     }
     *out = g_scratch_ptr[device];
@@ -231,9 +221,9 @@ static int linear_impl(const void* x, int x_dtype, const uint8_t* qweight, const
                            out_features, in_features};
     hipStream_t s = (hipStream_t)stream;
     if (rows <= w4g64::kGemvMaxRows) {
-        if (out_features > w4g64::kGemvMaxColumnBlocks * 64)
+        if (out_features > w4g64::kGemvMaxOutFeatures)
             return fail(W4G64_STATUS_UNSUPPORTED, "decode path supports at most %lld output features",
-                        (long long)(w4g64::kGemvMaxColumnBlocks * 64));
+                        (long long)(w4g64::kGemvMaxOutFeatures));
         w4g64::GemvPlan lean;
         if (w4g64::plan_seg(rows, out_features, in_features, p.x_kind, lean) && w4g64::seg_supported(p))
             return hip_status(w4g64::launch_gemv_seg(p, lean, s, (hipEvent_t)start_event, (hipEvent_t)stop_event),
@@ -279,7 +269,7 @@ int w4g64_linear_static_scratch(const void* x, int x_dtype, const uint8_t* qweig
                     "(use w4g64_linear with a caller-owned workspace)",
                     (long long)need, (long long)kScratchBytes);
     void* ptr = nullptr;
-    if (int st = device_scratch((hipStream_t)stream, &ptr)) return st;
+    if (int st = device_scratch(&ptr)) return st;
     return linear_impl(x, x_dtype, qweight, scales, zeros, bias, bias_dtype, y, rows, out_features, in_features, ptr,
                        kScratchBytes, stream, nullptr, nullptr);
 }
@@ -300,9 +290,9 @@ static int fused_common_checks(const uint8_t* qweight, const uint16_t* scales, c
     if (in_features <= 0 || in_features % 64 || in_features > (1ll << 24))
         return fail(W4G64_STATUS_INVALID_VALUE, "in_features must be a positive multiple of 64, got %lld",
                     (long long)in_features);
-    if (out_features <= 0 || out_features > w4g64::kGemvMaxColumnBlocks * 64)
+    if (out_features <= 0 || out_features > w4g64::kGemvMaxOutFeatures)
         return fail(W4G64_STATUS_INVALID_VALUE, "out_features must be in [1, %lld], got %lld",
-                    (long long)(w4g64::kGemvMaxColumnBlocks * 64), (long long)out_features);
+                    (long long)(w4g64::kGemvMaxOutFeatures), (long long)out_features);
     if (!qweight || !scales || !zeros || !y)
         return fail(W4G64_STATUS_INVALID_VALUE, "qweight, scales, zeros and y must be non-null device pointers");
     if (!aligned(qweight, 16)) return fail(W4G64_STATUS_INVALID_VALUE, "qweight must be 16-byte aligned");

@@ -733,10 +733,8 @@ __global__ __launch_bounds__(256) void split_planes_kernel(const void* x, uint16
     *(u32x4*)(planes + m * 2 * K + K + c) = lo;
 }
 
-// Workspace: [counter area][split-tile partials][fp32 activations: bf16 planes, 256-byte aligned]
-int64_t planes_offset(const Gemm2Plan& pl) {
-    return (kGemvCounterBytes + pl.partial_bytes + 255) / 256 * 256;
-}
+// Workspace: [split-tile partials][fp32 activations: bf16 planes, 256-byte aligned]
+int64_t planes_offset(const Gemm2Plan& pl) { return (pl.partial_bytes + 255) / 256 * 256; }
 
 }  // namespace
 
@@ -744,7 +742,7 @@ int64_t gemm2_workspace_bytes(int64_t rows, int64_t out_features, int64_t in_fea
     const bool f32 = x_kind == kF32 || x_kind == kSwiGLU;
     const Gemm2Plan pl = plan_gemm2(rows, out_features, f32 ? 2 * in_features : in_features);
     if (f32) return planes_offset(pl) + rows * in_features * 4;
-    return pl.partial_bytes ? kGemvCounterBytes + pl.partial_bytes : 0;
+    return pl.partial_bytes;
 }
 
 bool gemm2_supported(const LinearProblem& p) {
@@ -782,8 +780,7 @@ hipError_t launch_gemm2(const LinearProblem& p, void* workspace, hipStream_t str
     args.dp_tiles = pl.dp_tiles;
     args.splits = pl.splits;
     args.gps = pl.gps;
-    // partials follow the workspace's counter area, which they must not touch
-    args.partials = pl.split_tiles ? (float*)((char*)workspace + kGemvCounterBytes) : nullptr;
+    args.partials = pl.split_tiles ? (float*)workspace : nullptr;
     const dim3 grid((unsigned)(pl.dp_tiles + pl.split_tiles * pl.splits));
     const bool two = pl.split_tiles > 0;
     constexpr int kPerTile = kBM * kBN / (256 * 8);

@@ -46,11 +46,13 @@
 //   * each wave owns whole output features (all their segments and fp32
 //     parts), so the epilogue reduces within the wave, with no workgroup
 //     barrier.
-//   * optional K split across workgroups (only for many rows x few output
-//     features): partial sums go through device-coherent (sc1) stores; the
-//     last workgroup to arrive for a column block, known from a per-block
-//     atomic counter, adds them in split order (deterministic), adds the
-//     bias, stores the output and re-zeroes the counter.
+//   * optional K split across workgroups (long K at several rows): each
+//     workgroup stores its fp32 partial sums, and a second kernel in the same
+//     stream adds them in split order (deterministic), adds the bias and
+//     stores the output; the kernel boundary makes the partials visible.
+//     (An in-kernel last-arriver merge needs an agent-scope release and
+//     acquire per workgroup, which measured 3.7-6.3 us per call here against
+//     about 2 us for the second launch.)
 #include <stdio.h>
 
 #include "w4g64_device.h"
@@ -81,8 +83,7 @@ struct GemvArgs {
     int gps;     // groups per K split
     int splits;  // K splits across workgroups
     int mv;      // A rows in use (= M)
-    float* partials;     // [splits][M][N]
-    unsigned* counters;  // [column blocks]
+    float* partials;  // [splits][M][N]
     int paired;          // paired gate|up epilogue (y = bf16 planes [3][M][N/2])
     // RMSNorm prologue (kNormB / kNormF): x is the residual stream
     const void* delta;
@@ -127,7 +128,6 @@ __device__ __forceinline__ void store_silu_planes(void* y, int m, int i, int M, 
 template <int XK, int SW, int STEPS, int TILES>
 __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-    __shared__ int s_last;
     // fp32-class activations are staged as three bf16 planes; the fp32 and
     // SwiGLU kinds run them along K (three MFMA pairs per group step into
     // separate accumulators), the planes kind as A rows (virtual row p M + m,
@@ -561,44 +561,39 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
             v += load_bias(a.bias, a.bias_kind, nn);
             store_out<kOut>(a.y, (int64_t)m * a.N + nn, v);
         } else {
-            __hip_atomic_store(a.partials + ((int64_t)split * a.M + m) * a.N + nn, v, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
+            a.partials[((int64_t)split * a.M + m) * a.N + nn] = v;
         }
     }
-    if (a.splits == 1) return;
+}
 
-    // ---- K split across workgroups: the last arrival of the block reduces ----
-    // Partials travel through device-coherent (sc1) atomic stores and loads,
-    // published by the arrival's agent-scope release and acquired by the last
-    // arriver (arrive_last).
-    if (!arrive_last(a.counters + nb, (unsigned)a.splits, &s_last)) return;
-    auto reduce_partials = [&](int m, int nn) {
+// Second kernel of a K-split call: one thread per output (paired: per
+// (row, i) pair of gate and up features).
+struct SplitReduceArgs {
+    const float* partials;
+    const void* bias;
+    int bias_kind;
+    void* y;
+    int M;
+    int N;
+    int splits;
+};
+
+template <int OUT, bool PAIRED>
+__global__ __launch_bounds__(256) void split_reduce_kernel(SplitReduceArgs r) {
+    const int cols = PAIRED ? r.N / 2 : r.N;
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (int64_t)r.M * cols) return;
+    const int m = (int)(idx / cols);
+    const int c = (int)(idx - (int64_t)m * cols);
+    const int64_t stride = (int64_t)r.M * r.N;
+    auto total = [&](int nn) {
+        const float* src = r.partials + (int64_t)m * r.N + nn;
         float v = 0.0f;
-        for (int s = 0; s < a.splits; ++s)
-            v += __hip_atomic_load(a.partials + ((int64_t)s * a.M + m) * a.N + nn, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
-        return v + load_bias(a.bias, a.bias_kind, nn);
+        for (int s = 0; s < r.splits; ++s) v += src[s * stride];  // split order: deterministic
+        return v + load_bias(r.bias, r.bias_kind, nn);
     };
-    if (a.paired && R >= 2) {
-        for (int idx = tid; idx < a.M * (kBlockCols / 2); idx += kThreads) {
-            const int m = idx / (kBlockCols / 2);
-            const int pc = idx - m * (kBlockCols / 2);  // pair: wave pc / (R/2), offset pc % (R/2)
-            constexpr int kHalf = R >= 2 ? R / 2 : 1;
-            int i;
-            slot_feature((pc / kHalf) * R + pc % kHalf, i);
-            if (i >= half_n) continue;
-            store_silu_planes(a.y, m, i, a.M, half_n, reduce_partials(m, i), reduce_partials(m, half_n + i));
-        }
-    } else {
-        for (int idx = tid; idx < a.M * kBlockCols; idx += kThreads) {
-            const int m = idx / kBlockCols;
-            const int c = idx - m * kBlockCols;
-            const int nn = col0 + c;
-            if (nn >= a.N) continue;
-            store_out<kOut>(a.y, (int64_t)m * a.N + nn, reduce_partials(m, nn));
-        }
-    }
-    if (tid == 0) __hip_atomic_store(a.counters + nb, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if constexpr (PAIRED) store_silu_planes(r.y, m, c, r.M, cols, total(c), total(cols + c));
+    else store_out<OUT>(r.y, (int64_t)m * r.N + c, total(c));
 }
 
 template <int XK, int SW, int STEPS, int TILES>
@@ -606,8 +601,14 @@ hipError_t launch_typed(const GemvArgs& args, const GemvPlan& plan, hipStream_t 
                         hipEvent_t stop) {
     // the staging capacity of this instantiation (the planner never exceeds it)
     if ((int64_t)args.M * args.gps * 8 > (int64_t)stage_items<XK, SW, STEPS, TILES>() * kThreads) return hipErrorInvalidValue;
-    return launch_kernel(gemv_kernel<XK, SW, STEPS, TILES>, dim3(plan.n_blocks, plan.splits), dim3(kThreads),
-                         (size_t)plan.lds_bytes, stream, start, stop, args);
+    constexpr bool kNorm = XK == kNormB || XK == kNormF;
+    constexpr int kOut = (XK == kSwiGLU || XK == kPlanes) ? kF32 : (kNorm ? kBF16 : XK);
+    const bool split = plan.splits > 1;
+    hipError_t err = launch_kernel(gemv_kernel<XK, SW, STEPS, TILES>, dim3(plan.n_blocks, plan.splits),
+                                   dim3(kThreads), (size_t)plan.lds_bytes, stream, start, split ? nullptr : stop, args);
+    if (err != hipSuccess || !split) return err;
+    return launch_split_reduce(args.partials, args.bias, args.bias_kind, args.y, args.M, args.N, args.splits,
+                               args.paired != 0, kOut, stream, stop);
 }
 
 template <int XK, int SW, int TILES>
@@ -677,7 +678,6 @@ bool plan_rows16(int64_t rows, int64_t out_features, int64_t in_features, GemvPl
         gps = (groups + splits - 1) / splits;
     }
     splits = (groups + gps - 1) / gps;
-    if (splits > 1 && plan.n_blocks > kGemvMaxColumnBlocks) return false;
     plan.splits = (int)splits;
     plan.groups_per_split = (int)gps;
     const int64_t need = (gps + kw - 1) / kw;
@@ -688,8 +688,7 @@ bool plan_rows16(int64_t rows, int64_t out_features, int64_t in_features, GemvPl
             break;
         }
     plan.lds_bytes = lds_for(gps);
-    plan.counter_bytes = splits > 1 ? kGemvCounterBytes : 0;
-    plan.workspace_bytes = splits > 1 ? plan.counter_bytes + splits * rows * out_features * 4 : 0;
+    plan.workspace_bytes = splits > 1 ? splits * rows * out_features * 4 : 0;
     return true;
 }
 
@@ -732,8 +731,7 @@ GemvPlan plan_segmented(int64_t rows, int64_t out_features, int64_t in_features,
             break;
         }
     plan.lds_bytes = lds_for(gps);
-    plan.counter_bytes = splits > 1 ? kGemvCounterBytes : 0;
-    plan.workspace_bytes = splits > 1 ? plan.counter_bytes + splits * rows * out_features * 4 : 0;
+    plan.workspace_bytes = splits > 1 ? splits * rows * out_features * 4 : 0;
     return plan;
 }
 }  // namespace
@@ -837,8 +835,7 @@ hipError_t launch_gemv(const LinearProblem& p, const GemvPlan& plan, void* works
     args.norm_w = p.norm_weight;
     args.eps = p.norm_eps;
     args.out_sum = (uint16_t*)p.norm_out_sum;
-    args.counters = (unsigned*)workspace;
-    args.partials = workspace ? (float*)((char*)workspace + plan.counter_bytes) : nullptr;
+    args.partials = (float*)workspace;
     switch (p.x_kind) {
         case kF16:
             return launch_sw<kF16, 1>(args, plan, stream, start, stop);
@@ -858,6 +855,21 @@ hipError_t launch_gemv(const LinearProblem& p, const GemvPlan& plan, void* works
             return launch_steps<kPlanes, 1, 3>(args, plan, stream, start, stop);
         default:
             return launch_sw<kF32, 1>(args, plan, stream, start, stop);
+    }
+}
+
+hipError_t launch_split_reduce(const float* partials, const void* bias, int bias_kind, void* y, int M, int N,
+                               int splits, bool paired, int out_kind, hipStream_t stream, hipEvent_t stop) {
+    SplitReduceArgs r{partials, bias, bias_kind, y, M, N, splits};
+    if (!partials || splits < 2 || (paired && (N & 1))) return hipErrorInvalidValue;
+    const int64_t items = (int64_t)M * (paired ? N / 2 : N);
+    const dim3 grid((unsigned)((items + 255) / 256));
+    if (paired) return launch_kernel(split_reduce_kernel<kF32, true>, grid, dim3(256), 0, stream, nullptr, stop, r);
+    switch (out_kind) {
+        case kF16: return launch_kernel(split_reduce_kernel<kF16, false>, grid, dim3(256), 0, stream, nullptr, stop, r);
+        case kBF16: return launch_kernel(split_reduce_kernel<kBF16, false>, grid, dim3(256), 0, stream, nullptr, stop, r);
+        case kF32: return launch_kernel(split_reduce_kernel<kF32, false>, grid, dim3(256), 0, stream, nullptr, stop, r);
+        default: return hipErrorInvalidValue;
     }
 }
 

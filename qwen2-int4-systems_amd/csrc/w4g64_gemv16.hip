@@ -23,7 +23,8 @@
 //     pair); bf16: B = 128 + n' exact, and the group result is corrected by
 //     -(136 + zero) * sum_{k in g} x[m,k].
 //   * a K split across workgroups (long K: the staged range must fit LDS)
-//     uses the same coherent last-arriver protocol as the segmented kernel.
+//     stores fp32 partial sums that the split-reduce kernel adds up, as for
+//     the segmented kernel.
 #include "w4g64_device.h"
 #include "w4g64_internal.h"
 
@@ -46,8 +47,7 @@ struct Gemv16Args {
     int G;       // K / 64
     int gps;     // groups per K split
     int splits;  // K splits across workgroups
-    float* partials;     // [splits][M][N]
-    unsigned* counters;  // [column blocks]
+    float* partials;  // [splits][M][N]
 };
 
 // Activation items (8 values) a lane stages: 16 rows x KW STEPS groups x 8
@@ -69,7 +69,6 @@ template <int XK, int STEPS, int KW, int FB>
 __global__ __launch_bounds__(KW * FB * 64) void gemv16_kernel(Gemv16Args a) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     __shared__ float red[KW * FB][16][16];  // [wave][row][feature]
-    __shared__ int s_last;
     constexpr int kThreads16 = KW * FB * 64;
     constexpr int kStage = stage_items16<STEPS, FB>();
     constexpr int kCols = 16 * FB;  // output features per workgroup
@@ -218,28 +217,8 @@ __global__ __launch_bounds__(KW * FB * 64) void gemv16_kernel(Gemv16Args a) {
         if (a.splits == 1)
             store_out<XK>(a.y, (int64_t)m * a.N + nn, s + load_bias(a.bias, a.bias_kind, nn));
         else
-            __hip_atomic_store(a.partials + ((int64_t)split * a.M + m) * a.N + nn, s, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
+            a.partials[((int64_t)split * a.M + m) * a.N + nn] = s;
     }
-    if (a.splits == 1) return;
-
-    // ---- K split across workgroups: the last arrival of the block reduces ----
-    // Partials travel through device-coherent (sc1) atomic stores and loads,
-    // published by the arrival's agent-scope release and acquired by the last
-    // arriver (arrive_last).
-    if (!arrive_last(a.counters + nb, (unsigned)a.splits, &s_last)) return;
-    for (int idx = tid; idx < a.M * kCols; idx += kThreads16) {
-        const int m = idx / kCols;
-        const int c = idx - m * kCols;
-        const int nn = col0 + c;
-        if (nn >= a.N) continue;
-        float s = 0.0f;
-        for (int sp = 0; sp < a.splits; ++sp)
-            s += __hip_atomic_load(a.partials + ((int64_t)sp * a.M + m) * a.N + nn, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
-        store_out<XK>(a.y, (int64_t)m * a.N + nn, s + load_bias(a.bias, a.bias_kind, nn));
-    }
-    if (tid == 0) __hip_atomic_store(a.counters + nb, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <int XK, int STEPS, int KW, int FB>
@@ -248,8 +227,13 @@ hipError_t launch16(const Gemv16Args& args, const GemvPlan& plan, hipStream_t st
     // the staging capacity of this instantiation (the planner never exceeds it)
     if ((int64_t)args.M * args.gps * 8 > (int64_t)stage_items16<STEPS, FB>() * KW * FB * 64 || args.gps > KW * STEPS)
         return hipErrorInvalidValue;
-    return launch_kernel(gemv16_kernel<XK, STEPS, KW, FB>, dim3(plan.n_blocks, plan.splits), dim3(KW * FB * 64),
-                         (size_t)plan.lds_bytes, stream, start, stop, args);
+    const bool split = plan.splits > 1;
+    const hipError_t err = launch_kernel(gemv16_kernel<XK, STEPS, KW, FB>, dim3(plan.n_blocks, plan.splits),
+                                         dim3(KW * FB * 64), (size_t)plan.lds_bytes, stream, start,
+                                         split ? nullptr : stop, args);
+    if (err != hipSuccess || !split) return err;
+    return launch_split_reduce(args.partials, args.bias, args.bias_kind, args.y, args.M, args.N, args.splits, false,
+                               XK, stream, stop);
 }
 
 template <int XK, int KW, int FB>
@@ -297,8 +281,7 @@ hipError_t launch_gemv16(const LinearProblem& p, const GemvPlan& plan, void* wor
     args.G = (int)(p.in_features / 64);
     args.gps = plan.groups_per_split;
     args.splits = plan.splits;
-    args.counters = (unsigned*)workspace;
-    args.partials = workspace ? (float*)((char*)workspace + plan.counter_bytes) : nullptr;
+    args.partials = (float*)workspace;
     if (p.x_kind == kF16) return launch_shape16<kF16>(args, plan, stream, start, stop);
     return launch_shape16<kBF16>(args, plan, stream, start, stop);
 }

@@ -32,13 +32,10 @@ struct LinearProblem {
 
 // Decode GEMV (rows <= kGemvMaxRows).
 constexpr int kGemvMaxRows = 16;
-// Workspace layout of every split-K GEMV call: a fixed counter area (one
-// 32-bit arrival counter per 64-column block, zero between calls) followed by
-// the fp32 partial sums.  The counter area has the same offset and size for
-// every shape, so calls with different shapes can share one workspace without
-// their partial sums ever landing on another shape's counters.
-constexpr int64_t kGemvCounterBytes = 64 * 1024;
-constexpr int64_t kGemvMaxColumnBlocks = kGemvCounterBytes / 4;  // 1,048,576 output features
+// Largest out_features the decode path takes (its grid and index arithmetic
+// stay within 32 bits).
+constexpr int64_t kGemvMaxOutFeatures = int64_t(1) << 26;
+// Workspace of a split-K GEMV call: the fp32 partial sums [splits][rows][out_features].
 struct GemvPlan {
     int kind;              // 0: segmented kernel (any rows); 1: 9..16-row kernel (fp16/bf16)
     int waves;             // kind 1: waves per 16-feature block (they split its K range)
@@ -53,7 +50,6 @@ struct GemvPlan {
     int stage = 1;         // kind 2: staging loads per lane
     int64_t lds_bytes;     // dynamic LDS per workgroup
     int64_t workspace_bytes;
-    int64_t counter_bytes;
 };
 GemvPlan plan_gemv(int64_t rows, int64_t out_features, int64_t in_features, int x_kind);
 // Same, with the segment count and K split forced (> 0) -- for tuning sweeps.
@@ -61,6 +57,12 @@ GemvPlan plan_gemv(int64_t rows, int64_t out_features, int64_t in_features, int 
                    int force_splits);
 hipError_t launch_gemv(const LinearProblem& p, const GemvPlan& plan, void* workspace, hipStream_t stream,
                        hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
+// Second kernel of a K-split GEMV call (either decode GEMV kernel): adds the
+// fp32 partial sums [splits][M][N] in split order, adds the bias and stores
+// out_kind values; paired (N = 2 I gate|up features): stores the three bf16
+// planes of silu(bf16(gate)) * bf16(up) per (row, i).
+hipError_t launch_split_reduce(const float* partials, const void* bias, int bias_kind, void* y, int M, int N,
+                               int splits, bool paired, int out_kind, hipStream_t stream, hipEvent_t stop);
 const char* gemv_kernel_name(const GemvPlan& plan, int x_kind);
 // Plan of the paired gate|up GEMV (bf16, out_features = 2 I rows: gate then
 // up): the segmented kernel with at most 8 segments, so that every wave holds

@@ -51,9 +51,10 @@ def _aligned(tensor: torch.Tensor, bytes_: int) -> torch.Tensor:
 
 
 # ---------------------------------------------------------------------------
-# Workspace: split-K partials and arrival counters of the decode GEMV and the
-# GEMM.  One zero-filled buffer per (device, stream), grown on demand; the
-# kernels leave the counters at zero, so it is cleared only when allocated.
+# Workspace: split-K partial sums of the decode GEMV and the GEMM (and the
+# GEMM's bf16 planes of fp32 activations).  One buffer per (device, stream),
+# grown on demand; every call writes what it reads, so its contents between
+# calls do not matter.
 # A HIP graph captured on a stream keeps the raw address of the buffer it was
 # captured with, so a buffer is never freed once replaced: it moves to
 # ``_retired`` and lives as long as the process.  Growing (or creating) a

@@ -188,9 +188,9 @@ def test_gate_up_planes_and_planes_form_reject_before_launch():
                             null) == _lib.STATUS_INVALID_VALUE
     # queries: decode rows only.  The planes are 3 M virtual A rows (4 segments
     # at M = 1), so the 1536 x 8960 down projection splits K 6 ways (fp32
-    # partials after the counter area); the paired gate|up needs no split
+    # partials); the paired gate|up needs no split
     assert lib.w4g64_linear_kernel_name(1, 1536, 8960, planes) == b"gemv_kernel<planes_bf16,4,6,1>"
-    assert lib.w4g64_linear_workspace_bytes(1, 1536, 8960, planes) == 64 * 1024 + 6 * 1536 * 4
+    assert lib.w4g64_linear_workspace_bytes(1, 1536, 8960, planes) == 6 * 1536 * 4
     assert lib.w4g64_linear_kernel_name(1, 17920, 1536, _lib.DTYPE_BF16_GATE_UP) == b"gemv_kernel<bf16,4,6,1>"
     assert lib.w4g64_linear_workspace_bytes(1, 17920, 1536, _lib.DTYPE_BF16_GATE_UP) == 0
     assert lib.w4g64_linear_kernel_name(17, 1536, 8960, planes) == b"none"
@@ -216,23 +216,24 @@ def test_gate_up_planes_and_planes_form_reject_before_launch():
 
 def test_workspace_and_kernel_plan_queries():
     lib = _lib.load()
-    # decode shapes that split K across workgroups need a workspace with the
-    # fixed 64 KiB counter area; 9..16 rows stage the K range's activations in
-    # LDS (~60 KB: at most 28 groups at 16 rows), so long K splits across
-    # workgroups (140 groups -> 5 splits of 28; 145 groups -> 6 of 25); short
-    # K needs no workspace
-    assert lib.w4g64_linear_workspace_bytes(4, 1536, 8960, _lib.DTYPE_F16) > 64 * 1024
-    assert lib.w4g64_linear_workspace_bytes(16, 1536, 8960, _lib.DTYPE_F16) == 64 * 1024 + 5 * 16 * 1536 * 4
+    # decode shapes that split K across workgroups need a workspace for their
+    # fp32 partials [splits][rows][out_features]; 9..16 rows stage the K
+    # range's activations in LDS (~60 KB: at most 28 groups at 16 rows), so
+    # long K splits across workgroups (140 groups -> 5 splits of 28; 145
+    # groups -> 6 of 25); short K needs no workspace
+    assert lib.w4g64_linear_workspace_bytes(4, 1536, 8960, _lib.DTYPE_F16) % (4 * 1536 * 4) == 0
+    assert lib.w4g64_linear_workspace_bytes(4, 1536, 8960, _lib.DTYPE_F16) >= 2 * 4 * 1536 * 4
+    assert lib.w4g64_linear_workspace_bytes(16, 1536, 8960, _lib.DTYPE_F16) == 5 * 16 * 1536 * 4
     assert lib.w4g64_linear_workspace_bytes(16, 1536, 1536, _lib.DTYPE_F16) == 0
-    assert lib.w4g64_linear_workspace_bytes(16, 40, 9280, _lib.DTYPE_BF16) == 64 * 1024 + 6 * 16 * 40 * 4
+    assert lib.w4g64_linear_workspace_bytes(16, 40, 9280, _lib.DTYPE_BF16) == 6 * 16 * 40 * 4
     # prefill: 560 tiles of 128x256 on 512 workgroup slots (256 CUs, the default
     # when no device answers): 512 data-parallel tiles, the other 48 split in 4
-    # K ranges with fp32 partials after the counter area; whole rounds need none
-    assert lib.w4g64_linear_workspace_bytes(2048, 8960, 1536, _lib.DTYPE_BF16) == 64 * 1024 + 48 * 4 * 128 * 256 * 4
+    # K ranges with fp32 partials; whole rounds need none
+    assert lib.w4g64_linear_workspace_bytes(2048, 8960, 1536, _lib.DTYPE_BF16) == 48 * 4 * 128 * 256 * 4
     assert lib.w4g64_linear_workspace_bytes(2048, 8192, 1536, _lib.DTYPE_BF16) == 0
-    # fp32 GEMM activations: two bf16 planes (rows x 2 in_features x 2 B) after the counters and partials
+    # fp32 GEMM activations: two bf16 planes (rows x 2 in_features x 2 B) after the partials
     ws32 = lib.w4g64_linear_workspace_bytes(512, 1536, 8960, _lib.DTYPE_F32)
-    assert 64 * 1024 + 512 * 8960 * 4 <= ws32 <= 64 * 1024 + (64 << 20) + 512 * 8960 * 4 + 256
+    assert 512 * 8960 * 4 <= ws32 <= (64 << 20) + 512 * 8960 * 4 + 256
     assert lib.w4g64_linear_kernel_name(512, 1536, 8960, _lib.DTYPE_F32).startswith(b"gemm2_kernel<bf16 hi|lo")
     assert lib.w4g64_linear_workspace_bytes(1, 1536, 100, _lib.DTYPE_F16) == 0
     # one row of even-group shapes with at most three 16-byte weight loads per

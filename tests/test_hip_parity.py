@@ -425,8 +425,9 @@ def test_linear_rejects_noncanonical_contract():
 
 
 def test_determinism_and_workspace_reuse_across_shapes():
-    """Split-K partial sums are reduced in a fixed order and the arrival
-    counters reset themselves: repeated, interleaved calls are bitwise equal."""
+    """Split-K partial sums are reduced in a fixed order and every call writes
+    the partials it reads: repeated, interleaved calls on one workspace are
+    bitwise equal."""
     cases = []
     for (name, rows) in [("down_proj", 1), ("q_proj", 4), ("gate_proj", 1), ("k_proj", 16), ("down_proj", 16)]:
         n, k = SHAPES[name]
@@ -473,7 +474,7 @@ def test_quantlinear_dispatch_matches_oracle():
 
 
 def test_hip_graph_capture_replays_match_eager():
-    """The decode GEMV (split-K, self-resetting counters) and the GEMM inside a
+    """The decode GEMV (split-K: partials, then the split-reduce kernel) and the GEMM inside a
     captured HIP graph: several replays, with eager work and synchronizations
     between them, each equal to the eager result bit for bit."""
     calls = []
@@ -511,7 +512,7 @@ def test_graphs_captured_before_and_after_workspace_growth_both_replay():
     n, k = SHAPES["down_proj"]
     q, s, z = weights("sym", n, k, O.BASE_SEED + n + k)
     w = dev_weights(q, s, z)
-    small = to_dev(O.activations(4, k, seed=31, dtype="fp16"), "fp16")  # split-K GEMV: counters + partials
+    small = to_dev(O.activations(4, k, seed=31, dtype="fp16"), "fp16")  # split-K GEMV: partials
     large = to_dev(O.activations(200, k, seed=32, dtype="bf16"), "bf16")  # split-K GEMM: tens of MB of partials
     want_small = linear_canonical_w4g64_hip(small, *w)
     want_large = linear_canonical_w4g64_hip(large, *w)

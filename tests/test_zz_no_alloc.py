@@ -3,7 +3,7 @@ workspace one (w4g64_linear), through the C ABI.
 
 It shares w4g64_linear's kernels and plans, so outputs must be bit-identical:
 two calls in a row (the second on a smaller problem, so stale scratch from
-the first would show), a split-K shape whose arrival counters live in the
+the first would show), a split-K shape whose partial sums live in the
 scratch, and a HIP graph of the allocation-free call replayed several times.
 """
 
@@ -64,8 +64,8 @@ def test_static_scratch_matches_the_workspace_linear():
     lib = _lib.load()
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     assert lib.w4g64_static_scratch_bytes() == 4 << 20
-    # split-K decode shape (down 1536x8960 at 4 rows: arrival counters and
-    # partials in the scratch), then a smaller problem on the same scratch
+    # split-K decode shape (down 1536x8960 at 4 rows: partials in the
+    # scratch), then a smaller problem on the same scratch
     cases = [(1536, 8960, 4, "fp16"), (1536, 1536, 1, "fp16"), (2048, 1536, 16, "bf16"), (256, 1536, 3, "fp32")]
     for n, k, rows, dtype in cases:
         print(f"static scratch case n={n} k={k} rows={rows} {dtype}", flush=True)
@@ -93,7 +93,7 @@ def test_static_scratch_rejects_problems_beyond_its_size():
 
 def test_static_scratch_under_graph_capture():
     """The caller it exists for: a captured HIP graph of the allocation-free
-    call (split-K, self-resetting counters), replayed with eager calls of the
+    call (split-K partials in the scratch), replayed with eager calls of the
     same entry point in between; every replay equals the eager result."""
     lib = _lib.load()
     x, q, s, z = _problem(1536, 8960, 4, O.BASE_SEED + 77, "fp16")
