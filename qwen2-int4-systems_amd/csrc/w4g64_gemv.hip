@@ -586,10 +586,20 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(SplitReduceArgs r) {
     const int m = (int)(idx / cols);
     const int c = (int)(idx - (int64_t)m * cols);
     const int64_t stride = (int64_t)r.M * r.N;
+    // Up to 8 splits' loads are issued before the first add (a dependent
+    // load-add chain would pay one memory latency per split); the adds run in
+    // split order, so the sum is deterministic.
     auto total = [&](int nn) {
         const float* src = r.partials + (int64_t)m * r.N + nn;
         float v = 0.0f;
-        for (int s = 0; s < r.splits; ++s) v += src[s * stride];  // split order: deterministic
+        for (int s0 = 0; s0 < r.splits; s0 += 8) {
+            float part[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) part[u] = src[min(s0 + u, r.splits - 1) * stride];
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                if (s0 + u < r.splits) v += part[u];
+        }
         return v + load_bias(r.bias, r.bias_kind, nn);
     };
     if constexpr (PAIRED) store_silu_planes(r.y, m, c, r.M, cols, total(c), total(cols + c));
