@@ -265,8 +265,10 @@ __global__ __launch_bounds__(NR * NK * 64) void gemv_seg_kernel(SegArgs a) {
                                                             dequant8_bf16_biased(wv[t][u]), d, 0, 0, 0);
             }
         }
-        // scales and zero points of (row, groups 2 jj, 2 jj + 1)
-        const int jc = live ? jj : pbase;
+        // scales and zero points of (row, groups 2 jj, 2 jj + 1); a step past
+        // the part reads an in-range pair (a K part may hold no pair at all:
+        // pbase >= P) and adds s = 0 times those finite values
+        const int jc = live ? jj : min(pbase, P - 1);
         const uint32_t s2 = *(const uint32_t*)(sc + sc_row + 2 * jc);
         const uint32_t z2 = zb[zb_row + jc];
         const float s0 = live ? half_bits_to_float((uint16_t)s2) : 0.0f;
