@@ -489,7 +489,7 @@ def summarize_pmc(fetch_csv: str, write_csv: str, out_path: str) -> int:
         # a split GEMM call is two dispatches (GEMM + reduction): totals per call
         calls = len(PREFILL_SHAPES) * 2
         per_call = sum(a * f_scale + b * w_scale for a, b in zip(f_gem, w_gem)) * 1024 / calls
-        summary["gemm_2048"] = {"kernel": "gemm2_kernel<bf16,128> (+ split-K reduction)", "calls": calls,
+        summary["gemm_2048"] = {"kernel": "gemm_kernel<f16 a x int b,128x256> (+ activation staging, split-K reduction)", "calls": calls,
                                 "algorithmic_bytes_per_call": algorithmic_bytes(2048, 8960, 1536),
                                 "traffic_bytes_per_call": per_call}
     Path(out_path).parent.mkdir(parents=True, exist_ok=True)
@@ -547,7 +547,7 @@ def summarize_mfma(csv_path: str, out_path: str, cus: int = 256) -> int:
         d = per[key]
         if d.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0) <= 0:
             continue
-        label = "W4G64 gemm2_kernel" if "gemm2_kernel" in d["name"] else d["name"].split("_MT")[0][:48]
+        label = "W4G64 gemm_kernel" if "gemm_kernel" in d["name"] else d["name"].split("_MT")[0][:48]
         groups.setdefault((label, d["grid"], d["SQ_VALU_MFMA_BUSY_CYCLES"]), []).append(d)
     rows = []
     for (label, grid, busy), ds in groups.items():
@@ -942,7 +942,7 @@ def main() -> int:
             "value": round(tf, 2),
             "unit": "TFLOP/s",
             "dtype": "bf16",
-            "roofline": {"bound": "mfma", "kernel": "gemm2_kernel<bf16,128> (+ split-K reduction)",
+            "roofline": {"bound": "mfma", "kernel": "gemm_kernel<f16 a x int b,128x256> (+ activation staging, split-K reduction)",
                          "achieved": round(tf, 2), "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(tf / MFMA_PEAK_TFLOPS, 4),
                          "traffic": (round(gemm_traffic["traffic_bytes_per_call"])

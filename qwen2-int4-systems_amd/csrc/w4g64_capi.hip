@@ -146,12 +146,12 @@ int64_t w4g64_linear_workspace_bytes(int64_t rows, int64_t out_features, int64_t
     if (fused_form(x_dtype))
         return rows <= w4g64::kGemvMaxRows
                    ? w4g64::plan_gemv(rows, out_features, in_features, x_dtype).workspace_bytes
-                   : w4g64::gemm2_workspace_bytes(rows, out_features, in_features, x_dtype);
+                   : w4g64::gemm_workspace_bytes(rows, out_features, in_features, x_dtype);
     if (x_dtype != W4G64_DTYPE_F16 && x_dtype != W4G64_DTYPE_BF16 && x_dtype != W4G64_DTYPE_F32) return 0;
     if (rows > w4g64::kGemvMaxRows) {
         w4g64::LinearProblem p{nullptr, x_dtype, nullptr, nullptr, nullptr, nullptr, 0, nullptr, rows, out_features,
                                in_features};
-        return w4g64::gemm2_supported(p) ? w4g64::gemm2_workspace_bytes(rows, out_features, in_features, x_dtype) : 0;
+        return w4g64::gemm_supported(p) ? w4g64::gemm_workspace_bytes(rows, out_features, in_features, x_dtype) : 0;
     }
     return w4g64::plan_gemv(rows, out_features, in_features, x_dtype).workspace_bytes;
 }
@@ -233,9 +233,12 @@ static int linear_impl(const void* x, int x_dtype, const uint8_t* qweight, const
         return hip_status(w4g64::launch_gemv(p, plan, workspace, s, (hipEvent_t)start_event, (hipEvent_t)stop_event),
                           "gemv");
     }
-    const int64_t need = w4g64::gemm2_workspace_bytes(rows, out_features, in_features, x_dtype);
+    if (!w4g64::gemm_supported(p))
+        return fail(W4G64_STATUS_UNSUPPORTED, "GEMM path supports rows * in_features below 2^31 (2^30 for float32) "
+                    "and out_features * in_features below 2^32");
+    const int64_t need = w4g64::gemm_workspace_bytes(rows, out_features, in_features, x_dtype);
     if (int st = check_workspace(workspace, workspace_bytes, need)) return st;
-    return hip_status(w4g64::launch_gemm2(p, workspace, s, (hipEvent_t)start_event, (hipEvent_t)stop_event), "gemm");
+    return hip_status(w4g64::launch_gemm(p, workspace, s, (hipEvent_t)start_event, (hipEvent_t)stop_event), "gemm");
 }
 
 int w4g64_linear(const void* x, int x_dtype, const uint8_t* qweight, const uint16_t* scales, const uint8_t* zeros,
@@ -313,9 +316,12 @@ int w4g64_linear_swiglu(const void* gate_up, const uint8_t* qweight, const uint1
     w4g64::LinearProblem p{gate_up, w4g64::kSwiGLU, qweight, scales, zeros, bias, bias_dtype, y, rows, out_features,
                            in_features};
     if (rows > w4g64::kGemvMaxRows) {
-        const int64_t need = w4g64::gemm2_workspace_bytes(rows, out_features, in_features, w4g64::kSwiGLU);
+        if (!w4g64::gemm_supported(p))
+            return fail(W4G64_STATUS_UNSUPPORTED, "GEMM path supports rows * in_features below 2^30 and "
+                        "out_features * in_features below 2^32");
+        const int64_t need = w4g64::gemm_workspace_bytes(rows, out_features, in_features, w4g64::kSwiGLU);
         if (int st = check_workspace(workspace, workspace_bytes, need)) return st;
-        return hip_status(w4g64::launch_gemm2(p, workspace, (hipStream_t)stream), "gemm");
+        return hip_status(w4g64::launch_gemm(p, workspace, (hipStream_t)stream), "gemm");
     }
     const w4g64::GemvPlan plan = w4g64::plan_gemv(rows, out_features, in_features, w4g64::kSwiGLU);
     if (int st = check_workspace(workspace, workspace_bytes, plan.workspace_bytes)) return st;

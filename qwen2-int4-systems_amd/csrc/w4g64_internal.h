@@ -86,16 +86,18 @@ bool seg_supported(const LinearProblem& p);
 hipError_t launch_gemv_seg(const LinearProblem& p, const GemvPlan& plan, hipStream_t stream, hipEvent_t start,
                            hipEvent_t stop);
 
-// Prefill GEMM v2 (pipelined, fp16/bf16 activations).  Tiles of a last,
+// Prefill GEMM (rows > 16): a staging kernel writes the activations as fp16
+// rows (scaled by a power of two per row; fp32-class kinds as hi|lo planes)
+// into the workspace, the GEMM kernel multiplies them by the exact integer
+// (code - zero) and applies each group's scale in fp32.  Tiles of a last,
 // mostly empty round of workgroups (or all tiles, when there are fewer than
 // the device's workgroup slots) are split along K; their fp32 partial sums
-// live in the workspace after the counter area and a second kernel adds
-// them up.
-bool gemm2_supported(const LinearProblem& p);
-int64_t gemm2_workspace_bytes(int64_t rows, int64_t out_features, int64_t in_features, int x_kind);
+// live at the start of the workspace and a third kernel adds them up.
+bool gemm_supported(const LinearProblem& p);
+int64_t gemm_workspace_bytes(int64_t rows, int64_t out_features, int64_t in_features, int x_kind);
 const char* gemm_kernel_name(int64_t rows, int64_t out_features, int64_t in_features, int x_kind);
-hipError_t launch_gemm2(const LinearProblem& p, void* workspace, hipStream_t stream, hipEvent_t start = nullptr,
-                        hipEvent_t stop = nullptr);
+hipError_t launch_gemm(const LinearProblem& p, void* workspace, hipStream_t stream, hipEvent_t start = nullptr,
+                       hipEvent_t stop = nullptr);
 
 // Launch a kernel; with events, hipExtLaunchKernelGGL records them at the
 // kernel's own start and end (what a profiler reports as its duration).

@@ -158,7 +158,7 @@ def test_fused_swiglu_linear_rejects_before_launch():
         "gemv_kernel<swiglu_bf16,")
     assert lib.w4g64_linear_kernel_name(12, 1536, 8960, _lib.DTYPE_BF16_SWIGLU).decode().startswith(
         "gemv_kernel<swiglu_bf16,")
-    assert lib.w4g64_linear_kernel_name(64, 1536, 8960, _lib.DTYPE_BF16_SWIGLU).startswith(b"gemm2_kernel<bf16 hi|lo")
+    assert lib.w4g64_linear_kernel_name(64, 1536, 8960, _lib.DTYPE_BF16_SWIGLU).startswith(b"gemm_kernel<")
     assert lib.w4g64_linear_workspace_bytes(512, 1536, 8960, _lib.DTYPE_BF16_SWIGLU) == \
         lib.w4g64_linear_workspace_bytes(512, 1536, 8960, _lib.DTYPE_F32)
     assert lib.w4g64_linear_workspace_bytes(1, 64, 64, 4) == 0 and lib.w4g64_linear_kernel_name(1, 64, 64, 4) == b"none"
@@ -229,12 +229,15 @@ def test_workspace_and_kernel_plan_queries():
     # prefill: 560 tiles of 128x256 on 512 workgroup slots (256 CUs, the default
     # when no device answers): 512 data-parallel tiles, the other 48 split in 4
     # K ranges with fp32 partials; whole rounds need none
-    assert lib.w4g64_linear_workspace_bytes(2048, 8960, 1536, _lib.DTYPE_BF16) == 48 * 4 * 128 * 256 * 4
-    assert lib.w4g64_linear_workspace_bytes(2048, 8192, 1536, _lib.DTYPE_BF16) == 0
-    # fp32 GEMM activations: two bf16 planes (rows x 2 in_features x 2 B) after the partials
+    # and every GEMM stages its activations as fp16 rows (rows x in_features x 2 B)
+    # plus one fp32 row factor per tile row
+    staged = 2048 * 1536 * 2 + 16 * 128 * 4
+    assert lib.w4g64_linear_workspace_bytes(2048, 8960, 1536, _lib.DTYPE_BF16) == 48 * 4 * 128 * 256 * 4 + staged
+    assert lib.w4g64_linear_workspace_bytes(2048, 8192, 1536, _lib.DTYPE_BF16) == staged
+    # fp32 GEMM activations: two fp16 planes (rows x 2 in_features x 2 B) after the partials
     ws32 = lib.w4g64_linear_workspace_bytes(512, 1536, 8960, _lib.DTYPE_F32)
-    assert 512 * 8960 * 4 <= ws32 <= (64 << 20) + 512 * 8960 * 4 + 256
-    assert lib.w4g64_linear_kernel_name(512, 1536, 8960, _lib.DTYPE_F32).startswith(b"gemm2_kernel<bf16 hi|lo")
+    assert 512 * 8960 * 4 + 512 * 4 <= ws32 <= (64 << 20) + 512 * 8960 * 4 + 512 * 4 + 512
+    assert lib.w4g64_linear_kernel_name(512, 1536, 8960, _lib.DTYPE_F32).startswith(b"gemm_kernel<")
     assert lib.w4g64_linear_workspace_bytes(1, 1536, 100, _lib.DTYPE_F16) == 0
     # one row of even-group shapes with at most three 16-byte weight loads per
     # lane: the lean kernel (no workspace)
@@ -250,7 +253,7 @@ def test_workspace_and_kernel_plan_queries():
     assert lib.w4g64_linear_kernel_name(16, 8960, 1536, _lib.DTYPE_F16) == b"gemv16_kernel<f16,6,4,3>"
     assert lib.w4g64_linear_kernel_name(16, 1536, 1536, _lib.DTYPE_F16) == b"gemv16_kernel<f16,3,8,1>"
     assert lib.w4g64_linear_kernel_name(16, 1536, 8960, _lib.DTYPE_F32).startswith(b"gemv_kernel<f32")
-    assert lib.w4g64_linear_kernel_name(2048, 8960, 1536, _lib.DTYPE_BF16).startswith(b"gemm2_kernel<bf16")
+    assert lib.w4g64_linear_kernel_name(2048, 8960, 1536, _lib.DTYPE_BF16).startswith(b"gemm_kernel<")
     assert lib.w4g64_linear_kernel_name(1, 8960, 1536, 8) == b"none"
 
 

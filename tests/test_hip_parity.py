@@ -253,7 +253,7 @@ def test_gemm_multiplies_exact_weights(rows, name, kind, dtype):
 
     n, k = SHAPES[name]
     torch_dtype = torch.float16 if dtype == "fp16" else torch.bfloat16
-    assert linear_kernel_name(rows, n, k, torch_dtype).startswith("gemm2_kernel")
+    assert linear_kernel_name(rows, n, k, torch_dtype).startswith("gemm_kernel")
     q, s, z = weights(kind, n, k, O.BASE_SEED + 17 * rows + n)
     x = O.activations(rows, k, seed=O.BASE_SEED + 19 * rows + k, dtype=dtype, outliers=kind != "sym")
     out, ref = check_linear(x, q, s, z, None, n, k, dtype)
@@ -308,6 +308,61 @@ def test_fp32_gemm_ragged_shapes(n, k, rows):
     q, s, z = weights("awq", n, k, O.BASE_SEED + 3 * n + k)
     x = O.activations(rows, k, seed=O.BASE_SEED + rows + n, dtype="fp32")
     check_linear(x, q, s, z, None, n, k, "fp32", normwise=1e-5, tol=(1e-4, 1e-4))
+
+
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+def test_lean_kernel_with_an_empty_k_part_ignores_lds_leftovers(dtype):
+    """K = 384 (3 group pairs) over the lean kernel's 4 K parts leaves the
+    last part empty; its steps must read only in-range staged data.  A GEMM
+    over NaN activations first fills the LDS of every CU with NaN, which an
+    out-of-range read of the group sums would turn into NaN outputs (0 * NaN)."""
+    from qwen_int4_hip import linear_kernel_name
+
+    torch_dtype = torch.float16 if dtype == "fp16" else torch.bfloat16
+    poison = torch.full((2048, 1536), float("nan"), dtype=torch_dtype, device=DEV)
+    q8, s8, z8 = weights("sym", 8960, 1536, O.BASE_SEED + 5)
+    for n in (384, 128):
+        kind = "f16" if dtype == "fp16" else "bf16"
+        assert linear_kernel_name(1, n, 384, torch_dtype).startswith(f"gemv_seg_kernel<{kind},4,1,4,")
+        q, s, z = weights("asym", n, 384, O.BASE_SEED + n)
+        x = O.activations(1, 384, seed=O.BASE_SEED + 3 * n, dtype=dtype)
+        bias = O._from_f32(np.linspace(-1, 1, n, dtype=np.float32), "bf16")
+        for _ in range(3):
+            hip_w4g64_linear(poison, *dev_weights(q8, s8, z8), None, out_features=8960, in_features=1536,
+                             group_size=64, packing=PackingFormat.CANONICAL)
+            check_linear(x, q, s, z, bias, n, 384, dtype)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "fp32"])
+@pytest.mark.parametrize("k", [1536, 16448])
+def test_gemm_row_scaling_keeps_every_row_exact(dtype, k):
+    """The GEMM stages each activation row as fp16 times a power of two
+    chosen from the row's largest magnitude.  Rows whose magnitudes lie far
+    outside fp16's range (1e-30, 1e30 -- representable in bf16 and fp32), a
+    zero row and rows with one large outlier must each match the oracle to
+    the same per-row relative error as ordinary rows.  k = 16448 stages rows
+    longer than a staging thread holds (a second read of the row)."""
+    n, rows = 72, 24
+    q, s, z = weights("asym", n, k, O.BASE_SEED + k)
+    base = np.random.default_rng(k).standard_normal((rows, k)).astype(np.float32)
+    factors = np.array([1e-30, 1e30, 0.0, 1.0, 3e-8, 6e4, 1e-3, 1e5] * 3, dtype=np.float32)
+    x32 = base * factors[:, None]
+    x32[3, 17] = np.float32(5e4)  # one outlier: the rest of its row sits 2^15..2^20 below it
+    x = O._from_f32(x32, dtype)
+    xt = to_dev(x, dtype)
+    got = from_dev(hip_w4g64_linear(xt, *dev_weights(q, s, z), None, out_features=n, in_features=k, group_size=64,
+                                    packing=PackingFormat.CANONICAL))
+    ref = O._to_f32(O.reference_linear(x, q, s, z, None, out_features=n, in_features=k, x_dtype=dtype,
+                                       bias_dtype="bf16"), dtype)
+    assert np.isfinite(got).all()
+    assert not got[2].any() and not ref[2].any()
+    for r in range(rows):
+        scale = float(np.abs(ref[r]).max())
+        if scale == 0.0:
+            continue
+        err = float(np.abs(got[r] - ref[r]).max()) / scale
+        # bf16 outputs: half an output ulp plus summation order; fp32: near-fp32
+        assert err <= (5e-3 if dtype == "bf16" else 1e-5), (r, err)
 
 
 @pytest.mark.parametrize("rows", [2, 40])
