@@ -24,7 +24,8 @@ extern "C" {
 
 /* Residual add + RMSNorm over `rows` rows of `hidden` bf16 values:
  *   s        = x                                   (delta == NULL)
- *            = bf16(x + bf16(delta))               (delta bf16 or fp32, as delta_dtype)
+ *            = bf16(x + bf16(delta))               (delta bf16, fp32, or fp32 partial
+ *                                                   sums: W4G64_DTYPE_F32_PARTIALS)
  *   out_sum  = s                                   (may be NULL; may alias x)
  *   out_norm = bf16(bf16(s * rsqrt(mean(s^2) + eps)) * weight)
  * in fp32 arithmetic with the reference's two roundings.  hidden is a

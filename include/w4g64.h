@@ -59,6 +59,14 @@ extern "C" {
 #define W4G64_DTYPE_BF16_PLANES 6
 #define W4G64_DTYPE_BF16_GATE_UP 7
 
+/* Residual delta given as `parts` fp32 partial sums [parts][rows][hidden] of a
+ * split-K projection (w4g64_linear_partials), accepted as delta_dtype by
+ * qwen2_add_rmsnorm (1..255 parts) and w4g64_linear_rmsnorm (1..8 parts): the
+ * delta is their sum in order from part 0, exactly the fp32 value the split-K
+ * reduction of w4g64_linear stores. */
+#define W4G64_DTYPE_F32_PARTIALS(parts) (0x100 | (parts))
+#define W4G64_DTYPE_F32_PARTS_OF(code) ((((code) & ~0xFF) == 0x100) ? ((code) & 0xFF) : 0)
+
 /* Version of this ABI (bumped on any signature or contract change). */
 int w4g64_abi_version(void);
 
@@ -169,7 +177,8 @@ int w4g64_linear_gate_up_planes(const void* x, const uint8_t* qweight, const uin
 
 /* Decode linear (one row, bf16: batch-1 decode) with the decoder's residual add and
  * RMSNorm formed in its activation staging:
- *   s      = bf16(residual + bf16(delta))          (delta bf16 or fp32)
+ *   s      = bf16(residual + bf16(delta))          (delta bf16, fp32, or 1..8 fp32
+ *                                                   partial sums: W4G64_DTYPE_F32_PARTIALS)
  *   x      = bf16(bf16(s * rsqrt(mean(s^2) + eps)) * norm_weight)
  *   y      = x @ dequant(W)^T (+ bias), bf16 [rows, out_features]
  *            -- or, with gate_up_planes != 0, the planes of
@@ -188,6 +197,25 @@ int w4g64_linear_rmsnorm(const void* residual, const void* delta, int delta_dtyp
                          const void* bias, int bias_dtype, void* y, int gate_up_planes, int64_t rows,
                          int64_t out_features, int64_t in_features, void* workspace, int64_t workspace_bytes,
                          void* stream);
+
+/* Number of fp32 partial sums per output w4g64_linear_partials writes for this
+ * problem (its K splits; 1 = unsplit), or 0 when the problem does not take
+ * that form: x_dtype W4G64_DTYPE_BF16_PLANES or W4G64_DTYPE_F32, 1..16 rows. */
+int64_t w4g64_linear_partial_count(int64_t rows, int64_t out_features, int64_t in_features, int x_dtype);
+
+/* The decode linear of w4g64_linear (x_dtype W4G64_DTYPE_BF16_PLANES or
+ * W4G64_DTYPE_F32, 1..16 rows, no bias) without its split-K reduction
+ * launch: writes the fp32 partial sums partials[s][rows][out_features],
+ * s < count = w4g64_linear_partial_count(...), whose sum in order from s = 0
+ * is w4g64_linear's output (count 1: that output).  The next residual add
+ * takes them as delta_dtype W4G64_DTYPE_F32_PARTIALS(count).  partials 16-byte
+ * aligned, partials_bytes >= count * rows * out_features * 4; no workspace.
+ * Replaces: the down projection of QwenMLP.forward and the residual add that
+ *           consumes it (src/qwen_int4/model.py:136, :149-154), split so that
+ *           the add performs the reduction. */
+int w4g64_linear_partials(const void* x, int x_dtype, const uint8_t* qweight, const uint16_t* scales,
+                          const uint8_t* zeros, float* partials, int64_t partials_bytes, int64_t rows,
+                          int64_t out_features, int64_t in_features, void* stream);
 
 /* Name of the kernel w4g64_linear launches for this problem (for profiles
  * and reports); never NULL. */

@@ -56,10 +56,14 @@ constexpr int kMaxLength = kMaxChunks * kChunk;
 // load is unconditional at a clamped address and issued before any use (a
 // guarded load would be waited for on its own); pieces past the row end are
 // masked out of the sum and not stored.
+// delta_kind kNormP: delta holds delta_parts fp32 partial sums [parts][rows][hidden]
+// of a split-K projection, added in order from 0 and then + 0 (no bias): the
+// value the split-K reduction would have stored as an fp32 delta.
 __global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(const uint16_t* x, const void* delta,
-                                                                   int delta_kind, const uint16_t* weight,
-                                                                   float eps, uint16_t* out_sum,
-                                                                   uint16_t* out_norm, int hidden) {
+                                                                   int delta_kind, int delta_parts,
+                                                                   const uint16_t* weight, float eps,
+                                                                   uint16_t* out_sum, uint16_t* out_norm,
+                                                                   int hidden) {
     constexpr int kStride = kNormThreads * 8;
     const int64_t base = (int64_t)blockIdx.x * hidden;
     int col[kNormIters];
@@ -77,6 +81,28 @@ __global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(const uint16_
             dr[i][1] = *(const u32x4*)((const float*)delta + base + c + 4);
         }
     }
+    if (delta_kind == kNormP) {
+        const int64_t part_stride = (int64_t)gridDim.x * hidden;
+#pragma unroll
+        for (int i = 0; i < kNormIters; ++i) {
+            const int c = min(col[i], hidden - 8);
+            float t[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            for (int pt = 0; pt < delta_parts; ++pt) {
+                const float* src = (const float*)delta + pt * part_stride + base + c;
+                const float4v lo = *(const float4v*)src, hi = *(const float4v*)(src + 4);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    t[e] += lo[e];
+                    t[4 + e] += hi[e];
+                }
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                dr[i][0][e] = __builtin_bit_cast(uint32_t, t[e] + 0.0f);
+                dr[i][1][e] = __builtin_bit_cast(uint32_t, t[4 + e] + 0.0f);
+            }
+        }
+    }
     float v[kNormIters][8];
     float sq = 0.0f;
 #pragma unroll
@@ -88,7 +114,7 @@ __global__ __launch_bounds__(kNormThreads) void add_rmsnorm_kernel(const uint16_
             if (delta_kind == kBF16) {
                 const uint32_t dw = dr[i][0][e / 2];
                 s = bf16_round(s + bf16_bits_to_float(e & 1 ? dw >> 16 : dw & 0xFFFFu));
-            } else if (delta_kind == kF32) {
+            } else if (delta_kind == kF32 || delta_kind == kNormP) {
                 // (a scalar copy first: bit_cast of a vector element lvalue reads element 0)
                 const uint32_t bits = dr[i][e / 4][e % 4];
                 s = bf16_round(s + bf16_round(__builtin_bit_cast(float, bits)));
@@ -698,8 +724,9 @@ int qwen2_add_rmsnorm(const void* x, const void* delta, int delta_dtype, const v
     if (hidden <= 0 || hidden % 8 || hidden > kNormThreads * 8 * kNormIters)
         return set_error(W4G64_STATUS_INVALID_VALUE, "hidden must be a multiple of 8 in [8, %d], got %lld",
                          kNormThreads * 8 * kNormIters, (long long)hidden);
-    if (delta && delta_dtype != W4G64_DTYPE_BF16 && delta_dtype != W4G64_DTYPE_F32)
-        return set_error(W4G64_STATUS_INVALID_DTYPE, "residual delta must be bf16 or fp32");
+    const int parts = W4G64_DTYPE_F32_PARTS_OF(delta_dtype);
+    if (delta && delta_dtype != W4G64_DTYPE_BF16 && delta_dtype != W4G64_DTYPE_F32 && parts == 0)
+        return set_error(W4G64_STATUS_INVALID_DTYPE, "residual delta must be bf16, fp32 or fp32 partial sums");
     if (rows == 0) return clear_error();
     if (!x || !weight || !out_norm)
         return set_error(W4G64_STATUS_INVALID_VALUE, "x, weight and out_norm must be non-null device pointers");
@@ -707,9 +734,10 @@ int qwen2_add_rmsnorm(const void* x, const void* delta, int delta_dtype, const v
         (delta && !aligned16(delta)))
         return set_error(W4G64_STATUS_INVALID_VALUE, "add_rmsnorm tensors must be 16-byte aligned");
     if (rows > 0x7FFFFFFF) return set_error(W4G64_STATUS_INVALID_VALUE, "too many rows");
+    const int kind = !delta ? 0 : (parts ? (int)kNormP : delta_dtype);
     hipLaunchKernelGGL(add_rmsnorm_kernel, dim3((unsigned)rows), dim3(kNormThreads), 0, (hipStream_t)stream,
-                       (const uint16_t*)x, delta, delta ? delta_dtype : 0, (const uint16_t*)weight, eps,
-                       (uint16_t*)out_sum, (uint16_t*)out_norm, (int)hidden);
+                       (const uint16_t*)x, delta, kind, parts, (const uint16_t*)weight, eps, (uint16_t*)out_sum,
+                       (uint16_t*)out_norm, (int)hidden);
     return launch_status(hipGetLastError(), "add_rmsnorm");
 }
 

@@ -96,7 +96,7 @@ int w4g64::clear_error() {
 
 extern "C" {
 
-int w4g64_abi_version(void) { return 2; }
+int w4g64_abi_version(void) { return 3; }
 
 const char* w4g64_last_error(void) { return g_error; }
 
@@ -337,8 +337,12 @@ int w4g64_linear_rmsnorm(const void* residual, const void* delta, int delta_dtyp
         return st;
     if (rows != 1)
         return fail(W4G64_STATUS_INVALID_VALUE, "the fused RMSNorm linear takes one row, got %lld", (long long)rows);
-    if (delta_dtype != W4G64_DTYPE_BF16 && delta_dtype != W4G64_DTYPE_F32)
-        return fail(W4G64_STATUS_INVALID_DTYPE, "delta must have dtype bfloat16 or float32");
+    const int parts = W4G64_DTYPE_F32_PARTS_OF(delta_dtype);
+    if (delta_dtype != W4G64_DTYPE_BF16 && delta_dtype != W4G64_DTYPE_F32 && parts == 0)
+        return fail(W4G64_STATUS_INVALID_DTYPE, "delta must have dtype bfloat16, float32 or fp32 partial sums");
+    if (parts > w4g64::kMaxDeltaParts)
+        return fail(W4G64_STATUS_UNSUPPORTED, "the fused RMSNorm linear adds at most %d partial sums, got %d",
+                    w4g64::kMaxDeltaParts, parts);
     if (!residual || !delta || !norm_weight || !out_sum)
         return fail(W4G64_STATUS_INVALID_VALUE, "residual, delta, norm_weight and out_sum must be non-null");
     if (!aligned(residual, 16) || !aligned(delta, 16) || !aligned(norm_weight, 16) || !aligned(out_sum, 16))
@@ -351,10 +355,11 @@ int w4g64_linear_rmsnorm(const void* residual, const void* delta, int delta_dtyp
     if (gate_up_planes && out_features % 2)
         return fail(W4G64_STATUS_INVALID_VALUE, "out_features must be even (gate rows then up rows), got %lld",
                     (long long)out_features);
-    const int kind = delta_dtype == W4G64_DTYPE_BF16 ? w4g64::kNormB : w4g64::kNormF;
+    const int kind = delta_dtype == W4G64_DTYPE_BF16 ? w4g64::kNormB : (parts ? w4g64::kNormP : w4g64::kNormF);
     w4g64::LinearProblem p{residual, kind, qweight, scales, zeros, bias, bias_dtype, y, rows, out_features,
                            in_features, gate_up_planes ? 1 : 0};
     p.norm_delta = delta;
+    p.norm_delta_parts = parts ? parts : 1;
     p.norm_weight = (const uint16_t*)norm_weight;
     p.norm_eps = eps;
     p.norm_out_sum = out_sum;
@@ -366,6 +371,42 @@ int w4g64_linear_rmsnorm(const void* residual, const void* delta, int delta_dtyp
                     (long long)in_features);
     if (int st = check_workspace(workspace, workspace_bytes, plan.workspace_bytes)) return st;
     return hip_status(w4g64::launch_gemv(p, plan, workspace, (hipStream_t)stream), "gemv");
+}
+
+int64_t w4g64_linear_partial_count(int64_t rows, int64_t out_features, int64_t in_features, int x_dtype) {
+    if (rows < 1 || rows > w4g64::kGemvMaxRows || out_features <= 0 || out_features > w4g64::kGemvMaxOutFeatures ||
+        in_features <= 0 || in_features % 64 || in_features > (1ll << 24))
+        return 0;
+    if (x_dtype != W4G64_DTYPE_BF16_PLANES && x_dtype != W4G64_DTYPE_F32) return 0;
+    const w4g64::GemvPlan plan =
+        w4g64::plan_gemv(rows, out_features, in_features, x_dtype == W4G64_DTYPE_F32 ? w4g64::kF32 : w4g64::kPlanes);
+    return plan.kind == 0 ? plan.splits : 0;
+}
+
+int w4g64_linear_partials(const void* x, int x_dtype, const uint8_t* qweight, const uint16_t* scales,
+                          const uint8_t* zeros, float* partials, int64_t partials_bytes, int64_t rows,
+                          int64_t out_features, int64_t in_features, void* stream) {
+    if (int st = fused_common_checks(qweight, scales, zeros, nullptr, W4G64_DTYPE_NONE, partials, 16, rows,
+                                     out_features, in_features))
+        return st;
+    if (x_dtype != W4G64_DTYPE_BF16_PLANES && x_dtype != W4G64_DTYPE_F32)
+        return fail(W4G64_STATUS_INVALID_DTYPE, "partial sums take bf16-planes or float32 activations");
+    const int64_t count = w4g64_linear_partial_count(rows, out_features, in_features, x_dtype);
+    if (count <= 0)
+        return fail(W4G64_STATUS_UNSUPPORTED, "partial sums are a decode form (1..%d rows), got %lld rows",
+                    w4g64::kGemvMaxRows, (long long)rows);
+    if (!x) return fail(W4G64_STATUS_INVALID_VALUE, "x must be a non-null device pointer");
+    if (!aligned(x, 16)) return fail(W4G64_STATUS_INVALID_VALUE, "x must be 16-byte aligned");
+    const int64_t need = count * rows * out_features * 4;
+    if (partials_bytes < need)
+        return fail(W4G64_STATUS_INVALID_VALUE, "partials must hold %lld bytes (%lld partial sums), got %lld",
+                    (long long)need, (long long)count, (long long)partials_bytes);
+    const int kind = x_dtype == W4G64_DTYPE_F32 ? w4g64::kF32 : w4g64::kPlanes;
+    w4g64::LinearProblem p{x, kind, qweight, scales, zeros, nullptr, W4G64_DTYPE_NONE, partials, rows, out_features,
+                           in_features};
+    p.partials_out = partials;
+    const w4g64::GemvPlan plan = w4g64::plan_gemv(rows, out_features, in_features, kind);
+    return hip_status(w4g64::launch_gemv(p, plan, nullptr, (hipStream_t)stream), "gemv");
 }
 
 int w4g64_linear_gate_up_planes(const void* x, const uint8_t* qweight, const uint16_t* scales, const uint8_t* zeros,

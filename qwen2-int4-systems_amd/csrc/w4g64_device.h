@@ -33,9 +33,12 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 enum XKind : int {
     kF16 = 1, kBF16 = 2, kF32 = 3, kSwiGLU = 5, kPlanes = 6,
     // bf16 activations formed in the decode GEMV's staging as RMSNorm(residual
-    // + delta), delta bf16 (kNormB) or fp32 (kNormF); internal kinds
-    kNormB = 7, kNormF = 8
+    // + delta), delta bf16 (kNormB), fp32 (kNormF) or the sum of up to
+    // kMaxDeltaParts fp32 split-K partial sums of the previous projection
+    // (kNormP); internal kinds
+    kNormB = 7, kNormF = 8, kNormP = 9
 };
+constexpr int kMaxDeltaParts = 8;
 
 // Slot order of the 8 values in an MFMA operand: slot p holds k = kSlotK[p].
 // (Used by host-side documentation/tests; kernels permute with v_perm.)

@@ -85,8 +85,9 @@ struct GemvArgs {
     int mv;      // A rows in use (= M)
     float* partials;  // [splits][M][N]
     int paired;          // paired gate|up epilogue (y = bf16 planes [3][M][N/2])
-    // RMSNorm prologue (kNormB / kNormF): x is the residual stream
+    // RMSNorm prologue (kNormB / kNormF / kNormP): x is the residual stream
     const void* delta;
+    int delta_parts;  // kNormP: partial sums [delta_parts][M][K] in delta
     const uint16_t* norm_w;
     float eps;
     uint16_t* out_sum;
@@ -98,7 +99,7 @@ struct GemvArgs {
 // The RMSNorm kinds take one row: SW STEPS groups x 8 items over 256 lanes.
 template <int XK, int SW, int STEPS, int TILES>
 constexpr int stage_items() {
-    if constexpr (XK == kNormB || XK == kNormF) return (SW * STEPS + 31) / 32;
+    if constexpr (XK == kNormB || XK == kNormF || XK == kNormP) return (SW * STEPS + 31) / 32;
     return XK == kPlanes ? (TILES * STEPS + 5) / 6 : (TILES * STEPS + 1) / 2;
 }
 
@@ -136,13 +137,16 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
     constexpr int kStaged = (XK == kF32 || XK == kSwiGLU || XK == kPlanes) ? 3 : 1;
     constexpr int kParts = (XK == kF32 || XK == kSwiGLU) ? 3 : 1;  // along K
     constexpr int kRowParts = XK == kPlanes ? 3 : 1;                // as A rows
-    constexpr bool kNorm = XK == kNormB || XK == kNormF;
+    constexpr bool kNorm = XK == kNormB || XK == kNormF || XK == kNormP;
     constexpr int kOut = (XK == kSwiGLU || XK == kPlanes) ? kF32 : (kNorm ? kBF16 : XK);  // output kind
     constexpr int R = 16 / SW;              // output features per wave
     constexpr int kBlockCols = kWaves * R;  // output features per workgroup
     constexpr int kStage = stage_items<XK, SW, STEPS, TILES>();
     // 16-byte loads per item (norm kinds: residual, delta, norm weight)
-    constexpr int kVecs = (XK == kF16 || XK == kBF16) ? 1 : (XK == kPlanes || XK == kNormB ? 3 : (XK == kNormF ? 4 : 2));
+    // (kNormP: residual, two per partial sum, norm weight)
+    constexpr int kVecs = (XK == kF16 || XK == kBF16) ? 1
+                          : (XK == kPlanes || XK == kNormB ? 3
+                                                           : (XK == kNormF ? 4 : (XK == kNormP ? 2 + 2 * kMaxDeltaParts : 2)));
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -228,10 +232,19 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
             v[u][0] = *(const u32x4*)((const uint16_t*)a.x + (int64_t)m * a.K + 8 * c);
             if constexpr (XK == kNormB) {
                 v[u][1] = *(const u32x4*)((const uint16_t*)a.delta + (int64_t)m * a.K + 8 * c);
-            } else {
+            } else if constexpr (XK == kNormF) {
                 const float* dsrc = (const float*)a.delta + (int64_t)m * a.K + 8 * c;
                 v[u][1] = *(const u32x4*)dsrc;
                 v[u][2] = *(const u32x4*)(dsrc + 4);
+            } else {
+                // every partial sum's item; parts past delta_parts re-read the last one
+#pragma unroll
+                for (int pt = 0; pt < kMaxDeltaParts; ++pt) {
+                    const int pc = min(pt, a.delta_parts - 1);
+                    const float* dsrc = (const float*)a.delta + ((int64_t)pc * a.M + m) * a.K + 8 * c;
+                    v[u][1 + 2 * pt] = *(const u32x4*)dsrc;
+                    v[u][2 + 2 * pt] = *(const u32x4*)(dsrc + 4);
+                }
             }
             v[u][kVecs - 1] = *(const u32x4*)(a.norm_w + 8 * c);
         } else {
@@ -289,9 +302,18 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
                     if constexpr (XK == kNormB) {
                         const uint32_t dw = v[u][1][e / 2];
                         dv = bf16_bits_to_float(h ? dw >> 16 : dw & 0xFFFFu);
-                    } else {
+                    } else if constexpr (XK == kNormF) {
                         const uint32_t bits = v[u][1 + (e + h) / 4][(e + h) % 4];  // element to a scalar first
                         dv = bf16_round(__builtin_bit_cast(float, bits));
+                    } else {
+                        // the split-K reduction's sum: parts in order from 0, then + 0 (no bias)
+                        float t = 0.0f;
+#pragma unroll
+                        for (int pt = 0; pt < kMaxDeltaParts; ++pt) {
+                            const uint32_t bits = v[u][1 + 2 * pt + (e + h) / 4][(e + h) % 4];
+                            t = pt < a.delta_parts ? t + __builtin_bit_cast(float, bits) : t;
+                        }
+                        dv = bf16_round(t + 0.0f);
                     }
                     sv[h] = bf16_round(xv + dv);
                     ps += __fmul_rn(sv[h], sv[h]);
@@ -608,12 +630,12 @@ __global__ __launch_bounds__(256) void split_reduce_kernel(SplitReduceArgs r) {
 
 template <int XK, int SW, int STEPS, int TILES>
 hipError_t launch_typed(const GemvArgs& args, const GemvPlan& plan, hipStream_t stream, hipEvent_t start,
-                        hipEvent_t stop) {
+                        hipEvent_t stop, bool unreduced) {
     // the staging capacity of this instantiation (the planner never exceeds it)
     if ((int64_t)args.M * args.gps * 8 > (int64_t)stage_items<XK, SW, STEPS, TILES>() * kThreads) return hipErrorInvalidValue;
-    constexpr bool kNorm = XK == kNormB || XK == kNormF;
+    constexpr bool kNorm = XK == kNormB || XK == kNormF || XK == kNormP;
     constexpr int kOut = (XK == kSwiGLU || XK == kPlanes) ? kF32 : (kNorm ? kBF16 : XK);
-    const bool split = plan.splits > 1;
+    const bool split = plan.splits > 1 && !unreduced;
     hipError_t err = launch_kernel(gemv_kernel<XK, SW, STEPS, TILES>, dim3(plan.n_blocks, plan.splits),
                                    dim3(kThreads), (size_t)plan.lds_bytes, stream, start, split ? nullptr : stop, args);
     if (err != hipSuccess || !split) return err;
@@ -623,26 +645,26 @@ hipError_t launch_typed(const GemvArgs& args, const GemvPlan& plan, hipStream_t 
 
 template <int XK, int SW, int TILES>
 hipError_t launch_steps(const GemvArgs& args, const GemvPlan& plan, hipStream_t stream, hipEvent_t start,
-                        hipEvent_t stop) {
+                        hipEvent_t stop, bool unreduced) {
     switch (plan.steps) {
-        case 2: return launch_typed<XK, SW, 2, TILES>(args, plan, stream, start, stop);
-        case 3: return launch_typed<XK, SW, 3, TILES>(args, plan, stream, start, stop);
-        case 6: return launch_typed<XK, SW, 6, TILES>(args, plan, stream, start, stop);
-        case 9: return launch_typed<XK, SW, 9, TILES>(args, plan, stream, start, stop);
-        case 12: return launch_typed<XK, SW, 12, TILES>(args, plan, stream, start, stop);
-        default: return launch_typed<XK, SW, 16, TILES>(args, plan, stream, start, stop);
+        case 2: return launch_typed<XK, SW, 2, TILES>(args, plan, stream, start, stop, unreduced);
+        case 3: return launch_typed<XK, SW, 3, TILES>(args, plan, stream, start, stop, unreduced);
+        case 6: return launch_typed<XK, SW, 6, TILES>(args, plan, stream, start, stop, unreduced);
+        case 9: return launch_typed<XK, SW, 9, TILES>(args, plan, stream, start, stop, unreduced);
+        case 12: return launch_typed<XK, SW, 12, TILES>(args, plan, stream, start, stop, unreduced);
+        default: return launch_typed<XK, SW, 16, TILES>(args, plan, stream, start, stop, unreduced);
     }
 }
 
 template <int XK, int TILES>
 hipError_t launch_sw(const GemvArgs& args, const GemvPlan& plan, hipStream_t stream, hipEvent_t start,
-                     hipEvent_t stop) {
+                     hipEvent_t stop, bool unreduced) {
     switch (plan.segments) {
-        case 16: return launch_steps<XK, 16, TILES>(args, plan, stream, start, stop);
-        case 8: return launch_steps<XK, 8, TILES>(args, plan, stream, start, stop);
-        case 4: return launch_steps<XK, 4, TILES>(args, plan, stream, start, stop);
-        case 2: return launch_steps<XK, 2, TILES>(args, plan, stream, start, stop);
-        default: return launch_steps<XK, 1, TILES>(args, plan, stream, start, stop);
+        case 16: return launch_steps<XK, 16, TILES>(args, plan, stream, start, stop, unreduced);
+        case 8: return launch_steps<XK, 8, TILES>(args, plan, stream, start, stop, unreduced);
+        case 4: return launch_steps<XK, 4, TILES>(args, plan, stream, start, stop, unreduced);
+        case 2: return launch_steps<XK, 2, TILES>(args, plan, stream, start, stop, unreduced);
+        default: return launch_steps<XK, 1, TILES>(args, plan, stream, start, stop, unreduced);
     }
 }
 
@@ -722,7 +744,8 @@ GemvPlan plan_segmented(int64_t rows, int64_t out_features, int64_t in_features,
     // staged activations (virtual rows x split width, 16-bit), the group
     // sums and the epilogue's per-segment results
     // (norm kinds: plus the per-item partial sums of squares and the row factors)
-    const int64_t norm_extra = (x_kind == kNormB || x_kind == kNormF) ? rows * (in_features / 64) * 8 * 4 + rows * 4 : 0;
+    const int64_t norm_extra =
+        (x_kind == kNormB || x_kind == kNormF || x_kind == kNormP) ? rows * (in_features / 64) * 8 * 4 + rows * 4 : 0;
     auto lds_for = [&](int64_t g) {
         return planes * (g * 64 + 8) * 2 + planes * g * 4 + mv * kWaves * 16 * 4 + norm_extra;
     };
@@ -835,36 +858,48 @@ hipError_t launch_gemv(const LinearProblem& p, const GemvPlan& plan, void* works
     args.mv = (int)(p.rows * (p.x_kind == kPlanes ? 3 : 1));
     if (plan.tiles != 1 && p.x_kind != kPlanes) return hipErrorInvalidValue;  // rows <= 16 fit one A tile
     args.paired = p.paired;
-    const bool norm = p.x_kind == kNormB || p.x_kind == kNormF;
+    const bool norm = p.x_kind == kNormB || p.x_kind == kNormF || p.x_kind == kNormP;
     if (p.paired && ((p.x_kind != kBF16 && !norm) || plan.segments > 8 || (p.out_features & 1)))
         return hipErrorInvalidValue;
     // the norm prologue needs the whole row in every workgroup
     if (norm && (plan.kind != 0 || plan.splits != 1 || !p.norm_delta || !p.norm_weight || !p.norm_out_sum))
         return hipErrorInvalidValue;
     args.delta = p.norm_delta;
+    args.delta_parts = p.norm_delta_parts;
+    if (p.x_kind == kNormP && (p.norm_delta_parts < 1 || p.norm_delta_parts > kMaxDeltaParts)) return hipErrorInvalidValue;
     args.norm_w = p.norm_weight;
     args.eps = p.norm_eps;
     args.out_sum = (uint16_t*)p.norm_out_sum;
-    args.partials = (float*)workspace;
+    // unreduced: the partial sums (or, unsplit, the fp32 result) go to the caller's buffer
+    const bool unreduced = p.partials_out != nullptr;
+    if (unreduced) {
+        constexpr int kNoOut = -1;
+        const int out_kind = (p.x_kind == kSwiGLU || p.x_kind == kPlanes || p.x_kind == kF32) ? kF32 : kNoOut;
+        if (out_kind != kF32 || p.bias || p.paired) return hipErrorInvalidValue;
+        args.y = p.partials_out;
+    }
+    args.partials = unreduced ? p.partials_out : (float*)workspace;
     switch (p.x_kind) {
         case kF16:
-            return launch_sw<kF16, 1>(args, plan, stream, start, stop);
+            return launch_sw<kF16, 1>(args, plan, stream, start, stop, unreduced);
         case kBF16:
-            return launch_sw<kBF16, 1>(args, plan, stream, start, stop);
+            return launch_sw<kBF16, 1>(args, plan, stream, start, stop, unreduced);
         case kSwiGLU:
-            return launch_sw<kSwiGLU, 1>(args, plan, stream, start, stop);
+            return launch_sw<kSwiGLU, 1>(args, plan, stream, start, stop, unreduced);
         case kNormB:
-            return launch_sw<kNormB, 1>(args, plan, stream, start, stop);
+            return launch_sw<kNormB, 1>(args, plan, stream, start, stop, unreduced);
         case kNormF:
-            return launch_sw<kNormF, 1>(args, plan, stream, start, stop);
+            return launch_sw<kNormF, 1>(args, plan, stream, start, stop, unreduced);
+        case kNormP:
+            return launch_sw<kNormP, 1>(args, plan, stream, start, stop, unreduced);
         case kPlanes:
             // 3 rows x rows: more than 16 virtual rows only with one segment per wave
-            if (plan.tiles == 1) return launch_sw<kPlanes, 1>(args, plan, stream, start, stop);
+            if (plan.tiles == 1) return launch_sw<kPlanes, 1>(args, plan, stream, start, stop, unreduced);
             if (plan.segments != 1 || plan.tiles > 3) return hipErrorInvalidValue;
-            if (plan.tiles == 2) return launch_steps<kPlanes, 1, 2>(args, plan, stream, start, stop);
-            return launch_steps<kPlanes, 1, 3>(args, plan, stream, start, stop);
+            if (plan.tiles == 2) return launch_steps<kPlanes, 1, 2>(args, plan, stream, start, stop, unreduced);
+            return launch_steps<kPlanes, 1, 3>(args, plan, stream, start, stop, unreduced);
         default:
-            return launch_sw<kF32, 1>(args, plan, stream, start, stop);
+            return launch_sw<kF32, 1>(args, plan, stream, start, stop, unreduced);
     }
 }
 

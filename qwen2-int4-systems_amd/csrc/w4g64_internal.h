@@ -28,6 +28,10 @@ struct LinearProblem {
     const uint16_t* norm_weight = nullptr;
     float norm_eps = 0.0f;
     void* norm_out_sum = nullptr;
+    int norm_delta_parts = 1;  // kNormP: fp32 partial sums [parts][rows][in_features] added in order
+    // decode GEMV: write the fp32 split-K partial sums [splits][rows][out_features]
+    // here (no bias, no reduction launch; one split: the fp32 result)
+    float* partials_out = nullptr;
 };
 
 // Decode GEMV (rows <= kGemvMaxRows).

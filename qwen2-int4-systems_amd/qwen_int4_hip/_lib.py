@@ -29,6 +29,14 @@ DTYPE_BF16_SWIGLU = 5  # activation form of w4g64_linear_swiglu (workspace / ker
 DTYPE_BF16_PLANES = 6  # three bf16 planes of an fp32 activation (w4g64_linear, 1..16 rows, fp32 out)
 DTYPE_BF16_GATE_UP = 7  # workspace / kernel-name queries of w4g64_linear_gate_up_planes
 
+
+def dtype_f32_partials(parts: int) -> int:
+    """Residual-delta code of ``parts`` fp32 partial sums (W4G64_DTYPE_F32_PARTIALS)."""
+    if not 1 <= parts <= 255:
+        raise ValueError(f"partial sum count must be in [1, 255], got {parts}")
+    return 0x100 | parts
+
+
 # (name, restype, argtypes) for every symbol include/*.h declares.
 _p, _i64, _int = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
 SIGNATURES = {
@@ -40,6 +48,8 @@ SIGNATURES = {
     "w4g64_linear": (_int, [_p, _int, _p, _p, _p, _p, _int, _p, _i64, _i64, _i64, _p, _i64, _p]),
     "w4g64_linear_timed": (_int, [_p, _int, _p, _p, _p, _p, _int, _p, _i64, _i64, _i64, _p, _i64, _p, _p, _p]),
     "w4g64_linear_kernel_name": (ctypes.c_char_p, [_i64, _i64, _i64, _int]),
+    "w4g64_linear_partial_count": (_i64, [_i64, _i64, _i64, _int]),
+    "w4g64_linear_partials": (_int, [_p, _int, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p]),
     "w4g64_linear_static_scratch": (_int, [_p, _int, _p, _p, _p, _p, _int, _p, _i64, _i64, _i64, _p]),
     "w4g64_static_scratch_bytes": (_i64, []),
     "w4g64_linear_swiglu": (_int, [_p, _p, _p, _p, _p, _int, _p, _i64, _i64, _i64, _p, _i64, _p]),

@@ -178,6 +178,14 @@ class FusedDecodeStep:
         else:
             self.gate_up = buf(2 * self.inter)
         self.down = buf(self.hidden, torch.float32)
+        # the planes down projection leaves its split-K partial sums to the
+        # next residual add (the fused norm linear adds at most 8)
+        self.down_parts = 0
+        if self.paired:
+            parts = self.lib.w4g64_linear_partial_count(batch, self.hidden, self.inter, _lib.DTYPE_BF16_PLANES)
+            if 1 <= parts <= (8 if self.fused_norm else 255):
+                self.down_parts = parts
+                self.down_partials = torch.empty((parts, batch, self.hidden), dtype=torch.float32, device=device)
         shapes = [(self.qkv.shape[1], self.hidden, _lib.DTYPE_BF16),
                   (self.hidden, self.heads * self.head_dim, _lib.DTYPE_BF16),
                   (2 * self.inter, self.hidden, _lib.DTYPE_BF16_GATE_UP if self.paired else _lib.DTYPE_BF16),
@@ -264,7 +272,12 @@ class FusedDecodeStep:
                     _ptr(self.normed), _ptr(gu["qweight"]), _ptr(gu["scales"]), _ptr(gu["zeros"]), _ptr(gu["bias"]),
                     _lib.DTYPE_NONE if gu["bias"] is None else _lib.DTYPE_BF16, _ptr(self.planes), self.batch,
                     2 * self.inter, self.hidden, _ptr(self.workspace), self.workspace.numel(), stream))
-            if self.paired:
+            if self.paired and self.down_parts:
+                _lib.check(self.lib.w4g64_linear_partials(
+                    _ptr(self.planes), _lib.DTYPE_BF16_PLANES, _ptr(down.qweight), _ptr(down.scales),
+                    _ptr(down.zeros), _ptr(self.down_partials), self.down_partials.numel() * 4, self.batch,
+                    self.hidden, self.inter, stream))
+            elif self.paired:
                 _lib.check(self.lib.w4g64_linear(
                     _ptr(self.planes), _lib.DTYPE_BF16_PLANES, _ptr(down.qweight), _ptr(down.scales),
                     _ptr(down.zeros), None, _lib.DTYPE_NONE, _ptr(self.down), self.batch, self.hidden, self.inter,
@@ -275,7 +288,10 @@ class FusedDecodeStep:
                     _ptr(self.gate_up), _ptr(down.qweight), _ptr(down.scales), _ptr(down.zeros), None,
                     _lib.DTYPE_NONE, _ptr(self.down), self.batch, self.hidden, self.inter, _ptr(self.workspace),
                     self.workspace.numel(), stream))
-            delta, delta_code = self.down, _lib.DTYPE_F32
+            if self.paired and self.down_parts:
+                delta, delta_code = self.down_partials, _lib.dtype_f32_partials(self.down_parts)
+            else:
+                delta, delta_code = self.down, _lib.DTYPE_F32
         self._norm_at(cur, delta, delta_code, model.model.norm.weight, stream)
         if not self.hip_head:
             logits = F.linear(self.normed, model.lm_head.weight)

@@ -41,7 +41,7 @@ def test_library_exports_every_declared_symbol():
     for name in declared:
         assert hasattr(lib, name), f"{name} declared in include/*.h but not exported"
     assert set(declared) == set(_lib.SIGNATURES), "ctypes signatures out of sync with the header"
-    assert lib.w4g64_abi_version() == 2
+    assert lib.w4g64_abi_version() == 3
 
 
 def test_c_layer_rejects_before_launch():
@@ -212,6 +212,44 @@ def test_gate_up_planes_and_planes_form_reject_before_launch():
         _lib.STATUS_INVALID_VALUE
     # 9..16 rows pair inside the segmented kernel (one segment per wave)
     assert lib.w4g64_linear_kernel_name(16, 17920, 1536, _lib.DTYPE_BF16_GATE_UP).startswith(b"gemv_kernel<bf16,1,")
+
+
+def test_partial_sum_forms_reject_before_launch():
+    lib = _lib.load()
+    null = None
+    buf = ctypes.create_string_buffer(1 << 16)
+    base = (ctypes.addressof(buf) + 255) & ~255
+    p = ctypes.c_void_p(base)
+    f = ctypes.c_float(1e-6)
+    planes = _lib.DTYPE_BF16_PLANES
+    # the decode down projection (1 row, planes) splits K; more rows, other
+    # activation kinds or GEMM rows do not take the form
+    count = lib.w4g64_linear_partial_count(1, 1536, 8960, planes)
+    assert 2 <= count <= 8
+    assert lib.w4g64_linear_partial_count(1, 1536, 8960, _lib.DTYPE_F32) >= 1
+    assert lib.w4g64_linear_partial_count(17, 1536, 8960, planes) == 0
+    assert lib.w4g64_linear_partial_count(1, 1536, 8960, _lib.DTYPE_BF16) == 0
+    assert lib.w4g64_linear_partial_count(0, 1536, 8960, planes) == 0
+    assert lib.w4g64_linear_partial_count(1, 1536, 100, planes) == 0
+    need = count * 1536 * 4
+    assert lib.w4g64_linear_partials(p, _lib.DTYPE_BF16, p, p, p, p, need, 1, 1536, 8960,
+                                     null) == _lib.STATUS_INVALID_DTYPE
+    assert lib.w4g64_linear_partials(p, planes, p, p, p, p, 1 << 30, 17, 1536, 8960, null) == _lib.STATUS_UNSUPPORTED
+    assert lib.w4g64_linear_partials(p, planes, p, p, p, p, need - 4, 1, 1536, 8960,
+                                     null) == _lib.STATUS_INVALID_VALUE
+    assert b"partial sums" in lib.w4g64_last_error()
+    assert lib.w4g64_linear_partials(ctypes.c_void_p(base + 8), planes, p, p, p, p, need, 1, 1536, 8960,
+                                     null) == _lib.STATUS_INVALID_VALUE
+    assert lib.w4g64_linear_partials(null, planes, p, p, p, p, need, 1, 1536, 8960, null) == _lib.STATUS_INVALID_VALUE
+    # the residual-delta code: 1..255 parts; the fused norm linear adds at most 8
+    assert _lib.dtype_f32_partials(6) == 0x106
+    with pytest.raises(ValueError):
+        _lib.dtype_f32_partials(0)
+    assert lib.qwen2_add_rmsnorm(p, p, 0x200, p, f, p, p, 1, 1536, null) == _lib.STATUS_INVALID_DTYPE
+    assert lib.w4g64_linear_rmsnorm(p, p, _lib.dtype_f32_partials(9), p, f, ctypes.c_void_p(base + 4096), p, p, p,
+                                    null, 0, p, 0, 1, 64, 64, null, 0, null) == _lib.STATUS_UNSUPPORTED
+    assert lib.w4g64_linear_rmsnorm(p, p, 0x300, p, f, ctypes.c_void_p(base + 4096), p, p, p, null, 0, p, 0, 1, 64,
+                                    64, null, 0, null) == _lib.STATUS_INVALID_DTYPE
 
 
 def test_workspace_and_kernel_plan_queries():

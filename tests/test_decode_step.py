@@ -301,6 +301,97 @@ def test_linear_planes_form_matches_reference_linear(rows, n, k):
     assert bool(torch.isfinite(y).all()) and _normwise(y, want) <= 1e-5
 
 
+def _partials_and_reduced(lib, x, code, qw, sc, z, rows, n, k):
+    """w4g64_linear_partials' partial sums and w4g64_linear's reduced output."""
+    parts = lib.w4g64_linear_partial_count(rows, n, k, code)
+    assert parts >= 1
+    partials = torch.empty((parts, rows, n), dtype=torch.float32, device="cuda")
+    _lib.check(lib.w4g64_linear_partials(_p(x), code, _p(qw), _p(sc), _p(z), _p(partials), partials.numel() * 4,
+                                         rows, n, k, _stream()))
+    ws = torch.zeros(max(1, lib.w4g64_linear_workspace_bytes(rows, n, k, code)), dtype=torch.uint8, device="cuda")
+    y = torch.empty((rows, n), dtype=torch.float32, device="cuda")
+    _lib.check(lib.w4g64_linear(_p(x), code, _p(qw), _p(sc), _p(z), None, 0, _p(y), rows, n, k, _p(ws), ws.numel(),
+                                _stream()))
+    torch.cuda.synchronize()
+    return partials, y
+
+
+def _sum_in_order(partials):
+    total = torch.zeros_like(partials[0])
+    for part in partials:
+        total = total + part
+    return total + 0.0
+
+
+@pytest.mark.parametrize("code", [_lib.DTYPE_BF16_PLANES, _lib.DTYPE_F32])
+@pytest.mark.parametrize("rows", [1, 2, 5, 16])
+@pytest.mark.parametrize("n,k", [(1536, 8960), (100, 128)])
+def test_linear_partials_sum_to_the_reduced_linear(code, rows, n, k):
+    """w4g64_linear_partials leaves the split-K partial sums to the caller:
+    their sum in order from part 0 is w4g64_linear's fp32 output bit for bit
+    (the reduction kernel adds them in that order)."""
+    lib = _lib.load()
+    g = _gen(rows * 29 + n + k + code)
+    h = torch.randn((rows, k), generator=g, device="cuda") * 2
+    x = _split3(h) if code == _lib.DTYPE_BF16_PLANES else h
+    qw, sc, z = _weights(n, k, 31, asymmetric=True)
+    partials, y = _partials_and_reduced(lib, x, code, qw, sc, z, rows, n, k)
+    assert torch.equal(_sum_in_order(partials), y)
+    if n == 1536 and k == 8960 and code == _lib.DTYPE_BF16_PLANES:
+        assert partials.shape[0] > 1  # the decode down projection splits K
+
+
+@pytest.mark.parametrize("rows", [1, 3])
+def test_add_rmsnorm_adds_partial_sums_like_the_reduced_delta(rows):
+    """qwen2_add_rmsnorm with delta W4G64_DTYPE_F32_PARTIALS(count) = with the
+    reduced fp32 delta, bit for bit (sum and norm)."""
+    lib = _lib.load()
+    hidden, k = 1536, 8960
+    g = _gen(rows + 41)
+    x = (torch.randn((rows, hidden), generator=g, device="cuda") * 3).to(torch.bfloat16)
+    planes = _split3(torch.randn((rows, k), generator=g, device="cuda") * 2)
+    qw, sc, z = _weights(hidden, k, 37, asymmetric=False)
+    partials, y = _partials_and_reduced(lib, planes, _lib.DTYPE_BF16_PLANES, qw, sc, z, rows, hidden, k)
+    weight = (torch.rand(hidden, generator=g, device="cuda") + 0.5).to(torch.bfloat16)
+    outs = []
+    for delta, code in ((y, _lib.DTYPE_F32), (partials, _lib.dtype_f32_partials(partials.shape[0]))):
+        out_sum, out = torch.empty_like(x), torch.empty_like(x)
+        _lib.check(lib.qwen2_add_rmsnorm(_p(x), _p(delta), code, _p(weight), ctypes.c_float(1e-6), _p(out_sum),
+                                         _p(out), rows, hidden, _stream()))
+        outs.append((out_sum, out))
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+
+
+@pytest.mark.parametrize("form,n", [("linear", 2048), ("planes", 17920)])
+def test_linear_rmsnorm_adds_partial_sums_like_the_reduced_delta(form, n):
+    """w4g64_linear_rmsnorm with the down projection's partial sums as delta =
+    with their reduced fp32 output: residual sum and linear output bit for bit."""
+    lib = _lib.load()
+    hidden, inter = 1536, 8960
+    g = _gen(n + 43)
+    x = (torch.randn((1, hidden), generator=g, device="cuda") * 3).to(torch.bfloat16)
+    planes = _split3(torch.randn((1, inter), generator=g, device="cuda") * 2)
+    dq, ds, dz = _weights(hidden, inter, 47, asymmetric=True)
+    partials, y = _partials_and_reduced(lib, planes, _lib.DTYPE_BF16_PLANES, dq, ds, dz, 1, hidden, inter)
+    assert 1 < partials.shape[0] <= 8
+    qw, sc, z = _weights(n, hidden, 53, asymmetric=True)
+    weight = (torch.rand(hidden, generator=g, device="cuda") + 0.5).to(torch.bfloat16)
+    pl = form == "planes"
+    ws = torch.zeros(1 << 20, dtype=torch.uint8, device="cuda")
+    outs = []
+    for delta, code in ((y, _lib.DTYPE_F32), (partials, _lib.dtype_f32_partials(partials.shape[0]))):
+        out_sum = torch.empty_like(x)
+        out = (torch.empty((3, 1, n // 2), dtype=torch.bfloat16, device="cuda") if pl
+               else torch.empty((1, n), dtype=torch.bfloat16, device="cuda"))
+        _lib.check(lib.w4g64_linear_rmsnorm(_p(x), _p(delta), code, _p(weight), ctypes.c_float(1e-6), _p(out_sum),
+                                            _p(qw), _p(sc), _p(z), None, 0, _p(out), 1 if pl else 0, 1, n, hidden,
+                                            _p(ws), ws.numel(), _stream()))
+        outs.append((out_sum, out))
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+
+
 @pytest.mark.parametrize("rows", [1, 4, 9, 16])
 @pytest.mark.parametrize("inter,k", [(8960, 1536), (100, 128), (72, 192)])
 @pytest.mark.parametrize("with_bias", [False, True])
