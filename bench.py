@@ -462,16 +462,17 @@ def summarize_pmc(fetch_csv: str, write_csv: str, out_path: str) -> int:
     def split(rows):
         cal = [v for _, name, v in rows if "unpack_kernel" in name]
         dec = [v for _, name, v in rows if "gemv" in name]
+        red = [v for _, name, v in rows if "split_reduce" in name]  # second dispatch of a split-K decode call
         gem = [v for _, name, v in rows if "gemm" in name]
         if len(cal) != 1 or len(dec) % 21 or not dec:
             raise SystemExit(f"unexpected dispatch sequence: {len(cal)} calibration, {len(dec)} decode dispatches")
-        return cal[0], dec, gem
+        return cal[0], dec + red, gem
 
     f_cal, f_dec, f_gem = split(fetch)
     w_cal, w_dec, w_gem = split(write)
     f_scale = (CALIBRATION_PACKED_BYTES / 1024) / f_cal   # true KiB per counted KiB
     w_scale = (2 * CALIBRATION_PACKED_BYTES / 1024) / w_cal
-    steps = len(f_dec) // 21
+    steps = sum(1 for _, name, _ in fetch if "gemv" in name) // 21
     step_bytes = sum(algorithmic_bytes(r, n, k) for r in DECODE_ROWS for (n, k) in QWEN2_SHAPES.values())
     fetch_step = sum(f_dec) * f_scale * 1024 / steps
     write_step = sum(w_dec) * w_scale * 1024 / steps

@@ -157,8 +157,8 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
     // (id % 8); XCD x gets the contiguous tile range [start_x, start_x +
     // count_x) -- a bijection on [0, dp_tiles) -- so an XCD's workgroups share
     // activation row bands in their L2.  Split tiles follow: `splits`
-    // consecutive workgroups per tile, each over its own K range, writing fp32
-    // partial sums that a second kernel adds up in range order.
+    // workgroups per tile, each over its own K range, writing fp32 partial
+    // sums that a second kernel adds up in range order.
     const int bid = blockIdx.x;
     int t, gbeg, gcnt, slot = -1;
     if (bid < a.dp_tiles) {
@@ -169,9 +169,23 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
         gbeg = 0;
         gcnt = a.G;
     } else {
-        slot = bid - a.dp_tiles;
-        t = a.dp_tiles + slot / a.splits;
-        gbeg = (slot % a.splits) * a.gps;
+        // split workgroups: the (K range, tile) list in K-range-major order is
+        // dealt to the XCDs in contiguous runs, so an XCD's workgroups share
+        // K ranges, and the activation slice of a row band (read by every
+        // column tile) and the weight slice of a column tile (read by every
+        // row band) stay in its L2
+        const int split_tiles = a.tiles_m * a.tiles_n - a.dp_tiles;
+        const int total = split_tiles * a.splits;
+        const int sb = bid - a.dp_tiles;
+        const int xcd = sb % kXcds;
+        const int base = total / kXcds;
+        const int extra = total % kXcds;
+        const int e = xcd * base + (xcd < extra ? xcd : extra) + sb / kXcds;
+        const int piece = e / split_tiles;
+        const int ti = e - piece * split_tiles;
+        t = a.dp_tiles + ti;
+        slot = ti * a.splits + piece;  // partial-sum slot: tile-major, as the reduction reads them
+        gbeg = piece * a.gps;
         gcnt = min(a.gps, a.G - gbeg);
     }
     const int tile_m = t / a.tiles_n;
