@@ -480,7 +480,7 @@ def summarize_pmc(fetch_csv: str, write_csv: str, out_path: str) -> int:
         "calibration": {"kernel": "unpack_kernel", "reads_bytes": CALIBRATION_PACKED_BYTES,
                         "writes_bytes": 2 * CALIBRATION_PACKED_BYTES, "FETCH_SIZE_KiB": f_cal, "WRITE_SIZE_KiB": w_cal,
                         "fetch_scale": f_scale, "write_scale": w_scale},
-        "decode": {"kernel": "gemv kernels (all 21 calls of a step)", "steps": steps, "launches_per_step": 21,
+        "decode": {"kernel": "decode GEMV kernels and their split-K reductions (all 21 calls of a step)", "steps": steps, "launches_per_step": 21,
                    "algorithmic_bytes_per_launch": step_bytes / 21,
                    "fetch_bytes_per_launch": fetch_step / 21, "write_bytes_per_launch": write_step / 21,
                    "traffic_bytes_per_launch": (fetch_step + write_step) / 21,
@@ -890,7 +890,7 @@ def main() -> int:
         "parity": parity,
         "roofline": {
             "bound": "hbm",
-            "kernel": "gemv_kernel / gemv16_kernel (all 21 calls of a step)",
+            "kernel": "gemv_seg_kernel / gemv_kernel / gemv16_kernel + split_reduce_kernel (all 21 calls of a step)",
             "achieved": round(achieved, 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
