@@ -5,11 +5,15 @@
  * a HIP stream as `void*`, int status codes W4G64_STATUS_*, the message of a
  * failed call in w4g64_last_error().  Nothing here allocates or synchronizes.
  *
- * With these, one decoder layer's decode step is six launches:
+ * With these, one decoder layer's decode step is at most seven launches:
  *   add_rmsnorm -> W4G64 q|k|v (one N = (H + 2 KVH) * D launch, bias)
  *   -> decode_attention -> W4G64 o_proj -> add_rmsnorm
- *   -> W4G64 gate|up (one N = 2 I launch) -> w4g64_linear_swiglu down_proj,
+ *   -> W4G64 gate|up (one N = 2 I launch) -> W4G64 down_proj,
  * and the step ends with add_rmsnorm -> lm_head (logits and greedy token).
+ * At batch 1 it is five: each add_rmsnorm after the first is formed in the
+ * staging of the linear that follows it (w4g64_linear_rmsnorm), and the down
+ * projection's K-split partial sums are added there too
+ * (w4g64_linear_partials, W4G64_DTYPE_F32_PARTIALS).
  */
 #ifndef QWEN_INT4_HIP_QWEN2_DECODE_H
 #define QWEN_INT4_HIP_QWEN2_DECODE_H

@@ -6,7 +6,7 @@
 //     y[m, n] = rowscale[m] * sum_g scale[n, g] * D_g[m, n]  (+ bias[n]),
 //     D_g[m, n] = sum_{k in g} a[m, k] * (code[n, k] - zero[n, g]),
 // where D_g is one 64-wide group's contraction on the matrix cores
-// (v_mfma_f32_32x32x16_f16, fp32 accumulation) and the group scale is
+// (v_mfma_f32_16x16x32_f16, fp32 accumulation) and the group scale is
 // applied to it in fp32 (one FMA per output per group).
 //   * B = (code - zero) is an integer in [-15, 15]: exact in fp16, built from
 //     the packed nibbles by one bitwise select and one v_pk_add_f16 per pair.
@@ -31,7 +31,7 @@
 //     lane), so the weights need no byte shuffle.
 //
 // Workgroup = 4 waves, output tile 128 x 256: wave w owns all 128 rows of the
-// 64 output features [n0 + 64 w, n0 + 64 w + 64), as 4 x 2 blocks of 32 x 32.
+// 64 output features [n0 + 64 w, n0 + 64 w + 64), as 8 x 4 blocks of 16 x 16.
 // One K step = one 64-wide group.  Two workgroups share a CU (78 KB of LDS,
 // at most 256 registers per lane each).
 //   * Every load is a gfx950 direct global->LDS load into a ring of S = 3
@@ -41,10 +41,11 @@
 //     chunks of a row are XOR-swizzled by a_swizzle(row), which the fragment
 //     reads undo, so fragment reads are conflict-free.
 //   * Per step, a wave decodes its own 64 columns' (code - zero) for the
-//     whole group (4 sub-steps x 2 column blocks), then walks its 4 row
-//     blocks: for each, the two column blocks' 4-MFMA chains over the group
-//     (lane group q of 2 takes K values [32 q, 32 q + 32) of the group,
-//     sub-step kk uses [32 q + 8 kk, + 8)), then acc += scale * D.
+//     whole group (4 column blocks x 2 MFMAs), then walks its 8 row blocks:
+//     for each, the four column blocks' 2-MFMA chains over the group (lane
+//     group q of 4 takes K values [16 q, 16 q + 16) of the group, MFMA h
+//     uses [16 q + 8 h, + 8)), then acc += scale * D, issued after the next
+//     row block's MFMAs so the matrix cores and the FMAs overlap.
 //   * Waits are explicit: every step issues the same number of vector memory
 //     operations, so "step s has landed" is a vmcnt bound known at compile
 //     time (steps past the end are not issued; the last waits tighten).
