@@ -88,6 +88,8 @@ struct GemmArgs {
 };
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
+// Word 3 of a raw gfx9 buffer resource (32-bit data format; no swizzle, no stride).
+constexpr int kRsrcWord3 = 0x00020000;
 
 // s_waitcnt with only the vector memory counter constrained (gfx9 encoding:
 // vmcnt bits [3:0] and [15:14], expcnt [6:4] and lgkmcnt [11:8] left at max).
@@ -151,7 +153,8 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    // uniform, so the LDS destinations (M0) and stage offsets derived from it stay scalar
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
     // ---- tile and K range of this workgroup ----
     // Data-parallel tiles: workgroup ids are dealt to the XCDs round robin
@@ -194,7 +197,11 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
     const int64_t m0 = (int64_t)tile_m * kBM;
     const int64_t nw = (int64_t)tile_n * kBN + 64 * wave;  // this wave's first output feature
 
-    // ---- per-lane DMA sources (32-bit offsets; the host keeps every operand below 2^31 elements) ----
+    // ---- per-lane DMA sources ----
+    // Each load address is a uniform base advanced per step (scalar
+    // registers) plus a fixed 32-bit per-lane byte offset, so a step's loads
+    // cost no vector instructions.  The host keeps the staged rows and the
+    // packed weights below 2^31 elements, so the byte offsets fit 32 bits.
     // activations: instruction d writes tile rows [8 (wave kDma + d), +8), 16 B per lane
     uint32_t a_off[kDma];
 #pragma unroll
@@ -203,7 +210,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
         const int chunk = (lane & 7) ^ a_swizzle(r);
         int m = (int)m0 + r;
         m = m < a.M ? m : a.M - 1;  // rows past M load a valid row; their outputs are not stored
-        a_off[d] = (uint32_t)m * (uint32_t)a.K + (uint32_t)gbeg * 64u + 8u * (uint32_t)chunk;
+        a_off[d] = 2u * ((uint32_t)m * (uint32_t)a.K + 8u * (uint32_t)chunk);
     }
     // weights: DMA instruction b, lane L -> column nw + 32 b + L % 32, bytes [16 (L / 32), +16)
     const int c = lane & 15;   // this lane's column within a 16-column block / row within a 16-row block
@@ -215,31 +222,46 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
         n = n < a.N ? n : a.N - 1;
         w_off[b] = (uint32_t)n * (uint32_t)a.wg * 32u + 16u * (uint32_t)(lane >> 5);
     }
-    // scale / zero of column nw + lane
+    // scale / zero of column nw + lane: element s_row + gw of weight group gw.
+    // The zero nibble's byte is (s_row + gw) >> 1 = (s_row >> 1) + (s_row & gw & 1).
     int ncol = (int)nw + lane;
     ncol = ncol < a.N ? ncol : a.N - 1;
     const uint32_t s_row = (uint32_t)ncol * (uint32_t)a.wg;  // scale / zero element of weight group 0
+    const uint32_t s_off = 2u * s_row;
+    const uint32_t z_off_even = s_row >> 1, z_off_odd = (s_row >> 1) + (s_row & 1u);
     // weight group of this workgroup's K step gg (one wrap at most: K' <= 2 in_features)
     auto wgroup = [&](int gg) {
         const int gabs = gbeg + gg;
         return gabs >= a.wg ? gabs - a.wg : gabs;
     };
 
+    // Buffer resources over the four operands (raw, stride 0, exact byte
+    // sizes): a load's address is the per-lane offset plus a per-step scalar
+    // offset, and a step's issue costs scalar instructions only.
+    const __amdgpu_buffer_rsrc_t x_rsrc =
+        __builtin_amdgcn_make_buffer_rsrc((void*)a.x, 0, (int)(2u * (uint32_t)a.M * (uint32_t)a.K), kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t w_rsrc =
+        __builtin_amdgcn_make_buffer_rsrc((void*)a.qweight, 0, (int)((uint32_t)a.N * (uint32_t)a.wg * 32u), kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t s_rsrc =
+        __builtin_amdgcn_make_buffer_rsrc((void*)a.scales, 0, (int)((uint32_t)a.N * (uint32_t)a.wg * 2u), kRsrcWord3);
+    const __amdgpu_buffer_rsrc_t z_rsrc =
+        __builtin_amdgcn_make_buffer_rsrc((void*)a.zeros, 0, (int)(((uint32_t)a.N * (uint32_t)a.wg + 1u) >> 1), kRsrcWord3);
     auto issue = [&](int gg) {  // callers pass gg < G only
         unsigned char* st = smem[gg % kStages];
         const int gw = wgroup(gg);
+        const uint32_t z_off = (gw & 1) ? z_off_odd : z_off_even;
 #pragma unroll
         for (int d = 0; d < kDma; ++d)
-            __builtin_amdgcn_global_load_lds((const void*)(a.x + (a_off[d] + 64u * (uint32_t)gg)),
-                                             (lds_ptr_t)(st + 1024 * (wave * kDma + d)), 16, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(x_rsrc, (lds_ptr_t)(st + 1024 * (wave * kDma + d)), 16, a_off[d],
+                                                     128 * (gbeg + gg), 0, 0);
 #pragma unroll
         for (int bj = 0; bj < 2; ++bj)
-            __builtin_amdgcn_global_load_lds((const void*)(a.qweight + (w_off[bj] + 32u * (uint32_t)gw)),
-                                             (lds_ptr_t)(st + kABytes + 2048 * wave + 1024 * bj), 16, 0, 0);
-        __builtin_amdgcn_global_load_lds((const void*)(a.scales + (s_row + (uint32_t)gw)),
-                                         (lds_ptr_t)(st + kABytes + kWBytes + 256 * wave), 2, 0, 0);
-        __builtin_amdgcn_global_load_lds((const void*)(a.zeros + ((s_row + (uint32_t)gw) >> 1)),
-                                         (lds_ptr_t)(st + kABytes + kWBytes + kSBytes + 256 * wave), 1, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rsrc, (lds_ptr_t)(st + kABytes + 2048 * wave + 1024 * bj), 16,
+                                                     w_off[bj], 32 * gw, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(s_rsrc, (lds_ptr_t)(st + kABytes + kWBytes + 256 * wave), 2, s_off,
+                                                 2 * gw, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(z_rsrc, (lds_ptr_t)(st + kABytes + kWBytes + kSBytes + 256 * wave), 1,
+                                                 z_off, gw >> 1, 0, 0);
     };
 
     float4v acc[RB][4];
@@ -248,13 +270,12 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
 #pragma unroll
         for (int bj = 0; bj < 4; ++bj) acc[i][bj] = float4v{0.f, 0.f, 0.f, 0.f};
 
-    // parity of each of this lane's four columns' zero element index at weight group 0
-    int zpar[4];
-#pragma unroll
-    for (int bj = 0; bj < 4; ++bj) {
-        const int n = (int)nw + 16 * bj + c;
-        zpar[bj] = (int)(((uint32_t)(n < a.N ? n : a.N - 1) * (uint32_t)a.wg) & 1u);
-    }
+    // Bit position of the zero nibble of this lane's columns nw + 16 bj + c in
+    // its byte: the parity of the element index n wg + gw, i.e. of c wg + gw
+    // (nw and 16 bj are even), for gw even / odd.  A column past N (clamped to
+    // N - 1 in the loads) may take the other nibble: its outputs are not stored.
+    const int cpar = c & a.wg & 1;
+    const int zsh_even = 4 * cpar, zsh_odd = 4 * (cpar ^ 1);
 
     // Packed weights of step g for column block bj, read back from the stage:
     // the 8 bytes = K values [16 kq, 16 kq + 16) of column nw + 16 bj + c;
@@ -274,18 +295,21 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
         r.zb = st[kABytes + kWBytes + kSBytes + 256 * wave + 4 * col];
         return r;
     };
-    // Per-group constants of one column: the zero point's magic offsets and the scale.
+    // Per-group constants of one column: the zero point's magic offsets and
+    // the scale.  zsh = bit position of the column's zero nibble in its byte.
     struct BConst {
-        uint32_t zlo;  // fp16 pair (1032 + z, 1032 + z)
-        uint32_t zhi;  // fp16 pair (72 + z, 72 + z)
+        half2v zlo;  // (1032 + z, 1032 + z)
+        half2v zhi;  // (72 + z, 72 + z)
         float s;
     };
-    auto group_const = [&](int g, int bj, const BRaw& r) {
-        int zn = (int)(((zpar[bj] ^ wgroup(g)) & 1) ? (r.zb >> 4) : (r.zb & 0xF));
-        zn -= (zn & 8) << 1;
+    auto group_const = [&](int zsh, const BRaw& r) {
+        const int zn = __builtin_amdgcn_sbfe((int)r.zb, zsh, 4);  // signed zero point
+        // fp16 bits of 1032 + z (mantissa unit 1) and of 72 + z (mantissa unit 1/16)
+        const _Float16 zl = __builtin_bit_cast(_Float16, (uint16_t)(0x6408 + zn));
+        const _Float16 zh = __builtin_bit_cast(_Float16, (uint16_t)(0x5480 + 16 * zn));
         BConst k;
-        k.zlo = (0x6408u + (uint32_t)zn) * 0x00010001u;         // fp16 bits of 1032 + z (mantissa unit 1)
-        k.zhi = (0x5480u + 16u * (uint32_t)zn) * 0x00010001u;   // fp16 bits of 72 + z (mantissa unit 1/16)
+        k.zlo = half2v{zl, zl};
+        k.zhi = half2v{zh, zh};
         k.s = half_bits_to_float((uint16_t)r.sbits);
         return k;
     };
@@ -329,14 +353,13 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
         // the group, and the four column scales.
         u32x4 f[4][2];
         float sc[4];
+        const int zsh = (wgroup(g) & 1) ? zsh_odd : zsh_even;
 #pragma unroll
         for (int bj = 0; bj < 4; ++bj) {
             const BRaw r = read_b(g, bj);
-            const BConst k = group_const(g, bj, r);
-            const half2v zlo = __builtin_bit_cast(half2v, k.zlo);
-            const half2v zhi = __builtin_bit_cast(half2v, k.zhi);
+            const BConst k = group_const(zsh, r);
 #pragma unroll
-            for (int h = 0; h < 2; ++h) f[bj][h] = decode_codes(r.w[h], zlo, zhi);
+            for (int h = 0; h < 2; ++h) f[bj][h] = decode_codes(r.w[h], k.zlo, k.zhi);
             sc[bj] = k.s;
         }
         u32x4 a0 = read_a(st, 0, 0), a1 = read_a(st, 0, 1);
