@@ -327,13 +327,15 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
     };
 
     // ---- software pipeline ----
-    // Step g: decode B of step g (read during step g - 1); then per row block
-    // the four column blocks' two-MFMA group chains and the scaled
-    // accumulation, with the next row block's A fragments read as soon as the
-    // current ones have been issued.  Before the last row block: wait for this
-    // wave's loads of step g + 1, workgroup barrier (every wave has finished
-    // reading stage g, and all of step g + 1 has landed), refill of stage g
-    // with step g + 3, and the B data of step g + 1.
+    // Step g: per row block the four column blocks' two-MFMA group chains and
+    // the scaled accumulation of the previous row block, with the A fragments
+    // of the row block two ahead read as soon as the current ones have been
+    // issued; in row block 0 each column block's B (read at the end of step
+    // g - 1) is decoded right before its first MFMA.  Before the last row
+    // block: wait for this wave's loads of step g + 1, workgroup barrier
+    // (every wave has finished reading stage g, and all of step g + 1 has
+    // landed), refill of stage g with step g + 3; after it, the packed B of
+    // step g + 1.
     // "Step s has landed" for this wave = its vector memory counter is at most
     // the number of operations issued after step s's (in-order completion).
     const int G = gcnt;  // steps of this workgroup's K range
@@ -345,24 +347,25 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
     else wait_vmcnt<0>();
     block_barrier();
 
+    // Packed B of step 0 (every load of the first steps has landed and the
+    // barrier above made them visible).  Stage g is refilled only after step
+    // g's own barrier, so the B of step g + 1 can be read at the end of step
+    // g, after that step's barrier.
+    BRaw rb[4];
+#pragma unroll
+    for (int bj = 0; bj < 4; ++bj) rb[bj] = read_b(0, bj);
+
     for (int g = 0; g < G; ++g) {
         const unsigned char* st = smem[g % kStages];
-        // B of step g: this wave's own loads of step g have landed (waited
-        // for in step g - 1), and stage g is refilled only after this step's
-        // barrier.  (code - zero) of the four column blocks, both MFMAs of
-        // the group, and the four column scales.
-        u32x4 f[4][2];
-        float sc[4];
+        u32x4 f[4][2];  // (code - zero) of the four column blocks, both MFMAs of the group
+        float sc[4];    // the four column scales
         const int zsh = (wgroup(g) & 1) ? zsh_odd : zsh_even;
-#pragma unroll
-        for (int bj = 0; bj < 4; ++bj) {
-            const BRaw r = read_b(g, bj);
-            const BConst k = group_const(zsh, r);
-#pragma unroll
-            for (int h = 0; h < 2; ++h) f[bj][h] = decode_codes(r.w[h], k.zlo, k.zhi);
-            sc[bj] = k.s;
-        }
-        u32x4 a0 = read_a(st, 0, 0), a1 = read_a(st, 0, 1);
+        // A fragments of row blocks bi (ab[bi & 1]), read two row blocks ahead
+        u32x4 ab[2][2];
+        ab[0][0] = read_a(st, 0, 0);
+        ab[0][1] = read_a(st, 0, 1);
+        ab[1][0] = read_a(st, 1, 0);
+        ab[1][1] = read_a(st, 1, 1);
         // Row block bi's group products D go to dd[bi & 1]; its scaled
         // accumulation runs after row block bi + 1's MFMAs have been issued,
         // so the matrix cores and the FMAs of one wave overlap.
@@ -378,8 +381,24 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
 #pragma unroll
             for (int bj = 0; bj < 4; ++bj) asm volatile("" : "+v"(acc[bi][bj]));
         };
+        // Row block 0: each column block's B is decoded right before its first
+        // MFMA, so the decode of the next column blocks overlaps the products.
 #pragma unroll
-        for (int bi = 0; bi < RB; ++bi) {
+        for (int bj = 0; bj < 4; ++bj) {
+            const BConst k = group_const(zsh, rb[bj]);
+#pragma unroll
+            for (int h = 0; h < 2; ++h) f[bj][h] = decode_codes(rb[bj].w[h], k.zlo, k.zhi);
+            sc[bj] = k.s;
+            dd[0][bj] = mfma(ab[0][0], f[bj][0], float4v{0.f, 0.f, 0.f, 0.f});
+            __builtin_amdgcn_sched_barrier(0);  // keeps the next decode behind this product
+        }
+        ab[0][0] = read_a(st, 2, 0);
+#pragma unroll
+        for (int bj = 0; bj < 4; ++bj) dd[0][bj] = mfma(ab[0][1], f[bj][1], dd[0][bj]);
+        ab[0][1] = read_a(st, 2, 1);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int bi = 1; bi < RB; ++bi) {
             if (bi + 1 == RB) {
                 // every A read of stage g has been issued; this wave's loads
                 // of step g + 1 have landed once at most those of step g + 2
@@ -394,15 +413,21 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
             }
             float4v(&d)[4] = dd[bi & 1];
 #pragma unroll
-            for (int bj = 0; bj < 4; ++bj) d[bj] = mfma(a0, f[bj][0], float4v{0.f, 0.f, 0.f, 0.f});
-            if (bi + 1 < RB) a0 = read_a(st, bi + 1, 0);
+            for (int bj = 0; bj < 4; ++bj) d[bj] = mfma(ab[bi & 1][0], f[bj][0], float4v{0.f, 0.f, 0.f, 0.f});
+            if (bi + 2 < RB) ab[bi & 1][0] = read_a(st, bi + 2, 0);
 #pragma unroll
-            for (int bj = 0; bj < 4; ++bj) d[bj] = mfma(a1, f[bj][1], d[bj]);
-            if (bi + 1 < RB) a1 = read_a(st, bi + 1, 1);
-            if (bi > 0) scale_add(bi - 1);
+            for (int bj = 0; bj < 4; ++bj) d[bj] = mfma(ab[bi & 1][1], f[bj][1], d[bj]);
+            if (bi + 2 < RB) ab[bi & 1][1] = read_a(st, bi + 2, 1);
+            scale_add(bi - 1);
             // the scheduling barrier stops later blocks' reads and products
             // from being hoisted (registers the accumulators need)
             __builtin_amdgcn_sched_barrier(0);
+        }
+        // packed B of step g + 1 (visible since this step's barrier); its LDS
+        // reads are in flight during the last row block's accumulation
+        if (g + 1 < G) {
+#pragma unroll
+            for (int bj = 0; bj < 4; ++bj) rb[bj] = read_b(g + 1, bj);
         }
         scale_add(RB - 1);
     }
