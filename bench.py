@@ -572,6 +572,88 @@ def summarize_mfma(csv_path: str, out_path: str, cus: int = 256) -> int:
     return 0
 
 
+TIMELINE_PHASES = ("entry", "loads issued", "staging landed", "LDS barrier", "MFMA steps done",
+                   "reduction barrier", "stores issued", "stores complete")
+STREAM_PHASES = ("entry", "load issued", "data landed")
+
+
+def timeline_pass() -> int:
+    """Per-workgroup phase timelines of the one-row decode GEMV (gemv_seg_kernel)
+    and of a bare streaming kernel over the same bytes, from the profiling
+    build libw4g64_hip_timeline.so: chip-wide s_memrealtime stamps (100 MHz),
+    cold caches (a 512 MiB write before each call), eager launches; the last
+    of 5 calls is reported, relative to the first workgroup's entry."""
+    import torch
+
+    from qwen_int4_hip import _lib, build as hip_build
+    from qwen_int4_hip.kernels import _workspace
+
+    if not hip_build.TIMELINE_LIBRARY.exists():
+        raise SystemExit(f"{hip_build.TIMELINE_LIBRARY} is missing: run __graft_entry__.build() first")
+    if not torch.cuda.is_available():
+        raise SystemExit("bench.py --timeline needs a ROCm GPU")
+    lib = ctypes.CDLL(str(hip_build.TIMELINE_LIBRARY))
+    for name, (res, argtypes) in _lib.SIGNATURES.items():
+        if hasattr(lib, name):
+            getattr(lib, name).restype = res
+            getattr(lib, name).argtypes = argtypes
+    lib.w4g64_timeline_register.restype = ctypes.c_int
+    lib.w4g64_timeline_register.argtypes = [ctypes.c_void_p, ctypes.c_int64]
+    lib.w4g64_timeline_stream.restype = ctypes.c_int
+    lib.w4g64_timeline_stream.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p]
+    max_wgs = 4096
+    stamps = torch.zeros(max_wgs * 8, dtype=torch.int64, device="cuda")
+    lib.w4g64_timeline_register(ctypes.c_void_p(stamps.data_ptr()), max_wgs)
+    scrub = torch.empty(512 << 20, dtype=torch.uint8, device="cuda")
+    sink = torch.zeros(256, dtype=torch.int32, device="cuda")
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def report(label, phases, run):
+        for i in range(5):
+            scrub.fill_(i + 1)
+            stamps.zero_()
+            torch.cuda.synchronize()
+            run()
+            torch.cuda.synchronize()
+        t = stamps.view(max_wgs, 8).cpu()
+        used = t[:, 0] != 0
+        t = t[used][:, :len(phases) if label.startswith("stream") else 8].double()
+        t0 = float(t[:, 0].min())
+        rel = (t - t0) * 0.01  # 100 MHz ticks -> us
+        print(f"\n{label}: {int(used.sum())} workgroups; us after the first workgroup's entry")
+        print("| point | p10 | p50 | p90 | max |")
+        print("|---|---:|---:|---:|---:|")
+        cols = list(range(len(phases))) if label.startswith("stream") else [0, 1, 2, 3, 4, 5, 6, 7]
+        names = phases if label.startswith("stream") else TIMELINE_PHASES
+        for c, nm in zip(cols, names):
+            v = rel[:, c].sort().values
+            q = lambda f: float(v[min(len(v) - 1, int(f * (len(v) - 1)))])
+            print(f"| {nm} | {q(.1):.2f} | {q(.5):.2f} | {q(.9):.2f} | {q(1):.2f} |")
+
+    for nbytes in (7_434_240, 1_327_104):
+        src = torch.zeros(nbytes, dtype=torch.uint8, device="cuda")
+        report(f"stream {nbytes / 1e6:.2f} MB (one 16-byte load per lane)", STREAM_PHASES,
+               lambda: _lib.check(lib.w4g64_timeline_stream(ctypes.c_void_p(src.data_ptr()), nbytes,
+                                                            ctypes.c_void_p(sink.data_ptr()), stream)))
+    for name in ("gate_proj", "q_proj"):
+        n, k = QWEN2_SHAPES[name]
+        q, s_, z = gen_weights(n, k, BASE_SEED + n + k, torch)
+        x = gen_activations(1, k, BASE_SEED + 3, torch.float16, torch)
+        y = torch.empty((1, n), dtype=torch.float16, device="cuda")
+        ws = _workspace(torch.device("cuda"), max(16, lib.w4g64_linear_workspace_bytes(1, n, k, _lib.DTYPE_F16)))
+        kname = lib.w4g64_linear_kernel_name(1, n, k, _lib.DTYPE_F16).decode()
+
+        def call():
+            _lib.check(lib.w4g64_linear(ctypes.c_void_p(x.data_ptr()), _lib.DTYPE_F16, ctypes.c_void_p(q.data_ptr()),
+                                        ctypes.c_void_p(s_.data_ptr()), ctypes.c_void_p(z.data_ptr()), None,
+                                        _lib.DTYPE_NONE, ctypes.c_void_p(y.data_ptr()), 1, n, k,
+                                        ctypes.c_void_p(ws.data_ptr()), ws.numel(), stream))
+
+        report(f"{name} {n}x{k}, 1 fp16 row, {algorithmic_bytes(1, n, k) / 1e6:.2f} MB: {kname}", TIMELINE_PHASES, call)
+    lib.w4g64_timeline_register(None, 0)
+    return 0
+
+
 def committed_traffic():
     try:
         return json.loads(PMC_TRAFFIC_FILE.read_text())
@@ -757,6 +839,9 @@ def main() -> int:
     parser.add_argument("--mfma-pass", action="store_true",
                         help=f"untimed rows-2048 GEMMs (W4G64, then dense bf16) for rocprofv3 --pmc "
                              f"{MFMA_PASS_COUNTERS}")
+    parser.add_argument("--timeline", action="store_true",
+                        help="per-workgroup phase timelines of the one-row decode GEMV and a bare stream "
+                             "(profiling build libw4g64_hip_timeline.so)")
     parser.add_argument("--summarize-mfma", nargs=2, metavar=("COUNTER_CSV", "OUT_JSON"),
                         help="shader clock and MFMA busy fraction per GEMM kernel from an --mfma-pass counter file")
     args = parser.parse_args()
@@ -772,6 +857,8 @@ def main() -> int:
         return profile_pass()
     if args.mfma_pass:
         return mfma_pass()
+    if args.timeline:
+        return timeline_pass()
 
     import torch
 

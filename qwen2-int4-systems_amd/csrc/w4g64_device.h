@@ -158,6 +158,32 @@ __device__ __forceinline__ float bf16_round(float v) { return bf16_bits_to_float
 // merge sees every other workgroup's stores under the HIP memory model
 // (happens-before is transitive across the workgroup and agent scopes).
 // `flag` is a __shared__ int of the caller.  Every thread must call this.
+// ---- workgroup timelines (profiling builds only) ----
+// Built with -DW4G64_TIMELINE (a separate library, libw4g64_hip_timeline.so),
+// an instrumented kernel records up to 8 chip-wide timestamps (s_memrealtime,
+// 100 MHz) of its phases in registers, and thread 0 of each workgroup below
+// the registered count stores them to stamps[workgroup][8] at exit, after its
+// own stores have completed.  Without the define every macro is empty.
+#ifdef W4G64_TIMELINE
+#define W4G64_TIMELINE_FIELDS unsigned long long* tl_stamps; int tl_workgroups;
+#define W4G64_TIMELINE_DECL unsigned long long tl_[8] = {0, 0, 0, 0, 0, 0, 0, 0}
+#define W4G64_STAMP(k) (tl_[(k)] = __builtin_amdgcn_s_memrealtime())
+#define W4G64_TIMELINE_STORE(args)                                                                   \
+    do {                                                                                             \
+        __builtin_amdgcn_s_waitcnt(0);                                                               \
+        W4G64_STAMP(7);                                                                              \
+        if ((args).tl_stamps && threadIdx.x == 0 && (int)blockIdx.x < (args).tl_workgroups)          \
+            for (int k_ = 0; k_ < 8; ++k_) (args).tl_stamps[(int64_t)blockIdx.x * 8 + k_] = tl_[k_]; \
+    } while (0)
+#define W4G64_TIMELINE_SET(args) ((args).tl_stamps = ::w4g64::g_timeline_stamps, (args).tl_workgroups = ::w4g64::g_timeline_workgroups)
+#else
+#define W4G64_TIMELINE_FIELDS
+#define W4G64_TIMELINE_DECL ((void)0)
+#define W4G64_STAMP(k) ((void)0)
+#define W4G64_TIMELINE_STORE(args) ((void)0)
+#define W4G64_TIMELINE_SET(args) ((void)0)
+#endif
+
 __device__ __forceinline__ bool arrive_last(unsigned* counter, unsigned expected, int* flag) {
     __builtin_amdgcn_s_waitcnt(0);  // this thread's stores have completed
     __syncthreads();

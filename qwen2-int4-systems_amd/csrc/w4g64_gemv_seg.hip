@@ -59,6 +59,7 @@ struct SegArgs {
     int G;   // groups (even)
     int P;   // group pairs
     int PK;  // pairs per K part
+    W4G64_TIMELINE_FIELDS
 };
 
 typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
@@ -121,6 +122,8 @@ __global__ __launch_bounds__(NR * NK * 64) void gemv_seg_kernel(SegArgs a) {
     const SegLayout L = seg_layout(M, K, RW, W, R, SW);
     const int row0 = blockIdx.x * RW;
     const int row_end = min(row0 + RW, N);
+    W4G64_TIMELINE_DECL;
+    W4G64_STAMP(0);
 
     // ---- 1. staging loads: activations, scales, zero bytes (16-byte chunks) ----
     const int64_t s_lo = ((int64_t)row0 * G * 2) & ~15ll;
@@ -180,8 +183,10 @@ __global__ __launch_bounds__(NR * NK * 64) void gemv_seg_kernel(SegArgs a) {
 #pragma unroll
     for (int u = 0; u < STAGE; ++u) asm volatile("" : "+v"(sv[u]));
 
+    W4G64_STAMP(1);
     // ---- 3. staging data into LDS ----
     wait_vm<STEPS + 1>();  // everything issued before the weights has landed
+    W4G64_STAMP(2);
     {
         float* xsum = (float*)(smem + L.xsum);
 #pragma unroll
@@ -214,6 +219,7 @@ __global__ __launch_bounds__(NR * NK * 64) void gemv_seg_kernel(SegArgs a) {
         if (tid < 16) ((uint32_t*)(smem + L.zero))[tid] = 0u;
     }
     lds_barrier();
+    W4G64_STAMP(3);
 
     // ---- 4. MFMA steps ----
     // A row of this lane: i = lane % 16 = 2 (m SW + s') + p; it reads x only
@@ -286,12 +292,14 @@ __global__ __launch_bounds__(NR * NK * 64) void gemv_seg_kernel(SegArgs a) {
         }
     }
 
+    W4G64_STAMP(4);
     // ---- 5. reduction over segments and K parts, then the outputs ----
     float* red = (float*)(smem + L.red);  // [wave][m][r][SW]
 #pragma unroll
     for (int h = 0; h < 2; ++h)
         if (hu[h]) red[((wave * M + hm[h]) * R + r) * SW + s] = acc[h];
     lds_barrier();
+    W4G64_STAMP(5);
     // outputs o = m RW + wr; the thread count is a multiple of RW, so every
     // output of this thread has the row (and bias) of tid % RW
     for (int o = tid; o < M * RW; o += kThreads) {
@@ -311,6 +319,8 @@ __global__ __launch_bounds__(NR * NK * 64) void gemv_seg_kernel(SegArgs a) {
             store_out<XK>(a.y, (int64_t)m * N + n, v);
         }
     }
+    W4G64_STAMP(6);
+    W4G64_TIMELINE_STORE(a);
 }
 
 template <int XK, int SW, int NR, int NK, int STEPS>
@@ -421,6 +431,7 @@ hipError_t launch_gemv_seg(const LinearProblem& p, const GemvPlan& plan, hipStre
     args.G = (int)(p.in_features / 64);
     args.P = args.G / 2;
     args.PK = plan.groups_per_split;
+    W4G64_TIMELINE_SET(args);
     if (args.M < 1 || args.M > 8 || args.G % 2 || args.PK < 1) return hipErrorInvalidValue;
     switch (p.x_kind) {
         case kF16: return launch_seg1<kF16>(args, plan, stream, start, stop);

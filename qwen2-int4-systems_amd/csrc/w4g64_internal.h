@@ -127,4 +127,10 @@ hipError_t launch_unpack(const uint8_t* packed, int8_t* out, int64_t elements, h
 hipError_t launch_dequant(const uint8_t* qweight, const uint16_t* scales, const uint8_t* zeros, float* out,
                           int64_t out_features, int64_t in_features, hipStream_t stream);
 
+#ifdef W4G64_TIMELINE
+// The timeline buffer registered by w4g64_timeline_register (profiling builds).
+extern unsigned long long* g_timeline_stamps;
+extern int g_timeline_workgroups;
+#endif
+
 }  // namespace w4g64
