@@ -651,6 +651,30 @@ def timeline_pass() -> int:
 
         report(f"{name} {n}x{k}, 1 fp16 row, {algorithmic_bytes(1, n, k) / 1e6:.2f} MB: {kname}", TIMELINE_PHASES, call)
     lib.w4g64_timeline_register(None, 0)
+
+    # residency: the same product kernels with their weights resident in L2 (one copy), in the 256 MB
+    # Infinity Cache (~60 MB of copies) or cold (~600 MB of copies), graph replays of back-to-back launches
+    hip = Hip()
+    print("\n| call (1 fp16 row) | L2-resident | ~60 MB of copies | ~600 MB of copies |")
+    print("|---|---:|---:|---:|")
+    for name in ("q_proj", "gate_proj", "down_proj"):
+        n, k = QWEN2_SHAPES[name]
+        wbytes = n * k // 2 + n * (k // 64) * 2 + n * k // 128
+        cold = -(-600_000_000 // wbytes)
+        cold += cold % 3 == 0  # the replay visits copies with stride 3
+        mall = max(2, 60_000_000 // wbytes)
+        mall += mall % 3 == 0
+        base = gen_weights(n, k, BASE_SEED + n + k, torch)
+        pool = [tuple(t.clone() for t in base) for _ in range(cold)]
+        x = gen_activations(1, k, BASE_SEED + 11, torch.float16, torch)
+        cells = []
+        for copies in (1, mall, cold):
+            case = {"x": x, "copies": pool[:copies], "copy0": 0}
+            d = graph_kernel_durations([case], 10, hip, torch, launches=max(32, copies))[0]
+            cells.append(f"{statistics.median(d) * 1e3:.2f} us")
+        print(f"| {name} {n}x{k} | " + " | ".join(cells) + " |")
+        del pool
+        torch.cuda.empty_cache()
     return 0
 
 
