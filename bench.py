@@ -575,6 +575,8 @@ def summarize_mfma(csv_path: str, out_path: str, cus: int = 256) -> int:
 TIMELINE_PHASES = ("entry", "loads issued", "staging landed", "LDS barrier", "MFMA steps done",
                    "reduction barrier", "stores issued", "stores complete")
 STREAM_PHASES = ("entry", "load issued", "data landed")
+ATTENTION_PHASES = ("entry", "chunk staged in LDS", "scores", "softmax statistics", "partials stored",
+                    "arrival counted", "merge statistics (last arrival)", "stores complete")
 
 
 def timeline_pass() -> int:
@@ -608,27 +610,29 @@ def timeline_pass() -> int:
     sink = torch.zeros(256, dtype=torch.int32, device="cuda")
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
 
-    def report(label, phases, run):
+    def report(label, phases, run, scrubbed=True):
         for i in range(5):
-            scrub.fill_(i + 1)
+            if scrubbed:
+                scrub.fill_(i + 1)
             stamps.zero_()
             torch.cuda.synchronize()
             run()
             torch.cuda.synchronize()
         t = stamps.view(max_wgs, 8).cpu()
         used = t[:, 0] != 0
-        t = t[used][:, :len(phases) if label.startswith("stream") else 8].double()
+        t = t[used].double()
         t0 = float(t[:, 0].min())
-        rel = (t - t0) * 0.01  # 100 MHz ticks -> us
         print(f"\n{label}: {int(used.sum())} workgroups; us after the first workgroup's entry")
-        print("| point | p10 | p50 | p90 | max |")
-        print("|---|---:|---:|---:|---:|")
-        cols = list(range(len(phases))) if label.startswith("stream") else [0, 1, 2, 3, 4, 5, 6, 7]
-        names = phases if label.startswith("stream") else TIMELINE_PHASES
-        for c, nm in zip(cols, names):
-            v = rel[:, c].sort().values
+        print("| point | workgroups | p10 | p50 | p90 | max |")
+        print("|---|---:|---:|---:|---:|---:|")
+        cols = list(range(len(phases))) if phases is STREAM_PHASES else list(range(8))
+        for c, nm in zip(cols, phases):
+            v = t[:, c][t[:, c] != 0]  # points a workgroup did not reach stay 0
+            if v.numel() == 0:
+                continue
+            v = ((v - t0) * 0.01).sort().values  # 100 MHz ticks -> us
             q = lambda f: float(v[min(len(v) - 1, int(f * (len(v) - 1)))])
-            print(f"| {nm} | {q(.1):.2f} | {q(.5):.2f} | {q(.9):.2f} | {q(1):.2f} |")
+            print(f"| {nm} | {v.numel()} | {q(.1):.2f} | {q(.5):.2f} | {q(.9):.2f} | {q(1):.2f} |")
 
     for nbytes in (7_434_240, 1_327_104):
         src = torch.zeros(nbytes, dtype=torch.uint8, device="cuda")
@@ -650,6 +654,27 @@ def timeline_pass() -> int:
                                         ctypes.c_void_p(ws.data_ptr()), ws.numel(), stream))
 
         report(f"{name} {n}x{k}, 1 fp16 row, {algorithmic_bytes(1, n, k) / 1e6:.2f} MB: {kname}", TIMELINE_PHASES, call)
+
+    # decode attention of one Qwen2-1.5B layer: batch 1, 12 query / 2 key-value heads, position 575 of a
+    # 641-position cache (the e2e workload's midpoint); caches stay warm, as in the decode step
+    heads, kvh, hd, max_len, pos = 12, 2, 128, 641, 575
+    gen = torch.Generator(device="cuda").manual_seed(BASE_SEED + 5)
+    qkv = (torch.randn((1, (heads + 2 * kvh) * hd), generator=gen, device="cuda") * 0.5).to(torch.bfloat16)
+    ang = torch.arange(hd, device="cuda", dtype=torch.float32) * 0.01 * pos
+    cos, sin = ang.cos().to(torch.bfloat16)[None], ang.sin().to(torch.bfloat16)[None]
+    kc = (torch.randn((1, kvh, max_len, hd), generator=gen, device="cuda") * 0.5).to(torch.bfloat16)
+    vc = (torch.randn((1, kvh, max_len, hd), generator=gen, device="cuda") * 0.5).to(torch.bfloat16)
+    position = torch.full((1,), pos, dtype=torch.int64, device="cuda")
+    out = torch.empty((1, heads * hd), dtype=torch.bfloat16, device="cuda")
+    aws = torch.zeros(max(16, lib.qwen2_decode_attention_workspace_bytes(1, kvh, max_len)), dtype=torch.uint8,
+                      device="cuda")
+    p_ = lambda t: ctypes.c_void_p(t.data_ptr())
+    report(f"decode attention, position {pos} (chunks of 64 positions, one workgroup per chunk and key/value head)",
+           ATTENTION_PHASES,
+           lambda: _lib.check(lib.qwen2_decode_attention(p_(qkv), p_(cos), p_(sin), p_(kc), p_(vc), p_(position), p_(out),
+                                                         1, heads, kvh, hd, max_len, hd ** -0.5, p_(aws), aws.numel(),
+                                                         stream)),
+           scrubbed=False)
     lib.w4g64_timeline_register(None, 0)
 
     # residency: the same product kernels with their weights resident in L2 (one copy), in the 256 MB

@@ -165,6 +165,7 @@ struct AttnArgs {
     float scale;
     unsigned* counters;  // [batch * kv_heads]
     float* partials;     // [batch * kv_heads][chunks][kPartFloats]
+    W4G64_TIMELINE_FIELDS
 };
 
 // Element d of the rotated head vector: x * cos + rotate_half(x) * sin, with
@@ -242,6 +243,8 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
     float* part = a.partials + ((int64_t)slot * a.chunks + chunk) * kPartFloats;
     const int mj = lane & 15;  // MFMA row / column of this lane
     const int mq = lane >> 4;  // MFMA K-slot quarter of this lane
+    W4G64_TIMELINE_DECL;
+    W4G64_STAMP(0);
 
     // ---- loads that do not depend on the position: queries, rotary factors, new key/value ----
     constexpr int kQItems = kMaxGroup * kHeadDim / kAttnThreads;
@@ -262,35 +265,41 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
     const uint16_t kx = kvec[dk];
     const uint16_t kp = kvec[dk ^ (kHeadDim / 2)];
     const uint16_t vx = qkv[(a.heads + a.kv_heads + kvh) * kHeadDim + dk];
+    // The position is read first (its load returns before the chunk's), then
+    // the chunk's 64 cache rows are loaded without waiting for it: rows past
+    // the cache end re-read its last row, and rows at or past the position
+    // are replaced (the new key and value, zero values) or masked below, so
+    // no load address depends on the position.
     int64_t p64 = *a.position;
+    asm volatile("" ::: "memory");
+    const int t0 = chunk * kChunk;
+    const int last_row = a.max_len - 1 - t0;  // >= 0: the launch covers max_len with chunks
+    constexpr int kPieces = kChunk * (kHeadDim / 8) / kAttnThreads;
+    static_assert(kPieces == 4 && kAttnThreads == 16 * (kHeadDim / 8), "value staging: 16 columns x 4 rows");
+    // keys: piece e = tid + 256 i -> row e / 16, 16-byte column e % 16
+    // (row-major LDS stores); values: thread t takes column vc = t / 16 of
+    // the four rows 4 (t % 16) + i, so that it holds four consecutive
+    // positions of 8 dimensions for the transposed stores
+    const int vcol = tid / (kHeadDim / 8);
+    const int vrow0 = kPieces * (tid % (kHeadDim / 8));
+    u32x4 kr[kPieces], vr[kPieces];
+#pragma unroll
+    for (int i = 0; i < kPieces; ++i) {
+        const int e = tid + kAttnThreads * i;
+        const int r = min(e / (kHeadDim / 8), last_row);
+        kr[i] = *(const u32x4*)(a.k_cache + cache_base + (int64_t)(t0 + r) * kHeadDim + 8 * (e % (kHeadDim / 8)));
+        const int rv = min(vrow0 + i, last_row);
+        vr[i] = *(const u32x4*)(a.v_cache + cache_base + (int64_t)(t0 + rv) * kHeadDim + 8 * vcol);
+    }
+    // the new value's 8 dimensions of column vcol (used when pos is in this chunk)
+    const u32x4 vnew8 = *(const u32x4*)(qkv + (a.heads + a.kv_heads + kvh) * kHeadDim + 8 * vcol);
     p64 = p64 < 0 ? 0 : (p64 >= a.max_len ? a.max_len - 1 : p64);
     const int pos = (int)p64;
-    const int t0 = chunk * kChunk;
     const int nk = min(kChunk, pos + 1 - t0);  // positions of this chunk that are attended (<= 0: none)
 
     if (nk > 0) {
-        // cached rows t0 .. t0 + cached - 1: piece e = tid + 256 i -> row e / 16, 16-byte column e % 16;
-        // rows past `cached` re-read a valid row of this chunk and are not used
+        // cached rows t0 .. t0 + cached - 1 are used as loaded
         const int cached = min(nk, pos - t0);
-        constexpr int kPieces = kChunk * (kHeadDim / 8) / kAttnThreads;
-        static_assert(kPieces == 4 && kAttnThreads == 16 * (kHeadDim / 8), "value staging: 16 columns x 4 rows");
-        // keys: piece e -> row e / 16, 16-byte column e % 16 (row-major LDS
-        // stores); values: thread t takes column vc = t / 16 of the four rows
-        // 4 (t % 16) + i, so that it holds four consecutive positions of
-        // 8 dimensions for the transposed stores
-        const int vcol = tid / (kHeadDim / 8);
-        const int vrow0 = kPieces * (tid % (kHeadDim / 8));
-        u32x4 kr[kPieces], vr[kPieces];
-#pragma unroll
-        for (int i = 0; i < kPieces; ++i) {
-            const int e = tid + kAttnThreads * i;
-            const int r = min(e / (kHeadDim / 8), max(cached - 1, 0));
-            kr[i] = *(const u32x4*)(a.k_cache + cache_base + (int64_t)(t0 + r) * kHeadDim + 8 * (e % (kHeadDim / 8)));
-            const int rv = min(vrow0 + i, max(cached - 1, 0));
-            vr[i] = *(const u32x4*)(a.v_cache + cache_base + (int64_t)(t0 + rv) * kHeadDim + 8 * vcol);
-        }
-        // the new value's 8 dimensions of column vcol (used when pos is in this chunk)
-        const u32x4 vnew8 = *(const u32x4*)(qkv + (a.heads + a.kv_heads + kvh) * kHeadDim + 8 * vcol);
 #pragma unroll
         for (int i = 0; i < kQItems; ++i) {
             const int e = tid + kAttnThreads * i;
@@ -330,6 +339,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
             }
         }
         __syncthreads();
+        W4G64_STAMP(1);
 
         // ---- scores (MFMA): wave w, positions 16 w + mj ----
         {
@@ -349,6 +359,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
             }
         }
         __syncthreads();
+        W4G64_STAMP(2);
 
         // ---- chunk softmax statistics: wave w takes heads w, w + 4; lane = position ----
         for (int g = wave; g < group; g += kAttnThreads / 64) {
@@ -363,6 +374,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
             }
         }
         __syncthreads();
+        W4G64_STAMP(3);
 
         // ---- probability-weighted value sums (MFMA): wave w, dimensions 32 w .. 32 w + 31 ----
         float4v oacc[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
@@ -412,7 +424,13 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
     // ---- arrival: the last workgroup of this (sequence, head) merges ----
     // The partial stores are published by the arrival's agent-scope release
     // and acquired by the last arriver (arrive_last).
-    if (!arrive_last(a.counters + slot, (unsigned)a.chunks, &s_last)) return;
+    W4G64_STAMP(4);
+    if (!arrive_last(a.counters + slot, (unsigned)a.chunks, &s_last)) {
+        W4G64_STAMP(5);
+        W4G64_TIMELINE_STORE(a);
+        return;
+    }
+    W4G64_STAMP(5);
     // Every device-coherent load travels to memory, so the merge issues all of
     // them at once: the statistics into LDS and, per thread (dimension d,
     // heads g0, g0 + 2, ...), the weighted sums of up to kMergeBatch chunks.
@@ -458,6 +476,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
             scale_c[c * kMaxGroup + g] = c < used ? expf(stats[c * 2 * kMaxGroup + g] - m) / l : 0.0f;
     }
     __syncthreads();
+    W4G64_STAMP(6);
     float o[kMaxGroup / 2] = {0.0f, 0.0f, 0.0f, 0.0f};
     for (int c0 = 0; c0 < used; c0 += kMergeBatch) {
         if (c0 > 0) load_batch(c0);
@@ -476,6 +495,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
             a.out[(int64_t)b * a.heads * kHeadDim + (kvh * group + g0 + 2 * i) * kHeadDim + d] =
                 float_to_bf16_bits(o[i]);
     if (tid == 0) __hip_atomic_store(a.counters + slot, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    W4G64_TIMELINE_STORE(a);
 }
 
 // Reduction over the 16 lanes of a row (quad swaps, half-row and row
@@ -790,6 +810,7 @@ int qwen2_decode_attention(const void* qkv, const void* cos, const void* sin, vo
     args.scale = scale;
     args.counters = (unsigned*)workspace;
     args.partials = (float*)((char*)workspace + attention_counter_bytes(batch, num_kv_heads));
+    W4G64_TIMELINE_SET(args);
     hipLaunchKernelGGL(attention_kernel, dim3((unsigned)blocks), dim3(kAttnThreads), 0, (hipStream_t)stream, args);
     return launch_status(hipGetLastError(), "decode_attention");
 }
