@@ -59,8 +59,8 @@ int64_t qwen2_decode_attention_workspace_bytes(int64_t batch, int64_t num_kv_hea
  *   out[b, h * head_dim + d] = bf16( softmax_t(q_h . k_t * scale) . v_t[d] ),
  *   t = 0..p, query head h reading key/value head h / (num_heads / num_kv_heads),
  * with fp32 scores, softmax and sums.  head_dim == 128,
- * num_heads / num_kv_heads <= 8, max_length <= 17408.  qkv and the caches
- * must be 16-byte aligned.
+ * num_heads / num_kv_heads <= 8, max_length <= 17408.  qkv, the caches and
+ * the workspace must be 16-byte aligned, out 8-byte aligned.
  * Replaces: the rotary step and attention of QwenAttention.forward for one
  *           cached token (src/qwen_int4/model.py:17-31, :61-122). */
 int qwen2_decode_attention(const void* qkv, const void* cos, const void* sin, void* k_cache, void* v_cache,

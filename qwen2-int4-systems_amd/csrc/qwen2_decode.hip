@@ -404,20 +404,18 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
                                                                    __builtin_bit_cast(bf16x8, bv), oacc[cb], 0, 0, 0);
             }
         }
-        // partials travel through device-coherent atomic stores (the merging
-        // workgroup may run on another XCD)
+        // plain stores: the arrival below publishes them at agent scope (the
+        // merging workgroup may run on another XCD)
 #pragma unroll
         for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int g = 4 * mq + r;
-                if (g < group)
-                    __hip_atomic_store(part + 2 * kMaxGroup + g * kHeadDim + 32 * wave + 16 * cb + mj, oacc[cb][r],
-                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (g < group) part[2 * kMaxGroup + g * kHeadDim + 32 * wave + 16 * cb + mj] = oacc[cb][r];
             }
         if (tid < group) {
-            __hip_atomic_store(part + tid, stat_m[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(part + kMaxGroup + tid, stat_l[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            part[tid] = stat_m[tid];
+            part[kMaxGroup + tid] = stat_l[tid];
         }
     }
 
@@ -431,35 +429,33 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
         return;
     }
     W4G64_STAMP(5);
-    // Every device-coherent load travels to memory, so the merge issues all of
-    // them at once: the statistics into LDS and, per thread (dimension d,
-    // heads g0, g0 + 2, ...), the weighted sums of up to kMergeBatch chunks.
-    // Loads of chunks past `used` (or heads past `group`) re-read a valid
-    // partial; their scale is zero, so the accumulation needs no branches.
-    const int d = tid % kHeadDim;
-    const int g0 = tid / kHeadDim;
+    // After the acquire, plain loads see every other workgroup's partials.
+    // The merge issues them all at once: the statistics first (their loads
+    // return first), then per thread t < group * 32 the weighted sums of head
+    // t / 32, dimensions 4 (t % 32) .. + 3, of up to kMergeBatch chunks as
+    // 16-byte loads.  Loads of chunks past `used` (or threads past the
+    // group's heads) re-read a valid partial; their scale is zero (or their
+    // result is not stored), so the accumulation needs no branches.
     const int used = pos / kChunk + 1;  // chunks that hold positions 0..pos (all wrote partials)
     const float* base = a.partials + (int64_t)slot * a.chunks * kPartFloats;
-    float v[kMergeBatch][kMaxGroup / 2];
-    auto load_batch = [&](int c0) {
-#pragma unroll
-        for (int u = 0; u < kMergeBatch; ++u)
-#pragma unroll
-            for (int i = 0; i < kMaxGroup / 2; ++i)
-                v[u][i] = __hip_atomic_load(base + min(c0 + u, used - 1) * kPartFloats + 2 * kMaxGroup +
-                                                min(g0 + 2 * i, group - 1) * kHeadDim + d,
-                                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    };
-    load_batch(0);
     float* stats = (float*)&ks[0][0];    // [used][2 * kMaxGroup]: m, l per head
     float* scale_c = (float*)&vt[0][0];  // [kMaxChunks][kMaxGroup]: exp(m_c - m) / l, zero past `used`
     for (int e = tid; e < used * 2 * kMaxGroup; e += kAttnThreads)
-        stats[e] = __hip_atomic_load(base + (e / (2 * kMaxGroup)) * kPartFloats + e % (2 * kMaxGroup),
-                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        stats[e] = base[(e / (2 * kMaxGroup)) * kPartFloats + e % (2 * kMaxGroup)];
+    const int f = min(tid, group * (kHeadDim / 4) - 1);
+    const int gh = f / (kHeadDim / 4);     // head within the group
+    const int d4 = 4 * (f % (kHeadDim / 4));  // first of its four dimensions
+    float4v v[kMergeBatch];
+    auto load_batch = [&](int c0) {
+#pragma unroll
+        for (int u = 0; u < kMergeBatch; ++u)
+            v[u] = *(const float4v*)(base + min(c0 + u, used - 1) * kPartFloats + 2 * kMaxGroup + gh * kHeadDim + d4);
+    };
+    load_batch(0);
     __syncthreads();
     // per head g (wave w takes heads w, w + 4): lanes walk the chunks; the
     // head's maximum and rescaled sum are wave reductions.  Heads past
-    // `group` get zero scales (their clamped loads then add nothing).
+    // `group` get zero scales.
     for (int g = wave; g < kMaxGroup; g += kAttnThreads / 64) {
         if (g >= group) {
             for (int c = lane; c < kMaxChunks; c += 64) scale_c[c * kMaxGroup + g] = 0.0f;
@@ -477,23 +473,22 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
     }
     __syncthreads();
     W4G64_STAMP(6);
-    float o[kMaxGroup / 2] = {0.0f, 0.0f, 0.0f, 0.0f};
+    float4v o = {0.0f, 0.0f, 0.0f, 0.0f};
     for (int c0 = 0; c0 < used; c0 += kMergeBatch) {
         if (c0 > 0) load_batch(c0);
 #pragma unroll
-        for (int u = 0; u < kMergeBatch; ++u)
+        for (int u = 0; u < kMergeBatch; ++u) {
+            float sc = scale_c[min(c0 + u, kMaxChunks - 1) * kMaxGroup + gh];
+            sc = c0 + u < used ? sc : 0.0f;
 #pragma unroll
-            for (int i = 0; i < kMaxGroup / 2; ++i) {
-                float sc = scale_c[min(c0 + u, kMaxChunks - 1) * kMaxGroup + min(g0 + 2 * i, kMaxGroup - 1)];
-                sc = c0 + u < used ? sc : 0.0f;
-                o[i] = fmaf(v[u][i], sc, o[i]);
-            }
+            for (int i = 0; i < 4; ++i) o[i] = fmaf(v[u][i], sc, o[i]);
+        }
     }
-#pragma unroll
-    for (int i = 0; i < kMaxGroup / 2; ++i)
-        if (g0 + 2 * i < group)
-            a.out[(int64_t)b * a.heads * kHeadDim + (kvh * group + g0 + 2 * i) * kHeadDim + d] =
-                float_to_bf16_bits(o[i]);
+    if (tid < group * (kHeadDim / 4)) {
+        const uint32_t lo = float_to_bf16_bits(o[0]) | ((uint32_t)float_to_bf16_bits(o[1]) << 16);
+        const uint32_t hi = float_to_bf16_bits(o[2]) | ((uint32_t)float_to_bf16_bits(o[3]) << 16);
+        *(u32x2*)(a.out + (int64_t)b * a.heads * kHeadDim + (kvh * group + gh) * kHeadDim + d4) = u32x2{lo, hi};
+    }
     if (tid == 0) __hip_atomic_store(a.counters + slot, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     W4G64_TIMELINE_STORE(a);
 }
@@ -788,6 +783,9 @@ int qwen2_decode_attention(const void* qkv, const void* cos, const void* sin, vo
         return set_error(W4G64_STATUS_INVALID_VALUE, "all tensors must be non-null device pointers");
     if (!aligned16(qkv) || !aligned16(k_cache) || !aligned16(v_cache))
         return set_error(W4G64_STATUS_INVALID_VALUE, "qkv, k_cache and v_cache must be 16-byte aligned");
+    if (((uintptr_t)out) & 7) return set_error(W4G64_STATUS_INVALID_VALUE, "out must be 8-byte aligned");
+    if (workspace && !aligned16(workspace))
+        return set_error(W4G64_STATUS_WORKSPACE, "attention workspace must be 16-byte aligned");
     const int64_t need = qwen2_decode_attention_workspace_bytes(batch, num_kv_heads, max_length);
     if (!workspace || workspace_bytes < need)
         return set_error(W4G64_STATUS_WORKSPACE, "attention workspace of %lld bytes required, got %lld",

@@ -102,6 +102,13 @@ def test_decode_step_entry_points_reject_before_launch():
     assert lib.qwen2_decode_attention(p, p, p, odd, p, p, p, 1, 12, 2, 128, 640, f(0.1), p, ws,
                                       null) == _lib.STATUS_INVALID_VALUE
     assert b"aligned" in lib.w4g64_last_error()
+    # the merge stores four bf16 outputs at once and loads the partial sums 16 bytes at a time
+    odd4 = ctypes.c_void_p(p.value + 4)
+    assert lib.qwen2_decode_attention(p, p, p, p, p, p, odd4, 1, 12, 2, 128, 640, f(0.1), p, ws,
+                                      null) == _lib.STATUS_INVALID_VALUE
+    assert b"out must be 8-byte aligned" in lib.w4g64_last_error()
+    assert lib.qwen2_decode_attention(*args, 1, 12, 2, 128, 640, f(0.1), odd4, ws, null) == _lib.STATUS_WORKSPACE
+    assert b"16-byte aligned" in lib.w4g64_last_error()
     # prefill attention: head_dim, grouping, length vs cache, workspace, alignment
     pws = lib.qwen2_prefill_attention_workspace_bytes(1, 12, 512)
     assert pws == 12 * 512 * 128 * 2
