@@ -575,6 +575,8 @@ def summarize_mfma(csv_path: str, out_path: str, cus: int = 256) -> int:
 TIMELINE_PHASES = ("entry", "loads issued", "staging landed", "LDS barrier", "MFMA steps done",
                    "reduction barrier", "stores issued", "stores complete")
 STREAM_PHASES = ("entry", "load issued", "data landed")
+GEMV_PHASES = ("entry", "staging landed", "staged in LDS", "LDS barrier", "MFMA steps done",
+               "partial sums combined", "stores issued", "stores complete")
 ATTENTION_PHASES = ("entry", "chunk staged in LDS", "scores", "softmax statistics", "partials stored",
                     "arrival counted", "merge statistics (last arrival)", "stores complete")
 
@@ -639,21 +641,24 @@ def timeline_pass() -> int:
         report(f"stream {nbytes / 1e6:.2f} MB (one 16-byte load per lane)", STREAM_PHASES,
                lambda: _lib.check(lib.w4g64_timeline_stream(ctypes.c_void_p(src.data_ptr()), nbytes,
                                                             ctypes.c_void_p(sink.data_ptr()), stream)))
-    for name in ("gate_proj", "q_proj"):
+    for name, rows in (("gate_proj", 1), ("q_proj", 1), ("down_proj", 1), ("gate_proj", 4), ("gate_proj", 16),
+                       ("down_proj", 16)):
         n, k = QWEN2_SHAPES[name]
         q, s_, z = gen_weights(n, k, BASE_SEED + n + k, torch)
-        x = gen_activations(1, k, BASE_SEED + 3, torch.float16, torch)
-        y = torch.empty((1, n), dtype=torch.float16, device="cuda")
-        ws = _workspace(torch.device("cuda"), max(16, lib.w4g64_linear_workspace_bytes(1, n, k, _lib.DTYPE_F16)))
-        kname = lib.w4g64_linear_kernel_name(1, n, k, _lib.DTYPE_F16).decode()
+        x = gen_activations(rows, k, BASE_SEED + 3, torch.float16, torch)
+        y = torch.empty((rows, n), dtype=torch.float16, device="cuda")
+        ws = _workspace(torch.device("cuda"), max(16, lib.w4g64_linear_workspace_bytes(rows, n, k, _lib.DTYPE_F16)))
+        kname = lib.w4g64_linear_kernel_name(rows, n, k, _lib.DTYPE_F16).decode()
 
         def call():
             _lib.check(lib.w4g64_linear(ctypes.c_void_p(x.data_ptr()), _lib.DTYPE_F16, ctypes.c_void_p(q.data_ptr()),
                                         ctypes.c_void_p(s_.data_ptr()), ctypes.c_void_p(z.data_ptr()), None,
-                                        _lib.DTYPE_NONE, ctypes.c_void_p(y.data_ptr()), 1, n, k,
+                                        _lib.DTYPE_NONE, ctypes.c_void_p(y.data_ptr()), rows, n, k,
                                         ctypes.c_void_p(ws.data_ptr()), ws.numel(), stream))
 
-        report(f"{name} {n}x{k}, 1 fp16 row, {algorithmic_bytes(1, n, k) / 1e6:.2f} MB: {kname}", TIMELINE_PHASES, call)
+        label = (f"{name} {n}x{k}, {rows} fp16 row{'s' if rows > 1 else ''}, "
+                 f"{algorithmic_bytes(rows, n, k) / 1e6:.2f} MB: {kname}")
+        report(label, TIMELINE_PHASES if kname.startswith("gemv_seg") else GEMV_PHASES, call)
 
     # decode attention of one Qwen2-1.5B layer: batch 1, 12 query / 2 key-value heads, position 575 of a
     # 641-position cache (the e2e workload's midpoint); caches stay warm, as in the decode step

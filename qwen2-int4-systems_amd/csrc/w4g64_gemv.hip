@@ -91,6 +91,7 @@ struct GemvArgs {
     const uint16_t* norm_w;
     float eps;
     uint16_t* out_sum;
+    W4G64_TIMELINE_FIELDS
 };
 
 // Activation items (8 values each) a lane stages: M x groups-per-split x 8
@@ -151,6 +152,8 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
+    W4G64_TIMELINE_DECL;
+    W4G64_STAMP(0);
     const int nb = blockIdx.x;
     const int split = blockIdx.y;
     const int g0 = split * a.gps;
@@ -274,6 +277,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
     for (int u = 0; u < kStage; ++u)
 #pragma unroll
         for (int k = 0; k < kVecs; ++k) asm volatile("" : "+v"(v[u][k]));
+    W4G64_STAMP(1);
 
     // ---- 3a. RMSNorm prologue (model.py:40-44, residual adds :149-154) ----
     // s = bf16(x + bf16(delta)); the activation is bf16(bf16(s * r) * w) with
@@ -430,10 +434,12 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
             }
         }
     }
+    W4G64_STAMP(2);
     // A barrier over LDS alone: the weight loads stay in flight through it.
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    W4G64_STAMP(3);
 
     // ---- 4. MFMA over the group steps ----
     // One accumulator per fp32 part: the bf16 path's biased codes make each
@@ -531,6 +537,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
         }
     }
 
+    W4G64_STAMP(4);
     // ---- 5. epilogue (per wave): keep the block diagonal, sum the segments ----
     // The wave writes and reads only its own features' slots of `red`; LDS
     // operations of one wave complete in order, so no barrier is needed.
@@ -546,6 +553,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
             if (i % SW == sj && m < a.mv) red[(m * kBlockCols + wave * R + rj) * SW + sj] = v;
         }
     }
+    W4G64_STAMP(5);
     const int col0 = nb * kBlockCols;
     if constexpr (R >= 2) {  // paired plans keep at most 8 segments (R >= 2)
         if (a.paired && a.splits == 1) {
@@ -565,6 +573,8 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
                 store_silu_planes(a.y, m, i, a.M, half_n, g + load_bias(a.bias, a.bias_kind, i),
                                   up + load_bias(a.bias, a.bias_kind, half_n + i));
             }
+            W4G64_STAMP(6);
+            W4G64_TIMELINE_STORE(a);
             return;
         }
     }
@@ -586,6 +596,8 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
             a.partials[((int64_t)split * a.M + m) * a.N + nn] = v;
         }
     }
+    W4G64_STAMP(6);
+    W4G64_TIMELINE_STORE(a);
 }
 
 // Second kernel of a K-split call: one thread per output (paired: per
@@ -875,6 +887,7 @@ hipError_t launch_gemv(const LinearProblem& p, const GemvPlan& plan, void* works
     args.norm_w = p.norm_weight;
     args.eps = p.norm_eps;
     args.out_sum = (uint16_t*)p.norm_out_sum;
+    W4G64_TIMELINE_SET(args);
     // unreduced: the partial sums (or, unsplit, the fp32 result) go to the caller's buffer
     const bool unreduced = p.partials_out != nullptr;
     if (unreduced) {

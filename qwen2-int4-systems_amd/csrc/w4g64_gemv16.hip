@@ -48,6 +48,7 @@ struct Gemv16Args {
     int gps;     // groups per K split
     int splits;  // K splits across workgroups
     float* partials;  // [splits][M][N]
+    W4G64_TIMELINE_FIELDS
 };
 
 // Activation items (8 values) a lane stages: 16 rows x KW STEPS groups x 8
@@ -76,6 +77,8 @@ __global__ __launch_bounds__(KW * FB * 64) void gemv16_kernel(Gemv16Args a) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
+    W4G64_TIMELINE_DECL;
+    W4G64_STAMP(0);
     const int fb = wave % FB;  // this wave's 16-feature block
     const int kw = wave / FB;  // this wave's share of the groups
     const int nb = blockIdx.x;
@@ -92,7 +95,6 @@ __global__ __launch_bounds__(KW * FB * 64) void gemv16_kernel(Gemv16Args a) {
     const bool nvalid = n < a.N;
     const int nrow = nvalid ? n : 0;
     const uint8_t* wrow = a.qweight + (int64_t)nrow * (a.K / 2) + 8 * q;
-    const int64_t sbase = (int64_t)nrow * a.G;
 
     // ---- 1. activation loads: item it = kThreads16 u + tid (8 values of row m) ----
     // Lanes past the last item take the item at the same place in the last
@@ -117,26 +119,62 @@ __global__ __launch_bounds__(KW * FB * 64) void gemv16_kernel(Gemv16Args a) {
         item_rc(it < total ? it : total - 8 + (tid & 7), m, c);
         v[u] = *(const u32x4*)((const uint16_t*)a.x + (int64_t)m * a.K + kbase + 8 * c);
     }
+    // ---- 1b. scale and zero-point runs of the workgroup's features over its K range ----
+    // Feature slot f (n = nb kCols + f, clamped to N - 1) has its scales at
+    // bytes [2 (n G + g0), + 2 cnt) and its zero nibbles at elements
+    // [n G + g0, + cnt); each run is staged in 16-byte chunks from the
+    // aligned-down start, one scale chunk and one zero chunk per thread
+    // (clamped thread indices repeat the last chunk).  Buffer resources
+    // bound-check the chunks that straddle an array's end.
+    constexpr int kScChunks = (2 * KW * STEPS + 15) / 16 + 1;
+    constexpr int kZbChunks = (KW * STEPS / 2 + 1 + 15) / 16 + 1;
+    static_assert(16 * FB * kScChunks <= kThreads16 && 16 * FB * kZbChunks <= kThreads16, "one chunk per thread");
+    __shared__ __attribute__((aligned(16))) unsigned char scl[kCols][kScChunks * 16];
+    __shared__ __attribute__((aligned(16))) unsigned char zbl[kCols][kZbChunks * 16];
+    auto run_start = [&](int nf, bool zeros) {
+        const uint32_t e = (uint32_t)nf * (uint32_t)a.G + (uint32_t)g0;
+        return zeros ? (e >> 1) & ~15u : (2u * e) & ~15u;
+    };
+    const int ts = min(tid, kCols * kScChunks - 1), tz = min(tid, kCols * kZbChunks - 1);
+    const int fs = ts / kScChunks, cs = ts - fs * kScChunks;
+    const int fz = tz / kZbChunks, cz = tz - fz * kZbChunks;
+    u32x4 svec, zvec;
+    {
+        const uint32_t ng = (uint32_t)a.N * (uint32_t)a.G;
+        const __amdgpu_buffer_rsrc_t s_rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)a.scales, 0, (int)(2u * ng), 0x00020000);
+        const __amdgpu_buffer_rsrc_t z_rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)a.zeros, 0, (int)((ng + 1u) >> 1), 0x00020000);
+        svec = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                             s_rsrc, (int)(run_start(min(nb * kCols + fs, a.N - 1), false) + 16u * cs), 0, 0));
+        zvec = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                             z_rsrc, (int)(run_start(min(nb * kCols + fz, a.N - 1), true) + 16u * cz), 0, 0));
+    }
     // (the empty asm statements with a memory clobber fix the issue order)
     asm volatile("" ::: "memory");
+    // Every wave's activation loads are issued before any wave's weight
+    // loads: a CU returns vector memory data in issue order, so a wave whose
+    // activation loads queue behind another wave's weight stream receives
+    // them (measured) 1.3-1.5 us late for every wave ahead of it on its SIMD.
+    // The barrier waits for no memory.
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
 
-    // ---- 2. weight / scale / zero loads of every step, in step order ----
+    // ---- 2. weight loads of every step, in step order ----
     // Steps past the K range re-read group g0 and get a zero scale.
     u32x2 wq[STEPS];
-    uint32_t sraw[STEPS];
-    uint32_t zraw[STEPS];
 #pragma unroll
     for (int t = 0; t < STEPS; ++t) {
         const int gl = kw + KW * t;
         const int g = gl < cnt ? g0 + gl : g0;
         wq[t] = __builtin_nontemporal_load((const u32x2*)(wrow + (int64_t)g * 32));
-        sraw[t] = a.scales[sbase + g];
-        zraw[t] = a.zeros[(sbase + g) >> 1];
         asm volatile("" ::: "memory");
     }
     // Nothing that uses the activations may move above the last load issue.
 #pragma unroll
     for (int u = 0; u < kStage; ++u) asm volatile("" : "+v"(v[u]));
+    asm volatile("" : "+v"(svec), "+v"(zvec));
+    *(u32x4*)&scl[fs][16 * cs] = svec;
+    *(u32x4*)&zbl[fz][16 * cz] = zvec;
+    W4G64_STAMP(1);
 
     // ---- 3. activations into LDS (slot order); bf16 group sums ----
 #pragma unroll
@@ -154,12 +192,17 @@ __global__ __launch_bounds__(KW * FB * 64) void gemv16_kernel(Gemv16Args a) {
             sx[m * a.gps + (c >> 3)] = s;
         }
     }
+    W4G64_STAMP(2);
     // A barrier over LDS alone: the weight loads stay in flight through it.
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+    W4G64_STAMP(3);
 
     // ---- 4. MFMA over the steps: A row = activation row (rows past M read row M - 1) ----
+    // this lane's feature row as staged (clamped to N - 1) and its runs' starts
+    const int nrowc = min(n, a.N - 1);
+    const uint32_t s_run = run_start(nrowc, false), z_run = run_start(nrowc, true);
     const int mrow = min(j, a.M - 1);
     float4v acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -171,10 +214,13 @@ __global__ __launch_bounds__(KW * FB * 64) void gemv16_kernel(Gemv16Args a) {
         const u16x8 a1 = *(const u16x8*)(src + 8);
         // wait for this step's weight, scale and zero alone; the empty asm keeps
         // their decoding here
-        asm volatile("" : "+v"(wq[t]), "+v"(sraw[t]), "+v"(zraw[t]));
-        const float sct = (nvalid && gl < cnt) ? half_bits_to_float((uint16_t)sraw[t]) : 0.0f;
+        asm volatile("" : "+v"(wq[t]));
         const int gz = gl < cnt ? g0 + gl : g0;  // the group this step loaded
-        const int zn = (((sbase + gz) & 1) ? (zraw[t] >> 4) : zraw[t]) & 0xF;
+        const uint32_t e_sz = (uint32_t)nrowc * (uint32_t)a.G + (uint32_t)gz;  // its scale / zero element
+        const uint16_t s_bits = *(const uint16_t*)&scl[fb * 16 + j][2u * e_sz - s_run];
+        const uint32_t z_byte = zbl[fb * 16 + j][(e_sz >> 1) - z_run];
+        const float sct = (nvalid && gl < cnt) ? half_bits_to_float(s_bits) : 0.0f;
+        const int zn = ((e_sz & 1) ? (z_byte >> 4) : z_byte) & 0xF;
         const int zrt = zn - ((zn & 8) << 1);
         float4v d;
         if constexpr (XK == kF16) {
@@ -200,10 +246,12 @@ __global__ __launch_bounds__(KW * FB * 64) void gemv16_kernel(Gemv16Args a) {
         for (int r = 0; r < 4; ++r) acc[r] = fmaf(sct, d[r], acc[r]);
     }
 
+    W4G64_STAMP(4);
     // ---- 5. combine the KW waves of each block: D row = 4 q + r, column = j ----
 #pragma unroll
     for (int r = 0; r < 4; ++r) red[wave][4 * q + r][j] = acc[r];
     __syncthreads();
+    W4G64_STAMP(5);
 
     const int col0 = nb * kCols;
     for (int idx = tid; idx < a.M * kCols; idx += kThreads16) {
@@ -219,6 +267,8 @@ __global__ __launch_bounds__(KW * FB * 64) void gemv16_kernel(Gemv16Args a) {
         else
             a.partials[((int64_t)split * a.M + m) * a.N + nn] = s;
     }
+    W4G64_STAMP(6);
+    W4G64_TIMELINE_STORE(a);
 }
 
 template <int XK, int STEPS, int KW, int FB>
@@ -282,6 +332,7 @@ hipError_t launch_gemv16(const LinearProblem& p, const GemvPlan& plan, void* wor
     args.gps = plan.groups_per_split;
     args.splits = plan.splits;
     args.partials = (float*)workspace;
+    W4G64_TIMELINE_SET(args);
     if (p.x_kind == kF16) return launch_shape16<kF16>(args, plan, stream, start, stop);
     return launch_shape16<kBF16>(args, plan, stream, start, stop);
 }
