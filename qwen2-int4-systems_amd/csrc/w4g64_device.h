@@ -158,12 +158,27 @@ __device__ __forceinline__ float bf16_round(float v) { return bf16_bits_to_float
 // merge sees every other workgroup's stores under the HIP memory model
 // (happens-before is transitive across the workgroup and agent scopes).
 // `flag` is a __shared__ int of the caller.  Every thread must call this.
+// 16 bytes at byte offset `off` of a buffer resource over `size` bytes;
+// bytes past the end read as 0.  A raw buffer load that reaches past the
+// resource's end returns zero as a whole, so the chunk that straddles the
+// end is read byte by byte (each byte load is in range or reads 0).
+__device__ __forceinline__ u32x4 load16_bounded(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t size) {
+    if (off + 16u <= size) return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+    u32x4 v = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const uint32_t b = __builtin_amdgcn_raw_buffer_load_b8(r, (int)(off + (uint32_t)i), 0, 0);
+        v[i >> 2] |= (b & 0xFFu) << (8 * (i & 3));
+    }
+    return v;
+}
+
 // ---- workgroup timelines (profiling builds only) ----
 // Built with -DW4G64_TIMELINE (a separate library, libw4g64_hip_timeline.so),
 // an instrumented kernel records up to 8 chip-wide timestamps (s_memrealtime,
-// 100 MHz) of its phases in registers, and thread 0 of each workgroup below
-// the registered count stores them to stamps[workgroup][8] at exit, after its
-// own stores have completed.  Without the define every macro is empty.
+// 100 MHz) of its phases in registers, and thread 0 of each workgroup (linear
+// id x + X y) below the registered count stores them to stamps[workgroup][8]
+// at exit, after its own stores have completed.  Without the define every macro is empty.
 #ifdef W4G64_TIMELINE
 #define W4G64_TIMELINE_FIELDS unsigned long long* tl_stamps; int tl_workgroups;
 #define W4G64_TIMELINE_DECL unsigned long long tl_[8] = {0, 0, 0, 0, 0, 0, 0, 0}
@@ -172,8 +187,9 @@ __device__ __forceinline__ float bf16_round(float v) { return bf16_bits_to_float
     do {                                                                                             \
         __builtin_amdgcn_s_waitcnt(0);                                                               \
         W4G64_STAMP(7);                                                                              \
-        if ((args).tl_stamps && threadIdx.x == 0 && (int)blockIdx.x < (args).tl_workgroups)          \
-            for (int k_ = 0; k_ < 8; ++k_) (args).tl_stamps[(int64_t)blockIdx.x * 8 + k_] = tl_[k_]; \
+        const int wg_ = (int)(blockIdx.x + gridDim.x * blockIdx.y);                                  \
+        if ((args).tl_stamps && threadIdx.x == 0 && wg_ < (args).tl_workgroups)                      \
+            for (int k_ = 0; k_ < 8; ++k_) (args).tl_stamps[(int64_t)wg_ * 8 + k_] = tl_[k_];        \
     } while (0)
 #define W4G64_TIMELINE_SET(args) ((args).tl_stamps = ::w4g64::g_timeline_stamps, (args).tl_workgroups = ::w4g64::g_timeline_workgroups)
 #else

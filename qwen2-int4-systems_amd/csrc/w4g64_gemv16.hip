@@ -124,8 +124,8 @@ __global__ __launch_bounds__(KW * FB * 64) void gemv16_kernel(Gemv16Args a) {
     // bytes [2 (n G + g0), + 2 cnt) and its zero nibbles at elements
     // [n G + g0, + cnt); each run is staged in 16-byte chunks from the
     // aligned-down start, one scale chunk and one zero chunk per thread
-    // (clamped thread indices repeat the last chunk).  Buffer resources
-    // bound-check the chunks that straddle an array's end.
+    // (clamped thread indices repeat the last chunk); bytes past an
+    // array's end read 0.
     constexpr int kScChunks = (2 * KW * STEPS + 15) / 16 + 1;
     constexpr int kZbChunks = (KW * STEPS / 2 + 1 + 15) / 16 + 1;
     static_assert(16 * FB * kScChunks <= kThreads16 && 16 * FB * kZbChunks <= kThreads16, "one chunk per thread");
@@ -143,10 +143,8 @@ __global__ __launch_bounds__(KW * FB * 64) void gemv16_kernel(Gemv16Args a) {
         const uint32_t ng = (uint32_t)a.N * (uint32_t)a.G;
         const __amdgpu_buffer_rsrc_t s_rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)a.scales, 0, (int)(2u * ng), 0x00020000);
         const __amdgpu_buffer_rsrc_t z_rsrc = __builtin_amdgcn_make_buffer_rsrc((void*)a.zeros, 0, (int)((ng + 1u) >> 1), 0x00020000);
-        svec = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                             s_rsrc, (int)(run_start(min(nb * kCols + fs, a.N - 1), false) + 16u * cs), 0, 0));
-        zvec = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                             z_rsrc, (int)(run_start(min(nb * kCols + fz, a.N - 1), true) + 16u * cz), 0, 0));
+        svec = load16_bounded(s_rsrc, run_start(min(nb * kCols + fs, a.N - 1), false) + 16u * cs, 2u * ng);
+        zvec = load16_bounded(z_rsrc, run_start(min(nb * kCols + fz, a.N - 1), true) + 16u * cz, (ng + 1u) >> 1);
     }
     // (the empty asm statements with a memory clobber fix the issue order)
     asm volatile("" ::: "memory");
@@ -200,9 +198,21 @@ __global__ __launch_bounds__(KW * FB * 64) void gemv16_kernel(Gemv16Args a) {
     W4G64_STAMP(3);
 
     // ---- 4. MFMA over the steps: A row = activation row (rows past M read row M - 1) ----
-    // this lane's feature row as staged (clamped to N - 1) and its runs' starts
-    const int nrowc = min(n, a.N - 1);
-    const uint32_t s_run = run_start(nrowc, false), z_run = run_start(nrowc, true);
+    // this lane's scale bits and zero nibbles of every step (feature row as
+    // staged, clamped to N - 1), read from LDS together
+    uint32_t sreg[STEPS], zreg[STEPS];
+    {
+        const int nrowc = min(n, a.N - 1);
+        const uint32_t s_run = run_start(nrowc, false), z_run = run_start(nrowc, true);
+#pragma unroll
+        for (int t = 0; t < STEPS; ++t) {
+            const int gl = kw + KW * t;
+            const uint32_t e_sz = (uint32_t)nrowc * (uint32_t)a.G + (uint32_t)(gl < cnt ? g0 + gl : g0);
+            sreg[t] = *(const uint16_t*)&scl[fb * 16 + j][2u * e_sz - s_run];
+            const uint32_t zb = zbl[fb * 16 + j][(e_sz >> 1) - z_run];
+            zreg[t] = (e_sz & 1) ? zb >> 4 : zb & 0xFu;
+        }
+    }
     const int mrow = min(j, a.M - 1);
     float4v acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -215,12 +225,8 @@ __global__ __launch_bounds__(KW * FB * 64) void gemv16_kernel(Gemv16Args a) {
         // wait for this step's weight, scale and zero alone; the empty asm keeps
         // their decoding here
         asm volatile("" : "+v"(wq[t]));
-        const int gz = gl < cnt ? g0 + gl : g0;  // the group this step loaded
-        const uint32_t e_sz = (uint32_t)nrowc * (uint32_t)a.G + (uint32_t)gz;  // its scale / zero element
-        const uint16_t s_bits = *(const uint16_t*)&scl[fb * 16 + j][2u * e_sz - s_run];
-        const uint32_t z_byte = zbl[fb * 16 + j][(e_sz >> 1) - z_run];
-        const float sct = (nvalid && gl < cnt) ? half_bits_to_float(s_bits) : 0.0f;
-        const int zn = ((e_sz & 1) ? (z_byte >> 4) : z_byte) & 0xF;
+        const float sct = (nvalid && gl < cnt) ? half_bits_to_float((uint16_t)sreg[t]) : 0.0f;
+        const int zn = (int)zreg[t];
         const int zrt = zn - ((zn & 8) << 1);
         float4v d;
         if constexpr (XK == kF16) {

@@ -414,10 +414,14 @@ def test_one_hot_activations_reproduce_dequantized_weights_exactly(rows, dtype):
 
 @pytest.mark.parametrize(
     ("rows", "n", "k"),
-    [(1, 6, 128), (3, 100, 64), (16, 200, 640), (17, 64, 128), (33, 1000, 192), (127, 130, 256), (129, 72, 512)],
+    [(1, 6, 128), (3, 100, 64), (4, 7, 192), (16, 200, 640), (17, 64, 128), (33, 1000, 192), (127, 130, 256),
+     (129, 72, 512)],
 )
 @pytest.mark.parametrize("dtype", ["fp16", "bf16"])
 def test_ragged_shapes(rows, n, k, dtype):
+    """Ragged feature counts and K: the scale and zero-point arrays end
+    mid-way through a 16-byte chunk (6 x 2 groups, 7 x 3 groups), which the
+    decode kernels stage per workgroup in 16-byte chunks."""
     q, s, z = weights("asym", n, k, rows * 1000 + n + k)
     x = O.activations(rows, k, seed=rows + n, dtype=dtype)
     bias = O._from_f32(np.linspace(-0.3, 0.3, n, dtype=np.float32), "fp16")
@@ -427,7 +431,7 @@ def test_ragged_shapes(rows, n, k, dtype):
 @pytest.mark.parametrize(
     ("rows", "n", "k"),
     [(9, 1536, 1536), (12, 256, 1536), (16, 8960, 1536), (16, 1536, 8960), (13, 72, 3072), (16, 40, 9280),
-     (10, 96, 64), (9, 8200, 512)],
+     (10, 96, 64), (9, 8200, 512), (12, 7, 192), (16, 13, 8960)],
 )
 @pytest.mark.parametrize("dtype", ["fp16", "bf16"])
 def test_decode_nine_to_sixteen_rows(rows, n, k, dtype):
