@@ -80,6 +80,7 @@ struct GemmArgs {
     int wg;  // weight groups (in_features / 64): step g reads weight group g mod wg
     int tiles_m;
     int tiles_n;
+    int band_group;  // row bands per group of the tile order (tile_coords)
     int vec_out;    // y is 16-byte aligned and N % 8 == 0 (fp32: N % 4): 16-byte output stores
     int dp_tiles;   // tiles [0, dp_tiles): one workgroup each over the whole K range
     int splits;     // tiles [dp_tiles, tiles): `splits` workgroups each, one K range apiece
@@ -138,6 +139,29 @@ __device__ __forceinline__ u32x4 decode_codes(uint32_t w, half2v zlo, half2v zhi
     return r;
 }
 
+// Tile t -> (row band, column tile): bands in groups of bg, each group's
+// tiles column by column (t = group-major, then column, then band), leftover
+// bands row by row (bg = 1: row-major).  With data-parallel tiles (bg = 4),
+// consecutive tiles -- what one XCD's workgroups take -- cover a few row
+// bands by a run of column tiles, whose weights stay in that XCD's L2 while
+// its bands are read (gate 8960x1536 at 2048 rows: GEMM fetch 107 -> 54 MB).
+// Split-only GEMMs keep row-major tiles: their K-range-major deal already
+// keeps a band's activation slice in one L2 (down 1536x8960: 63 MB against
+// 75 with bg = 4).
+__device__ __forceinline__ void tile_coords(int t, int tiles_m, int tiles_n, int bg, int& tm, int& tn) {
+    const int grouped = (tiles_m / bg) * bg * tiles_n;
+    if (t < grouped) {
+        const int g = t / (bg * tiles_n);
+        const int w = t - g * (bg * tiles_n);
+        tn = w / bg;
+        tm = g * bg + (w - tn * bg);
+    } else {
+        const int r = t - grouped;
+        tm = (tiles_m / bg) * bg + r / tiles_n;
+        tn = r - (r / tiles_n) * tiles_n;
+    }
+}
+
 template <int OUTK>
 __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
     constexpr int RB = kBM / 16;                // 16-row MFMA blocks per wave
@@ -192,8 +216,8 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
         gbeg = piece * a.gps;
         gcnt = min(a.gps, a.G - gbeg);
     }
-    const int tile_m = t / a.tiles_n;
-    const int tile_n = t - tile_m * a.tiles_n;
+    int tile_m, tile_n;
+    tile_coords(t, a.tiles_m, a.tiles_n, a.band_group, tile_m, tile_n);
     const int64_t m0 = (int64_t)tile_m * kBM;
     const int64_t nw = (int64_t)tile_n * kBN + 64 * wave;  // this wave's first output feature
 
@@ -559,8 +583,8 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmArgs a) {
     const int row = e / kBN;
     const int col = e % kBN;
     const int t = a.dp_tiles + idx;
-    const int tile_m = t / a.tiles_n;
-    const int tile_n = t - tile_m * a.tiles_n;
+    int tile_m, tile_n;
+    tile_coords(t, a.tiles_m, a.tiles_n, a.band_group, tile_m, tile_n);
     const int64_t m = (int64_t)tile_m * kBM + row;
     const int64_t n = (int64_t)tile_n * kBN + col;
     if (m >= a.M || n >= a.N) return;
@@ -871,6 +895,7 @@ hipError_t launch_gemm(const LinearProblem& p, void* workspace, hipStream_t stre
     args.wg = (int)(p.in_features / 64);
     args.tiles_m = pl.tiles_m;
     args.tiles_n = pl.tiles_n;
+    args.band_group = pl.dp_tiles > 0 ? 4 : 1;
     args.vec_out = (((uintptr_t)p.y & 15) == 0) && (p.out_features % (two ? 4 : 8) == 0);
     args.dp_tiles = pl.dp_tiles;
     args.splits = pl.splits;
