@@ -581,6 +581,67 @@ ATTENTION_PHASES = ("entry", "chunk staged in LDS", "scores", "softmax statistic
                     "arrival counted", "merge statistics (last arrival)", "stores complete")
 
 
+SUSTAINED_CASES = (  # (rows, out_features, in_features, what the tall shape stacks)
+    (1, 17920 * 28, 1536, "gate and up of 28 layers"),
+    (1, 1536 * 28, 8960, "down_proj of 28 layers (stacked output rows)"),
+    (4, 17920 * 28, 1536, "gate and up of 28 layers"),
+    (16, 17920 * 28, 1536, "gate and up of 28 layers"),
+    (16, 1536 * 28, 8960, "down_proj of 28 layers (stacked output rows)"),
+)
+
+
+def sustained_pass() -> int:
+    """Steady-state rate of the decode GEMV kernels: one launch over a tall
+    weight matrix (the listed projection stacked over 28 layers, 200-420 MB),
+    so that launch and the per-workgroup latency chain are amortised.  Random
+    packed codes, fp16 scales in [0.001, 0.011), zero codes 0 (the kernels'
+    work does not depend on the values); fp16 activations; HIP events around
+    each of 10 launches after 3 warm-ups, the median reported."""
+    import torch
+
+    from qwen_int4_hip import _lib
+    from qwen_int4_hip.kernels import _workspace
+
+    if not torch.cuda.is_available():
+        raise SystemExit("bench.py --sustained needs a ROCm GPU")
+    lib = _lib.load()
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    gen = torch.Generator(device="cuda").manual_seed(BASE_SEED + 9)
+    print("| rows | out x in | stacks | MB | kernel | us (p50) | GB/s | of 8 TB/s |")
+    print("|---:|---|---|---:|---|---:|---:|---:|")
+    for rows, n, k, what in SUSTAINED_CASES:
+        q = torch.randint(0, 256, (n, k // 2), dtype=torch.uint8, device="cuda", generator=gen)
+        sc = (torch.rand((n, k // 64), device="cuda", generator=gen) * 0.01 + 0.001).to(torch.float16)
+        z = torch.zeros((n * (k // 64) + 1) // 2, dtype=torch.uint8, device="cuda")
+        x = torch.randn((rows, k), device="cuda", generator=gen).to(torch.float16)
+        y = torch.empty((rows, n), dtype=torch.float16, device="cuda")
+        ws = _workspace(torch.device("cuda"), max(16, lib.w4g64_linear_workspace_bytes(rows, n, k, _lib.DTYPE_F16)))
+        name = lib.w4g64_linear_kernel_name(rows, n, k, _lib.DTYPE_F16).decode()
+        p_ = lambda t: ctypes.c_void_p(t.data_ptr())
+
+        def call():
+            _lib.check(lib.w4g64_linear(p_(x), _lib.DTYPE_F16, p_(q), p_(sc), p_(z), None, _lib.DTYPE_NONE, p_(y), rows,
+                                        n, k, p_(ws), ws.numel(), stream))
+
+        for _ in range(3):
+            call()
+        torch.cuda.synchronize()
+        times = []
+        for _ in range(10):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            call()
+            e1.record()
+            torch.cuda.synchronize()
+            times.append(e0.elapsed_time(e1) * 1e3)
+        us = statistics.median(times)
+        nbytes = algorithmic_bytes(rows, n, k)
+        print(f"| {rows} | {n}x{k} | {what} | {nbytes / 1e6:.1f} | {name} | {us:.1f} | {nbytes / us / 1e3:.0f} | "
+              f"{nbytes / us / 1e3 / HBM_PEAK_GBS:.1%} |", flush=True)
+        del q, sc, z, x, y
+    return 0
+
+
 def timeline_pass() -> int:
     """Per-workgroup phase timelines of the one-row decode GEMV (gemv_seg_kernel)
     and of a bare streaming kernel over the same bytes, from the profiling
@@ -896,6 +957,8 @@ def main() -> int:
     parser.add_argument("--timeline", action="store_true",
                         help="per-workgroup phase timelines of the one-row decode GEMV and a bare stream "
                              "(profiling build libw4g64_hip_timeline.so)")
+    parser.add_argument("--sustained", action="store_true",
+                        help="steady-state GB/s of the decode GEMV kernels over tall stacked weights (one launch each)")
     parser.add_argument("--summarize-mfma", nargs=2, metavar=("COUNTER_CSV", "OUT_JSON"),
                         help="shader clock and MFMA busy fraction per GEMM kernel from an --mfma-pass counter file")
     args = parser.parse_args()
@@ -913,6 +976,8 @@ def main() -> int:
         return mfma_pass()
     if args.timeline:
         return timeline_pass()
+    if args.sustained:
+        return sustained_pass()
 
     import torch
 
