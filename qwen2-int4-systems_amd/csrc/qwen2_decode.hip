@@ -602,28 +602,44 @@ __global__ __launch_bounds__(256) void prefill_attention_kernel(PrefillArgs a) {
 #pragma unroll
     for (int cb = 0; cb < kHeadDim / 16; ++cb) oacc[cb] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
 
+    // Keys: piece e = tid + 256 u -> key e / 16, dimensions 8 (e % 16) .. + 7
+    // (row-major LDS stores).  Values: thread t takes dimensions 8 vcol .. + 7,
+    // vcol = t / 16, of the four consecutive keys vrow0 + u, vrow0 = 4 (t % 16),
+    // so that one 8-byte store writes four keys of a transposed dimension row.
+    // Keys past the prompt re-read its last row (their scores are masked).
+    // A block's loads are issued while the previous block is computed.
+    const int vcol = tid / 16;
+    const int vrow0 = 4 * (tid % 16);
+    u32x4 kr[4], vr[4];
+    auto load_kv = [&](int kb) {
+        const int t0 = kb * kPrefillBlock;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int e = tid + 256 * u;
+            const int key = min(t0 + e / 16, a.length - 1);
+            kr[u] = *(const u32x4*)(kc + (int64_t)key * kHeadDim + 8 * (e % 16));
+            const int vkey = min(t0 + vrow0 + u, a.length - 1);
+            vr[u] = *(const u32x4*)(vc + (int64_t)vkey * kHeadDim + 8 * vcol);
+        }
+    };
+    load_kv(0);
     for (int kb = 0; kb <= qb; ++kb) {
         const int t0 = kb * kPrefillBlock;
-        // ---- stage keys and transposed values: piece e -> key e / 16, 8 dimensions 8 (e % 16) ----
-        {
-            u32x4 kr[4], vr[4];
+        // ---- stage the block's keys and transposed values ----
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int e = tid + 256 * u;
-                const int key = min(t0 + e / 16, a.length - 1);
-                kr[u] = *(const u32x4*)(kc + (int64_t)key * kHeadDim + 8 * (e % 16));
-                vr[u] = *(const u32x4*)(vc + (int64_t)key * kHeadDim + 8 * (e % 16));
-            }
+        for (int u = 0; u < 4; ++u) {
+            const int e = tid + 256 * u;
+            *(u32x4*)&ks[e / 16][8 * (e % 16)] = kr[u];
+        }
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int e = tid + 256 * u;
-                const int r = e / 16, c = e % 16;
-                *(u32x4*)&ks[r][8 * c] = kr[u];
-#pragma unroll
-                for (int h = 0; h < 8; ++h) vt[8 * c + h][r] = (uint16_t)(vr[u][h / 2] >> (16 * (h & 1)));
-            }
+        for (int h = 0; h < 8; ++h) {
+            const uint32_t sel = (h & 1) ? 0x07060302u : 0x05040100u;  // high or low halves
+            const uint32_t p01 = __builtin_amdgcn_perm(vr[1][h / 2], vr[0][h / 2], sel);
+            const uint32_t p23 = __builtin_amdgcn_perm(vr[3][h / 2], vr[2][h / 2], sel);
+            *(u32x2*)&vt[8 * vcol + h][vrow0] = u32x2{p01, p23};
         }
         __syncthreads();
+        if (kb < qb) load_kv(kb + 1);  // in flight during this block's products
         // ---- scores ----
         float s[4][4];
 #pragma unroll
