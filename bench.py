@@ -590,25 +590,20 @@ SUSTAINED_CASES = (  # (rows, out_features, in_features, what the tall shape sta
 )
 
 
-def sustained_pass() -> int:
+def sustained_rates(torch) -> list:
     """Steady-state rate of the decode GEMV kernels: one launch over a tall
-    weight matrix (the listed projection stacked over 28 layers, 200-420 MB),
+    weight matrix (the listed projection stacked over 28 layers, 200-430 MB),
     so that launch and the per-workgroup latency chain are amortised.  Random
     packed codes, fp16 scales in [0.001, 0.011), zero codes 0 (the kernels'
     work does not depend on the values); fp16 activations; HIP events around
     each of 10 launches after 3 warm-ups, the median reported."""
-    import torch
-
     from qwen_int4_hip import _lib
     from qwen_int4_hip.kernels import _workspace
 
-    if not torch.cuda.is_available():
-        raise SystemExit("bench.py --sustained needs a ROCm GPU")
     lib = _lib.load()
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     gen = torch.Generator(device="cuda").manual_seed(BASE_SEED + 9)
-    print("| rows | out x in | stacks | MB | kernel | us (p50) | GB/s | of 8 TB/s |")
-    print("|---:|---|---|---:|---|---:|---:|---:|")
+    out = []
     for rows, n, k, what in SUSTAINED_CASES:
         q = torch.randint(0, 256, (n, k // 2), dtype=torch.uint8, device="cuda", generator=gen)
         sc = (torch.rand((n, k // 64), device="cuda", generator=gen) * 0.01 + 0.001).to(torch.float16)
@@ -636,9 +631,24 @@ def sustained_pass() -> int:
             times.append(e0.elapsed_time(e1) * 1e3)
         us = statistics.median(times)
         nbytes = algorithmic_bytes(rows, n, k)
-        print(f"| {rows} | {n}x{k} | {what} | {nbytes / 1e6:.1f} | {name} | {us:.1f} | {nbytes / us / 1e3:.0f} | "
-              f"{nbytes / us / 1e3 / HBM_PEAK_GBS:.1%} |", flush=True)
+        out.append({"rows": rows, "n": n, "k": k, "stacks": what, "kernel": name, "us_p50": round(us, 2),
+                    "MB": round(nbytes / 1e6, 1), "GBps": round(nbytes / us / 1e3, 1),
+                    "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)})
         del q, sc, z, x, y
+    return out
+
+
+def sustained_pass() -> int:
+    """The steady-state table (sustained_rates) as markdown."""
+    import torch
+
+    if not torch.cuda.is_available():
+        raise SystemExit("bench.py --sustained needs a ROCm GPU")
+    print("| rows | out x in | stacks | MB | kernel | us (p50) | GB/s | of 8 TB/s |")
+    print("|---:|---|---|---:|---|---:|---:|---:|")
+    for r in sustained_rates(torch):
+        print(f"| {r['rows']} | {r['n']}x{r['k']} | {r['stacks']} | {r['MB']} | {r['kernel']} | {r['us_p50']} | "
+              f"{r['GBps']:.0f} | {r['frac']:.1%} |", flush=True)
     return 0
 
 
@@ -1069,6 +1079,11 @@ def main() -> int:
             f"p95 {p['kernel_us_p95']:6.2f})  {p['GBps']:8.1f} GB/s")
     log(f"decode kernels: {achieved:.1f} GB/s over all calls; M=1: {m1_gbs:.1f} GB/s; M=1 MLP shapes "
         f"{m1_mlp_gbs:.1f} GB/s")
+    # the same kernels at steady state (one launch over a 28-layer stack of a projection)
+    steady = sustained_rates(torch)
+    for r in steady:
+        log(f"  steady state rows={r['rows']:2d} {r['n']}x{r['k']} ({r['stacks']}): {r['us_p50']:.1f} us, "
+            f"{r['GBps']:.0f} GB/s ({r['frac']:.1%})")
 
     result = {
         "metric": METRIC,
@@ -1110,6 +1125,7 @@ def main() -> int:
                                 "us_mean": round(dominant["kernel_us_mean"], 3),
                                 "achieved_GBps": round(dominant["GBps"], 1),
                                 "frac": round(dominant["GBps"] / HBM_PEAK_GBS, 4)},
+            "steady_state": steady,
         },
     }
     traffic = committed_traffic()

@@ -112,6 +112,20 @@ __device__ __forceinline__ float sum8_lanes(float s) {
     return s;
 }
 
+// Sum over the 64 lanes of a wave (quad swaps, half-row and row mirrors give
+// every lane its row's sum; row broadcasts 15 and 31 add the rows up in
+// lane 63), read from lane 63: one fixed order of additions.
+__device__ __forceinline__ float wave_sum64(float v) {
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false));
+    // lanes outside a broadcast's row mask receive the `old` operand, 0
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x142, 0xA, 0xF, false));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x143, 0xC, 0xF, false));
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
 // h = silu(bf16(g)) * bf16(up) in fp32 (the projections' outputs are bf16,
 // model.py:133-135; silu(x) = x / (1 + exp(-x))), stored as its exact
 // three-way bf16 split: planes [3][M][I], hi + mid + lo == h.
@@ -282,11 +296,17 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
     // ---- 3a. RMSNorm prologue (model.py:40-44, residual adds :149-154) ----
     // s = bf16(x + bf16(delta)); the activation is bf16(bf16(s * r) * w) with
     // r = rsqrt(mean(s^2) + eps) over the whole row (squares rounded before
-    // the fp32 sum, as x.pow(2) is).  Workgroup (0, 0) stores s.
+    // the fp32 sum, as x.pow(2) is).  Workgroup (0, 0) stores s.  One row (the
+    // decode step): each thread sums the squares of its items, a wave sum
+    // each, the four waves' sums added in order after one barrier.  More
+    // rows: per-item sums in LDS, reduced per row by wave 0.
+    float r_one = 0.0f;
     if constexpr (kNorm) {
         float* nsq = red + a.mv * kBlockCols * SW;  // [M][items per row] partial sums of squares
         float* rinv = nsq + a.M * items_per_row;    // [M]
         const bool writer = nb == 0 && split == 0;
+        const bool one_row = a.M == 1;
+        float pt = 0.0f;
 #pragma unroll
         for (int u = 0; u < kStage; ++u) {
             const int it = kThreads * u + tid;
@@ -325,30 +345,43 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
                 sb[e / 2] = float_to_bf16_bits(sv[0]) | ((uint32_t)float_to_bf16_bits(sv[1]) << 16);
             }
             v[u][0] = sb;  // s replaces the residual item
-            nsq[itc] = ps;
+            if (one_row) pt += it < total ? ps : 0.0f;  // clamped items repeat a real one
+            else nsq[itc] = ps;
             if (writer) *(u32x4*)(a.out_sum + (int64_t)m * a.K + 8 * c) = sb;
         }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-        __builtin_amdgcn_s_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-        if (wave == 0) {
-            for (int m = 0; m < a.M; ++m) {
-                float sq = 0.0f;
-                for (int l = lane; l < items_per_row; l += 64) sq += nsq[m * items_per_row + l];
+        if (one_row) {
+            const float wsum = wave_sum64(pt);
+            if (lane == 0) nsq[wave] = wsum;
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+            float sq = nsq[0];
 #pragma unroll
-                for (int off = 32; off > 0; off >>= 1) sq += __shfl_xor(sq, off);
-                if (lane == 0) rinv[m] = rsqrtf(sq / (float)a.K + a.eps);
+            for (int w = 1; w < kWaves; ++w) sq += nsq[w];
+            r_one = rsqrtf(sq / (float)a.K + a.eps);
+        } else {
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+            if (wave == 0) {
+                for (int m = 0; m < a.M; ++m) {
+                    float sq = 0.0f;
+                    for (int l = lane; l < items_per_row; l += 64) sq += nsq[m * items_per_row + l];
+#pragma unroll
+                    for (int off = 32; off > 0; off >>= 1) sq += __shfl_xor(sq, off);
+                    if (lane == 0) rinv[m] = rsqrtf(sq / (float)a.K + a.eps);
+                }
             }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
         }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-        __builtin_amdgcn_s_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 #pragma unroll
         for (int u = 0; u < kStage; ++u) {
             const int it = kThreads * u + tid;
             int m, c;
             item_rc(it < total ? it : total - 8 + (tid & 7), m, c);
-            const float r = rinv[m];
+            const float r = one_row ? r_one : rinv[m];
             u32x4 nbits;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
