@@ -363,6 +363,9 @@ int w4g64_linear_rmsnorm(const void* residual, const void* delta, int delta_dtyp
     p.norm_weight = (const uint16_t*)norm_weight;
     p.norm_eps = eps;
     p.norm_out_sum = out_sum;
+    w4g64::GemvPlan lean;
+    if (gate_up_planes && w4g64::plan_seg_norm_planes(p, lean))
+        return hip_status(w4g64::launch_gemv_seg_norm_planes(p, lean, (hipStream_t)stream), "gemv");
     const w4g64::GemvPlan plan = gate_up_planes ? w4g64::plan_gemv_paired(rows, out_features, in_features, kind)
                                                 : w4g64::plan_gemv(rows, out_features, in_features, kind);
     if (plan.kind != 0 || plan.splits != 1)

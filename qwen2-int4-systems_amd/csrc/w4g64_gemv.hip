@@ -112,35 +112,6 @@ __device__ __forceinline__ float sum8_lanes(float s) {
     return s;
 }
 
-// Sum over the 64 lanes of a wave (quad swaps, half-row and row mirrors give
-// every lane its row's sum; row broadcasts 15 and 31 add the rows up in
-// lane 63), read from lane 63: one fixed order of additions.
-__device__ __forceinline__ float wave_sum64(float v) {
-    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
-    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
-    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
-    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false));
-    // lanes outside a broadcast's row mask receive the `old` operand, 0
-    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x142, 0xA, 0xF, false));
-    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x143, 0xC, 0xF, false));
-    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
-}
-
-// h = silu(bf16(g)) * bf16(up) in fp32 (the projections' outputs are bf16,
-// model.py:133-135; silu(x) = x / (1 + exp(-x))), stored as its exact
-// three-way bf16 split: planes [3][M][I], hi + mid + lo == h.
-__device__ __forceinline__ void store_silu_planes(void* y, int m, int i, int M, int I, float g, float up) {
-    const float gb = bf16_round(g), ub = bf16_round(up);
-    const float h = (gb / (1.0f + expf(-gb))) * ub;
-    uint16_t hi, mid, lo;
-    split3_bf16(h, hi, mid, lo);
-    uint16_t* planes = (uint16_t*)y;
-    const int64_t at = (int64_t)m * I + i, plane = (int64_t)M * I;
-    planes[at] = hi;
-    planes[plane + at] = mid;
-    planes[2 * plane + at] = lo;
-}
-
 template <int XK, int SW, int STEPS, int TILES>
 __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];

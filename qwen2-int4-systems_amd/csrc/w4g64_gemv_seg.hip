@@ -323,6 +323,253 @@ __global__ __launch_bounds__(NR * NK * 64) void gemv_seg_kernel(SegArgs a) {
     W4G64_TIMELINE_STORE(a);
 }
 
+// ---- one bf16 row of the decode step's MLP entry: residual add + RMSNorm,
+// then the paired gate|up projection with the SiLU product as bf16 planes ----
+//
+// The same layout as gemv_seg_kernel with 4 segments and 4 row blocks of 4
+// rows (16 rows per workgroup), its rows the 8 gate rows i0 .. i0 + 7 (row
+// blocks 0, 1) and the matching up rows I + i0 .. (row blocks 2, 3), i0 = 8
+// (workgroup).  Staging: every thread below K / 8 loads 8 values of the
+// residual, the delta and the norm weight; the others load 16-byte chunks
+// of the two rows' scale spans and zero-byte spans.  s = bf16(x + delta)
+// (workgroup 0 stores it), the squares' fp32 sum per thread, a wave sum per
+// wave and the four waves' sums after one barrier give r = rsqrt(mean + eps);
+// the activation bf16(bf16(s r) w) goes to LDS as the bf16 kernel's does.
+// The epilogue stores h = silu(bf16(gate)) * bf16(up) as three bf16 planes.
+struct SegNormArgs {
+    const uint16_t* resid;   // [K] bf16 residual row
+    const uint16_t* delta;   // [K] bf16
+    const uint16_t* norm_w;  // [K] bf16
+    float eps;
+    uint16_t* out_sum;       // [K] bf16: resid + delta (workgroup 0)
+    const uint8_t* qweight;  // [2 I][K / 2]
+    const uint16_t* scales;  // [2 I][G]
+    const uint8_t* zeros;    // [2 I][G / 2] bytes
+    uint16_t* planes;        // [3][I] bf16
+    int I;   // pairs (gate rows), a multiple of 8
+    int K;   // in_features (<= 2048: one activation item per thread)
+    int G;
+    int P;
+    W4G64_TIMELINE_FIELDS
+};
+constexpr int kNormPairs = 8;
+constexpr int kNormPlanesThreads = 256;
+
+// LDS layout (bytes): xs [K] | 64 zero bytes | xsum [G] fp32 | scale chunks of
+// the gate span then the up span | zero-byte chunks likewise | red [4][4][4]
+// fp32 | wave sums [4] fp32.
+struct SegNormLayout {
+    int zero, xsum, sc, zb, red, wsum, total;
+};
+__host__ __device__ inline SegNormLayout seg_norm_layout(int K) {
+    const int G = K / 64, P = G / 2;
+    SegNormLayout L;
+    L.zero = K * 2;
+    L.xsum = L.zero + 64;
+    L.sc = (L.xsum + G * 4 + 15) & ~15;
+    L.zb = L.sc + 2 * ((kNormPairs * G * 2 + 32 + 15) & ~15);
+    L.red = L.zb + 2 * ((kNormPairs * P + 32 + 15) & ~15);
+    L.wsum = L.red + 4 * 4 * 4 * 4;
+    L.total = L.wsum + 4 * 4;
+    return L;
+}
+
+template <int STEPS, int STAGE>
+__global__ __launch_bounds__(kNormPlanesThreads) void gemv_seg_norm_planes_kernel(SegNormArgs a) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    constexpr int SW = 4, R = 4;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int K = a.K, G = a.G, P = a.P, I = a.I;
+    const SegNormLayout L = seg_norm_layout(K);
+    const int i0 = blockIdx.x * kNormPairs;
+    W4G64_TIMELINE_DECL;
+    W4G64_STAMP(0);
+
+    // ---- 1. staging loads ----
+    // spans h = 0 (gate rows i0 ..) and 1 (up rows I + i0 ..), 16-byte aligned
+    int64_t s_lo[2], z_lo[2];
+    int SI[2], ZI[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int64_t r0 = (int64_t)h * I + i0;
+        s_lo[h] = (r0 * G * 2) & ~15ll;
+        const int64_t s_hi = min(((r0 + kNormPairs) * G * 2 + 15) & ~15ll, (int64_t)2 * I * G * 2);
+        z_lo[h] = (r0 * P) & ~15ll;
+        const int64_t z_hi = min(((r0 + kNormPairs) * P + 15) & ~15ll, (int64_t)2 * I * P);
+        SI[h] = (int)((s_hi - s_lo[h]) >> 4);
+        ZI[h] = (int)((z_hi - z_lo[h]) >> 4);
+    }
+    const int XI = K / 8;  // <= kNormPlanesThreads: activation items are u = 0 only
+    const int items = XI + SI[0] + SI[1] + ZI[0] + ZI[1];
+    u32x4 xr = {0u, 0u, 0u, 0u}, xd = {0u, 0u, 0u, 0u}, xw = {0u, 0u, 0u, 0u};
+    u32x4 sv[STAGE];
+#pragma unroll
+    for (int u = 0; u < STAGE; ++u) {
+        int it = kNormPlanesThreads * u + tid;
+        it = it < items ? it : items - 1;
+        sv[u] = u32x4{0u, 0u, 0u, 0u};
+        if (it < XI) {
+            xr = *(const u32x4*)(a.resid + 8 * it);
+            xd = *(const u32x4*)(a.delta + 8 * it);
+            xw = *(const u32x4*)(a.norm_w + 8 * it);
+        } else {
+            int c = it - XI;
+            const uint8_t* src;
+            if (c < SI[0]) src = (const uint8_t*)a.scales + s_lo[0] + 16 * (int64_t)c;
+            else if ((c -= SI[0]) < SI[1]) src = (const uint8_t*)a.scales + s_lo[1] + 16 * (int64_t)c;
+            else if ((c -= SI[1]) < ZI[0]) src = a.zeros + z_lo[0] + 16 * (int64_t)c;
+            else src = a.zeros + z_lo[1] + 16 * (int64_t)(c - ZI[0]);
+            sv[u] = *(const u32x4*)src;
+        }
+    }
+    asm volatile("" ::: "memory");
+
+    // ---- 2. weight loads: lane (c, q) -> row r, segment s of row block `wave` ----
+    const int c = lane & 15;
+    const int q = lane >> 4;
+    const int r = c / SW;
+    const int s = c % SW;
+    const int wrow = wave * R + r;              // 0..15: gate rows 0..7, then up rows
+    const int half = wrow >> 3;
+    const int row = half * I + i0 + (wrow & 7);
+    const uint8_t* wsrc = a.qweight + (int64_t)row * (K / 2) + 16 * q;
+    u32x4 wv[STEPS];
+#pragma unroll
+    for (int t = 0; t < STEPS; ++t) {
+        const int jj = s + SW * t;
+        wv[t] = __builtin_nontemporal_load((const u32x4*)(wsrc + 64 * (jj < P ? jj : 0)));
+    }
+    asm volatile("" ::: "memory");
+    asm volatile("" : "+v"(xr), "+v"(xd), "+v"(xw));
+#pragma unroll
+    for (int u = 0; u < STAGE; ++u) asm volatile("" : "+v"(sv[u]));
+    W4G64_STAMP(1);
+    wait_vm<STEPS>();  // everything issued before the weights has landed
+    W4G64_STAMP(2);
+
+    // ---- 3. residual add and RMSNorm (model.py:40-44, :149-154) ----
+    const bool xitem = tid < XI;
+    u32x4 sb;
+    float pt = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        float sv2[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const float xv = bf16_bits_to_float(h ? xr[e] >> 16 : xr[e] & 0xFFFFu);
+            const float dv = bf16_bits_to_float(h ? xd[e] >> 16 : xd[e] & 0xFFFFu);
+            sv2[h] = bf16_round(xv + dv);
+            pt += __fmul_rn(sv2[h], sv2[h]);
+        }
+        sb[e] = float_to_bf16_bits(sv2[0]) | ((uint32_t)float_to_bf16_bits(sv2[1]) << 16);
+    }
+    pt = xitem ? pt : 0.0f;
+    if (xitem && blockIdx.x == 0) *(u32x4*)(a.out_sum + 8 * tid) = sb;
+    float* wsum = (float*)(smem + L.wsum);
+    const float ws = wave_sum64(pt);
+    if (lane == 0) wsum[wave] = ws;
+    lds_barrier();
+    const float rinv = rsqrtf((((wsum[0] + wsum[1]) + wsum[2]) + wsum[3]) / (float)K + a.eps);
+    u32x4 xb;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const float n0 = bf16_round(bf16_bits_to_float(sb[e] & 0xFFFFu) * rinv) * bf16_bits_to_float(xw[e] & 0xFFFFu);
+        const float n1 = bf16_round(bf16_bits_to_float(sb[e] >> 16) * rinv) * bf16_bits_to_float(xw[e] >> 16);
+        xb[e] = float_to_bf16_bits(n0) | ((uint32_t)float_to_bf16_bits(n1) << 16);
+    }
+    // ---- 4. staging into LDS: activations (slot order) with their group sums, scale and zero chunks ----
+    {
+        float gs = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) gs += __builtin_bit_cast(float, xb[e] << 16) + __builtin_bit_cast(float, xb[e] & 0xFFFF0000u);
+        gs = dpp_sum8(gs);  // the 8 items of one group sit in 8 aligned lanes (K / 8 is a multiple of 8)
+        float* xsum = (float*)(smem + L.xsum);
+        if (xitem) {
+            *(u32x4*)(smem + 16 * tid) = permute_slots(xb);
+            if ((tid & 7) == 0) xsum[tid >> 3] = gs;
+        }
+#pragma unroll
+        for (int u = 0; u < STAGE; ++u) {
+            const int it = kNormPlanesThreads * u + tid;
+            if (it >= XI && it < items) {
+                const int cc = it - XI;
+                const int scs = SI[0] + SI[1];
+                *(u32x4*)(smem + (cc < scs ? L.sc + 16 * cc : L.zb + 16 * (cc - scs))) = sv[u];
+            }
+        }
+        if (tid < 16) ((uint32_t*)(smem + L.zero))[tid] = 0u;
+    }
+    lds_barrier();
+    W4G64_STAMP(3);
+
+    // ---- 5. MFMA steps (the bf16 path of gemv_seg_kernel, one activation row) ----
+    const int ai = lane & 15;
+    const int am = ai / (2 * SW), as = (ai >> 1) % SW, ap = ai & 1;
+    const bool a_live = am < 1 && (q >> 1) == ap;
+    bool hu[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) hu[h] = (2 * q + h) == s;  // one row: segment s' = 2 q + h
+    const uint16_t* sc = (const uint16_t*)(smem + L.sc);
+    const uint8_t* zb = smem + L.zb;
+    const float* xsum = (const float*)(smem + L.xsum);
+    const int sc_row = (half ? 8 * SI[0] : 0) + (int)(((int64_t)row * G * 2 - s_lo[half]) >> 1);
+    const int zb_row = (half ? 16 * ZI[0] : 0) + (int)((int64_t)row * P - z_lo[half]);
+    float acc[2] = {0.0f, 0.0f};
+#pragma unroll
+    for (int t = 0; t < STEPS; ++t) {
+        const int jj = s + SW * t;
+        const int ja = as + SW * t;
+        const bool live = jj < P;
+        const bool alive = a_live && ja < P;
+        const unsigned char* asrc = alive ? smem + (128 * ja + 32 * q) * 2 : smem + L.zero;
+        u16x8 av[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) av[u] = *(const u16x8*)(asrc + (alive ? 16 * u : 0));
+        float4v d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, av[u]), dequant8_bf16_biased(wv[t][u]),
+                                                        d, 0, 0, 0);
+        const int jc = live ? jj : 0;
+        const uint32_t s2 = *(const uint32_t*)(sc + sc_row + 2 * jc);
+        const uint32_t z2 = zb[zb_row + jc];
+        const float s0 = live ? half_bits_to_float((uint16_t)s2) : 0.0f;
+        const float s1 = live ? half_bits_to_float((uint16_t)(s2 >> 16)) : 0.0f;
+        int z0 = (int)(z2 & 0xF), z1 = (int)(z2 >> 4);
+        z0 -= (z0 & 8) << 1;
+        z1 -= (z1 & 8) << 1;
+        const float c0 = 136.0f + (float)z0, c1 = 136.0f + (float)z1;
+        const float x0 = xsum[2 * jc], x1 = xsum[2 * jc + 1];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {  // halves of other segments accumulate what is never read
+            acc[h] = fmaf(s0, fmaf(-c0, x0, d[2 * h]), acc[h]);
+            acc[h] = fmaf(s1, fmaf(-c1, x1, d[2 * h + 1]), acc[h]);
+        }
+    }
+    W4G64_STAMP(4);
+
+    // ---- 6. segments summed through LDS; the SiLU product as planes ----
+    float* red = (float*)(smem + L.red);  // [wave][r][SW]
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+        if (hu[h]) red[(wave * R + r) * SW + s] = acc[h];
+    lds_barrier();
+    W4G64_STAMP(5);
+    if (tid < kNormPairs) {
+        float g = 0.0f, up = 0.0f;
+#pragma unroll
+        for (int s2 = 0; s2 < SW; ++s2) {
+            g += red[tid * SW + s2];                     // row tid: block tid / 4, row tid % 4
+            up += red[(kNormPairs + tid) * SW + s2];     // row 8 + tid
+        }
+        store_silu_planes(a.planes, 0, i0 + tid, 1, I, g, up);
+    }
+    W4G64_STAMP(6);
+    W4G64_TIMELINE_STORE(a);
+}
+
 template <int XK, int SW, int NR, int NK, int STEPS>
 hipError_t launch_seg3(const SegArgs& args, const GemvPlan& plan, hipStream_t stream, hipEvent_t start,
                        hipEvent_t stop) {
@@ -413,6 +660,62 @@ bool plan_seg(int64_t rows, int64_t out_features, int64_t in_features, int x_kin
 bool seg_supported(const LinearProblem& p) {
     return ((uintptr_t)p.scales % 16) == 0 && ((uintptr_t)p.zeros % 16) == 0 && ((uintptr_t)p.qweight % 16) == 0 &&
            ((uintptr_t)p.x % 16) == 0 && ((uintptr_t)p.bias % 4) == 0 && !p.paired && p.norm_delta == nullptr;
+}
+
+// The one-row RMSNorm + gate|up planes form of the lean kernel: bf16
+// residual and delta, no bias, I = out_features / 2 a multiple of 8, in_features
+// a multiple of 128 of at most 1536 (three 16-byte weight steps per lane).
+bool plan_seg_norm_planes(const LinearProblem& p, GemvPlan& plan) {
+    if (p.rows != 1 || p.x_kind != kNormB || !p.paired || p.bias || p.norm_delta_parts != 1) return false;
+    if (p.out_features % 16 || p.in_features % 128 || p.in_features > 1536 || p.out_features > kGemvMaxOutFeatures)
+        return false;
+    if (((uintptr_t)p.scales % 16) || ((uintptr_t)p.zeros % 16) || ((uintptr_t)p.qweight % 16)) return false;
+    const int64_t G = p.in_features / 64, P = G / 2, I = p.out_features / 2;
+    const int steps = (int)((P + 3) / 4);
+    // items: activation chunks, then both spans' scale and zero-byte chunks (at most)
+    const int64_t items = p.in_features / 8 + 2 * ((kNormPairs * G * 2 + 30) / 16 + 1) + 2 * ((kNormPairs * P + 30) / 16 + 1);
+    const int stage = (int)((items + kNormPlanesThreads - 1) / kNormPlanesThreads);
+    if (steps < 1 || steps > 3 || stage > 2) return false;
+    plan = GemvPlan{};
+    plan.kind = 3;
+    plan.segments = 4;
+    plan.fblocks = 4;
+    plan.kparts = 1;
+    plan.steps = steps;
+    plan.stage = stage;
+    plan.tiles = 1;
+    plan.n_blocks = (int)(I / kNormPairs);
+    plan.splits = 1;
+    plan.groups_per_split = (int)P;
+    plan.lds_bytes = seg_norm_layout((int)p.in_features).total;
+    return true;
+}
+
+hipError_t launch_gemv_seg_norm_planes(const LinearProblem& p, const GemvPlan& plan, hipStream_t stream) {
+    SegNormArgs a{};
+    a.resid = (const uint16_t*)p.x;
+    a.delta = (const uint16_t*)p.norm_delta;
+    a.norm_w = p.norm_weight;
+    a.eps = p.norm_eps;
+    a.out_sum = (uint16_t*)p.norm_out_sum;
+    a.qweight = p.qweight;
+    a.scales = p.scales;
+    a.zeros = p.zeros;
+    a.planes = (uint16_t*)p.y;
+    a.I = (int)(p.out_features / 2);
+    a.K = (int)p.in_features;
+    a.G = a.K / 64;
+    a.P = a.G / 2;
+    W4G64_TIMELINE_SET(a);
+    const dim3 grid(plan.n_blocks), block(kNormPlanesThreads);
+    const size_t lds = (size_t)plan.lds_bytes;
+#define W4G64_NORM_PLANES(S, T)                                                                                     \
+    if (plan.steps == S && plan.stage == T)                                                                         \
+        return launch_kernel(gemv_seg_norm_planes_kernel<S, T>, grid, block, lds, stream, nullptr, nullptr, a);
+    W4G64_NORM_PLANES(1, 1) W4G64_NORM_PLANES(2, 1) W4G64_NORM_PLANES(3, 1)
+    W4G64_NORM_PLANES(1, 2) W4G64_NORM_PLANES(2, 2) W4G64_NORM_PLANES(3, 2)
+#undef W4G64_NORM_PLANES
+    return hipErrorInvalidValue;
 }
 
 hipError_t launch_gemv_seg(const LinearProblem& p, const GemvPlan& plan, hipStream_t stream, hipEvent_t start,

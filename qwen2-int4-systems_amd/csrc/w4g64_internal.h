@@ -89,6 +89,11 @@ bool plan_seg(int64_t rows, int64_t out_features, int64_t in_features, int x_kin
 bool seg_supported(const LinearProblem& p);
 hipError_t launch_gemv_seg(const LinearProblem& p, const GemvPlan& plan, hipStream_t stream, hipEvent_t start,
                            hipEvent_t stop);
+// One-row RMSNorm + gate|up planes form of the lean kernel (plan.kind = 3):
+// bf16 residual and delta, no bias, out_features / 2 a multiple of 8,
+// in_features a multiple of 128 up to 1536, 16-byte aligned weights.
+bool plan_seg_norm_planes(const LinearProblem& p, GemvPlan& plan);
+hipError_t launch_gemv_seg_norm_planes(const LinearProblem& p, const GemvPlan& plan, hipStream_t stream);
 
 // Prefill GEMM (rows > 16): a staging kernel writes the activations as fp16
 // rows (scaled by a power of two per row; fp32-class kinds as hi|lo planes)
