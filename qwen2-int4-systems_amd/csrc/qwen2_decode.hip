@@ -719,6 +719,31 @@ __global__ __launch_bounds__(256) void prefill_attention_kernel(PrefillArgs a) {
     }
 }
 
+// Decode-step prologue, one workgroup per sequence: the token's embedding
+// row into x, and the rotary factors of the common position p: angle =
+// float(p) * inv_freq[d % (D/2)] (one fp32 product), cos/sin in fp32, then
+// bf16 (model.py: the embedding lookup and RotaryEmbedding.forward for one
+// position).  A token id outside [0, vocab) gives a row of NaN.
+__global__ __launch_bounds__(256) void decode_prologue_kernel(const int64_t* token_ids, const uint16_t* embed,
+                                                              const int64_t* position, const float* inv_freq,
+                                                              uint16_t* x, uint16_t* cos_out, uint16_t* sin_out,
+                                                              int hidden, int64_t vocab) {
+    const int b = blockIdx.x;
+    const int tid = threadIdx.x;
+    const int64_t tok = token_ids[b];
+    const bool valid = tok >= 0 && tok < vocab;
+    const uint16_t* src = embed + (valid ? tok : 0) * (int64_t)hidden;
+    uint16_t* dst = x + (int64_t)b * hidden;
+    const u32x4 nan4 = {0x7FC07FC0u, 0x7FC07FC0u, 0x7FC07FC0u, 0x7FC07FC0u};
+    for (int c = tid; c < hidden / 8; c += 256)
+        *(u32x4*)(dst + 8 * c) = valid ? *(const u32x4*)(src + 8 * c) : nan4;
+    if (tid < kHeadDim) {
+        const float angle = (float)*position * inv_freq[tid % (kHeadDim / 2)];
+        cos_out[(int64_t)b * kHeadDim + tid] = float_to_bf16_bits(cosf(angle));
+        sin_out[(int64_t)b * kHeadDim + tid] = float_to_bf16_bits(sinf(angle));
+    }
+}
+
 __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* gate_up, float* out, int64_t total,
                                                        int inter) {
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -880,6 +905,29 @@ int qwen2_prefill_attention(const void* qkv, const void* cos, const void* sin, v
     hipLaunchKernelGGL(prefill_attention_kernel, dim3((unsigned)(batch * num_heads * qblocks)), dim3(256), 0,
                        (hipStream_t)stream, args);
     return launch_status(hipGetLastError(), "prefill_attention");
+}
+
+int qwen2_decode_prologue(const int64_t* token_ids, const void* embed, const int64_t* position, const float* inv_freq,
+                          void* x, void* cos, void* sin, int64_t batch, int64_t hidden, int64_t vocab,
+                          int64_t head_dim, void* stream) {
+    if (batch < 0) return set_error(W4G64_STATUS_INVALID_VALUE, "batch must be non-negative");
+    if (head_dim != kHeadDim)
+        return set_error(W4G64_STATUS_UNSUPPORTED, "head_dim must be %d, got %lld", kHeadDim, (long long)head_dim);
+    if (hidden <= 0 || hidden % 8 || hidden > (1 << 20))
+        return set_error(W4G64_STATUS_INVALID_VALUE, "hidden must be a positive multiple of 8, got %lld",
+                         (long long)hidden);
+    if (vocab <= 0) return set_error(W4G64_STATUS_INVALID_VALUE, "vocab must be positive");
+    if (batch == 0) return clear_error();
+    if (batch > 0x7FFFFFFF) return set_error(W4G64_STATUS_INVALID_VALUE, "problem too large");
+    if (!token_ids || !embed || !position || !inv_freq || !x || !cos || !sin)
+        return set_error(W4G64_STATUS_INVALID_VALUE, "all tensors must be non-null device pointers");
+    if (!aligned16(embed) || !aligned16(x) || ((uintptr_t)cos & 1) || ((uintptr_t)sin & 1) ||
+        ((uintptr_t)token_ids & 7) || ((uintptr_t)position & 7) || ((uintptr_t)inv_freq & 3))
+        return set_error(W4G64_STATUS_INVALID_VALUE, "embed and x must be 16-byte aligned, the others element aligned");
+    hipLaunchKernelGGL(decode_prologue_kernel, dim3((unsigned)batch), dim3(256), 0, (hipStream_t)stream, token_ids,
+                       (const uint16_t*)embed, position, inv_freq, (uint16_t*)x, (uint16_t*)cos, (uint16_t*)sin,
+                       (int)hidden, vocab);
+    return launch_status(hipGetLastError(), "decode_prologue");
 }
 
 int qwen2_silu_mul(const void* gate_up, float* out, int64_t rows, int64_t intermediate, void* stream) {

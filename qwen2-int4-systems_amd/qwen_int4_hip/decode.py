@@ -163,6 +163,9 @@ class FusedDecodeStep:
             return torch.empty((batch, cols), dtype=dtype, device=device)
 
         self.x = buf(self.hidden)          # residual stream
+        self.cos = buf(self.head_dim)      # rotary factors of the step's position
+        self.sin = buf(self.head_dim)
+        self.inv_freq = model.model.rotary_emb.inv_freq.to(device=device, dtype=torch.float32).contiguous()
         # batch 1: the norms fuse into the next linear, whose workgroups all
         # read the residual while one writes the updated one -- a second buffer
         self.fused_norm = batch == 1
@@ -237,10 +240,12 @@ class FusedDecodeStep:
         check_static_caches(caches, layers=len(model.model.layers), batch=self.batch, kv_heads=self.kv_heads,
                             head_dim=self.head_dim, min_length=1, device=self.device)
         stream = ctypes.c_void_p(torch.cuda.current_stream(self.device).cuda_stream)
-        torch.index_select(model.model.embed_tokens.weight, 0, token_ids.reshape(-1), out=self.x)
-        cos, sin = model.model.rotary_emb(position.view(1, 1).expand(self.batch, 1), torch.bfloat16)
-        cos = cos.reshape(self.batch, self.head_dim).contiguous()
-        sin = sin.reshape(self.batch, self.head_dim).contiguous()
+        embed = model.model.embed_tokens.weight
+        token_ids = token_ids if token_ids.is_contiguous() else token_ids.contiguous()
+        cos, sin = self.cos, self.sin
+        _lib.check(self.lib.qwen2_decode_prologue(
+            _ptr(token_ids), _ptr(embed), _ptr(position), _ptr(self.inv_freq), _ptr(self.x), _ptr(cos), _ptr(sin),
+            self.batch, self.hidden, embed.shape[0], self.head_dim, stream))
         delta, delta_code = None, _lib.DTYPE_NONE
         cur, other = self.x, self.x_alt  # residual stream (fused norms: read cur, write other)
         for layer, fused, (k_cache, v_cache) in zip(model.model.layers, self.fused, caches):

@@ -172,6 +172,35 @@ def test_decode_attention_matches_torch(batch, heads, kv_heads, max_length, posi
             assert cos_sim.item() >= 0.99999, (pos, cos_sim.item())
 
 
+@pytest.mark.parametrize("batch,hidden,vocab", [(1, 1536, 151936), (3, 256, 512)])
+def test_decode_prologue_matches_embedding_and_rotary(batch, hidden, vocab):
+    """qwen2_decode_prologue = the embedding lookup and RotaryEmbedding.forward
+    of one position (model.py:22-31, :182, :190), bit for bit, at positions up
+    to a 17408-position cache; an id outside [0, vocab) gives a NaN row."""
+    lib = _lib.load()
+    g = _gen(batch * 31 + hidden)
+    embed = (torch.randn((vocab, hidden), generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+    rot = RotaryEmbedding(128, 1_000_000.0).cuda()
+    x = torch.empty((batch, hidden), dtype=torch.bfloat16, device="cuda")
+    cos = torch.empty((batch, 128), dtype=torch.bfloat16, device="cuda")
+    sin = torch.empty_like(cos)
+    for pos in (0, 1, 63, 511, 640, 4095, 17407):
+        ids = torch.randint(0, vocab, (batch,), generator=g, device="cuda", dtype=torch.int64)
+        position = torch.tensor([pos], dtype=torch.int64, device="cuda")
+        _lib.check(lib.qwen2_decode_prologue(_p(ids), _p(embed), _p(position), _p(rot.inv_freq), _p(x), _p(cos),
+                                             _p(sin), batch, hidden, vocab, 128, _stream()))
+        want_cos, want_sin = rot(position.view(1, 1).expand(batch, 1), torch.bfloat16)
+        torch.cuda.synchronize()
+        assert torch.equal(x, embed[ids]), pos
+        assert torch.equal(cos, want_cos.reshape(batch, 128)), pos
+        assert torch.equal(sin, want_sin.reshape(batch, 128)), pos
+    bad = torch.full((batch,), vocab, dtype=torch.int64, device="cuda")
+    _lib.check(lib.qwen2_decode_prologue(_p(bad), _p(embed), _p(position), _p(rot.inv_freq), _p(x), _p(cos), _p(sin),
+                                         batch, hidden, vocab, 128, _stream()))
+    torch.cuda.synchronize()
+    assert bool(torch.isnan(x.float()).all())
+
+
 @pytest.mark.parametrize("batch,heads,kv_heads,length,max_length", [
     (1, 12, 2, 512, 640),  # the prefill of the model's workload
     (2, 8, 1, 100, 128),   # a partial last block; group 8
