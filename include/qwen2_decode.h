@@ -32,13 +32,18 @@ extern "C" {
  *                                                for an id outside [0, vocab))
  *   cos[b][d], sin[b][d] = bf16(cos / sin(float(p) * inv_freq[d % (head_dim / 2)]))
  *                                              (bf16 [batch, head_dim], fp32 math)
- * token_ids int64 [batch], embed bf16 [vocab, hidden] (16-byte aligned, as x),
- * inv_freq fp32 [head_dim / 2] (the rotary module's buffer).  head_dim == 128.
- * Replaces: the embedding lookup of QwenModel.forward and RotaryEmbedding.forward
- *           for one position (src/qwen_int4/model.py:22-31, :182, :190). */
+ *   normed[b] = bf16(bf16(x[b] * rsqrt(mean(x[b]^2) + eps)) * norm_weight)
+ *                                              (only when norm_weight and normed are
+ *                                                given: the first layer's input norm)
+ * token_ids int64 [batch], embed bf16 [vocab, hidden] (16-byte aligned, as x,
+ * norm_weight and normed), inv_freq fp32 [head_dim / 2] (the rotary module's
+ * buffer).  head_dim == 128.
+ * Replaces: the embedding lookup of QwenModel.forward, RotaryEmbedding.forward
+ *           for one position and the first layer's input RMSNorm
+ *           (src/qwen_int4/model.py:22-31, :40-44, :182, :190). */
 int qwen2_decode_prologue(const int64_t* token_ids, const void* embed, const int64_t* position, const float* inv_freq,
-                          void* x, void* cos, void* sin, int64_t batch, int64_t hidden, int64_t vocab,
-                          int64_t head_dim, void* stream);
+                          void* x, void* cos, void* sin, const void* norm_weight, float eps, void* normed,
+                          int64_t batch, int64_t hidden, int64_t vocab, int64_t head_dim, void* stream);
 
 /* Residual add + RMSNorm over `rows` rows of `hidden` bf16 values:
  *   s        = x                                   (delta == NULL)

@@ -723,11 +723,15 @@ __global__ __launch_bounds__(256) void prefill_attention_kernel(PrefillArgs a) {
 // row into x, and the rotary factors of the common position p: angle =
 // float(p) * inv_freq[d % (D/2)] (one fp32 product), cos/sin in fp32, then
 // bf16 (model.py: the embedding lookup and RotaryEmbedding.forward for one
-// position).  A token id outside [0, vocab) gives a row of NaN.
+// position).  A token id outside [0, vocab) gives a row of NaN.  With a norm
+// weight, also the first layer's input RMSNorm of x into `normed`
+// (bf16(bf16(x r) w), r = rsqrt(mean(x^2) + eps), as add_rmsnorm_kernel).
 __global__ __launch_bounds__(256) void decode_prologue_kernel(const int64_t* token_ids, const uint16_t* embed,
                                                               const int64_t* position, const float* inv_freq,
                                                               uint16_t* x, uint16_t* cos_out, uint16_t* sin_out,
+                                                              const uint16_t* norm_w, float eps, uint16_t* normed,
                                                               int hidden, int64_t vocab) {
+    __shared__ float wsum[4];
     const int b = blockIdx.x;
     const int tid = threadIdx.x;
     const int64_t tok = token_ids[b];
@@ -735,8 +739,35 @@ __global__ __launch_bounds__(256) void decode_prologue_kernel(const int64_t* tok
     const uint16_t* src = embed + (valid ? tok : 0) * (int64_t)hidden;
     uint16_t* dst = x + (int64_t)b * hidden;
     const u32x4 nan4 = {0x7FC07FC0u, 0x7FC07FC0u, 0x7FC07FC0u, 0x7FC07FC0u};
-    for (int c = tid; c < hidden / 8; c += 256)
-        *(u32x4*)(dst + 8 * c) = valid ? *(const u32x4*)(src + 8 * c) : nan4;
+    float sq = 0.0f;
+    for (int c = tid; c < hidden / 8; c += 256) {
+        const u32x4 v = valid ? *(const u32x4*)(src + 8 * c) : nan4;
+        *(u32x4*)(dst + 8 * c) = v;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float f = bf16_bits_to_float((uint16_t)(v[e / 2] >> (16 * (e & 1))));
+            sq += __fmul_rn(f, f);
+        }
+    }
+    if (normed) {
+        const float ws = wave_sum64(sq);
+        if ((tid & 63) == 0) wsum[tid >> 6] = ws;
+        __syncthreads();
+        const float r = rsqrtf((((wsum[0] + wsum[1]) + wsum[2]) + wsum[3]) / (float)hidden + eps);
+        uint16_t* ndst = normed + (int64_t)b * hidden;
+        for (int c = tid; c < hidden / 8; c += 256) {
+            const u32x4 v = valid ? *(const u32x4*)(src + 8 * c) : nan4;
+            const u32x4 w = *(const u32x4*)(norm_w + 8 * c);
+            u32x4 o;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float n0 = bf16_round(bf16_bits_to_float(v[e] & 0xFFFFu) * r) * bf16_bits_to_float(w[e] & 0xFFFFu);
+                const float n1 = bf16_round(bf16_bits_to_float(v[e] >> 16) * r) * bf16_bits_to_float(w[e] >> 16);
+                o[e] = float_to_bf16_bits(n0) | ((uint32_t)float_to_bf16_bits(n1) << 16);
+            }
+            *(u32x4*)(ndst + 8 * c) = o;
+        }
+    }
     if (tid < kHeadDim) {
         const float angle = (float)*position * inv_freq[tid % (kHeadDim / 2)];
         cos_out[(int64_t)b * kHeadDim + tid] = float_to_bf16_bits(cosf(angle));
@@ -908,8 +939,8 @@ int qwen2_prefill_attention(const void* qkv, const void* cos, const void* sin, v
 }
 
 int qwen2_decode_prologue(const int64_t* token_ids, const void* embed, const int64_t* position, const float* inv_freq,
-                          void* x, void* cos, void* sin, int64_t batch, int64_t hidden, int64_t vocab,
-                          int64_t head_dim, void* stream) {
+                          void* x, void* cos, void* sin, const void* norm_weight, float eps, void* normed,
+                          int64_t batch, int64_t hidden, int64_t vocab, int64_t head_dim, void* stream) {
     if (batch < 0) return set_error(W4G64_STATUS_INVALID_VALUE, "batch must be non-negative");
     if (head_dim != kHeadDim)
         return set_error(W4G64_STATUS_UNSUPPORTED, "head_dim must be %d, got %lld", kHeadDim, (long long)head_dim);
@@ -924,9 +955,13 @@ int qwen2_decode_prologue(const int64_t* token_ids, const void* embed, const int
     if (!aligned16(embed) || !aligned16(x) || ((uintptr_t)cos & 1) || ((uintptr_t)sin & 1) ||
         ((uintptr_t)token_ids & 7) || ((uintptr_t)position & 7) || ((uintptr_t)inv_freq & 3))
         return set_error(W4G64_STATUS_INVALID_VALUE, "embed and x must be 16-byte aligned, the others element aligned");
+    if ((norm_weight == nullptr) != (normed == nullptr))
+        return set_error(W4G64_STATUS_INVALID_VALUE, "norm_weight and normed must both be given or both be null");
+    if (normed && (!aligned16(norm_weight) || !aligned16(normed)))
+        return set_error(W4G64_STATUS_INVALID_VALUE, "norm_weight and normed must be 16-byte aligned");
     hipLaunchKernelGGL(decode_prologue_kernel, dim3((unsigned)batch), dim3(256), 0, (hipStream_t)stream, token_ids,
                        (const uint16_t*)embed, position, inv_freq, (uint16_t*)x, (uint16_t*)cos, (uint16_t*)sin,
-                       (int)hidden, vocab);
+                       (const uint16_t*)norm_weight, eps, (uint16_t*)normed, (int)hidden, vocab);
     return launch_status(hipGetLastError(), "decode_prologue");
 }
 

@@ -243,8 +243,10 @@ class FusedDecodeStep:
         embed = model.model.embed_tokens.weight
         token_ids = token_ids if token_ids.is_contiguous() else token_ids.contiguous()
         cos, sin = self.cos, self.sin
+        # embedding rows, rotary factors and the first layer's input norm (into self.normed)
         _lib.check(self.lib.qwen2_decode_prologue(
             _ptr(token_ids), _ptr(embed), _ptr(position), _ptr(self.inv_freq), _ptr(self.x), _ptr(cos), _ptr(sin),
+            _ptr(model.model.layers[0].input_layernorm.weight), ctypes.c_float(self.eps), _ptr(self.normed),
             self.batch, self.hidden, embed.shape[0], self.head_dim, stream))
         delta, delta_code = None, _lib.DTYPE_NONE
         cur, other = self.x, self.x_alt  # residual stream (fused norms: read cur, write other)
@@ -254,7 +256,8 @@ class FusedDecodeStep:
                                   False, other, stream)
                 cur, other = other, cur
             else:
-                self._norm_at(cur, delta, delta_code, layer.input_layernorm.weight, stream)
+                if delta is not None:  # the first layer's norm came with the prologue
+                    self._norm_at(cur, delta, delta_code, layer.input_layernorm.weight, stream)
                 self._linear(self.normed, _lib.DTYPE_BF16, fused["qkv"], self.qkv, stream)
             _lib.check(self.lib.qwen2_decode_attention(
                 _ptr(self.qkv), _ptr(cos), _ptr(sin), _ptr(k_cache), _ptr(v_cache), _ptr(position),

@@ -88,13 +88,15 @@ def test_decode_step_entry_points_reject_before_launch():
     assert lib.qwen2_add_rmsnorm(null, null, 0, p, f(1e-6), p, p, 1, 64, null) == _lib.STATUS_INVALID_VALUE
     assert lib.qwen2_add_rmsnorm(null, null, 0, null, f(1e-6), null, null, 0, 64, null) == _lib.STATUS_OK
     # decode-step prologue: head_dim, hidden, vocab, null and misaligned pointers; an empty batch is a no-op
-    pro = [p] * 7
+    pro = [p] * 7 + [p, f(1e-6), p]  # ids .. sin, norm_weight, eps, normed
     assert lib.qwen2_decode_prologue(*pro, 1, 1536, 100, 64, null) == _lib.STATUS_UNSUPPORTED
     assert lib.qwen2_decode_prologue(*pro, 1, 1530, 100, 128, null) == _lib.STATUS_INVALID_VALUE
     assert lib.qwen2_decode_prologue(*pro, 1, 1536, 0, 128, null) == _lib.STATUS_INVALID_VALUE
     assert lib.qwen2_decode_prologue(null, *pro[1:], 1, 1536, 100, 128, null) == _lib.STATUS_INVALID_VALUE
     assert lib.qwen2_decode_prologue(p, odd2, *pro[2:], 1, 1536, 100, 128, null) == _lib.STATUS_INVALID_VALUE
-    assert lib.qwen2_decode_prologue(*[null] * 7, 0, 1536, 100, 128, null) == _lib.STATUS_OK
+    half = [p] * 7 + [p, f(1e-6), null]  # a norm weight without an output
+    assert lib.qwen2_decode_prologue(*half, 1, 1536, 100, 128, null) == _lib.STATUS_INVALID_VALUE
+    assert lib.qwen2_decode_prologue(*[null] * 7, null, f(1e-6), null, 0, 1536, 100, 128, null) == _lib.STATUS_OK
     # attention: head_dim, head grouping, workspace, alignment
     ws = lib.qwen2_decode_attention_workspace_bytes(1, 2, 640)
     assert ws == 256 + 1 * 2 * 10 * (16 + 8 * 128) * 4

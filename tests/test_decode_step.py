@@ -176,27 +176,43 @@ def test_decode_attention_matches_torch(batch, heads, kv_heads, max_length, posi
 def test_decode_prologue_matches_embedding_and_rotary(batch, hidden, vocab):
     """qwen2_decode_prologue = the embedding lookup and RotaryEmbedding.forward
     of one position (model.py:22-31, :182, :190), bit for bit, at positions up
-    to a 17408-position cache; an id outside [0, vocab) gives a NaN row."""
+    to a 17408-position cache, and the first layer's RMSNorm to its bar; an id
+    outside [0, vocab) gives a NaN row."""
     lib = _lib.load()
     g = _gen(batch * 31 + hidden)
     embed = (torch.randn((vocab, hidden), generator=g, device="cuda") * 0.02).to(torch.bfloat16)
     rot = RotaryEmbedding(128, 1_000_000.0).cuda()
     x = torch.empty((batch, hidden), dtype=torch.bfloat16, device="cuda")
+    normed = torch.empty_like(x)
+    norm = RMSNorm(hidden, 1e-6).cuda()
+    with torch.no_grad():
+        norm.weight.copy_((torch.rand(hidden, generator=g, device="cuda") + 0.5).to(torch.bfloat16))
     cos = torch.empty((batch, 128), dtype=torch.bfloat16, device="cuda")
     sin = torch.empty_like(cos)
     for pos in (0, 1, 63, 511, 640, 4095, 17407):
         ids = torch.randint(0, vocab, (batch,), generator=g, device="cuda", dtype=torch.int64)
         position = torch.tensor([pos], dtype=torch.int64, device="cuda")
         _lib.check(lib.qwen2_decode_prologue(_p(ids), _p(embed), _p(position), _p(rot.inv_freq), _p(x), _p(cos),
-                                             _p(sin), batch, hidden, vocab, 128, _stream()))
+                                             _p(sin), _p(norm.weight), ctypes.c_float(1e-6), _p(normed), batch,
+                                             hidden, vocab, 128, _stream()))
         want_cos, want_sin = rot(position.view(1, 1).expand(batch, 1), torch.bfloat16)
+        want_x = embed[ids]
+        want_n = norm(want_x)
         torch.cuda.synchronize()
-        assert torch.equal(x, embed[ids]), pos
+        assert torch.equal(x, want_x), pos
         assert torch.equal(cos, want_cos.reshape(batch, 128)), pos
         assert torch.equal(sin, want_sin.reshape(batch, 128)), pos
+        # the norm to RMSNorm's bar (the fp32 sum of squares runs in another order)
+        rel = ((normed.float() - want_n.float()).abs() / want_n.float().abs().clamp_min(1e-30)).max().item()
+        assert (normed == want_n).float().mean().item() >= 0.99 and rel <= 2.0 ** -7, (pos, rel)
+    # without the norm: x, cos and sin only
+    _lib.check(lib.qwen2_decode_prologue(_p(ids), _p(embed), _p(position), _p(rot.inv_freq), _p(x), _p(cos), _p(sin),
+                                         None, ctypes.c_float(1e-6), None, batch, hidden, vocab, 128, _stream()))
+    torch.cuda.synchronize()
+    assert torch.equal(x, embed[ids])
     bad = torch.full((batch,), vocab, dtype=torch.int64, device="cuda")
     _lib.check(lib.qwen2_decode_prologue(_p(bad), _p(embed), _p(position), _p(rot.inv_freq), _p(x), _p(cos), _p(sin),
-                                         batch, hidden, vocab, 128, _stream()))
+                                         None, ctypes.c_float(1e-6), None, batch, hidden, vocab, 128, _stream()))
     torch.cuda.synchronize()
     assert bool(torch.isnan(x.float()).all())
 
