@@ -69,7 +69,7 @@ def test_add_rmsnorm_matches_torch(rows, hidden, delta_dtype):
 @pytest.mark.parametrize("delta_dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("form,n,k", [("linear", 2048, 1536), ("linear", 200, 640), ("planes", 8960, 1536),
                                       ("planes", 72, 192), ("planes", 256, 256), ("planes", 2064, 640),
-                                      ("planes", 17920, 1536)])
+                                      ("planes", 17920, 1536), ("planes", 512, 2048)])
 def test_linear_rmsnorm_matches_norm_then_linear(delta_dtype, form, n, k):
     """w4g64_linear_rmsnorm (one row) = qwen2_add_rmsnorm followed by the
     plain linear (or the gate|up planes entry): the residual sum bit-exact
