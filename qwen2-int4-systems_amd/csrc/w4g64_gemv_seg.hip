@@ -672,8 +672,9 @@ bool plan_seg_norm_planes(const LinearProblem& p, GemvPlan& plan) {
     if (((uintptr_t)p.scales % 16) || ((uintptr_t)p.zeros % 16) || ((uintptr_t)p.qweight % 16)) return false;
     const int64_t G = p.in_features / 64, P = G / 2, I = p.out_features / 2;
     const int steps = (int)((P + 3) / 4);
-    // items: activation chunks, then both spans' scale and zero-byte chunks (at most)
-    const int64_t items = p.in_features / 8 + 2 * ((kNormPairs * G * 2 + 30) / 16 + 1) + 2 * ((kNormPairs * P + 30) / 16 + 1);
+    // items: activation chunks, then both spans' scale and zero-byte chunks (a span of
+    // L bytes at any offset covers at most (L + 30) / 16 aligned 16-byte chunks)
+    const int64_t items = p.in_features / 8 + 2 * ((kNormPairs * G * 2 + 30) / 16) + 2 * ((kNormPairs * P + 30) / 16);
     const int stage = (int)((items + kNormPlanesThreads - 1) / kNormPlanesThreads);
     if (steps < 1 || steps > 3 || stage > 2) return false;
     plan = GemvPlan{};
