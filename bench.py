@@ -577,6 +577,8 @@ TIMELINE_PHASES = ("entry", "loads issued", "staging landed", "LDS barrier", "MF
 STREAM_PHASES = ("entry", "load issued", "data landed")
 GEMV_PHASES = ("entry", "staging landed", "staged in LDS", "LDS barrier", "MFMA steps done",
                "partial sums combined", "stores issued", "stores complete")
+PIPE_PHASES = ("entry", "staging landed, first loads issued", "LDS barrier", "steps done", "stores issued", "-", "-",
+               "stores complete")
 ATTENTION_PHASES = ("entry", "chunk staged in LDS", "scores", "softmax statistics", "partials stored",
                     "arrival counted", "merge statistics (last arrival)", "stores complete")
 
@@ -664,7 +666,7 @@ def timeline_pass() -> int:
     from qwen_int4_hip.kernels import _workspace
 
     if not hip_build.TIMELINE_LIBRARY.exists():
-        raise SystemExit(f"{hip_build.TIMELINE_LIBRARY} is missing: run __graft_entry__.build() first")
+        hip_build.build(timeline=True)  # the profiling build is made on demand
     if not torch.cuda.is_available():
         raise SystemExit("bench.py --timeline needs a ROCm GPU")
     lib = ctypes.CDLL(str(hip_build.TIMELINE_LIBRARY))
@@ -729,7 +731,8 @@ def timeline_pass() -> int:
 
         label = (f"{name} {n}x{k}, {rows} fp16 row{'s' if rows > 1 else ''}, "
                  f"{algorithmic_bytes(rows, n, k) / 1e6:.2f} MB: {kname}")
-        report(label, TIMELINE_PHASES if kname.startswith("gemv_seg") else GEMV_PHASES, call)
+        report(label, TIMELINE_PHASES if kname.startswith("gemv_seg") else
+               (PIPE_PHASES if kname.startswith("gemv_pipe") else GEMV_PHASES), call)
 
     # decode attention of one Qwen2-1.5B layer: batch 1, 12 query / 2 key-value heads, position 575 of a
     # 641-position cache (the e2e workload's midpoint); caches stay warm, as in the decode step

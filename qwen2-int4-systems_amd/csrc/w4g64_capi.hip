@@ -153,7 +153,13 @@ int64_t w4g64_linear_workspace_bytes(int64_t rows, int64_t out_features, int64_t
                                in_features};
         return w4g64::gemm_supported(p) ? w4g64::gemm_workspace_bytes(rows, out_features, in_features, x_dtype) : 0;
     }
-    return w4g64::plan_gemv(rows, out_features, in_features, x_dtype).workspace_bytes;
+    // the larger of the pipelined plan's and the other decode kernels' needs
+    // (which kernel runs also depends on pointer alignment)
+    int64_t need = w4g64::plan_gemv(rows, out_features, in_features, x_dtype).workspace_bytes;
+    w4g64::GemvPlan pipe;
+    if (w4g64::plan_pipe(rows, out_features, in_features, x_dtype, pipe) && pipe.workspace_bytes > need)
+        need = pipe.workspace_bytes;
+    return need;
 }
 
 const char* w4g64_linear_kernel_name(int64_t rows, int64_t out_features, int64_t in_features, int x_dtype) {
@@ -170,6 +176,8 @@ const char* w4g64_linear_kernel_name(int64_t rows, int64_t out_features, int64_t
     if (x_dtype != W4G64_DTYPE_F16 && x_dtype != W4G64_DTYPE_BF16 && x_dtype != W4G64_DTYPE_F32) return "none";
     if (rows <= w4g64::kGemvMaxRows) {
         w4g64::GemvPlan lean;
+        if (in_features % 256 == 0 && w4g64::plan_pipe(rows, out_features, in_features, x_dtype, lean))
+            return w4g64::gemv_kernel_name(lean, x_dtype);  // with aligned operands
         if (w4g64::plan_seg(rows, out_features, in_features, x_dtype, lean))
             return w4g64::gemv_kernel_name(lean, x_dtype);  // with 16-byte aligned operands
         return w4g64::gemv_kernel_name(w4g64::plan_gemv(rows, out_features, in_features, x_dtype), x_dtype);
@@ -225,6 +233,12 @@ static int linear_impl(const void* x, int x_dtype, const uint8_t* qweight, const
             return fail(W4G64_STATUS_UNSUPPORTED, "decode path supports at most %lld output features",
                         (long long)(w4g64::kGemvMaxOutFeatures));
         w4g64::GemvPlan lean;
+        if (w4g64::pipe_supported(p) && w4g64::plan_pipe(rows, out_features, in_features, p.x_kind, lean)) {
+            if (int st = check_workspace(workspace, workspace_bytes, lean.workspace_bytes)) return st;
+            return hip_status(w4g64::launch_gemv_pipe(p, lean, workspace, s, (hipEvent_t)start_event,
+                                                      (hipEvent_t)stop_event),
+                              "gemv");
+        }
         if (w4g64::plan_seg(rows, out_features, in_features, p.x_kind, lean) && w4g64::seg_supported(p))
             return hip_status(w4g64::launch_gemv_seg(p, lean, s, (hipEvent_t)start_event, (hipEvent_t)stop_event),
                               "gemv");

@@ -844,6 +844,12 @@ const char* gemv_kernel_name(const GemvPlan& plan, int x_kind) {
     static thread_local char name[64];
     static const char* kinds[] = {"?", "f16", "bf16", "f32", "?", "swiglu_bf16", "planes_bf16", "rmsnorm_bf16",
                                   "rmsnorm_f32delta"};
+    if (plan.kind == 4) {
+        snprintf(name, sizeof(name), "gemv_pipe_kernel<%s,%d,%d,%d,%d,%d,%d,%d>",
+                 kinds[x_kind >= 1 && x_kind <= 8 ? x_kind : 0], plan.segments, plan.tiles, plan.fblocks, plan.kparts,
+                 plan.rbw, plan.steps, plan.depth);
+        return name;
+    }
     if (plan.kind == 2) {
         snprintf(name, sizeof(name), "gemv_seg_kernel<%s,%d,%d,%d,%d>", kinds[x_kind >= 1 && x_kind <= 8 ? x_kind : 0],
                  plan.segments, plan.fblocks, plan.kparts, plan.steps);

@@ -1,0 +1,665 @@
+// Decode path, pipelined form: fused unpack + dequant + GEMV for 1..16
+// fp16/bf16 activation rows, 16-byte weight loads kept in flight by a
+// software pipeline for the whole life of every wave.
+//
+// y[m, n] = sum_g scale[n,g] * sum_{k in g} x[m,k] * (code[n,k] - zero[n,g])  (+ bias[n])
+// -- the reference's (x.float() @ W.t() + bias).to(x.dtype)
+// (src/qwen_int4/backends.py:73-98) with each group's scale applied in fp32.
+//
+// Unit of work: a chunk, 16 B columns x one 16-byte load per lane = 1 KB of
+// packed weights.  v_mfma_f32_16x16x32_{f16,bf16}:
+//   * B column c = (row r, segment s), c = r SW + s, R = 16 / SW rows per
+//     wave row block.  Lane (c, q) loads bytes [16 q, 16 q + 16) of group
+//     pair jj = pb + s + SW t of its row at step t, so one load instruction
+//     reads R rows x SW x 64 contiguous bytes.  Dword u of the lane feeds
+//     MFMA u: K values 32 q + 8 u + 0..7 of the pair, so lanes q = 0, 1
+//     carry the pair's first group and q = 2, 3 its second.
+//   * A row i of tile mt = (virtual row v = 8 mt + i / 2, half p = i % 2),
+//     v = m SW + s': x[m] over the pair of segment s' in the K slots of the
+//     lanes q with q / 2 == p, zero elsewhere.  D[i, c] with s' == s is the
+//     dot product of activation row m with weight row r over group 2 jj + p
+//     alone; the other blocks are never read.  2 M SW <= 16 MT.
+//   * fp16: B = code - zero exactly (1024 + n' and 64 + n' magic numbers,
+//     one v_pk_add_f16 per pair of values subtracting 1032 + z / 72 + z);
+//     bf16: B = 136 + code exactly, and the group result is corrected by
+//     -(136 + zero) * sum_g x[m] (group sums formed once at staging).  The
+//     group scale then multiplies in fp32.
+//   * The activation range of the workgroup is staged once in LDS in MFMA
+//     slot order.  Every wave first issues its share of the staging loads;
+//     a barrier that waits for no memory keeps every weight load behind
+//     every staging load (a CU returns vector memory data in issue order),
+//     then each wave issues the loads of its first PF chunks (weights, the
+//     row's two group scales, the zero byte), stages, and meets the others
+//     at a barrier over LDS alone.
+//   * Steps: each chunk waits for its own three loads alone, runs its
+//     MFMAs and scaling, and issues the loads of the chunk PF chunks ahead,
+//     so PF KB per wave stay in flight until the wave's last chunks.
+//   * A wave owns RBW row blocks (interleaved with the other WR wave rows)
+//     over its K part of SW T pairs; WK waves split the workgroup's K range
+//     and meet in LDS at the end; K splits across workgroups (grid y) store
+//     fp32 partial sums for the split-reduce kernel.
+#include <stdio.h>
+
+#include "w4g64_device.h"
+#include "w4g64_internal.h"
+
+namespace w4g64 {
+namespace {
+
+typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
+
+struct PipeArgs {
+    const void* x;
+    const uint8_t* qweight;
+    const uint16_t* scales;
+    const uint8_t* zeros;
+    const void* bias;
+    void* y;
+    float* partials;  // [splits][M][N] (grid y > 1 or unreduced output)
+    int bias_kind;
+    int M;   // activation rows
+    int N;   // out_features
+    int K;   // in_features (a multiple of 128)
+    int G;   // groups
+    int P;   // group pairs
+    int PS;  // pairs per K split
+    W4G64_TIMELINE_FIELDS
+};
+
+// LDS layout (bytes): xs [M][PS 128 + 8] slot-ordered activations | 64 zero
+// bytes | sx [M][2 PS] fp32 group sums (bf16) | red (epilogue partial sums).
+struct PipeLayout {
+    int xw, zero, sx, red, total;
+};
+__host__ __device__ inline PipeLayout pipe_layout(int M, int PS, int red_floats) {
+    PipeLayout L;
+    L.xw = PS * 128 + 8;  // 16-bit elements per staged row (16 B of padding)
+    L.zero = M * L.xw * 2;
+    L.sx = L.zero + 64;
+    L.red = L.sx + M * 2 * PS * 4;
+    L.total = L.red + red_floats * 4;
+    return L;
+}
+
+// Floats of the epilogue's reduction area: one K part per workgroup and
+// several segments -- a private [RBW][M][R][SW] area per wave (no
+// workgroup barrier); several K parts -- [WK][M][rows][SW] shared by the
+// workgroup; one K part and one segment -- none (every lane stores its own).
+__host__ __device__ constexpr int pipe_red_floats(int M, int SW, int WR, int WK, int RBW) {
+    return WK == 1 ? (SW == 1 ? 0 : WR * RBW * M * (16 / SW) * SW) : WK * M * (WR * RBW * (16 / SW)) * SW;
+}
+
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+__device__ __forceinline__ float sum8_lanes(float s) {
+    s += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, s), 0xB1, 0xF, 0xF, false));
+    s += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, s), 0x4E, 0xF, 0xF, false));
+    s += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, s), 0x141, 0xF, 0xF, false));
+    return s;
+}
+
+// ((w ^ 0x88888888) & mask) | magic in one v_bitop3_b32 with truth table
+// 0x9A over (w, b, c): bits with (b, c) = (0, 0) pass w, (0, 1) pass ~w,
+// (1, 0) give 0 and (1, 1) give 1, so b = ~mask and c = (mask & 0x88888888)
+// | (~mask & magic).  (clang exposes no builtin for the instruction.)
+__device__ __forceinline__ uint32_t bitop3_9a(uint32_t w, uint32_t b, uint32_t c) {
+    uint32_t r;
+    asm("v_bitop3_b32 %0, %1, %2, %3 bitop3:0x9a" : "=v"(r) : "v"(w), "s"(b), "v"(c));
+    return r;
+}
+constexpr uint32_t kLoB = 0xFFF0FFF0u;     // ~0x000F000F
+constexpr uint32_t kHiB = 0xFF0FFF0Fu;     // ~0x00F000F0
+constexpr uint32_t kF16LoC = 0x64086408u;  // magic 1024 (fp16) with the sign flip of nibble bit 3
+constexpr uint32_t kF16HiC = 0x54805480u;  // magic 64 (fp16), nibble in bits 4-7
+constexpr uint32_t kBF16C = 0x43084308u;   // magic 128 (bf16)
+
+// Exact (code - zero) of one packed dword as fp16 in slot order [k0 k4 k1 k5
+// k2 k6 k3 k7]: 1024 + n' and 64 + n' (n' = code + 8) minus 1032 + z and
+// 72 + z, whose fp16 bits are 0x6408 + z and 0x5480 + 16 z (ulps 1 and 1/16).
+__device__ __forceinline__ half8 codes8_f16(uint32_t w, uint32_t clo, uint32_t chi) {
+    const uint32_t w8 = w >> 8;
+    const half2v c_lo = __builtin_bit_cast(half2v, clo), c_hi = __builtin_bit_cast(half2v, chi);
+    const half2v h0 = __builtin_bit_cast(half2v, bitop3_9a(w, kLoB, kF16LoC)) - c_lo;
+    const half2v h1 = __builtin_bit_cast(half2v, bitop3_9a(w, kHiB, kF16HiC)) - c_hi;
+    const half2v h2 = __builtin_bit_cast(half2v, bitop3_9a(w8, kLoB, kF16LoC)) - c_lo;
+    const half2v h3 = __builtin_bit_cast(half2v, bitop3_9a(w8, kHiB, kF16HiC)) - c_hi;
+    half8 v = {h0[0], h0[1], h1[0], h1[1], h2[0], h2[1], h3[0], h3[1]};
+    return v;
+}
+
+// bf16 values 128 + n' = 136 + code (exact), slot order.
+__device__ __forceinline__ bf16x8 codes8_bf16_biased(uint32_t w) {
+    u32x4 v;
+    v[0] = bitop3_9a(w, kLoB, kBF16C);
+    v[1] = bitop3_9a(w >> 4, kLoB, kBF16C);
+    v[2] = bitop3_9a(w >> 8, kLoB, kBF16C);
+    v[3] = bitop3_9a(w >> 12, kLoB, kBF16C);
+    return __builtin_bit_cast(bf16x8, v);
+}
+
+// A 16-bit load's bits, zero-extended where this statement stands.  The
+// load is typed _Float16, which lives in a 32-bit register with undefined
+// upper bits, so its raw register goes straight into the volatile asm: the
+// compiler inserts no zero extension of its own, which it would schedule
+// early (waiting for the load there), and cannot move this one across the
+// other ordering statements.
+__device__ __forceinline__ uint32_t take_u16(_Float16 raw) {
+    uint32_t r;
+    asm volatile("v_and_b32 %0, 0xffff, %1" : "=v"(r) : "v"(raw));
+    return r;
+}
+
+template <int XK, int SW, int MT, int WR, int WK, int RBW, int T, int DP, int STG>
+__global__ __launch_bounds__(WR * WK * 64) void gemv_pipe_kernel(PipeArgs a) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    constexpr int W = WR * WK;
+    constexpr int kThreads = W * 64;
+    constexpr int R = 16 / SW;          // rows per wave row block
+    constexpr int RWG = WR * RBW * R;   // rows per workgroup
+    constexpr int C = T * RBW;          // chunks per wave
+    constexpr int PF = DP * RBW < C ? DP * RBW : C;  // chunks in flight
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wr = wave % WR;
+    const int wk = wave / WR;
+    const int M = a.M, N = a.N, K = a.K, G = a.G, P = a.P;
+    const int p0 = blockIdx.y * a.PS;        // first pair of the workgroup's K range
+    const int pe = min(p0 + a.PS, P);        // end of its range
+    const int ps = pe - p0;                  // pairs staged (>= 1)
+    const int row0 = blockIdx.x * RWG;
+    const PipeLayout L = pipe_layout(M, a.PS, pipe_red_floats(M, SW, WR, WK, RBW));
+    W4G64_TIMELINE_DECL;
+    W4G64_STAMP(0);
+
+    // ---- lane roles ----
+    const int c = lane & 15;
+    const int q = lane >> 4;
+    const int r = c / SW;
+    const int s = c % SW;
+    const int pb = p0 + wk * SW * T;  // this wave's first pair
+    // the rows a thread stores: with one K part per workgroup, lane l stores
+    // rows (b WR + wr) R + l % R of its row blocks b; otherwise thread t
+    // stores row t % RWG of the workgroup (kThreads % RWG == 0)
+    constexpr bool kWaveLocal = WK == 1;
+    constexpr int NB = kWaveLocal ? RBW : 1;
+    static_assert(kWaveLocal || kThreads % RWG == 0, "a thread's outputs share its row");
+
+    // ---- 0. bias of the stored outputs (raw bits, decoded at the stores) ----
+    // one load whatever the kind (from the scales when there is no bias)
+    // (fp32: the two halves of the element as two short loads)
+    _Float16 bias_lo[NB], bias_hi[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        int brow = kWaveLocal ? row0 + (b * WR + wr) * R + lane % R : row0 + tid % RWG;
+        brow = min(brow, N - 1);
+        const _Float16* bp = (const _Float16*)(a.bias_kind == 0 ? (const void*)a.scales : a.bias);
+        const int e = a.bias_kind == kF32 ? 2 * brow : (a.bias_kind == 0 ? 0 : brow);
+        bias_lo[b] = bp[e];
+        bias_hi[b] = bp[a.bias_kind == kF32 ? e + 1 : e];
+    }
+    auto bias_of = [&](int b) {
+        const uint32_t lo = take_u16(bias_lo[b]);
+        if (a.bias_kind == kF32) return __builtin_bit_cast(float, lo | (take_u16(bias_hi[b]) << 16));
+        if (a.bias_kind == kF16) return half_bits_to_float((uint16_t)lo);
+        if (a.bias_kind == kBF16) return bf16_bits_to_float(lo);
+        return 0.0f;
+    };
+
+    // ---- 1. staging loads: item it = 8 activation values of row m ----
+    const int per_row = ps * 16;
+    const int items = M * per_row;
+    u32x4 xv[STG];
+    int xit[STG];
+#pragma unroll
+    for (int u = 0; u < STG; ++u) {
+        int it = kThreads * u + tid;
+        it = it < items ? it : items - 1;
+        xit[u] = it;
+        const int m = it / per_row;
+        const int k8 = it - m * per_row;
+        xv[u] = *(const u32x4*)((const uint16_t*)a.x + (int64_t)m * K + (int64_t)p0 * 128 + 8 * k8);
+    }
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();  // every wave's staging loads issue before any weight load
+    asm volatile("" ::: "memory");
+
+    // ---- 2. the first PF chunks' loads ----
+    // chunk i = t RBW + b: row block b, step t; pairs past the range re-read
+    // the range's first pair and get a zero scale
+    const uint8_t* wbase[RBW];
+    const uint16_t* sbase[RBW];
+    const uint8_t* zbase[RBW];  // P is even, so a zero byte's parity is its pair's
+#pragma unroll
+    for (int b = 0; b < RBW; ++b) {
+        const int row = min(row0 + (b * WR + wr) * R + r, N - 1);
+        wbase[b] = a.qweight + (int64_t)row * (K / 2) + 16 * q;
+        sbase[b] = a.scales + (int64_t)row * G;
+        zbase[b] = a.zeros + (int64_t)row * P;
+    }
+    u32x4 wbuf[PF];
+    uint32_t sbuf[PF];
+    _Float16 zbuf[PF];  // the aligned 16 bits holding the zero byte (raw)
+    auto issue = [&](int i) {
+        const int t = i / RBW, b = i % RBW;
+        const int jj = pb + s + SW * t;
+        const int jl = jj < pe ? jj : p0;
+        wbuf[i % PF] = __builtin_nontemporal_load((const u32x4*)(wbase[b] + 64 * (int64_t)jl));
+        sbuf[i % PF] = *(const uint32_t*)(sbase[b] + 2 * jl);
+        zbuf[i % PF] = *(const _Float16*)(zbase[b] + (jl & ~1));
+        asm volatile("" ::: "memory");
+    };
+#pragma unroll
+    for (int i = 0; i < PF; ++i) issue(i);
+#pragma unroll
+    for (int u = 0; u < STG; ++u) asm volatile("" : "+v"(xv[u]));
+    W4G64_STAMP(1);
+
+    // ---- 3. staging into LDS (slot order) with the bf16 group sums ----
+    {
+        float* sx = (float*)(smem + L.sx);
+#pragma unroll
+        for (int u = 0; u < STG; ++u) {
+            const int it = xit[u];
+            const int m = it / per_row;
+            const int k8 = it - m * per_row;
+            *(u32x4*)(smem + 2 * (m * L.xw + 8 * k8)) = permute_slots(xv[u]);
+            if constexpr (XK == kBF16) {
+                float sum = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    sum += __builtin_bit_cast(float, xv[u][e] << 16) + __builtin_bit_cast(float, xv[u][e] & 0xFFFF0000u);
+                sum = sum8_lanes(sum);  // the 8 items of one (row, group) sit in 8 aligned lanes
+                if ((it & 7) == 0) sx[m * 2 * a.PS + (k8 >> 3)] = sum;
+            }
+        }
+        if (tid < 16) ((uint32_t*)(smem + L.zero))[tid] = 0u;
+    }
+    lds_barrier();
+    W4G64_STAMP(2);
+
+    // ---- 4. steps ----
+    // A row of this lane in tile mt: i = lane % 16 -> v = 8 mt + i / 2, half
+    // p = i % 2; it reads x only for m < M and q / 2 == p.
+    const int ai = lane & 15;
+    const int ap = ai & 1;
+    int am[MT], as_[MT];
+    bool alive0[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        const int v = 8 * mt + (ai >> 1);
+        am[mt] = v / SW;
+        as_[mt] = v % SW;
+        alive0[mt] = am[mt] < M && (q >> 1) == ap;
+    }
+    // D rows of this lane: i = 4 q + r' -> v = 8 mt + 2 q + r' / 2, p = r' % 2
+    const float* sxl = (const float*)(smem + L.sx);
+    const unsigned char* xs = smem;
+    float4v acc[MT][RBW];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int b = 0; b < RBW; ++b) acc[mt][b] = float4v{0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+        // this step's A fragments (shared by the RBW row blocks)
+        u16x8 av[MT][4];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            const int ja = pb + as_[mt] + SW * t;
+            const bool alive = alive0[mt] && ja < pe;
+            // (dead lanes read the 64 zero bytes)
+            const unsigned char* asrc =
+                alive ? xs + 2 * (am[mt] * L.xw + (ja - p0) * 128 + 32 * q) : smem + L.zero;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) av[mt][u] = *(const u16x8*)(asrc + 16 * u);
+        }
+        // bf16 group sums of the D rows' (m, pair) (clamped into the staged range)
+        float2v gsum[MT][2];
+        if constexpr (XK == kBF16) {
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const int v = 8 * mt + 2 * q + h;
+                    const int m = min(v / SW, M - 1);
+                    const int jp = min(pb + (v % SW) + SW * t - p0, ps - 1);
+                    gsum[mt][h] = *(const float2v*)(sxl + m * 2 * a.PS + 2 * jp);
+                }
+        }
+        const int jj = pb + s + SW * t;  // this lane's pair (column side)
+#pragma unroll
+        for (int b = 0; b < RBW; ++b) {
+            const int i = t * RBW + b;
+            u32x4 w = wbuf[i % PF];
+            uint32_t sw2 = sbuf[i % PF];
+            asm volatile("" : "+v"(w), "+v"(sw2));  // this chunk's loads land here
+            const uint32_t zb = take_u16(zbuf[i % PF]);
+            const int zoff = 8 * ((jj < pe ? jj : p0) & 1);  // the zero byte's half
+            // a pair past the range re-reads an in-range pair and has zero A
+            // fragments, so it adds 0; bf16 also zeroes its scale, as its
+            // group correction (an in-range group's sum) is not zero
+            const bool live = XK == kF16 || jj < pe;
+            const float s0 = live ? half_bits_to_float((uint16_t)(sw2 & 0xFFFFu)) : 0.0f;
+            const float s1 = live ? half_bits_to_float((uint16_t)(sw2 >> 16)) : 0.0f;
+            float4v d[MT];
+            if constexpr (XK == kF16) {
+                // the zero point of this lane's own group (q / 2)
+                const int zl = (int)__builtin_amdgcn_sbfe((int)zb, zoff + 4 * (q >> 1), 4);
+                const uint32_t clo = (uint32_t)(0x6408 + zl) * 0x00010001u;
+                const uint32_t chi = (uint32_t)(0x5480 + 16 * zl) * 0x00010001u;
+                half8 bv[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) bv[u] = codes8_f16(w[u], clo, chi);
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    d[mt] = float4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int u = 0; u < 4; ++u)
+                        d[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, av[mt][u]), bv[u],
+                                                                       d[mt], 0, 0, 0);
+                }
+            } else {
+                bf16x8 bv[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) bv[u] = codes8_bf16_biased(w[u]);
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    d[mt] = float4v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int u = 0; u < 4; ++u)
+                        d[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, av[mt][u]), bv[u],
+                                                                        d[mt], 0, 0, 0);
+                }
+                const float c0 = 136.0f + (float)(int)__builtin_amdgcn_sbfe((int)zb, zoff, 4);  // (the builtin is unsigned)
+                const float c1 = 136.0f + (float)(int)__builtin_amdgcn_sbfe((int)zb, zoff + 4, 4);
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        d[mt][2 * h] = fmaf(-c0, gsum[mt][h][0], d[mt][2 * h]);
+                        d[mt][2 * h + 1] = fmaf(-c1, gsum[mt][h][1], d[mt][2 * h + 1]);
+                    }
+            }
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    acc[mt][b][2 * h] = fmaf(s0, d[mt][2 * h], acc[mt][b][2 * h]);
+                    acc[mt][b][2 * h + 1] = fmaf(s1, d[mt][2 * h + 1], acc[mt][b][2 * h + 1]);
+                }
+            asm volatile("" ::: "memory");
+            if (i + PF < C) issue(i + PF);
+        }
+    }
+    W4G64_STAMP(3);
+
+    // ---- 5. outputs ----
+    const bool split_out = a.partials != nullptr;
+    auto emit = [&](int m, int n, float v, int b) {
+        if (split_out) a.partials[((int64_t)blockIdx.y * M + m) * N + n] = v;
+        else store_out<XK>(a.y, (int64_t)m * N + n, v + bias_of(b));
+    };
+    if constexpr (kWaveLocal && SW == 1) {
+        // lane (q, c): rows v = 8 mt + 2 q + h of D are activation rows m = v
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int b = 0; b < RBW; ++b)
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const int m = 8 * mt + 2 * q + h;
+                    const int n = row0 + (b * WR + wr) * R + r;
+                    if (m < M && n < N) emit(m, n, acc[mt][b][2 * h] + acc[mt][b][2 * h + 1], b);
+                }
+    } else if constexpr (kWaveLocal) {
+        // the segments of a row meet in a private area of the wave: no
+        // workgroup barrier, only the wave's own LDS order
+        float* red = (float*)(smem + L.red) + wave * (RBW * M * R * SW);  // [RBW][M][R][SW]
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int b = 0; b < RBW; ++b)
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const int v = 8 * mt + 2 * q + h;
+                    const int m = v / SW;
+                    if ((v % SW) == s && m < M)
+                        red[((b * M + m) * R + r) * SW + s] = acc[mt][b][2 * h] + acc[mt][b][2 * h + 1];
+                }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+#pragma unroll
+        for (int b = 0; b < RBW; ++b)
+            for (int o = lane; o < M * R; o += 64) {  // 64 % R == 0: row r = lane % R
+                const int m = o / R, rr = o % R;
+                const int n = row0 + (b * WR + wr) * R + rr;
+                if (n < N) {
+                    float v = 0.0f;
+#pragma unroll
+                    for (int s2 = 0; s2 < SW; ++s2) v += red[((b * M + m) * R + rr) * SW + s2];
+                    emit(m, n, v, b);
+                }
+            }
+    } else {
+        float* red = (float*)(smem + L.red);  // [WK][M][RWG][SW]
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int b = 0; b < RBW; ++b)
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const int v = 8 * mt + 2 * q + h;
+                    const int m = v / SW;
+                    if ((v % SW) == s && m < M) {
+                        const int wrow = (b * WR + wr) * R + r;
+                        red[((wk * M + m) * RWG + wrow) * SW + s] = acc[mt][b][2 * h] + acc[mt][b][2 * h + 1];
+                    }
+                }
+        lds_barrier();
+        for (int o = tid; o < M * RWG; o += kThreads) {
+            const int m = o / RWG, wrow = o % RWG;
+            const int n = row0 + wrow;
+            if (n < N) {
+                float v = 0.0f;
+#pragma unroll
+                for (int k2 = 0; k2 < WK; ++k2)
+#pragma unroll
+                    for (int s2 = 0; s2 < SW; ++s2) v += red[((k2 * M + m) * RWG + wrow) * SW + s2];
+                emit(m, n, v, 0);
+            }
+        }
+    }
+    W4G64_STAMP(4);
+    W4G64_TIMELINE_STORE(a);
+}
+
+// ---- instantiations ----
+// (SW, MT, WR, WK, RBW, T, DP, STG): the shapes the planner produces.
+#define W4G64_PIPE_SHAPES(X)   \
+    X(8, 1, 8, 1, 1, 9, 3, 3)  \
+    X(8, 1, 4, 1, 1, 9, 5, 5)  \
+    X(4, 1, 4, 1, 2, 3, 3, 1)  \
+    X(4, 1, 1, 3, 1, 1, 1, 1)  \
+    X(4, 1, 4, 1, 1, 3, 3, 1)  \
+    X(2, 1, 2, 7, 1, 1, 1, 1)  \
+    X(2, 1, 4, 1, 2, 6, 3, 3)  \
+    X(2, 1, 2, 2, 1, 3, 3, 3)  \
+    X(1, 1, 1, 7, 1, 2, 2, 4)  \
+    X(1, 1, 1, 4, 1, 3, 3, 6)  \
+    X(1, 2, 2, 7, 1, 2, 2, 4)  \
+    X(1, 2, 4, 2, 1, 6, 3, 6)  \
+    X(1, 2, 1, 12, 1, 1, 1, 4)
+
+typedef void (*PipeKernel)(PipeArgs);
+struct PipeEntry {
+    int sw, mt, wr, wk, rbw, t, dp, stg;
+    PipeKernel f16, bf16;
+};
+
+#define W4G64_PIPE_ENTRY(SW, MT, WR, WK, RBW, T, DP, STG)                              \
+    {SW, MT, WR, WK, RBW, T, DP, STG, gemv_pipe_kernel<kF16, SW, MT, WR, WK, RBW, T, DP, STG>, \
+     gemv_pipe_kernel<kBF16, SW, MT, WR, WK, RBW, T, DP, STG>},
+
+const PipeEntry kPipeTable[] = {
+    W4G64_PIPE_SHAPES(W4G64_PIPE_ENTRY)
+#ifdef W4G64_PIPE_EXTRA_SHAPES  // tuning builds: more shapes, fp16 only
+#define W4G64_PIPE_ENTRY_F16(SW, MT, WR, WK, RBW, T, DP, STG) \
+    {SW, MT, WR, WK, RBW, T, DP, STG, gemv_pipe_kernel<kF16, SW, MT, WR, WK, RBW, T, DP, STG>, nullptr},
+    W4G64_PIPE_EXTRA_SHAPES(W4G64_PIPE_ENTRY_F16)
+#endif
+};
+
+const PipeEntry* find_pipe(const GemvPlan& plan) {
+    for (const PipeEntry& e : kPipeTable)
+        if (e.sw == plan.segments && e.mt == plan.tiles && e.wr == plan.fblocks && e.wk == plan.kparts &&
+            e.rbw == plan.rbw && e.t == plan.steps && e.dp == plan.depth && e.stg == plan.stage)
+            return &e;
+    return nullptr;
+}
+
+}  // namespace
+
+constexpr int64_t kPipeMaxLds = 160 * 1024;  // gfx950: the whole LDS of a CU per workgroup
+
+// Fills the derived fields of a pipelined plan (tiles, blocks, splits, LDS,
+// workspace, staging loads) from its shape; false if it does not fit.
+bool finish_pipe_plan(int64_t rows, int64_t out_features, int64_t in_features, GemvPlan& plan) {
+    const int64_t P = in_features / 128;
+    const int sw = plan.segments, wr = plan.fblocks, wk = plan.kparts, rbw = plan.rbw, t = plan.steps;
+    if (rows < 1 || rows > kGemvMaxRows || in_features % 128 || sw < 1 || 16 % sw) return false;
+    if (2 * rows * sw > 16 * plan.tiles) return false;
+    const int64_t span = (int64_t)wk * sw * t;  // pairs per workgroup K range
+    const int64_t splits = (P + span - 1) / span;
+    plan.splits = (int)splits;
+    plan.groups_per_split = (int)span;  // pairs per split (PS)
+    const int64_t rwg = (int64_t)wr * rbw * (16 / sw);
+    plan.n_blocks = (int)((out_features + rwg - 1) / rwg);
+    const int64_t items = rows * (span < P ? span : P) * 16;
+    const int64_t threads = (int64_t)wr * wk * 64;
+    if (items > (int64_t)plan.stage * threads) return false;
+    const int red = pipe_red_floats((int)rows, sw, wr, wk, rbw);
+    plan.lds_bytes = pipe_layout((int)rows, (int)span, red).total;
+    if (plan.lds_bytes > kPipeMaxLds) return false;
+    plan.workspace_bytes = splits > 1 ? splits * rows * out_features * 4 : 0;
+    plan.kind = 4;
+    return true;
+}
+
+// Launch shapes by rows, pairs (K / 128) and out_features, first match
+// first: (SW, MT, WR, WK, RBW, T, DP); the staging loads per lane are the
+// smallest instantiated count that fits.  Chosen from forced-shape sweeps
+// over cold weights, graph-replayed (decode calls) and one launch over a
+// 28-layer stack (steady state): one row, gate 8960x1536 4.3 us, down
+// 1536x8960 4.6 us, the stacked gate|up 5.7 TB/s and down 4.5 TB/s; 16
+// rows, gate 6.4 us, down 8.5 us (five K splits and the reduction).  A K
+// range longer than a shape's span is split across workgroups.
+struct PipeShape {
+    int min_rows, max_rows;
+    int64_t min_pairs, max_pairs;
+    int64_t min_n, max_n;
+    int sw, mt, wr, wk, rbw, t, dp;
+};
+constexpr int64_t kAnyN = int64_t(1) << 40;
+const PipeShape kPipeShapes[] = {
+    // one row: long K (span 72)
+    {1, 1, 48, 1 << 20, 32768, kAnyN, 8, 1, 8, 1, 1, 9, 3},
+    {1, 1, 48, 1 << 20, 1, kAnyN, 8, 1, 4, 1, 1, 9, 5},
+    // one row: span 12
+    {1, 1, 1, 47, 32768, kAnyN, 4, 1, 4, 1, 2, 3, 3},
+    {1, 1, 1, 47, 1, 512, 4, 1, 1, 3, 1, 1, 1},
+    {1, 1, 1, 47, 1, kAnyN, 4, 1, 4, 1, 1, 3, 3},
+    // 2..4 rows
+    {2, 4, 48, 1 << 20, 1, kAnyN, 2, 1, 2, 7, 1, 1, 1},
+    {2, 4, 1, 47, 32768, kAnyN, 2, 1, 4, 1, 2, 6, 3},
+    {2, 4, 1, 47, 1, kAnyN, 2, 1, 2, 2, 1, 3, 3},
+    // 5..8 rows
+    {5, 8, 48, 1 << 20, 1, kAnyN, 1, 1, 1, 7, 1, 2, 2},
+    {5, 8, 1, 47, 1, kAnyN, 1, 1, 1, 4, 1, 3, 3},
+    // 9..16 rows
+    {9, 16, 48, 1 << 20, 1, kAnyN, 1, 2, 2, 7, 1, 2, 2},
+    {9, 16, 1, 47, 4096, kAnyN, 1, 2, 4, 2, 1, 6, 3},
+    {9, 16, 1, 47, 1, kAnyN, 1, 2, 1, 12, 1, 1, 1},
+};
+
+bool plan_pipe(int64_t rows, int64_t out_features, int64_t in_features, int x_kind, GemvPlan& plan) {
+    if ((x_kind != kF16 && x_kind != kBF16) || in_features % 128 || rows < 1 || rows > kGemvMaxRows) return false;
+    const int64_t P = in_features / 128;
+    for (const PipeShape& sh : kPipeShapes) {
+        if (rows < sh.min_rows || rows > sh.max_rows || P < sh.min_pairs || P > sh.max_pairs ||
+            out_features < sh.min_n || out_features > sh.max_n)
+            continue;
+        const PipeEntry* best = nullptr;
+        for (const PipeEntry& e : kPipeTable) {
+            if (e.sw != sh.sw || e.mt != sh.mt || e.wr != sh.wr || e.wk != sh.wk || e.rbw != sh.rbw || e.t != sh.t ||
+                e.dp != sh.dp || !e.bf16)
+                continue;
+            GemvPlan cand{};
+            cand.segments = e.sw;
+            cand.tiles = e.mt;
+            cand.fblocks = e.wr;
+            cand.kparts = e.wk;
+            cand.rbw = e.rbw;
+            cand.steps = e.t;
+            cand.depth = e.dp;
+            cand.stage = e.stg;
+            if (finish_pipe_plan(rows, out_features, in_features, cand) && (!best || e.stg < best->stg)) {
+                best = &e;
+                plan = cand;
+            }
+        }
+        if (best) return true;
+    }
+    return false;
+}
+
+bool pipe_supported(const LinearProblem& p) {
+    // zero bytes are read as the aligned 16-bit words holding them: with an
+    // even pair count per row (in_features a multiple of 256) every row's
+    // bytes start at an even index, and no word reaches past its row
+    return (p.x_kind == kF16 || p.x_kind == kBF16) && p.in_features % 256 == 0 && ((uintptr_t)p.qweight % 16) == 0 &&
+           ((uintptr_t)p.x % 16) == 0 && ((uintptr_t)p.scales % 4) == 0 && ((uintptr_t)p.zeros % 2) == 0 &&
+           !p.paired && p.norm_delta == nullptr;
+}
+
+bool pipe_plan_launchable(const GemvPlan& plan) { return find_pipe(plan) != nullptr; }
+
+hipError_t launch_gemv_pipe(const LinearProblem& p, const GemvPlan& plan, void* workspace, hipStream_t stream,
+                            hipEvent_t start, hipEvent_t stop) {
+    const PipeEntry* e = find_pipe(plan);
+    if (!e || plan.kind != 4) return hipErrorInvalidValue;
+    PipeArgs a{};
+    a.x = p.x;
+    a.qweight = p.qweight;
+    a.scales = p.scales;
+    a.zeros = p.zeros;
+    a.bias = p.bias;
+    a.bias_kind = p.bias_kind;
+    a.y = p.y;
+    a.M = (int)p.rows;
+    a.N = (int)p.out_features;
+    a.K = (int)p.in_features;
+    a.G = a.K / 64;
+    a.P = a.G / 2;
+    a.PS = plan.groups_per_split;
+    W4G64_TIMELINE_SET(a);
+    const bool unreduced = p.partials_out != nullptr;
+    const bool split = plan.splits > 1 && !unreduced;
+    a.partials = unreduced ? p.partials_out : (plan.splits > 1 ? (float*)workspace : nullptr);
+    if (plan.splits > 1 && !a.partials) return hipErrorInvalidValue;
+    PipeKernel k = p.x_kind == kF16 ? e->f16 : e->bf16;
+    if (!k) return hipErrorInvalidValue;
+    const dim3 grid(plan.n_blocks, plan.splits), block(plan.fblocks * plan.kparts * 64);
+    hipError_t err = launch_kernel(k, grid, block, (size_t)plan.lds_bytes, stream, start, split ? nullptr : stop, a);
+    if (err != hipSuccess || !split) return err;
+    return launch_split_reduce(a.partials, p.bias, p.bias_kind, p.y, a.M, a.N, plan.splits, false, p.x_kind, stream,
+                               stop);
+}
+
+}  // namespace w4g64

@@ -51,7 +51,9 @@ struct GemvPlan {
     int groups_per_split;  // 64-wide K groups per split
     int tiles;             // 16-row MFMA A tiles (fp32 input uses 3 bf16 parts per row)
     int kparts = 1;        // kind 2: K parts per workgroup (its waves split K)
-    int stage = 1;         // kind 2: staging loads per lane
+    int stage = 1;         // kind 2, 4: staging loads per lane
+    int rbw = 1;           // kind 4: row blocks per wave
+    int depth = 1;         // kind 4: steps of loads kept in flight
     int64_t lds_bytes;     // dynamic LDS per workgroup
     int64_t workspace_bytes;
 };
@@ -94,6 +96,20 @@ hipError_t launch_gemv_seg(const LinearProblem& p, const GemvPlan& plan, hipStre
 // in_features a multiple of 128 up to 1536, 16-byte aligned weights.
 bool plan_seg_norm_planes(const LinearProblem& p, GemvPlan& plan);
 hipError_t launch_gemv_seg_norm_planes(const LinearProblem& p, const GemvPlan& plan, hipStream_t stream);
+
+// Pipelined decode GEMV (plan.kind = 4; 1..16 fp16/bf16 rows, in_features a
+// multiple of 128): segments, tiles (A tiles), fblocks (wave rows), kparts
+// (K parts per workgroup), rbw (row blocks per wave), steps (pair steps per
+// wave), depth (steps in flight) and stage (staging loads per lane) select
+// the kernel; finish_pipe_plan fills in the grid, K splits, LDS and
+// workspace.  K splits store fp32 partial sums reduced by the split-reduce
+// kernel (or, with partials_out, left to the caller).
+bool finish_pipe_plan(int64_t rows, int64_t out_features, int64_t in_features, GemvPlan& plan);
+bool plan_pipe(int64_t rows, int64_t out_features, int64_t in_features, int x_kind, GemvPlan& plan);
+bool pipe_supported(const LinearProblem& p);
+bool pipe_plan_launchable(const GemvPlan& plan);
+hipError_t launch_gemv_pipe(const LinearProblem& p, const GemvPlan& plan, void* workspace, hipStream_t stream,
+                            hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
 
 // Prefill GEMM (rows > 16): a staging kernel writes the activations as fp16
 // rows (scaled by a power of two per row; fp32-class kinds as hi|lo planes)

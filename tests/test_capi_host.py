@@ -294,19 +294,28 @@ def test_workspace_and_kernel_plan_queries():
     assert 512 * 8960 * 4 + 512 * 4 <= ws32 <= (64 << 20) + 512 * 8960 * 4 + 512 * 4 + 512
     assert lib.w4g64_linear_kernel_name(512, 1536, 8960, _lib.DTYPE_F32).startswith(b"gemm_kernel<")
     assert lib.w4g64_linear_workspace_bytes(1, 1536, 100, _lib.DTYPE_F16) == 0
-    # one row of even-group shapes with at most three 16-byte weight loads per
-    # lane: the lean kernel (no workspace)
-    assert lib.w4g64_linear_kernel_name(1, 8960, 1536, _lib.DTYPE_F16) == b"gemv_seg_kernel<f16,4,4,1,3>"
-    assert lib.w4g64_linear_kernel_name(1, 1536, 1536, _lib.DTYPE_BF16) == b"gemv_seg_kernel<bf16,4,1,4,1>"
+    # fp16 / bf16 decode rows with in_features a multiple of 256: the pipelined
+    # GEMV, its launch shape by rows, K and out_features (no workspace unless
+    # K is split across workgroups)
+    assert lib.w4g64_linear_kernel_name(1, 8960, 1536, _lib.DTYPE_F16) == b"gemv_pipe_kernel<f16,4,1,4,1,1,3,3>"
+    assert lib.w4g64_linear_kernel_name(1, 1536, 1536, _lib.DTYPE_BF16) == b"gemv_pipe_kernel<bf16,4,1,4,1,1,3,3>"
+    assert lib.w4g64_linear_kernel_name(1, 256, 1536, _lib.DTYPE_F16) == b"gemv_pipe_kernel<f16,4,1,1,3,1,1,1>"
+    assert lib.w4g64_linear_kernel_name(1, 501760, 1536, _lib.DTYPE_F16) == b"gemv_pipe_kernel<f16,4,1,4,1,2,3,3>"
     assert lib.w4g64_linear_workspace_bytes(1, 8960, 1536, _lib.DTYPE_F16) == 0
-    # odd group counts, the long-K down projection and several rows keep the segmented kernel
+    assert lib.w4g64_linear_kernel_name(1, 1536, 8960, _lib.DTYPE_F16) == b"gemv_pipe_kernel<f16,8,1,4,1,1,9,5>"
+    assert lib.w4g64_linear_kernel_name(4, 1536, 1536, _lib.DTYPE_BF16) == b"gemv_pipe_kernel<bf16,2,1,2,2,1,3,3>"
+    assert lib.w4g64_linear_kernel_name(8, 1536, 8960, _lib.DTYPE_F16) == b"gemv_pipe_kernel<f16,1,1,1,7,1,2,2>"
+    assert lib.w4g64_linear_kernel_name(16, 1536, 8960, _lib.DTYPE_BF16) == b"gemv_pipe_kernel<bf16,1,2,2,7,1,2,2>"
+    assert lib.w4g64_linear_kernel_name(16, 8960, 1536, _lib.DTYPE_F16) == b"gemv_pipe_kernel<f16,1,2,4,2,1,6,3>"
+    assert lib.w4g64_linear_kernel_name(16, 1536, 1536, _lib.DTYPE_F16) == b"gemv_pipe_kernel<f16,1,2,1,12,1,1,1>"
+    # the down projection at 16 rows splits K in 5 (span 14 pairs): fp32 partial sums
+    assert lib.w4g64_linear_workspace_bytes(16, 1536, 8960, _lib.DTYPE_F16) >= 5 * 16 * 1536 * 4
+    # other K: one row of even-group shapes takes the lean kernel, the rest the
+    # segmented kernel (9..16 fp16/bf16 rows: the 16-row kernel)
+    assert lib.w4g64_linear_kernel_name(1, 256, 640, _lib.DTYPE_F16) == b"gemv_seg_kernel<f16,4,1,4,1>"
     assert lib.w4g64_linear_kernel_name(1, 64, 192, _lib.DTYPE_F16).startswith(b"gemv_kernel<f16")
-    assert lib.w4g64_linear_kernel_name(1, 1536, 8960, _lib.DTYPE_F16).startswith(b"gemv_kernel<f16")
-    assert lib.w4g64_linear_kernel_name(4, 1536, 1536, _lib.DTYPE_BF16).startswith(b"gemv_kernel<bf16")
-    assert lib.w4g64_linear_kernel_name(8, 1536, 8960, _lib.DTYPE_F16).startswith(b"gemv_kernel<f16")
-    assert lib.w4g64_linear_kernel_name(16, 1536, 8960, _lib.DTYPE_BF16) == b"gemv16_kernel<bf16,9,4,2>"
-    assert lib.w4g64_linear_kernel_name(16, 8960, 1536, _lib.DTYPE_F16) == b"gemv16_kernel<f16,6,4,3>"
-    assert lib.w4g64_linear_kernel_name(16, 1536, 1536, _lib.DTYPE_F16) == b"gemv16_kernel<f16,3,8,1>"
+    assert lib.w4g64_linear_kernel_name(4, 256, 640, _lib.DTYPE_BF16).startswith(b"gemv_kernel<bf16")
+    assert lib.w4g64_linear_kernel_name(16, 40, 9280, _lib.DTYPE_BF16).startswith(b"gemv16_kernel<bf16")
     assert lib.w4g64_linear_kernel_name(16, 1536, 8960, _lib.DTYPE_F32).startswith(b"gemv_kernel<f32")
     assert lib.w4g64_linear_kernel_name(2048, 8960, 1536, _lib.DTYPE_BF16).startswith(b"gemm_kernel<")
     assert lib.w4g64_linear_kernel_name(1, 8960, 1536, 8) == b"none"

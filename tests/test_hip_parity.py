@@ -182,23 +182,34 @@ def test_decode_all_qwen2_shapes_fp16(name, rows):
 
 
 LEAN_SHAPES = [(2048, 1536, "sym"), (17920, 1536, "asym"), (1536, 8960, "awq"), (200, 256, "asym"),
-                  (256, 1536, "sym")]
+                  (256, 1536, "sym"), (256, 640, "asym")]
+
+
+def decode_kernel_prefix(rows: int, k: int) -> str:
+    """The decode kernel the planner takes for fp16/bf16 activations with
+    16-byte aligned operands: the pipelined GEMV when in_features is a
+    multiple of 256, else the lean kernel for one row and the segmented /
+    9..16-row kernels for more."""
+    if k % 256 == 0:
+        return "gemv_pipe_kernel"
+    if rows == 1:
+        return "gemv_seg_kernel"
+    return "gemv16_kernel" if rows > 8 else "gemv_kernel"
 
 
 @pytest.mark.parametrize("dtype", ["fp16", "bf16"])
 @pytest.mark.parametrize("rows", [1, 2, 3, 5, 8])
 @pytest.mark.parametrize("n,k,kind", LEAN_SHAPES)
 def test_lean_decode_kernel(n, k, kind, rows, dtype):
-    """Decode shapes through the GEMV kernels: one row of the fused q|k|v and
-    gate|up widths, of a partial last row block (200 features) and of a
-    256-wide projection takes the lean kernel (16-byte weight loads, whole
-    rows per workgroup); the long-K down projection and several rows take the
-    segmented kernel.  Bias, asymmetric and AWQ-folded codes."""
+    """Decode shapes through the GEMV kernels: the fused q|k|v and gate|up
+    widths, the long-K down projection, a partial last row block (200
+    features) and a 256-wide projection take the pipelined kernel at 1..8
+    rows; K = 640 (an odd pair count) takes the lean kernel at one row and
+    the segmented kernel at more.  Bias, asymmetric and AWQ-folded codes."""
     from qwen_int4_hip import linear_kernel_name
 
     torch_dtype = torch.float16 if dtype == "fp16" else torch.bfloat16
-    lean = rows == 1 and k <= 1536
-    assert linear_kernel_name(rows, n, k, torch_dtype).startswith("gemv_seg_kernel" if lean else "gemv_kernel")
+    assert linear_kernel_name(rows, n, k, torch_dtype).startswith(decode_kernel_prefix(rows, k))
     q, s, z = weights(kind, n, k, O.BASE_SEED + n + k + rows)
     x = O.activations(rows, k, seed=O.BASE_SEED + 13 * rows + n, dtype=dtype, outliers=kind != "sym")
     bias = O.f32_to_bf16_bits(np.random.default_rng(n + rows).standard_normal(n).astype(np.float32) * np.float32(0.1))
@@ -210,15 +221,14 @@ def test_lean_decode_kernel(n, k, kind, rows, dtype):
 
 @pytest.mark.parametrize("name", ["gate_proj", "q_proj"])
 def test_lean_and_segmented_kernels_agree(name):
-    """The same problem through the lean kernel and, with a scales view that
-    is only 2-byte aligned (which the lean kernel does not take), through the
-    segmented kernel: both round fp32 values that differ only by summation
-    order (the lean kernel applies zero points after the MFMA), so they agree
-    within two fp16 ulps."""
+    """The same problem through the pipelined kernel and, with a scales view
+    that is only 2-byte aligned (which neither the pipelined nor the lean
+    kernel takes), through the segmented kernel: both round fp32 values that
+    differ only by summation order, so they agree within two fp16 ulps."""
     from qwen_int4_hip import linear_kernel_name
 
     n, k = SHAPES[name]
-    assert linear_kernel_name(1, n, k, torch.float16).startswith("gemv_seg_kernel")
+    assert linear_kernel_name(1, n, k, torch.float16).startswith("gemv_pipe_kernel")
     q, s, z = weights("asym", n, k, O.BASE_SEED + 5)
     xt = to_dev(O.activations(1, k, seed=O.BASE_SEED + 6, dtype="fp16"), "fp16")
     qd, sd, zd = dev_weights(q, s, z)
@@ -333,6 +343,31 @@ def test_lean_kernel_with_an_empty_k_part_ignores_lds_leftovers(dtype):
             check_linear(x, q, s, z, bias, n, 384, dtype)
 
 
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+@pytest.mark.parametrize("rows", [1, 3, 6, 12])
+@pytest.mark.parametrize("n,k", [(264, 4096), (1000, 3328), (40, 256)])
+def test_pipe_kernel_k_splits_and_pairs_past_the_range(n, k, rows, dtype):
+    """The pipelined GEMV with K split across workgroups whose last split is
+    mostly pairs past the range (K = 4096: spans of 12 pairs over 32 pairs;
+    K = 3328: 26 pairs, the last split 2 real pairs), a partial last row
+    block (n = 264, 1000, 40), and LDS left full of NaN by a GEMM over NaN
+    activations: steps past the range must add exactly nothing (their scales,
+    activations and, bf16, group sums are never taken from stale LDS)."""
+    from qwen_int4_hip import linear_kernel_name
+
+    torch_dtype = torch.float16 if dtype == "fp16" else torch.bfloat16
+    assert linear_kernel_name(rows, n, k, torch_dtype).startswith("gemv_pipe_kernel")
+    poison = torch.full((2048, 1536), float("nan"), dtype=torch_dtype, device=DEV)
+    q8, s8, z8 = weights("sym", 8960, 1536, O.BASE_SEED + 5)
+    q, s, z = weights("asym", n, k, O.BASE_SEED + n + k + rows)
+    x = O.activations(rows, k, seed=O.BASE_SEED + 5 * rows + n, dtype=dtype, outliers=True)
+    bias = O._from_f32(np.linspace(-1, 1, n, dtype=np.float32), "fp16")
+    for _ in range(2):
+        hip_w4g64_linear(poison, *dev_weights(q8, s8, z8), None, out_features=8960, in_features=1536,
+                         group_size=64, packing=PackingFormat.CANONICAL)
+        check_linear(x, q, s, z, bias, n, k, dtype, bias_dtype="fp16")
+
+
 @pytest.mark.parametrize("dtype", ["bf16", "fp32"])
 @pytest.mark.parametrize("k", [1536, 16448])
 def test_gemm_row_scaling_keeps_every_row_exact(dtype, k):
@@ -435,16 +470,15 @@ def test_ragged_shapes(rows, n, k, dtype):
 )
 @pytest.mark.parametrize("dtype", ["fp16", "bf16"])
 def test_decode_nine_to_sixteen_rows(rows, n, k, dtype):
-    """Rows 9..16 run the kernel that stages the activations in LDS and splits
-    K across the waves of each 16-feature block; long K (8960, 9280, and 3072
-    at 13 rows) also splits K across workgroups, and long K puts two feature
-    blocks in a workgroup (n = 40: the second block is partly past N).  Short
-    K with more than 512 16-feature blocks (n = 8960, 8200) puts three blocks
-    in a workgroup, the last workgroup partly past N."""
+    """Rows 9..16: K a multiple of 256 runs the pipelined kernel (two A tiles;
+    long K (8960) split across workgroups; n = 13, 72: one partial row
+    block), other K the 16-row kernel that stages the activations in LDS and
+    splits K across the waves of each 16-feature block (K = 9280 also across
+    workgroups; n = 40: the second block is partly past N)."""
     from qwen_int4_hip import linear_kernel_name
 
     assert linear_kernel_name(rows, n, k, torch.float16 if dtype == "fp16" else torch.bfloat16).startswith(
-        "gemv16_kernel")
+        decode_kernel_prefix(rows, k))
     q, s, z = weights("asym", n, k, rows * 7 + n + k)
     x = O.activations(rows, k, seed=rows + 2 * n, dtype=dtype, outliers=True)
     bias = O._from_f32(np.linspace(-0.5, 0.5, n, dtype=np.float32), dtype)
