@@ -61,6 +61,7 @@ from __future__ import annotations
 import argparse
 import ctypes
 import json
+import math
 import os
 import platform
 import statistics
@@ -290,6 +291,222 @@ def dense_library_gemm_ms(cases, torch, reps: int = 12):
         torch.cuda.synchronize()
         out.append(statistics.median(a.elapsed_time(b) for a, b in events))
     return out
+
+
+# ---------------------------------------------------------------------------
+# Floors and the reference's own operator profiles
+# ---------------------------------------------------------------------------
+
+STREAM_FLOOR_BYTES = (7_434_240, 1_327_104, 212_992)  # gate/down M=1, q/o M=1, k/v M=1 (rounded to 4 KiB)
+
+
+def _cold_pool_slices(torch, nbytes: int, pool_bytes: int = 640 << 20):
+    """One device buffer of >= pool_bytes split into slices of nbytes (4 KiB
+    aligned): graph launches that rotate over them read HBM, not the 256 MB
+    Infinity Cache."""
+    step = (nbytes + 4095) // 4096 * 4096
+    count = max(32, -(-pool_bytes // step))
+    pool = torch.empty(count * step, dtype=torch.uint8, device="cuda")
+    pool.fill_(1)
+    return pool, [pool[i * step: i * step + nbytes] for i in range(count)]
+
+
+def stream_floor(torch, hip, reps: int = 50, launches: int = 32) -> list:
+    """The bare-stream floor of a decode launch, measured the way the decode
+    calls are: a HIP graph of `launches` back-to-back launches of the stream
+    probe (w4g64_stream_probe: one 16-byte nontemporal load per lane over
+    exactly the call's bytes, nothing else), rotating over a 640 MB pool,
+    replayed between HIP events on the replay stream."""
+    from qwen_int4_hip import _lib
+
+    lib = _lib.load()
+    sink = torch.zeros(256, dtype=torch.int32, device="cuda")
+    side = torch.cuda.Stream()
+    sp = ctypes.c_void_p(side.cuda_stream)
+    out = []
+    for nbytes in STREAM_FLOOR_BYTES:
+        pool, slices = _cold_pool_slices(torch, nbytes)
+        torch.cuda.synchronize()
+        with torch.cuda.stream(side):
+            def probe(i):
+                _lib.check(lib.w4g64_stream_probe(ctypes.c_void_p(slices[i % len(slices)].data_ptr()), nbytes,
+                                                  ctypes.c_void_p(sink.data_ptr()), sp))
+            probe(0)
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=side):
+                for i in range(launches):
+                    probe(7 * i)
+            g.replay()
+            events = [(hip.event(), hip.event()) for _ in range(reps)]
+            for a, b in events:
+                hip.record(a, sp)
+                g.replay()
+                hip.record(b, sp)
+            torch.cuda.synchronize()
+            d = [hip.elapsed_ms(a, b) * 1e3 / launches for a, b in events]
+            for a, b in events:
+                hip.lib.hipEventDestroy(a)
+                hip.lib.hipEventDestroy(b)
+            del g
+        out.append({"bytes": nbytes, "us_p50": round(statistics.median(d), 3), "us_p95": round(percentile(d, 95), 3),
+                    "GBps": round(nbytes / statistics.median(d) / 1e3, 1)})
+        del pool, slices
+        torch.cuda.empty_cache()
+    return out
+
+
+# The reference's operator autotune profiles (configs/phase-e-triton-autotune-v1.json:17-21) and the
+# median kernel times its Triton kernel reached there (results/phase_e_triton_autotune_v1.json:18-56,
+# RTX 4090, CUDA events; other hardware, shown for context only).
+REFERENCE_PROFILES = (
+    ("v_projection_fp16", 1, 256, 1536, "fp16", 0.01, 0.0625, 79.904),
+    ("q_projection_bf16", 8, 1536, 1536, "bf16", 0.02, 0.25, 80.896),
+    ("mlp_down_projection_fp16", 4, 1536, 8960, "fp16", 0.01, 0.0625, 325.568),
+)
+
+
+def awq_weights_gpu(n: int, k: int, seed: int, torch):
+    """Asymmetric AWQ-style W4G64 drawn on the GPU (config 3): codes u in
+    [0, 15] and per-group zero points in [4, 11] stored as signed u - 8,
+    log-normal scales (mu = ln 0.003, sigma = 0.5) -- the distributions of an
+    AWQ export, whose input-channel scales are already folded into the
+    codes and scales (the kernels' work does not depend on the values)."""
+    from qwen_int4_hip import pack_int4
+
+    gen = torch.Generator(device="cuda").manual_seed(seed)
+    codes = torch.randint(0, 16, (n, k), generator=gen, device="cuda", dtype=torch.int16) - 8
+    zeros_u = torch.randint(4, 12, (n * (k // 64),), generator=gen, device="cuda", dtype=torch.int16) - 8
+    scales = torch.exp(torch.randn((n, k // 64), generator=gen, device="cuda") * 0.5 + float(math.log(0.003)))
+    return (pack_int4(codes.to(torch.int8)).reshape(n, k // 2), scales.to(torch.float16),
+            pack_int4(zeros_u.to(torch.int8)).reshape(-1, 1))
+
+
+def outlier_activations(rows: int, k: int, seed: int, dtype, torch):
+    """x ~ N(0, 1) with 1 % of the channels scaled by 20 (config 3)."""
+    gen = torch.Generator(device="cuda").manual_seed(seed)
+    x = torch.randn((rows, k), generator=gen, device="cuda", dtype=torch.float32)
+    channels = torch.randperm(k, generator=gen, device="cuda")[: max(1, k // 100)]
+    x[:, channels] *= 20.0
+    return x.to(dtype)
+
+
+def _awq_cases(torch, specs, copies_bytes: int = 640 << 20):
+    """Cases with cold weight copies for graph_kernel_durations: specs are
+    (name, rows, n, k, dtype, seed)."""
+    cases = []
+    for name, rows, n, k, dtype, seed in specs:
+        w = awq_weights_gpu(n, k, seed, torch)
+        wbytes = sum(t.numel() * t.element_size() for t in w)
+        ncopies = max(2, min(256, -(-copies_bytes // wbytes)))
+        ncopies += ncopies % 3 == 0  # the replay visits copies with stride 3
+        copies = [w] + [tuple(t.clone() for t in w) for _ in range(ncopies - 1)]
+        x = outlier_activations(rows, k, seed + 1, dtype, torch)
+        cases.append({"name": name, "rows": rows, "n": n, "k": k, "x": x, "w": w, "copies": copies, "copy0": 0,
+                      "bytes": algorithmic_bytes(rows, n, k)})
+    return cases
+
+
+def _oracle_check(case, torch, rtol=None, atol=None) -> float:
+    """Normwise relative error of the case's HIP output against the CPU
+    restatement of the reference's torch backend (and the reference's own
+    rtol/atol where given)."""
+    from oracle import oracle as O
+    from qwen_int4_hip import linear_canonical_w4g64_hip
+
+    got = linear_canonical_w4g64_hip(case["x"], *case["w"]).float().cpu()
+    x, q, s, z = case["x"].cpu(), *(t.cpu() for t in case["w"])
+    ref = O.reference_linear_torch(x, q, s, z, None, out_features=case["n"], in_features=case["k"], return_f32=True)
+    rel = float((got - ref).abs().max() / ref.abs().max().clamp_min(1e-30))
+    ok = bool(torch.isfinite(got).all()) and rel <= 1e-2
+    if rtol is not None:
+        ok = ok and bool(torch.allclose(got, ref, rtol=rtol, atol=atol))
+    if not ok:
+        raise SystemExit(f"parity failed for {case['name']} rows={case['rows']}: normwise relative error {rel:.3e}")
+    return rel
+
+
+def reference_profiles(torch, hip) -> list:
+    """The reference's three operator profiles on AWQ-style weights, cold,
+    graph-replayed as the decode calls are; median and p95 per launch."""
+    out = []
+    specs = [(name, m, n, k, torch.float16 if dt == "fp16" else torch.bfloat16, BASE_SEED + 31 * i)
+             for i, (name, m, n, k, dt, *_rest) in enumerate(REFERENCE_PROFILES)]
+    cases = _awq_cases(torch, specs)
+    durations = graph_kernel_durations(cases, 100, hip, torch)
+    from qwen_int4_hip import linear_kernel_name
+
+    for case, d, prof in zip(cases, durations, REFERENCE_PROFILES):
+        rel = _oracle_check(case, torch, rtol=prof[5], atol=prof[6])
+        us = [v * 1e3 for v in d]
+        p50 = statistics.median(us)
+        gbs = case["bytes"] / p50 / 1e3
+        out.append({"profile": prof[0], "shape_mnk": [case["rows"], case["n"], case["k"]], "dtype": prof[4],
+                    "kernel": linear_kernel_name(case["rows"], case["n"], case["k"], case["x"].dtype),
+                    "us_p50": round(p50, 3), "us_p95": round(percentile(us, 95), 3), "samples": len(us),
+                    "GBps": round(gbs, 1), "roofline": {"bound": "hbm", "achieved": round(gbs, 1),
+                                                       "peak": HBM_PEAK_GBS, "frac": round(gbs / HBM_PEAK_GBS, 4)},
+                    "parity_normwise_rel_err": rel, "parity_rtol_atol": [prof[5], prof[6]],
+                    "reference_rtx4090_triton_median_us": prof[7]})
+        log(f"  profile {prof[0]:26s} {case['rows']}x{case['n']}x{case['k']} {prof[4]}: p50 {p50:6.2f} us "
+            f"(p95 {percentile(us, 95):6.2f}), {gbs:7.1f} GB/s; reference Triton on RTX 4090: {prof[7]:.1f} us")
+    del cases
+    torch.cuda.empty_cache()
+    return out
+
+
+def awq_config3(torch, hip, gemm_reps: int = 100) -> dict:
+    """Config 3: asymmetric AWQ-style weights on the seven shapes at M = 1
+    (cold, graph-replayed; GB/s) and M = 2048 (event-timed launches; TFLOP/s),
+    fp16 activations with 1 % outlier channels x20; every M = 1 output and
+    the q_proj M = 2048 output checked against the CPU oracle first."""
+    from qwen_int4_hip import linear_kernel_name
+
+    specs1 = [(name, 1, n, k, torch.float16, BASE_SEED + 101 + i) for i, (name, (n, k)) in enumerate(QWEN2_SHAPES.items())]
+    cases1 = _awq_cases(torch, specs1)
+    worst = max(_oracle_check(c, torch) for c in cases1)
+    d1 = graph_kernel_durations(cases1, 100, hip, torch)
+    rows1, tot_b, tot_us = [], 0, 0.0
+    for c, d in zip(cases1, d1):
+        us = statistics.fmean(d) * 1e3
+        tot_b += c["bytes"]
+        tot_us += us
+        rows1.append({"name": c["name"], "n": c["n"], "k": c["k"], "kernel": linear_kernel_name(1, c["n"], c["k"], torch.float16),
+                      "us_mean": round(us, 3), "us_p50": round(statistics.median(d) * 1e3, 3),
+                      "us_p95": round(percentile(d, 95) * 1e3, 3), "GBps": round(c["bytes"] / us / 1e3, 1)})
+    del cases1
+    torch.cuda.empty_cache()
+    specs2 = [(name, 2048, n, k, torch.float16, BASE_SEED + 201 + i) for i, (name, (n, k)) in enumerate(QWEN2_SHAPES.items())]
+    cases2 = []
+    for name, rows, n, k, dtype, seed in specs2:
+        w = awq_weights_gpu(n, k, seed, torch)
+        cases2.append({"name": name, "rows": rows, "n": n, "k": k, "x": outlier_activations(rows, k, seed + 1, dtype, torch),
+                       "w": w, "copies": [w] + [tuple(t.clone() for t in w) for _ in range(3)], "copy0": 0})
+    worst = max(worst, _oracle_check(cases2[0], torch))
+    d2 = kernel_durations(cases2, gemm_reps, hip, torch)
+    rows2, tot_f, tot_ms = [], 0.0, 0.0
+    for c, d in zip(cases2, d2):
+        ms = statistics.fmean(d)
+        flops = 2.0 * c["rows"] * c["n"] * c["k"]
+        tot_f += flops
+        tot_ms += ms
+        rows2.append({"name": c["name"], "n": c["n"], "k": c["k"], "kernel": linear_kernel_name(2048, c["n"], c["k"], torch.float16),
+                      "us_mean": round(ms * 1e3, 2), "us_p50": round(statistics.median(d) * 1e3, 2),
+                      "us_p95": round(percentile(d, 95) * 1e3, 2), "TFLOPs": round(flops / ms / 1e9, 1)})
+    del cases2
+    torch.cuda.empty_cache()
+    m1 = tot_b / tot_us / 1e3
+    m2048 = tot_f / tot_ms / 1e9
+    log(f"config 3 (AWQ asymmetric, outliers): M=1 {m1:.1f} GB/s over 7 shapes ({tot_us:.1f} us); "
+        f"M=2048 {m2048:.1f} TFLOP/s over 7 shapes ({tot_ms * 1e3:.1f} us)")
+    return {"workload": "config 3: asymmetric AWQ-style W4G64 (codes 0..15, zero points 4..11, log-normal scales), "
+                        "seven Qwen2-1.5B shapes, fp16 activations with 1% outlier channels x20",
+            "parity_worst_normwise_rel_err": worst,
+            "m1": {"GBps": round(m1, 1), "roofline": {"bound": "hbm", "achieved": round(m1, 1), "peak": HBM_PEAK_GBS,
+                                                     "frac": round(m1 / HBM_PEAK_GBS, 4)}, "per_shape": rows1},
+            "m2048": {"TFLOPs": round(m2048, 1),
+                      "roofline": {"bound": "mfma", "achieved": round(m2048, 1), "peak": MFMA_PEAK_TFLOPS,
+                                   "frac": round(m2048 / MFMA_PEAK_TFLOPS, 4)}, "per_shape": rows2}}
 
 
 # ---------------------------------------------------------------------------
@@ -956,6 +1173,8 @@ def main() -> int:
                         help="skip the CPU timing of the baseline leg (its parity check always runs)")
     parser.add_argument("--no-gemm", action="store_true")
     parser.add_argument("--no-e2e", action="store_true", help="skip the end-to-end Qwen2-1.5B generation")
+    parser.add_argument("--no-profiles", action="store_true",
+                        help="skip the reference's operator profiles and config 3 (AWQ weights)")
     parser.add_argument("--e2e-only", action="store_true",
                         help="run only the end-to-end generation and print its object (for kernel-trace profiles)")
     parser.add_argument("--report", type=str, default="", help="write the detailed JSON report here")
@@ -1087,6 +1306,11 @@ def main() -> int:
     for r in steady:
         log(f"  steady state rows={r['rows']:2d} {r['n']}x{r['k']} ({r['stacks']}): {r['us_p50']:.1f} us, "
             f"{r['GBps']:.0f} GB/s ({r['frac']:.1%})")
+    # the bare-stream floor of a launch over the same bytes, measured the same way
+    floor = stream_floor(torch, hip)
+    for f in floor:
+        log(f"  stream floor {f['bytes'] / 1e6:5.2f} MB: p50 {f['us_p50']:.2f} us (p95 {f['us_p95']:.2f}), "
+            f"{f['GBps']:.0f} GB/s")
 
     result = {
         "metric": METRIC,
@@ -1114,7 +1338,8 @@ def main() -> int:
         "parity": parity,
         "roofline": {
             "bound": "hbm",
-            "kernel": "gemv_seg_kernel / gemv_kernel / gemv16_kernel + split_reduce_kernel (all 21 calls of a step)",
+            "kernel": "gemv_pipe_kernel (+ split_reduce_kernel for the K-split 4- and 16-row down projections; all 21 "
+                      "calls of a step)",
             "achieved": round(achieved, 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
@@ -1129,6 +1354,7 @@ def main() -> int:
                                 "achieved_GBps": round(dominant["GBps"], 1),
                                 "frac": round(dominant["GBps"] / HBM_PEAK_GBS, 4)},
             "steady_state": steady,
+            "stream_floor": floor,
         },
     }
     traffic = committed_traffic()
@@ -1178,6 +1404,11 @@ def main() -> int:
                                    "(hipBLASLt): the vendor library's rate on the same shapes, without dequantization"),
             "per_shape": gemm_rows,
         }
+
+    if not args.no_profiles:
+        # the reference's own operator profiles and config 3 (asymmetric AWQ weights, outlier activations)
+        result["reference_profiles"] = reference_profiles(torch, hip)
+        result["awq_config3"] = awq_config3(torch, hip)
 
     if not args.no_e2e:
         result["e2e"] = end_to_end(torch, hip)

@@ -130,7 +130,9 @@ int w4g64_linear_timed(const void* x, int x_dtype, const uint8_t* qweight, const
  * its split-K partial sums live in a file-scope device
  * array of the library (w4g64_static_scratch_bytes() bytes, 4 MiB, one per
  * GPU, held until the process ends), whose address is looked up once per
- * device on the first call there.  Problems that need more scratch than that
+ * device (hipGetSymbolAddress) on the first call there: make that first call
+ * on each device outside stream capture; the calls after it run nothing but
+ * the kernels and may be captured.  Problems that need more scratch than that
  * (the split-K prefill GEMM; every decode call of 1..16 rows of the
  * Qwen2-1.5B shapes fits) are rejected with W4G64_STATUS_UNSUPPORTED.  Calls
  * on one GPU share the array: calls that overlap on one GPU (on different
@@ -144,6 +146,13 @@ int w4g64_linear_static_scratch(const void* x, int x_dtype, const uint8_t* qweig
                                  int64_t out_features, int64_t in_features, void* stream);
 /* Size in bytes of w4g64_linear_static_scratch's per-GPU array. */
 int64_t w4g64_static_scratch_bytes(void);
+
+/* Measurement probe; no counterpart in the reference.  One 16-byte
+ * nontemporal load per lane over exactly `bytes` of src (16-byte aligned, a
+ * multiple of 4096), which practically never stores: the bare-stream floor a
+ * decode GEMV launch over the same bytes is measured against (bench.py).
+ * sink holds 256 uint32. */
+int w4g64_stream_probe(const void* src, int64_t bytes, void* sink, void* stream);
 
 /* Fusion of the SwiGLU product into the down projection: gate_up is
  * [rows, 2 * in_features] bf16 (gate | up), the activation is

@@ -455,16 +455,29 @@ int w4g64_linear_gate_up_planes(const void* x, const uint8_t* qweight, const uin
 namespace w4g64 {
 unsigned long long* g_timeline_stamps = nullptr;
 int g_timeline_workgroups = 0;
+}  // namespace w4g64
+
+// Registers the stamp buffer ([workgroups][8] uint64) read by the
+// instrumented kernels launched after this call (NULL: none).
+extern "C" int w4g64_timeline_register(void* stamps, int64_t workgroups) {
+    w4g64::g_timeline_stamps = (unsigned long long*)stamps;
+    w4g64::g_timeline_workgroups = stamps ? (int)workgroups : 0;
+    return ok();
+}
+#endif
+
+// ---- the bare-stream probe (measurement aid) ----
+namespace w4g64 {
 namespace {
 struct StreamArgs {
     const u32x4* src;
     uint32_t* sink;
     W4G64_TIMELINE_FIELDS
 };
-// Reference stream for the timelines: one 16-byte nontemporal load per lane
-// over exactly `bytes` (a multiple of 4096), and a store that practically
-// never happens (it keeps the loads).
-__global__ __launch_bounds__(256) void timeline_stream_kernel(StreamArgs a) {
+// One 16-byte nontemporal load per lane over exactly `bytes` (a multiple of
+// 4096) and a store that practically never happens (it keeps the loads):
+// the floor a decode GEMV launch over the same bytes is measured against.
+__global__ __launch_bounds__(256) void stream_probe_kernel(StreamArgs a) {
     W4G64_TIMELINE_DECL;
     W4G64_STAMP(0);
     const u32x4 v = __builtin_nontemporal_load(a.src + (int64_t)blockIdx.x * 256 + threadIdx.x);
@@ -477,25 +490,21 @@ __global__ __launch_bounds__(256) void timeline_stream_kernel(StreamArgs a) {
 }  // namespace
 }  // namespace w4g64
 
-// Registers the stamp buffer ([workgroups][8] uint64) read by the
-// instrumented kernels launched after this call (NULL: none).
-extern "C" int w4g64_timeline_register(void* stamps, int64_t workgroups) {
-    w4g64::g_timeline_stamps = (unsigned long long*)stamps;
-    w4g64::g_timeline_workgroups = stamps ? (int)workgroups : 0;
-    return ok();
-}
-
-// Launches the reference stream over `bytes` of `src` (16-byte aligned, a
-// multiple of 4096 bytes); sink holds 256 uint32.
-extern "C" int w4g64_timeline_stream(const void* src, int64_t bytes, void* sink, void* stream) {
-    if (!src || !sink || bytes <= 0 || bytes % 4096 || !aligned(src, 16))
-        return fail(W4G64_STATUS_INVALID_VALUE, "timeline stream needs a 16-byte aligned source of 4096-byte blocks");
+extern "C" int w4g64_stream_probe(const void* src, int64_t bytes, void* sink, void* stream) {
+    if (!src || !sink || bytes <= 0 || bytes % 4096 || bytes > (int64_t(1) << 40) || !aligned(src, 16))
+        return fail(W4G64_STATUS_INVALID_VALUE, "stream probe needs a 16-byte aligned source of 4096-byte blocks");
     w4g64::StreamArgs a{};
     a.src = (const w4g64::u32x4*)src;
     a.sink = (uint32_t*)sink;
     W4G64_TIMELINE_SET(a);
-    hipLaunchKernelGGL(w4g64::timeline_stream_kernel, dim3((unsigned)(bytes / 4096)), dim3(256), 0,
+    hipLaunchKernelGGL(w4g64::stream_probe_kernel, dim3((unsigned)(bytes / 4096)), dim3(256), 0,
                        (hipStream_t)stream, a);
-    return hip_status(hipGetLastError(), "timeline stream");
+    return hip_status(hipGetLastError(), "stream probe");
+}
+
+#ifdef W4G64_TIMELINE
+// The timelines' reference stream: the probe, with its stamps recorded.
+extern "C" int w4g64_timeline_stream(const void* src, int64_t bytes, void* sink, void* stream) {
+    return w4g64_stream_probe(src, bytes, sink, stream);
 }
 #endif

@@ -52,6 +52,7 @@ SIGNATURES = {
     "w4g64_linear_partials": (_int, [_p, _int, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _p]),
     "w4g64_linear_static_scratch": (_int, [_p, _int, _p, _p, _p, _p, _int, _p, _i64, _i64, _i64, _p]),
     "w4g64_static_scratch_bytes": (_i64, []),
+    "w4g64_stream_probe": (_int, [_p, _i64, _p, _p]),
     "w4g64_linear_swiglu": (_int, [_p, _p, _p, _p, _p, _int, _p, _i64, _i64, _i64, _p, _i64, _p]),
     "w4g64_linear_gate_up_planes": (_int, [_p, _p, _p, _p, _p, _int, _p, _i64, _i64, _i64, _p, _i64, _p]),
     "w4g64_linear_rmsnorm": (_int, [_p, _p, _int, _p, ctypes.c_float, _p, _p, _p, _p, _p, _int, _p, _int, _i64, _i64,

@@ -185,12 +185,19 @@ def load_quantized_checkpoint(model: torch.nn.Module, path: str | Path, *,
                            f"  shape_mismatches={mismatched}")
     keys = sorted(want)
     if metadata.get("format_version") == AWQ_FORMAT_VERSION:
-        t_want = {key: () for key in targets if key.endswith(AWQ_TRANSFORMED_SUFFIXES)}
-        t_have = {key: () for key in shapes if key.endswith(AWQ_TRANSFORMED_SUFFIXES)}
-        t_missing, t_unexpected, _ = _key_set_problems(t_want, t_have)
+        t_want = {key: tuple(t.shape) for key, t in targets.items() if key.endswith(AWQ_TRANSFORMED_SUFFIXES)}
+        t_have = {key: shape for key, shape in shapes.items() if key.endswith(AWQ_TRANSFORMED_SUFFIXES)}
+        t_missing, t_unexpected, t_shapes = _key_set_problems(t_want, t_have)
         if t_missing or t_unexpected:
             raise RuntimeError(f"AWQ transformed-state contract mismatch:\n  missing={t_missing}\n"
                                f"  unexpected={t_unexpected}")
+        if t_shapes:
+            # the reference loads these with load_state_dict, which rejects a
+            # shape that differs (torch's message); copy_ would broadcast
+            raise RuntimeError("Error(s) in loading state_dict:\n" + "\n".join(
+                f"\tsize mismatch for {key}: copying a param with shape {torch.Size(have_shape)} from checkpoint, "
+                f"the shape in current model is {torch.Size(want_shape)}."
+                for key, (want_shape, have_shape) in t_shapes.items()))
         keys += sorted(t_want)
     target = torch.device(device) if device is not None else _buffer_device(model)
     with safe_open(str(path), framework="pt", device=str(target)) as handle:

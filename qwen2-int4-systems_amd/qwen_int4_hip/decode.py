@@ -82,6 +82,16 @@ def check_token_ids(token_ids, *, batch: int, length: int | None, device, name: 
         raise ValueError(f"{name} must be an int64 tensor on {device}")
 
 
+def check_token_range(token_ids: torch.Tensor, vocab: int) -> None:
+    """Every id in [0, vocab), as the reference's embedding requires (it
+    raises torch's IndexError).  One device reduction read on the host: for
+    ids that come from a caller, outside any graph.  The fused decode step
+    itself never reads device memory on the host (it runs under graph
+    replay): an id outside the vocabulary gives that row a NaN embedding."""
+    if bool(((token_ids < 0) | (token_ids >= vocab)).any()):
+        raise IndexError("index out of range in self")
+
+
 def _fuse(modules: list[QuantLinear]) -> dict:
     """Concatenate the packed buffers of linears that share their input along
     the output dimension and re-point each module's buffers at its slice."""

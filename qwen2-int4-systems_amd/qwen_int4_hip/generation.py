@@ -15,7 +15,7 @@ from __future__ import annotations
 
 import torch
 
-from .decode import FusedDecodeStep, FusedPrefill
+from .decode import FusedDecodeStep, FusedPrefill, check_token_range
 
 
 def _is_left_padded(mask: torch.Tensor) -> bool:
@@ -135,6 +135,7 @@ class StaticGreedyDecoder:
         self.fused_prefill = FusedPrefill(model) if fused else None
         self.batch = batch
         self.max_length = max_length
+        self.vocab = model.model.embed_tokens.weight.shape[0]
         device = model.lm_head.weight.device
         self.caches = model.new_static_cache(batch, max_length, device)
         self.token = torch.zeros((batch, 1), dtype=torch.long, device=device)
@@ -150,6 +151,7 @@ class StaticGreedyDecoder:
         batch, length = input_ids.shape
         if batch != self.batch or length >= self.max_length:
             raise ValueError("prompt batch or length does not fit this decoder")
+        check_token_range(input_ids, self.vocab)
         with torch.inference_mode():
             if self.fused_prefill is not None:
                 logits = self.fused_prefill(input_ids, self.caches)
@@ -176,6 +178,9 @@ class StaticGreedyDecoder:
         if self.length >= self.max_length:
             raise RuntimeError("static cache is full")
         if token is not None:
+            if not isinstance(token, torch.Tensor) or tuple(token.shape) != tuple(self.token.shape):
+                raise ValueError(f"token must have shape {list(self.token.shape)}")
+            check_token_range(token, self.vocab)
             self.token.copy_(token)
         self.position.fill_(self.length)
         fused = self.fused is not None

@@ -210,6 +210,23 @@ def test_awq_loader_requires_the_transformed_state(tmp_path: Path):
         load_quantized_checkpoint(ToyQuantModel(), path)
 
 
+@pytest.mark.parametrize("norm_shape", [(1,), (64,)])
+def test_awq_loader_rejects_a_transformed_tensor_shape_before_any_copy(tmp_path: Path, norm_shape):
+    """A transformed norm of the wrong shape -- broadcastable ([1]) or not
+    ([64]) -- is a size mismatch, as the reference's load_state_dict reports
+    it, and the model is left untouched (quantized buffers included)."""
+    tensors = dict(_fill(ToyQuantModel(), 18).state_dict())
+    tensors["input_layernorm.weight"] = torch.full(norm_shape, 7.0)
+    path = tmp_path / "bad-norm.safetensors"
+    save_file(tensors, str(path), metadata=canonical_awq_metadata(group_size=64))
+    target = _fill(ToyQuantModel(), 19)
+    before = {k: v.clone() for k, v in target.state_dict().items()}
+    with pytest.raises(RuntimeError, match="size mismatch for input_layernorm.weight"):
+        load_quantized_checkpoint(target, path)
+    for key, value in target.state_dict().items():
+        assert torch.equal(value, before[key]), key
+
+
 def test_nonzero_zero_points_need_an_asymmetric_contract(tmp_path: Path):
     source = _fill(ToyQuantModel(), 16)
     source.proj.zeros.copy_(pack_int4(torch.tensor([-7, 5], dtype=torch.int8), packing=PackingFormat.CANONICAL)

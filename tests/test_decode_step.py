@@ -655,6 +655,27 @@ def test_fused_decode_step_matches_module_decode(batch):
         assert _cos(k0[:, :, :83], k1[:, :, :83]) >= 0.9999 and _cos(v0[:, :, :83], v1[:, :, :83]) >= 0.9999
 
 
+def test_static_decoder_rejects_out_of_vocabulary_tokens():
+    """Caller-supplied ids (a prompt, or the token given to step) outside
+    [0, vocab) raise the reference embedding's IndexError before anything
+    runs; the decoder's state is left as it was."""
+    from qwen_int4_hip.generation import StaticGreedyDecoder
+
+    model = _build(SMALL128, 23)
+    dec = StaticGreedyDecoder(model, 1, 32, use_graph=True, fused=True)
+    bad_prompt = torch.tensor([[1, SMALL128.vocab_size]], device="cuda")
+    with pytest.raises(IndexError, match="index out of range"):
+        dec.prefill(bad_prompt)
+    dec.prefill(torch.tensor([[1, 2, 3]], device="cuda"))
+    before = dec.token.clone()
+    for bad in (-1, SMALL128.vocab_size):
+        with pytest.raises(IndexError, match="index out of range"):
+            dec.step(torch.tensor([[bad]], device="cuda"))
+    assert dec.length == 3 and torch.equal(dec.token, before)
+    logits = dec.step(torch.tensor([[SMALL128.vocab_size - 1]], device="cuda"))
+    assert bool(torch.isfinite(logits.float()).all())
+
+
 @pytest.mark.parametrize("batch,length", [(1, 40), (2, 17)])
 def test_fused_prefill_matches_module_forward(batch, length):
     from qwen_int4_hip.decode import FusedPrefill
