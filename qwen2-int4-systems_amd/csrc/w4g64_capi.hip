@@ -137,12 +137,26 @@ static w4g64::GemvPlan decode_form_plan(int64_t rows, int64_t out_features, int6
     return x_dtype == W4G64_DTYPE_BF16_GATE_UP ? w4g64::plan_gemv_paired(rows, out_features, in_features)
                                                : w4g64::plan_gemv(rows, out_features, in_features, w4g64::kPlanes);
 }
+// The pipelined kernel's plan for a decode form (planes in / paired gate|up
+// out); it runs when the operands meet its alignment (16-byte x and
+// qweight, 4-byte scales, 2-byte zeros).
+static bool decode_form_pipe(int64_t rows, int64_t out_features, int64_t in_features, int x_dtype,
+                             w4g64::GemvPlan& plan) {
+    return x_dtype == W4G64_DTYPE_BF16_GATE_UP
+               ? w4g64::plan_pipe_fused(w4g64::kPlain, true, rows, out_features, in_features, plan)
+               : w4g64::plan_pipe_fused(w4g64::kPlanes3, false, rows, out_features, in_features, plan);
+}
 
 int64_t w4g64_linear_workspace_bytes(int64_t rows, int64_t out_features, int64_t in_features, int x_dtype) {
     if (rows <= 0 || out_features <= 0 || in_features <= 0 || in_features % 64) return 0;
-    if (decode_form(x_dtype))
-        return rows <= w4g64::kGemvMaxRows ? decode_form_plan(rows, out_features, in_features, x_dtype).workspace_bytes
-                                           : 0;
+    if (decode_form(x_dtype)) {
+        if (rows > w4g64::kGemvMaxRows) return 0;
+        int64_t need = decode_form_plan(rows, out_features, in_features, x_dtype).workspace_bytes;
+        w4g64::GemvPlan pipe;
+        if (decode_form_pipe(rows, out_features, in_features, x_dtype, pipe) && pipe.workspace_bytes > need)
+            need = pipe.workspace_bytes;
+        return need;
+    }
     if (fused_form(x_dtype))
         return rows <= w4g64::kGemvMaxRows
                    ? w4g64::plan_gemv(rows, out_features, in_features, x_dtype).workspace_bytes
@@ -164,11 +178,14 @@ int64_t w4g64_linear_workspace_bytes(int64_t rows, int64_t out_features, int64_t
 
 const char* w4g64_linear_kernel_name(int64_t rows, int64_t out_features, int64_t in_features, int x_dtype) {
     if (rows <= 0 || out_features <= 0 || in_features <= 0 || in_features % 64) return "none";
-    if (decode_form(x_dtype))
-        return rows <= w4g64::kGemvMaxRows
-                   ? w4g64::gemv_kernel_name(decode_form_plan(rows, out_features, in_features, x_dtype),
-                                             x_dtype == W4G64_DTYPE_BF16_GATE_UP ? w4g64::kBF16 : w4g64::kPlanes)
-                   : "none";
+    if (decode_form(x_dtype)) {
+        if (rows > w4g64::kGemvMaxRows) return "none";
+        const int kind = x_dtype == W4G64_DTYPE_BF16_GATE_UP ? w4g64::kBF16 : w4g64::kPlanes;
+        w4g64::GemvPlan pipe;
+        if (decode_form_pipe(rows, out_features, in_features, x_dtype, pipe))
+            return w4g64::gemv_kernel_name(pipe, kind);  // with aligned operands
+        return w4g64::gemv_kernel_name(decode_form_plan(rows, out_features, in_features, x_dtype), kind);
+    }
     if (fused_form(x_dtype))
         return rows <= w4g64::kGemvMaxRows
                    ? w4g64::gemv_kernel_name(w4g64::plan_gemv(rows, out_features, in_features, x_dtype), x_dtype)
@@ -233,7 +250,10 @@ static int linear_impl(const void* x, int x_dtype, const uint8_t* qweight, const
             return fail(W4G64_STATUS_UNSUPPORTED, "decode path supports at most %lld output features",
                         (long long)(w4g64::kGemvMaxOutFeatures));
         w4g64::GemvPlan lean;
-        if (w4g64::pipe_supported(p) && w4g64::plan_pipe(rows, out_features, in_features, p.x_kind, lean)) {
+        const bool pipe_plan = planes ? w4g64::plan_pipe_fused(w4g64::kPlanes3, false, rows, out_features,
+                                                                in_features, lean)
+                                      : w4g64::plan_pipe(rows, out_features, in_features, p.x_kind, lean);
+        if (pipe_plan && w4g64::pipe_supported(p)) {
             if (int st = check_workspace(workspace, workspace_bytes, lean.workspace_bytes)) return st;
             return hip_status(w4g64::launch_gemv_pipe(p, lean, workspace, s, (hipEvent_t)start_event,
                                                       (hipEvent_t)stop_event),
@@ -378,6 +398,15 @@ int w4g64_linear_rmsnorm(const void* residual, const void* delta, int delta_dtyp
     p.norm_eps = eps;
     p.norm_out_sum = out_sum;
     w4g64::GemvPlan lean;
+    // the pipelined kernel: bf16 delta with the paired gate|up epilogue, fp32
+    // delta or partial sums with a plain bf16 output
+    const bool pipe_plan =
+        gate_up_planes ? kind == w4g64::kNormB && w4g64::plan_pipe_fused(w4g64::kNormBf16, true, rows, out_features,
+                                                                         in_features, lean)
+                       : kind != w4g64::kNormB && w4g64::plan_pipe_fused(w4g64::kNormParts, false, rows,
+                                                                         out_features, in_features, lean);
+    if (pipe_plan && w4g64::pipe_supported(p))
+        return hip_status(w4g64::launch_gemv_pipe(p, lean, nullptr, (hipStream_t)stream), "gemv");
     if (gate_up_planes && w4g64::plan_seg_norm_planes(p, lean))
         return hip_status(w4g64::launch_gemv_seg_norm_planes(p, lean, (hipStream_t)stream), "gemv");
     const w4g64::GemvPlan plan = gate_up_planes ? w4g64::plan_gemv_paired(rows, out_features, in_features, kind)
@@ -395,6 +424,10 @@ int64_t w4g64_linear_partial_count(int64_t rows, int64_t out_features, int64_t i
         in_features <= 0 || in_features % 64 || in_features > (1ll << 24))
         return 0;
     if (x_dtype != W4G64_DTYPE_BF16_PLANES && x_dtype != W4G64_DTYPE_F32) return 0;
+    w4g64::GemvPlan pipe;
+    if (x_dtype == W4G64_DTYPE_BF16_PLANES &&
+        w4g64::plan_pipe_fused(w4g64::kPlanes3, false, rows, out_features, in_features, pipe))
+        return pipe.splits;
     const w4g64::GemvPlan plan =
         w4g64::plan_gemv(rows, out_features, in_features, x_dtype == W4G64_DTYPE_F32 ? w4g64::kF32 : w4g64::kPlanes);
     return plan.kind == 0 ? plan.splits : 0;
@@ -422,6 +455,16 @@ int w4g64_linear_partials(const void* x, int x_dtype, const uint8_t* qweight, co
     w4g64::LinearProblem p{x, kind, qweight, scales, zeros, nullptr, W4G64_DTYPE_NONE, partials, rows, out_features,
                            in_features};
     p.partials_out = partials;
+    w4g64::GemvPlan pipe;
+    if (kind == w4g64::kPlanes &&
+        w4g64::plan_pipe_fused(w4g64::kPlanes3, false, rows, out_features, in_features, pipe)) {
+        // the count above came from this plan: its operand alignment is required
+        if (!aligned(scales, 4) || !aligned(zeros, 2))
+            return fail(W4G64_STATUS_INVALID_VALUE,
+                        "partial sums over in_features %lld need 4-byte aligned scales and 2-byte aligned zeros",
+                        (long long)in_features);
+        return hip_status(w4g64::launch_gemv_pipe(p, pipe, nullptr, (hipStream_t)stream), "gemv");
+    }
     const w4g64::GemvPlan plan = w4g64::plan_gemv(rows, out_features, in_features, kind);
     return hip_status(w4g64::launch_gemv(p, plan, nullptr, (hipStream_t)stream), "gemv");
 }
@@ -442,6 +485,10 @@ int w4g64_linear_gate_up_planes(const void* x, const uint8_t* qweight, const uin
     if (!aligned(x, 16)) return fail(W4G64_STATUS_INVALID_VALUE, "x must be 16-byte aligned");
     w4g64::LinearProblem p{x, w4g64::kBF16, qweight, scales, zeros, bias, bias_dtype, planes, rows, out_features,
                            in_features, 1};
+    w4g64::GemvPlan pipe;
+    if (w4g64::plan_pipe_fused(w4g64::kPlain, true, rows, out_features, in_features, pipe) &&
+        w4g64::pipe_supported(p))
+        return hip_status(w4g64::launch_gemv_pipe(p, pipe, nullptr, (hipStream_t)stream), "gemv");
     const w4g64::GemvPlan plan = w4g64::plan_gemv_paired(rows, out_features, in_features);
     if (int st = check_workspace(workspace, workspace_bytes, plan.workspace_bytes)) return st;
     return hip_status(w4g64::launch_gemv(p, plan, workspace, (hipStream_t)stream), "gemv");

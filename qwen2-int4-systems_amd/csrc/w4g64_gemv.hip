@@ -841,13 +841,15 @@ GemvPlan plan_gemv_paired(int64_t rows, int64_t out_features, int64_t in_feature
 }
 
 const char* gemv_kernel_name(const GemvPlan& plan, int x_kind) {
-    static thread_local char name[64];
+    static thread_local char name[96];
     static const char* kinds[] = {"?", "f16", "bf16", "f32", "?", "swiglu_bf16", "planes_bf16", "rmsnorm_bf16",
                                   "rmsnorm_f32delta"};
     if (plan.kind == 4) {
-        snprintf(name, sizeof(name), "gemv_pipe_kernel<%s,%d,%d,%d,%d,%d,%d,%d>",
-                 kinds[x_kind >= 1 && x_kind <= 8 ? x_kind : 0], plan.segments, plan.tiles, plan.fblocks, plan.kparts,
-                 plan.rbw, plan.steps, plan.depth);
+        // the pipelined kernel's activation form comes from the plan
+        static const char* forms[] = {"", "planes_bf16", "rmsnorm_bf16", "rmsnorm_partials"};
+        const char* form = plan.form >= 1 && plan.form <= 3 ? forms[plan.form] : kinds[x_kind >= 1 && x_kind <= 8 ? x_kind : 0];
+        snprintf(name, sizeof(name), "gemv_pipe_kernel<%s%s,%d,%d,%d,%d,%d,%d,%d>", form, plan.pair ? "_gate_up" : "",
+                 plan.segments, plan.tiles, plan.fblocks, plan.kparts, plan.rbw, plan.steps, plan.depth);
         return name;
     }
     if (plan.kind == 2) {

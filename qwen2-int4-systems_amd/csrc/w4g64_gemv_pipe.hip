@@ -55,14 +55,25 @@ struct PipeArgs {
     const uint8_t* zeros;
     const void* bias;
     void* y;
-    float* partials;  // [splits][M][N] (grid y > 1 or unreduced output)
+    float* partials;  // [splits][Mo][N] (grid y > 1 or unreduced output)
     int bias_kind;
-    int M;   // activation rows
-    int N;   // out_features
+    int M;   // staged activation rows (bf16 planes: 3 Mo)
+    int Mo;  // output rows
+    int N;   // out_features (paired: 2 I)
+    int I;   // paired: gate rows
     int K;   // in_features (a multiple of 128)
     int G;   // groups
     int P;   // group pairs
     int PS;  // pairs per K split
+    // RMSNorm prologue (one row): x is the bf16 residual; the activation is
+    // RMSNorm(x + delta) with `norm_w` and `eps`; workgroup (0, 0) stores
+    // x + delta (bf16) to out_sum.  delta: bf16 [K] (FORM kNormBf16) or
+    // `delta_parts` fp32 partial sums [parts][K] added in order (kNormParts).
+    const void* delta;
+    int delta_parts;
+    const uint16_t* norm_w;
+    float eps;
+    uint16_t* out_sum;
     W4G64_TIMELINE_FIELDS
 };
 
@@ -77,7 +88,7 @@ __host__ __device__ inline PipeLayout pipe_layout(int M, int PS, int red_floats)
     L.zero = M * L.xw * 2;
     L.sx = L.zero + 64;
     L.red = L.sx + M * 2 * PS * 4;
-    L.total = L.red + red_floats * 4;
+    L.total = L.red + (red_floats > 16 ? red_floats : 16) * 4;  // >= 16 floats: the norm prologue's wave sums
     return L;
 }
 
@@ -102,20 +113,20 @@ __device__ __forceinline__ float sum8_lanes(float s) {
     return s;
 }
 
-// ((w ^ 0x88888888) & mask) | magic in one v_bitop3_b32 with truth table
-// 0x9A over (w, b, c): bits with (b, c) = (0, 0) pass w, (0, 1) pass ~w,
-// (1, 0) give 0 and (1, 1) give 1, so b = ~mask and c = (mask & 0x88888888)
-// | (~mask & magic).  (clang exposes no builtin for the instruction.)
-__device__ __forceinline__ uint32_t bitop3_9a(uint32_t w, uint32_t b, uint32_t c) {
-    uint32_t r;
-    asm("v_bitop3_b32 %0, %1, %2, %3 bitop3:0x9a" : "=v"(r) : "v"(w), "s"(b), "v"(c));
-    return r;
+// ((w ^ 0x88888888) & MASK) | MAGIC: four nibbles with bit 3 flipped (a
+// signed code c becomes c + 8) under a magic exponent.  Plain
+// C on purpose: the compiler forms one v_bitop3_b32 from it and, unlike for
+// inline asm, accounts for the wait states an MFMA needs after a VALU write
+// of its operands (and before a VALU write of an MFMA's accumulator input).
+template <uint32_t MASK, uint32_t MAGIC>
+__device__ __forceinline__ uint32_t nibbles_magic(uint32_t w) {
+    return ((w ^ 0x88888888u) & MASK) | MAGIC;
 }
-constexpr uint32_t kLoB = 0xFFF0FFF0u;     // ~0x000F000F
-constexpr uint32_t kHiB = 0xFF0FFF0Fu;     // ~0x00F000F0
-constexpr uint32_t kF16LoC = 0x64086408u;  // magic 1024 (fp16) with the sign flip of nibble bit 3
-constexpr uint32_t kF16HiC = 0x54805480u;  // magic 64 (fp16), nibble in bits 4-7
-constexpr uint32_t kBF16C = 0x43084308u;   // magic 128 (bf16)
+constexpr uint32_t kLoMask = 0x000F000Fu;
+constexpr uint32_t kHiMask = 0x00F000F0u;
+constexpr uint32_t kF16LoMagic = 0x64006400u;  // 1024 (fp16), nibble in bits 0-3
+constexpr uint32_t kF16HiMagic = 0x54005400u;  // 64 (fp16), nibble in bits 4-7
+constexpr uint32_t kBF16Magic = 0x43004300u;   // 128 (bf16)
 
 // Exact (code - zero) of one packed dword as fp16 in slot order [k0 k4 k1 k5
 // k2 k6 k3 k7]: 1024 + n' and 64 + n' (n' = code + 8) minus 1032 + z and
@@ -123,10 +134,10 @@ constexpr uint32_t kBF16C = 0x43084308u;   // magic 128 (bf16)
 __device__ __forceinline__ half8 codes8_f16(uint32_t w, uint32_t clo, uint32_t chi) {
     const uint32_t w8 = w >> 8;
     const half2v c_lo = __builtin_bit_cast(half2v, clo), c_hi = __builtin_bit_cast(half2v, chi);
-    const half2v h0 = __builtin_bit_cast(half2v, bitop3_9a(w, kLoB, kF16LoC)) - c_lo;
-    const half2v h1 = __builtin_bit_cast(half2v, bitop3_9a(w, kHiB, kF16HiC)) - c_hi;
-    const half2v h2 = __builtin_bit_cast(half2v, bitop3_9a(w8, kLoB, kF16LoC)) - c_lo;
-    const half2v h3 = __builtin_bit_cast(half2v, bitop3_9a(w8, kHiB, kF16HiC)) - c_hi;
+    const half2v h0 = __builtin_bit_cast(half2v, nibbles_magic<kLoMask, kF16LoMagic>(w)) - c_lo;
+    const half2v h1 = __builtin_bit_cast(half2v, nibbles_magic<kHiMask, kF16HiMagic>(w)) - c_hi;
+    const half2v h2 = __builtin_bit_cast(half2v, nibbles_magic<kLoMask, kF16LoMagic>(w8)) - c_lo;
+    const half2v h3 = __builtin_bit_cast(half2v, nibbles_magic<kHiMask, kF16HiMagic>(w8)) - c_hi;
     half8 v = {h0[0], h0[1], h1[0], h1[1], h2[0], h2[1], h3[0], h3[1]};
     return v;
 }
@@ -134,26 +145,24 @@ __device__ __forceinline__ half8 codes8_f16(uint32_t w, uint32_t clo, uint32_t c
 // bf16 values 128 + n' = 136 + code (exact), slot order.
 __device__ __forceinline__ bf16x8 codes8_bf16_biased(uint32_t w) {
     u32x4 v;
-    v[0] = bitop3_9a(w, kLoB, kBF16C);
-    v[1] = bitop3_9a(w >> 4, kLoB, kBF16C);
-    v[2] = bitop3_9a(w >> 8, kLoB, kBF16C);
-    v[3] = bitop3_9a(w >> 12, kLoB, kBF16C);
+    v[0] = nibbles_magic<kLoMask, kBF16Magic>(w);
+    v[1] = nibbles_magic<kLoMask, kBF16Magic>(w >> 4);
+    v[2] = nibbles_magic<kLoMask, kBF16Magic>(w >> 8);
+    v[3] = nibbles_magic<kLoMask, kBF16Magic>(w >> 12);
     return __builtin_bit_cast(bf16x8, v);
 }
 
 // A 16-bit load's bits, zero-extended where this statement stands.  The
-// load is typed _Float16, which lives in a 32-bit register with undefined
-// upper bits, so its raw register goes straight into the volatile asm: the
-// compiler inserts no zero extension of its own, which it would schedule
-// early (waiting for the load there), and cannot move this one across the
-// other ordering statements.
+// load is typed _Float16 and its register passes through an empty volatile
+// asm here: the compiler cannot hoist the zero extension (which waits for
+// the load) above this point, and -- as the asm emits nothing -- still sees
+// every instruction it must keep hazard-free.
 __device__ __forceinline__ uint32_t take_u16(_Float16 raw) {
-    uint32_t r;
-    asm volatile("v_and_b32 %0, 0xffff, %1" : "=v"(r) : "v"(raw));
-    return r;
+    asm volatile("" : "+v"(raw));
+    return (uint32_t)__builtin_bit_cast(uint16_t, raw);
 }
 
-template <int XK, int SW, int MT, int WR, int WK, int RBW, int T, int DP, int STG>
+template <int XK, int FORM, bool PAIRED, int SW, int MT, int WR, int WK, int RBW, int T, int DP, int STG>
 __global__ __launch_bounds__(WR * WK * 64) void gemv_pipe_kernel(PipeArgs a) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
     constexpr int W = WR * WK;
@@ -168,6 +177,10 @@ __global__ __launch_bounds__(WR * WK * 64) void gemv_pipe_kernel(PipeArgs a) {
     const int wr = wave % WR;
     const int wk = wave / WR;
     const int M = a.M, N = a.N, K = a.K, G = a.G, P = a.P;
+    constexpr int PL = FORM == kPlanes3 ? 3 : 1;  // staged rows per output row
+    constexpr bool kNorm = FORM == kNormBf16 || FORM == kNormParts;
+    static_assert(!PAIRED || (RBW == 2 && WK == 1), "paired: gate rows in row block 0, up rows in row block 1");
+    static_assert(XK == kBF16 || FORM == kPlain, "the fused forms are bf16");
     const int p0 = blockIdx.y * a.PS;        // first pair of the workgroup's K range
     const int pe = min(p0 + a.PS, P);        // end of its range
     const int ps = pe - p0;                  // pairs staged (>= 1)
@@ -182,9 +195,16 @@ __global__ __launch_bounds__(WR * WK * 64) void gemv_pipe_kernel(PipeArgs a) {
     const int r = c / SW;
     const int s = c % SW;
     const int pb = p0 + wk * SW * T;  // this wave's first pair
+    // Output row of row block b, row rl within the wave's block: blocks of
+    // the workgroup's rows in turn, or -- paired -- gate row i (block 0) and
+    // up row I + i (block 1) of the same i.
+    auto rowof = [&](int b, int rl) -> int {
+        if constexpr (PAIRED) return b * a.I + blockIdx.x * (WR * R) + wr * R + rl;
+        else return row0 + (b * WR + wr) * R + rl;
+    };
     // the rows a thread stores: with one K part per workgroup, lane l stores
-    // rows (b WR + wr) R + l % R of its row blocks b; otherwise thread t
-    // stores row t % RWG of the workgroup (kThreads % RWG == 0)
+    // row l % R of its row blocks b; otherwise thread t stores row t % RWG of
+    // the workgroup (kThreads % RWG == 0)
     constexpr bool kWaveLocal = WK == 1;
     constexpr int NB = kWaveLocal ? RBW : 1;
     static_assert(kWaveLocal || kThreads % RWG == 0, "a thread's outputs share its row");
@@ -195,7 +215,7 @@ __global__ __launch_bounds__(WR * WK * 64) void gemv_pipe_kernel(PipeArgs a) {
     _Float16 bias_lo[NB], bias_hi[NB];
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
-        int brow = kWaveLocal ? row0 + (b * WR + wr) * R + lane % R : row0 + tid % RWG;
+        int brow = kWaveLocal ? rowof(b, lane % R) : row0 + tid % RWG;
         brow = min(brow, N - 1);
         const _Float16* bp = (const _Float16*)(a.bias_kind == 0 ? (const void*)a.scales : a.bias);
         const int e = a.bias_kind == kF32 ? 2 * brow : (a.bias_kind == 0 ? 0 : brow);
@@ -211,9 +231,14 @@ __global__ __launch_bounds__(WR * WK * 64) void gemv_pipe_kernel(PipeArgs a) {
     };
 
     // ---- 1. staging loads: item it = 8 activation values of row m ----
+    // (norm forms: the residual's 8 values, the delta's and the norm
+    // weight's; parts past delta_parts re-read the last one)
     const int per_row = ps * 16;
     const int items = M * per_row;
+    constexpr int kDeltaVecs = FORM == kNormParts ? 2 * kMaxDeltaParts : (FORM == kNormBf16 ? 1 : 0);
     u32x4 xv[STG];
+    u32x4 dv[STG][kDeltaVecs > 0 ? kDeltaVecs : 1];
+    u32x4 nwv[STG];
     int xit[STG];
 #pragma unroll
     for (int u = 0; u < STG; ++u) {
@@ -223,6 +248,17 @@ __global__ __launch_bounds__(WR * WK * 64) void gemv_pipe_kernel(PipeArgs a) {
         const int m = it / per_row;
         const int k8 = it - m * per_row;
         xv[u] = *(const u32x4*)((const uint16_t*)a.x + (int64_t)m * K + (int64_t)p0 * 128 + 8 * k8);
+        if constexpr (FORM == kNormBf16) {
+            dv[u][0] = *(const u32x4*)((const uint16_t*)a.delta + 8 * k8);
+        } else if constexpr (FORM == kNormParts) {
+#pragma unroll
+            for (int pt = 0; pt < kMaxDeltaParts; ++pt) {
+                const float* dsrc = (const float*)a.delta + (int64_t)min(pt, a.delta_parts - 1) * K + 8 * k8;
+                dv[u][2 * pt] = *(const u32x4*)dsrc;
+                dv[u][2 * pt + 1] = *(const u32x4*)(dsrc + 4);
+            }
+        }
+        if constexpr (kNorm) nwv[u] = *(const u32x4*)(a.norm_w + 8 * k8);
     }
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();  // every wave's staging loads issue before any weight load
@@ -236,7 +272,7 @@ __global__ __launch_bounds__(WR * WK * 64) void gemv_pipe_kernel(PipeArgs a) {
     const uint8_t* zbase[RBW];  // P is even, so a zero byte's parity is its pair's
 #pragma unroll
     for (int b = 0; b < RBW; ++b) {
-        const int row = min(row0 + (b * WR + wr) * R + r, N - 1);
+        const int row = min(rowof(b, r), N - 1);
         wbase[b] = a.qweight + (int64_t)row * (K / 2) + 16 * q;
         sbase[b] = a.scales + (int64_t)row * G;
         zbase[b] = a.zeros + (int64_t)row * P;
@@ -256,8 +292,80 @@ __global__ __launch_bounds__(WR * WK * 64) void gemv_pipe_kernel(PipeArgs a) {
 #pragma unroll
     for (int i = 0; i < PF; ++i) issue(i);
 #pragma unroll
-    for (int u = 0; u < STG; ++u) asm volatile("" : "+v"(xv[u]));
+    for (int u = 0; u < STG; ++u) {
+        asm volatile("" : "+v"(xv[u]));
+        if constexpr (kNorm) asm volatile("" : "+v"(nwv[u]));
+#pragma unroll
+        for (int k = 0; k < kDeltaVecs; ++k) asm volatile("" : "+v"(dv[u][k]));
+    }
     W4G64_STAMP(1);
+
+    // ---- 2b. RMSNorm prologue (model.py:40-44, residual adds :149-154) ----
+    // s = bf16(x + bf16(delta)) (the partial sums added in order from 0, then
+    // + 0, as the split-K reduction does); the activation is
+    // bf16(bf16(s * r) * w), r = rsqrt(mean(s^2) + eps) over the whole row
+    // (squares rounded before the fp32 sum, as x.pow(2) is): each thread's
+    // items, a wave sum, the waves' sums added in order after one barrier.
+    // Workgroup (0, 0) stores s.
+    if constexpr (kNorm) {
+        float pt = 0.0f;
+#pragma unroll
+        for (int u = 0; u < STG; ++u) {
+            const int it = kThreads * u + tid;
+            float ps_ = 0.0f;
+            u32x4 sb;
+#pragma unroll
+            for (int e = 0; e < 8; e += 2) {
+                float sv[2];
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const uint32_t xw = xv[u][e / 2];
+                    const float xf = bf16_bits_to_float(h ? xw >> 16 : xw & 0xFFFFu);
+                    float df;
+                    if constexpr (FORM == kNormBf16) {
+                        const uint32_t dw = dv[u][0][e / 2];
+                        df = bf16_bits_to_float(h ? dw >> 16 : dw & 0xFFFFu);
+                    } else {
+                        float t = 0.0f;
+#pragma unroll
+                        for (int pt2 = 0; pt2 < kMaxDeltaParts; ++pt2) {
+                            const uint32_t bits = dv[u][2 * pt2 + (e + h) / 4][(e + h) % 4];
+                            t = pt2 < a.delta_parts ? t + __builtin_bit_cast(float, bits) : t;
+                        }
+                        df = bf16_round(t + 0.0f);
+                    }
+                    sv[h] = bf16_round(xf + df);
+                    ps_ += __fmul_rn(sv[h], sv[h]);
+                }
+                sb[e / 2] = float_to_bf16_bits(sv[0]) | ((uint32_t)float_to_bf16_bits(sv[1]) << 16);
+            }
+            xv[u] = sb;
+            pt += it < items ? ps_ : 0.0f;  // clamped items repeat a real one
+            if (blockIdx.x == 0 && blockIdx.y == 0 && it < items) *(u32x4*)(a.out_sum + 8 * xit[u]) = sb;
+        }
+        float* wsum = (float*)(smem + L.red);  // the epilogue's area, unused until then
+        const float ws = wave_sum64(pt);
+        if (lane == 0) wsum[wave] = ws;
+        lds_barrier();
+        float sq = wsum[0];
+#pragma unroll
+        for (int w = 1; w < W; ++w) sq += wsum[w];
+        const float rinv = rsqrtf(sq / (float)K + a.eps);
+#pragma unroll
+        for (int u = 0; u < STG; ++u) {
+            u32x4 xb;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float n0 = bf16_round(bf16_bits_to_float(xv[u][e] & 0xFFFFu) * rinv) *
+                                 bf16_bits_to_float(nwv[u][e] & 0xFFFFu);
+                const float n1 = bf16_round(bf16_bits_to_float(xv[u][e] >> 16) * rinv) * bf16_bits_to_float(nwv[u][e] >> 16);
+                xb[e] = float_to_bf16_bits(n0) | ((uint32_t)float_to_bf16_bits(n1) << 16);
+            }
+            xv[u] = xb;
+        }
+        // (the staging barrier below keeps the epilogue's later use of the
+        // area behind every wave's read of the sums)
+    }
 
     // ---- 3. staging into LDS (slot order) with the bf16 group sums ----
     {
@@ -400,12 +508,16 @@ __global__ __launch_bounds__(WR * WK * 64) void gemv_pipe_kernel(PipeArgs a) {
     W4G64_STAMP(3);
 
     // ---- 5. outputs ----
+    // value of staged row mv for row block b and row rl, summed over segments
+    // (and K parts) -- then, planes: the three staged rows of an output row
+    // added; paired: silu(gate) * up stored as bf16 planes
     const bool split_out = a.partials != nullptr;
+    const int Mo = a.Mo;
     auto emit = [&](int m, int n, float v, int b) {
-        if (split_out) a.partials[((int64_t)blockIdx.y * M + m) * N + n] = v;
-        else store_out<XK>(a.y, (int64_t)m * N + n, v + bias_of(b));
+        if (split_out) a.partials[((int64_t)blockIdx.y * Mo + m) * N + n] = v;
+        else store_out<FORM == kPlanes3 ? kF32 : XK>(a.y, (int64_t)m * N + n, v + bias_of(b));
     };
-    if constexpr (kWaveLocal && SW == 1) {
+    if constexpr (kWaveLocal && SW == 1 && PL == 1 && !PAIRED) {
         // lane (q, c): rows v = 8 mt + 2 q + h of D are activation rows m = v
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
@@ -414,7 +526,7 @@ __global__ __launch_bounds__(WR * WK * 64) void gemv_pipe_kernel(PipeArgs a) {
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
                     const int m = 8 * mt + 2 * q + h;
-                    const int n = row0 + (b * WR + wr) * R + r;
+                    const int n = rowof(b, r);
                     if (m < M && n < N) emit(m, n, acc[mt][b][2 * h] + acc[mt][b][2 * h + 1], b);
                 }
     } else if constexpr (kWaveLocal) {
@@ -435,18 +547,29 @@ __global__ __launch_bounds__(WR * WK * 64) void gemv_pipe_kernel(PipeArgs a) {
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+        auto total = [&](int b, int m, int rr) {  // planes in order, segments in order
+            float v = 0.0f;
 #pragma unroll
-        for (int b = 0; b < RBW; ++b)
-            for (int o = lane; o < M * R; o += 64) {  // 64 % R == 0: row r = lane % R
+            for (int pl = 0; pl < PL; ++pl)
+#pragma unroll
+                for (int s2 = 0; s2 < SW; ++s2) v += red[((b * M + pl * Mo + m) * R + rr) * SW + s2];
+            return v;
+        };
+        if constexpr (PAIRED) {
+            for (int o = lane; o < Mo * R; o += 64) {  // 64 % R == 0: row r = lane % R
                 const int m = o / R, rr = o % R;
-                const int n = row0 + (b * WR + wr) * R + rr;
-                if (n < N) {
-                    float v = 0.0f;
-#pragma unroll
-                    for (int s2 = 0; s2 < SW; ++s2) v += red[((b * M + m) * R + rr) * SW + s2];
-                    emit(m, n, v, b);
-                }
+                const int i = blockIdx.x * (WR * R) + wr * R + rr;
+                if (i < a.I) store_silu_planes(a.y, m, i, Mo, a.I, total(0, m, rr) + bias_of(0), total(1, m, rr) + bias_of(1));
             }
+        } else {
+#pragma unroll
+            for (int b = 0; b < RBW; ++b)
+                for (int o = lane; o < Mo * R; o += 64) {
+                    const int m = o / R, rr = o % R;
+                    const int n = rowof(b, rr);
+                    if (n < N) emit(m, n, total(b, m, rr), b);
+                }
+        }
     } else {
         float* red = (float*)(smem + L.red);  // [WK][M][RWG][SW]
 #pragma unroll
@@ -463,7 +586,7 @@ __global__ __launch_bounds__(WR * WK * 64) void gemv_pipe_kernel(PipeArgs a) {
                     }
                 }
         lds_barrier();
-        for (int o = tid; o < M * RWG; o += kThreads) {
+        for (int o = tid; o < Mo * RWG; o += kThreads) {
             const int m = o / RWG, wrow = o % RWG;
             const int n = row0 + wrow;
             if (n < N) {
@@ -471,7 +594,9 @@ __global__ __launch_bounds__(WR * WK * 64) void gemv_pipe_kernel(PipeArgs a) {
 #pragma unroll
                 for (int k2 = 0; k2 < WK; ++k2)
 #pragma unroll
-                    for (int s2 = 0; s2 < SW; ++s2) v += red[((k2 * M + m) * RWG + wrow) * SW + s2];
+                    for (int pl = 0; pl < PL; ++pl)
+#pragma unroll
+                        for (int s2 = 0; s2 < SW; ++s2) v += red[((k2 * M + pl * Mo + m) * RWG + wrow) * SW + s2];
                 emit(m, n, v, 0);
             }
         }
@@ -497,29 +622,52 @@ __global__ __launch_bounds__(WR * WK * 64) void gemv_pipe_kernel(PipeArgs a) {
     X(1, 2, 4, 2, 1, 6, 3, 6)  \
     X(1, 2, 1, 12, 1, 1, 1, 4)
 
+// The fused forms of the decode step (bf16): (FORM, PAIRED, SW, MT, WR, WK,
+// RBW, T, DP, STG).
+#define W4G64_PIPE_FUSED_SHAPES(X)                   \
+    X(kNormBf16, true, 4, 1, 4, 1, 2, 3, 3, 1)       \
+    X(kNormBf16, true, 4, 1, 2, 1, 2, 3, 3, 1)       \
+    X(kPlain, true, 4, 1, 4, 1, 2, 3, 3, 1)          \
+    X(kNormParts, false, 4, 1, 4, 1, 1, 3, 3, 1)     \
+    X(kNormParts, false, 4, 1, 2, 3, 1, 1, 1, 1)     \
+    X(kNormParts, false, 4, 1, 1, 3, 1, 1, 1, 1)     \
+    X(kPlanes3, false, 2, 1, 1, 7, 1, 5, 5, 8)       \
+    X(kPlanes3, false, 2, 1, 2, 7, 1, 1, 1, 1)       \
+    X(kPlanes3, false, 1, 1, 1, 7, 1, 5, 5, 4)       \
+    X(kPlanes3, false, 2, 1, 1, 7, 1, 2, 2, 3)
+
 typedef void (*PipeKernel)(PipeArgs);
 struct PipeEntry {
-    int sw, mt, wr, wk, rbw, t, dp, stg;
+    int form, paired, sw, mt, wr, wk, rbw, t, dp, stg;
     PipeKernel f16, bf16;
 };
 
-#define W4G64_PIPE_ENTRY(SW, MT, WR, WK, RBW, T, DP, STG)                              \
-    {SW, MT, WR, WK, RBW, T, DP, STG, gemv_pipe_kernel<kF16, SW, MT, WR, WK, RBW, T, DP, STG>, \
-     gemv_pipe_kernel<kBF16, SW, MT, WR, WK, RBW, T, DP, STG>},
+#define W4G64_PIPE_ENTRY(SW, MT, WR, WK, RBW, T, DP, STG)                                              \
+    {kPlain, 0, SW, MT, WR, WK, RBW, T, DP, STG,                                                       \
+     gemv_pipe_kernel<kF16, kPlain, false, SW, MT, WR, WK, RBW, T, DP, STG>,                           \
+     gemv_pipe_kernel<kBF16, kPlain, false, SW, MT, WR, WK, RBW, T, DP, STG>},
+#define W4G64_PIPE_FUSED_ENTRY(FORM, PAIRED, SW, MT, WR, WK, RBW, T, DP, STG)                          \
+    {FORM, PAIRED ? 1 : 0, SW, MT, WR, WK, RBW, T, DP, STG, nullptr,                                   \
+     gemv_pipe_kernel<kBF16, FORM, PAIRED, SW, MT, WR, WK, RBW, T, DP, STG>},
 
 const PipeEntry kPipeTable[] = {
     W4G64_PIPE_SHAPES(W4G64_PIPE_ENTRY)
+    W4G64_PIPE_FUSED_SHAPES(W4G64_PIPE_FUSED_ENTRY)
 #ifdef W4G64_PIPE_EXTRA_SHAPES  // tuning builds: more shapes, fp16 only
 #define W4G64_PIPE_ENTRY_F16(SW, MT, WR, WK, RBW, T, DP, STG) \
-    {SW, MT, WR, WK, RBW, T, DP, STG, gemv_pipe_kernel<kF16, SW, MT, WR, WK, RBW, T, DP, STG>, nullptr},
+    {kPlain, 0, SW, MT, WR, WK, RBW, T, DP, STG, gemv_pipe_kernel<kF16, kPlain, false, SW, MT, WR, WK, RBW, T, DP, STG>, nullptr},
     W4G64_PIPE_EXTRA_SHAPES(W4G64_PIPE_ENTRY_F16)
+#endif
+#ifdef W4G64_PIPE_EXTRA_FUSED_SHAPES  // tuning builds: more fused shapes
+    W4G64_PIPE_EXTRA_FUSED_SHAPES(W4G64_PIPE_FUSED_ENTRY)
 #endif
 };
 
 const PipeEntry* find_pipe(const GemvPlan& plan) {
     for (const PipeEntry& e : kPipeTable)
-        if (e.sw == plan.segments && e.mt == plan.tiles && e.wr == plan.fblocks && e.wk == plan.kparts &&
-            e.rbw == plan.rbw && e.t == plan.steps && e.dp == plan.depth && e.stg == plan.stage)
+        if (e.form == plan.form && e.paired == plan.pair && e.sw == plan.segments && e.mt == plan.tiles &&
+            e.wr == plan.fblocks && e.wk == plan.kparts && e.rbw == plan.rbw && e.t == plan.steps &&
+            e.dp == plan.depth && e.stg == plan.stage)
             return &e;
     return nullptr;
 }
@@ -529,23 +677,30 @@ const PipeEntry* find_pipe(const GemvPlan& plan) {
 constexpr int64_t kPipeMaxLds = 160 * 1024;  // gfx950: the whole LDS of a CU per workgroup
 
 // Fills the derived fields of a pipelined plan (tiles, blocks, splits, LDS,
-// workspace, staging loads) from its shape; false if it does not fit.
+// workspace, staging loads) from its shape and form; false if it does not
+// fit.
 bool finish_pipe_plan(int64_t rows, int64_t out_features, int64_t in_features, GemvPlan& plan) {
     const int64_t P = in_features / 128;
     const int sw = plan.segments, wr = plan.fblocks, wk = plan.kparts, rbw = plan.rbw, t = plan.steps;
     if (rows < 1 || rows > kGemvMaxRows || in_features % 128 || sw < 1 || 16 % sw) return false;
-    if (2 * rows * sw > 16 * plan.tiles) return false;
+    const int64_t staged = rows * (plan.form == kPlanes3 ? 3 : 1);
+    if (2 * staged * sw > 16 * plan.tiles) return false;
+    const bool norm = plan.form == kNormBf16 || plan.form == kNormParts;
+    if (norm && rows != 1) return false;
+    if (plan.pair && (rbw != 2 || wk != 1 || out_features % 2)) return false;
     const int64_t span = (int64_t)wk * sw * t;  // pairs per workgroup K range
     const int64_t splits = (P + span - 1) / span;
+    if ((norm || plan.pair) && splits != 1) return false;  // the whole row, the whole (gate, up) pair
     plan.splits = (int)splits;
     plan.groups_per_split = (int)span;  // pairs per split (PS)
-    const int64_t rwg = (int64_t)wr * rbw * (16 / sw);
-    plan.n_blocks = (int)((out_features + rwg - 1) / rwg);
-    const int64_t items = rows * (span < P ? span : P) * 16;
+    const int64_t rows_per_block = (int64_t)wr * (16 / sw);
+    plan.n_blocks = plan.pair ? (int)((out_features / 2 + rows_per_block - 1) / rows_per_block)
+                              : (int)((out_features + rows_per_block * rbw - 1) / (rows_per_block * rbw));
+    const int64_t items = staged * (span < P ? span : P) * 16;
     const int64_t threads = (int64_t)wr * wk * 64;
     if (items > (int64_t)plan.stage * threads) return false;
-    const int red = pipe_red_floats((int)rows, sw, wr, wk, rbw);
-    plan.lds_bytes = pipe_layout((int)rows, (int)span, red).total;
+    const int red = pipe_red_floats((int)staged, sw, wr, wk, rbw);
+    plan.lds_bytes = pipe_layout((int)staged, (int)span, red).total;
     if (plan.lds_bytes > kPipeMaxLds) return false;
     plan.workspace_bytes = splits > 1 ? splits * rows * out_features * 4 : 0;
     plan.kind = 4;
@@ -597,10 +752,60 @@ bool plan_pipe(int64_t rows, int64_t out_features, int64_t in_features, int x_ki
             continue;
         const PipeEntry* best = nullptr;
         for (const PipeEntry& e : kPipeTable) {
-            if (e.sw != sh.sw || e.mt != sh.mt || e.wr != sh.wr || e.wk != sh.wk || e.rbw != sh.rbw || e.t != sh.t ||
-                e.dp != sh.dp || !e.bf16)
+            if (e.form != kPlain || e.paired || e.sw != sh.sw || e.mt != sh.mt || e.wr != sh.wr || e.wk != sh.wk ||
+                e.rbw != sh.rbw || e.t != sh.t || e.dp != sh.dp || !e.bf16 || !e.f16)
                 continue;
             GemvPlan cand{};
+            cand.segments = e.sw;
+            cand.tiles = e.mt;
+            cand.fblocks = e.wr;
+            cand.kparts = e.wk;
+            cand.rbw = e.rbw;
+            cand.steps = e.t;
+            cand.depth = e.dp;
+            cand.stage = e.stg;
+            if (finish_pipe_plan(rows, out_features, in_features, cand) && (!best || e.stg < best->stg)) {
+                best = &e;
+                plan = cand;
+            }
+        }
+        if (best) return true;
+    }
+    return false;
+}
+
+// The decode step's fused forms (bf16, out_features rows; paired: gate rows
+// then up rows): one shape each, picked from the same forced-shape sweeps.
+// The RMSNorm and paired forms need the whole K range in one workgroup.
+struct PipeFusedShape {
+    int form;
+    bool paired;
+    int min_rows, max_rows;
+    int64_t max_pairs;
+    int sw, mt, wr, wk, rbw, t, dp;
+};
+const PipeFusedShape kPipeFusedShapes[] = {
+    {kNormBf16, true, 1, 1, 12, 4, 1, 4, 1, 2, 3, 3},
+    {kPlain, true, 1, 1, 12, 4, 1, 4, 1, 2, 3, 3},
+    {kNormParts, false, 1, 1, 12, 4, 1, 2, 3, 1, 1, 1},
+    {kPlanes3, false, 1, 1, 1 << 20, 2, 1, 2, 7, 1, 1, 1},
+};
+
+bool plan_pipe_fused(int form, bool paired, int64_t rows, int64_t out_features, int64_t in_features,
+                     GemvPlan& plan) {
+    if (in_features % 256) return false;
+    const int64_t P = in_features / 128;
+    for (const PipeFusedShape& sh : kPipeFusedShapes) {
+        if (sh.form != form || sh.paired != paired || rows < sh.min_rows || rows > sh.max_rows || P > sh.max_pairs)
+            continue;
+        const PipeEntry* best = nullptr;
+        for (const PipeEntry& e : kPipeTable) {
+            if (e.form != form || e.paired != (paired ? 1 : 0) || e.sw != sh.sw || e.mt != sh.mt || e.wr != sh.wr ||
+                e.wk != sh.wk || e.rbw != sh.rbw || e.t != sh.t || e.dp != sh.dp || !e.bf16)
+                continue;
+            GemvPlan cand{};
+            cand.form = form;
+            cand.pair = paired ? 1 : 0;
             cand.segments = e.sw;
             cand.tiles = e.mt;
             cand.fblocks = e.wr;
@@ -623,9 +828,14 @@ bool pipe_supported(const LinearProblem& p) {
     // zero bytes are read as the aligned 16-bit words holding them: with an
     // even pair count per row (in_features a multiple of 256) every row's
     // bytes start at an even index, and no word reaches past its row
-    return (p.x_kind == kF16 || p.x_kind == kBF16) && p.in_features % 256 == 0 && ((uintptr_t)p.qweight % 16) == 0 &&
-           ((uintptr_t)p.x % 16) == 0 && ((uintptr_t)p.scales % 4) == 0 && ((uintptr_t)p.zeros % 2) == 0 &&
-           !p.paired && p.norm_delta == nullptr;
+    const bool norm = p.x_kind == kNormB || p.x_kind == kNormP || p.x_kind == kNormF;
+    if (!(p.x_kind == kF16 || p.x_kind == kBF16 || p.x_kind == kPlanes || norm)) return false;
+    if (p.paired && p.x_kind == kF16) return false;  // the fused forms are bf16
+    if (norm &&
+        (((uintptr_t)p.norm_delta % 16) || ((uintptr_t)p.norm_weight % 16) || ((uintptr_t)p.norm_out_sum % 16)))
+        return false;
+    return p.in_features % 256 == 0 && ((uintptr_t)p.qweight % 16) == 0 && ((uintptr_t)p.x % 16) == 0 &&
+           ((uintptr_t)p.scales % 4) == 0 && ((uintptr_t)p.zeros % 2) == 0;
 }
 
 bool pipe_plan_launchable(const GemvPlan& plan) { return find_pipe(plan) != nullptr; }
@@ -642,8 +852,15 @@ hipError_t launch_gemv_pipe(const LinearProblem& p, const GemvPlan& plan, void* 
     a.bias = p.bias;
     a.bias_kind = p.bias_kind;
     a.y = p.y;
-    a.M = (int)p.rows;
+    a.Mo = (int)p.rows;
+    a.M = (int)p.rows * (plan.form == kPlanes3 ? 3 : 1);
     a.N = (int)p.out_features;
+    a.I = (int)(p.out_features / 2);
+    a.delta = p.norm_delta;
+    a.delta_parts = p.norm_delta_parts;
+    a.norm_w = p.norm_weight;
+    a.eps = p.norm_eps;
+    a.out_sum = (uint16_t*)p.norm_out_sum;
     a.K = (int)p.in_features;
     a.G = a.K / 64;
     a.P = a.G / 2;
@@ -654,12 +871,18 @@ hipError_t launch_gemv_pipe(const LinearProblem& p, const GemvPlan& plan, void* 
     a.partials = unreduced ? p.partials_out : (plan.splits > 1 ? (float*)workspace : nullptr);
     if (plan.splits > 1 && !a.partials) return hipErrorInvalidValue;
     PipeKernel k = p.x_kind == kF16 ? e->f16 : e->bf16;
-    if (!k) return hipErrorInvalidValue;
+    if (!k || (plan.pair != 0) != (p.paired != 0)) return hipErrorInvalidValue;
+    // an fp32 delta is the one-part case of the partial-sums form
+    const int want_form = p.x_kind == kPlanes                       ? kPlanes3
+                          : p.x_kind == kNormB                      ? kNormBf16
+                          : (p.x_kind == kNormP || p.x_kind == kNormF) ? kNormParts
+                                                                      : kPlain;
+    if (want_form != plan.form || (plan.pair && (split || unreduced))) return hipErrorInvalidValue;
     const dim3 grid(plan.n_blocks, plan.splits), block(plan.fblocks * plan.kparts * 64);
     hipError_t err = launch_kernel(k, grid, block, (size_t)plan.lds_bytes, stream, start, split ? nullptr : stop, a);
     if (err != hipSuccess || !split) return err;
-    return launch_split_reduce(a.partials, p.bias, p.bias_kind, p.y, a.M, a.N, plan.splits, false, p.x_kind, stream,
-                               stop);
+    return launch_split_reduce(a.partials, p.bias, p.bias_kind, p.y, a.Mo, a.N, plan.splits, false,
+                               plan.form == kPlanes3 ? kF32 : p.x_kind, stream, stop);
 }
 
 }  // namespace w4g64

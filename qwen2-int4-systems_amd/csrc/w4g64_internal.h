@@ -54,6 +54,8 @@ struct GemvPlan {
     int stage = 1;         // kind 2, 4: staging loads per lane
     int rbw = 1;           // kind 4: row blocks per wave
     int depth = 1;         // kind 4: steps of loads kept in flight
+    int form = 0;          // kind 4: activation form (0 plain, 1 bf16 planes, 2 / 3 RMSNorm with bf16 / fp32-parts delta)
+    int pair = 0;          // kind 4: paired gate|up epilogue (SiLU-product planes)
     int64_t lds_bytes;     // dynamic LDS per workgroup
     int64_t workspace_bytes;
 };
@@ -106,6 +108,16 @@ hipError_t launch_gemv_seg_norm_planes(const LinearProblem& p, const GemvPlan& p
 // kernel (or, with partials_out, left to the caller).
 bool finish_pipe_plan(int64_t rows, int64_t out_features, int64_t in_features, GemvPlan& plan);
 bool plan_pipe(int64_t rows, int64_t out_features, int64_t in_features, int x_kind, GemvPlan& plan);
+// Activation forms of the pipelined kernel (GemvPlan::form); each may be
+// paired (gate rows then up rows, SiLU-product planes out).
+enum PipeForm : int {
+    kPlain = 0,      // fp16 / bf16 rows
+    kPlanes3 = 1,    // three bf16 planes [3][Mo][K] (hi + mid + lo), staged as 3 Mo rows, summed; fp32 out
+    kNormBf16 = 2,   // RMSNorm(residual + bf16 delta), one row
+    kNormParts = 3,  // RMSNorm(residual + sum of fp32 partial sums), one row
+};
+bool plan_pipe_fused(int form, bool paired, int64_t rows, int64_t out_features, int64_t in_features,
+                     GemvPlan& plan);
 bool pipe_supported(const LinearProblem& p);
 bool pipe_plan_launchable(const GemvPlan& plan);
 hipError_t launch_gemv_pipe(const LinearProblem& p, const GemvPlan& plan, void* workspace, hipStream_t stream,

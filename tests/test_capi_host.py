@@ -203,13 +203,21 @@ def test_gate_up_planes_and_planes_form_reject_before_launch():
     assert lib.w4g64_linear(p, planes, p, p, p, null, 0, p, 17, 64, 64, null, 0, null) == _lib.STATUS_INVALID_VALUE
     assert lib.w4g64_linear(p, planes, p, p, p, null, 0, ctypes.c_void_p(base + 2), 1, 64, 64, null, 0,
                             null) == _lib.STATUS_INVALID_VALUE
-    # queries: decode rows only.  The planes are 3 M virtual A rows (4 segments
-    # at M = 1), so the 1536 x 8960 down projection splits K 6 ways (fp32
-    # partials); the paired gate|up needs no split
-    assert lib.w4g64_linear_kernel_name(1, 1536, 8960, planes) == b"gemv_kernel<planes_bf16,4,6,1>"
+    # queries: decode rows only.  One row runs the pipelined kernel: the planes
+    # are 3 staged rows, two segments of 7 K parts of one pair each, so the
+    # 1536 x 8960 down projection (70 pairs) splits K 5 ways (fp32 partials)
+    # and its workspace is the larger need of the two decode kernels (the
+    # other splits 6 ways); the paired gate|up needs no split.  Two rows run
+    # the earlier kernels.
+    assert lib.w4g64_linear_kernel_name(1, 1536, 8960, planes) == b"gemv_pipe_kernel<planes_bf16,2,1,2,7,1,1,1>"
+    assert lib.w4g64_linear_partial_count(1, 1536, 8960, planes) == 5
     assert lib.w4g64_linear_workspace_bytes(1, 1536, 8960, planes) == 6 * 1536 * 4
-    assert lib.w4g64_linear_kernel_name(1, 17920, 1536, _lib.DTYPE_BF16_GATE_UP) == b"gemv_kernel<bf16,4,6,1>"
+    assert lib.w4g64_linear_kernel_name(1, 17920, 1536, _lib.DTYPE_BF16_GATE_UP) == \
+        b"gemv_pipe_kernel<bf16_gate_up,4,1,4,1,2,3,3>"
     assert lib.w4g64_linear_workspace_bytes(1, 17920, 1536, _lib.DTYPE_BF16_GATE_UP) == 0
+    assert lib.w4g64_linear_kernel_name(2, 1536, 8960, planes) == b"gemv_kernel<planes_bf16,2,9,1>"
+    assert lib.w4g64_linear_partial_count(2, 1536, 8960, planes) == 10
+    assert lib.w4g64_linear_kernel_name(4, 17920, 1536, _lib.DTYPE_BF16_GATE_UP) == b"gemv_kernel<bf16,4,6,1>"
     assert lib.w4g64_linear_kernel_name(17, 1536, 8960, planes) == b"none"
     assert lib.w4g64_linear_workspace_bytes(17, 17920, 1536, _lib.DTYPE_BF16_GATE_UP) == 0
     # the fused RMSNorm linear: one row, bf16/fp32 delta, out_sum apart from the residual, even planes rows
