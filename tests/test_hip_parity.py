@@ -219,6 +219,24 @@ def test_lean_decode_kernel(n, k, kind, rows, dtype):
         assert np.mean(np.abs(out - ref) <= ulp) > 0.99
 
 
+@pytest.mark.parametrize("dtype", ["fp16", "bf16"])
+@pytest.mark.parametrize("rows", [1, 3])
+def test_pipe_kernel_two_row_blocks_per_wave(rows, dtype):
+    """32768+ output features at 1..4 rows: each wave of the pipelined kernel
+    owns two row blocks, so the codes of one block are formed right before
+    their MFMAs -- the schedule in which an operand written without the
+    MFMA's wait states once corrupted every second block of bf16 rows."""
+    from qwen_int4_hip import linear_kernel_name
+
+    n, k = 32768, 1536
+    torch_dtype = torch.float16 if dtype == "fp16" else torch.bfloat16
+    name = linear_kernel_name(rows, n, k, torch_dtype)
+    assert name.startswith("gemv_pipe_kernel") and name.split(",")[5] == "2", name  # RBW = 2
+    q, s, z = weights("asym", n, k, O.BASE_SEED + 7 * rows)
+    x = O.activations(rows, k, seed=O.BASE_SEED + 17 * rows, dtype=dtype, outliers=True)
+    check_linear(x, q, s, z, None, n, k, dtype)
+
+
 @pytest.mark.parametrize("name", ["gate_proj", "q_proj"])
 def test_lean_and_segmented_kernels_agree(name):
     """The same problem through the pipelined kernel and, with a scales view
