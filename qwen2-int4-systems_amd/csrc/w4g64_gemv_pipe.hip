@@ -92,12 +92,12 @@ __host__ __device__ inline PipeLayout pipe_layout(int M, int PS, int red_floats)
     return L;
 }
 
-// Floats of the epilogue's reduction area: one K part per workgroup and
-// several segments -- a private [RBW][M][R][SW] area per wave (no
-// workgroup barrier); several K parts -- [WK][M][rows][SW] shared by the
-// workgroup; one K part and one segment -- none (every lane stores its own).
-__host__ __device__ constexpr int pipe_red_floats(int M, int SW, int WR, int WK, int RBW) {
-    return WK == 1 ? (SW == 1 ? 0 : WR * RBW * M * (16 / SW) * SW) : WK * M * (WR * RBW * (16 / SW)) * SW;
+// Floats of the epilogue's reduction area: one K part per workgroup -- a
+// private [RBW][M][R][SW] area per wave (no workgroup barrier), or none when
+// every lane stores its own outputs (`direct`: one segment, plain rows, no
+// pairing); several K parts -- [WK][M][rows][SW] shared by the workgroup.
+__host__ __device__ constexpr int pipe_red_floats(int M, int SW, int WR, int WK, int RBW, bool direct) {
+    return WK == 1 ? (direct ? 0 : WR * RBW * M * (16 / SW) * SW) : WK * M * (WR * RBW * (16 / SW)) * SW;
 }
 
 __device__ __forceinline__ void lds_barrier() {
@@ -185,7 +185,7 @@ __global__ __launch_bounds__(WR * WK * 64) void gemv_pipe_kernel(PipeArgs a) {
     const int pe = min(p0 + a.PS, P);        // end of its range
     const int ps = pe - p0;                  // pairs staged (>= 1)
     const int row0 = blockIdx.x * RWG;
-    const PipeLayout L = pipe_layout(M, a.PS, pipe_red_floats(M, SW, WR, WK, RBW));
+    const PipeLayout L = pipe_layout(M, a.PS, pipe_red_floats(M, SW, WR, WK, RBW, SW == 1 && PL == 1 && !PAIRED));
     W4G64_TIMELINE_DECL;
     W4G64_STAMP(0);
 
@@ -625,16 +625,10 @@ __global__ __launch_bounds__(WR * WK * 64) void gemv_pipe_kernel(PipeArgs a) {
 // The fused forms of the decode step (bf16): (FORM, PAIRED, SW, MT, WR, WK,
 // RBW, T, DP, STG).
 #define W4G64_PIPE_FUSED_SHAPES(X)                   \
-    X(kNormBf16, true, 4, 1, 4, 1, 2, 3, 3, 1)       \
-    X(kNormBf16, true, 4, 1, 2, 1, 2, 3, 3, 1)       \
+    X(kNormBf16, true, 4, 1, 4, 1, 2, 3, 1, 1)       \
     X(kPlain, true, 4, 1, 4, 1, 2, 3, 3, 1)          \
     X(kNormParts, false, 4, 1, 4, 1, 1, 3, 3, 1)     \
-    X(kNormParts, false, 4, 1, 2, 3, 1, 1, 1, 1)     \
-    X(kNormParts, false, 4, 1, 1, 3, 1, 1, 1, 1)     \
-    X(kPlanes3, false, 2, 1, 1, 7, 1, 5, 5, 8)       \
-    X(kPlanes3, false, 2, 1, 2, 7, 1, 1, 1, 1)       \
-    X(kPlanes3, false, 1, 1, 1, 7, 1, 5, 5, 4)       \
-    X(kPlanes3, false, 2, 1, 1, 7, 1, 2, 2, 3)
+    X(kPlanes3, false, 2, 1, 4, 1, 1, 7, 4, 3)
 
 typedef void (*PipeKernel)(PipeArgs);
 struct PipeEntry {
@@ -699,7 +693,7 @@ bool finish_pipe_plan(int64_t rows, int64_t out_features, int64_t in_features, G
     const int64_t items = staged * (span < P ? span : P) * 16;
     const int64_t threads = (int64_t)wr * wk * 64;
     if (items > (int64_t)plan.stage * threads) return false;
-    const int red = pipe_red_floats((int)staged, sw, wr, wk, rbw);
+    const int red = pipe_red_floats((int)staged, sw, wr, wk, rbw, sw == 1 && plan.form != kPlanes3 && !plan.pair);
     plan.lds_bytes = pipe_layout((int)staged, (int)span, red).total;
     if (plan.lds_bytes > kPipeMaxLds) return false;
     plan.workspace_bytes = splits > 1 ? splits * rows * out_features * 4 : 0;
@@ -775,8 +769,13 @@ bool plan_pipe(int64_t rows, int64_t out_features, int64_t in_features, int x_ki
 }
 
 // The decode step's fused forms (bf16, out_features rows; paired: gate rows
-// then up rows): one shape each, picked from the same forced-shape sweeps.
-// The RMSNorm and paired forms need the whole K range in one workgroup.
+// then up rows): one shape each, from forced-shape sweeps of the Qwen2-1.5B
+// decode step at one row over cold weights, graph-replayed: RMSNorm + gate|up
+// 17920x1536 6.8 us (7.3 with three chunks in flight per row block), the
+// planes down projection 1536x8960 into five partial sums 4.4 us (5.3 with
+// seven K parts per workgroup), RMSNorm over five partial sums + q|k|v
+// 2048x1536 4.1 us (4.6 with three K parts).  The RMSNorm and paired forms
+// need the whole K range in one workgroup.
 struct PipeFusedShape {
     int form;
     bool paired;
@@ -785,10 +784,10 @@ struct PipeFusedShape {
     int sw, mt, wr, wk, rbw, t, dp;
 };
 const PipeFusedShape kPipeFusedShapes[] = {
-    {kNormBf16, true, 1, 1, 12, 4, 1, 4, 1, 2, 3, 3},
+    {kNormBf16, true, 1, 1, 12, 4, 1, 4, 1, 2, 3, 1},
     {kPlain, true, 1, 1, 12, 4, 1, 4, 1, 2, 3, 3},
-    {kNormParts, false, 1, 1, 12, 4, 1, 2, 3, 1, 1, 1},
-    {kPlanes3, false, 1, 1, 1 << 20, 2, 1, 2, 7, 1, 1, 1},
+    {kNormParts, false, 1, 1, 12, 4, 1, 4, 1, 1, 3, 3},
+    {kPlanes3, false, 1, 1, 1 << 20, 2, 1, 4, 1, 1, 7, 4},
 };
 
 bool plan_pipe_fused(int form, bool paired, int64_t rows, int64_t out_features, int64_t in_features,

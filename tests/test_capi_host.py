@@ -204,12 +204,12 @@ def test_gate_up_planes_and_planes_form_reject_before_launch():
     assert lib.w4g64_linear(p, planes, p, p, p, null, 0, ctypes.c_void_p(base + 2), 1, 64, 64, null, 0,
                             null) == _lib.STATUS_INVALID_VALUE
     # queries: decode rows only.  One row runs the pipelined kernel: the planes
-    # are 3 staged rows, two segments of 7 K parts of one pair each, so the
-    # 1536 x 8960 down projection (70 pairs) splits K 5 ways (fp32 partials)
-    # and its workspace is the larger need of the two decode kernels (the
-    # other splits 6 ways); the paired gate|up needs no split.  Two rows run
-    # the earlier kernels.
-    assert lib.w4g64_linear_kernel_name(1, 1536, 8960, planes) == b"gemv_pipe_kernel<planes_bf16,2,1,2,7,1,1,1>"
+    # are 3 staged rows, two segments of 7 steps of one pair each per wave, so
+    # the 1536 x 8960 down projection (70 pairs) splits K 5 ways (fp32
+    # partials) and its workspace is the larger need of the two decode
+    # kernels (the other splits 6 ways); the paired gate|up needs no split.
+    # Two rows run the earlier kernels.
+    assert lib.w4g64_linear_kernel_name(1, 1536, 8960, planes) == b"gemv_pipe_kernel<planes_bf16,2,1,4,1,1,7,4>"
     assert lib.w4g64_linear_partial_count(1, 1536, 8960, planes) == 5
     assert lib.w4g64_linear_workspace_bytes(1, 1536, 8960, planes) == 6 * 1536 * 4
     assert lib.w4g64_linear_kernel_name(1, 17920, 1536, _lib.DTYPE_BF16_GATE_UP) == \
