@@ -2,7 +2,13 @@
 the reference's explicit backend selection (src/qwen_int4/backends.py,
 src/qwen_int4/linear.py)."""
 
-from .backends import SUPPORTED_BACKENDS, hip_w4g64_linear, validate_canonical_w4g64_inputs
+from .backends import (
+    SUPPORTED_BACKENDS,
+    hip_w4g64_linear,
+    lpu_w4g64_linear,
+    torch_w4g64_linear,
+    validate_canonical_w4g64_inputs,
+)
 from .kernels import (
     dequantize_canonical_w4g64_hip,
     hip_available,
@@ -32,6 +38,8 @@ __all__ = [
     "dequantize_canonical_w4g64_hip",
     "hip_available",
     "hip_w4g64_linear",
+    "lpu_w4g64_linear",
+    "torch_w4g64_linear",
     "linear_canonical_w4g64_hip",
     "linear_kernel_name",
     "unpack_canonical_signed_int4_hip",

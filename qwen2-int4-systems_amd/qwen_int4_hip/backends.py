@@ -1,10 +1,21 @@
-"""The ``"hip"`` operator backend for quantized linear layers.
+"""Operator backends for quantized linear layers: the reference's registry
+(src/qwen_int4/backends.py:11) plus the ``"hip"`` backend.
 
-Counterpart of the reference's backend registry and Triton dispatch shim
-(src/qwen_int4/backends.py:11, :14-70, :153-181).  Selection stays explicit:
-a module picks a backend by name, there is no environment switch and no
-silent fallback -- fp32 activations, which the reference routes to its torch
-oracle (backends.py:172-177), run natively on the HIP kernels here.
+Counterpart of the reference's backend registry and dispatch shims
+(src/qwen_int4/backends.py:11, :14-70, :73-98, :101-150, :153-181).
+Selection stays explicit: a module picks a backend by name, there is no
+environment switch and no silent fallback between arms.
+  * ``"hip"``: the MI355X kernels; fails loudly without a ROCm GPU and the
+    built library.  fp32 activations, which the reference's Triton arm routes
+    to its torch path (backends.py:172-177), run natively here.
+  * ``"torch"``: dequantize the whole weight to fp32, then one fp32 matmul
+    (backends.py:73-98) -- plain PyTorch on whatever device the tensors live.
+  * ``"lpu"``: the reference's A/B/C-dataflow emulation (backends.py:101-150):
+    validated inputs, one fp32 product per 64-wide K group, accumulated in
+    group order.
+  * ``"triton"``: kept in the registry for configuration compatibility; this
+    build has no Triton, so the arm raises (as the reference's does without a
+    Triton installation, backends.py:166-167).
 """
 
 from __future__ import annotations
@@ -12,9 +23,9 @@ from __future__ import annotations
 import torch
 
 from .kernels import hip_available, linear_canonical_w4g64_hip
-from .quantization import PackingFormat
+from .quantization import PackingFormat, dequantize_groupwise, unpack_int4
 
-SUPPORTED_BACKENDS = ("hip",)
+SUPPORTED_BACKENDS = ("torch", "lpu", "triton", "hip")
 
 
 def validate_canonical_w4g64_inputs(
@@ -104,3 +115,75 @@ def hip_w4g64_linear(
         return x.new_empty((*x.shape[:-1], out_features))
     output = linear_canonical_w4g64_hip(x.reshape(-1, in_features).contiguous(), qweight, scales, zeros, bias)
     return output.reshape(*x.shape[:-1], out_features)
+
+
+def torch_w4g64_linear(
+    x: torch.Tensor,
+    qweight: torch.Tensor,
+    scales: torch.Tensor,
+    zeros: torch.Tensor,
+    bias: torch.Tensor | None,
+    *,
+    out_features: int,
+    in_features: int,
+    group_size: int,
+    packing: PackingFormat | str,
+) -> torch.Tensor:
+    """The reference's correctness-first arm (backends.py:73-98): the fp32
+    weight (code - zero) * scale, one fp32 matmul, fp32 bias, cast to
+    ``x.dtype``."""
+    weight = dequantize_groupwise(qweight, scales, zeros=zeros, out_features=out_features,
+                                  in_features=in_features, group_size=group_size, packing=packing)
+    out = torch.matmul(x.reshape(-1, in_features).to(torch.float32), weight.t())
+    if bias is not None:
+        out = out + bias.to(torch.float32)
+    return out.reshape(*x.shape[:-1], out_features).to(x.dtype)
+
+
+def lpu_w4g64_linear(
+    x: torch.Tensor,
+    qweight: torch.Tensor,
+    scales: torch.Tensor,
+    zeros: torch.Tensor,
+    bias: torch.Tensor | None,
+    *,
+    out_features: int,
+    in_features: int,
+    group_size: int,
+    packing: PackingFormat | str,
+) -> torch.Tensor:
+    """The reference's LPU-style dataflow emulation (backends.py:101-150):
+    validated canonical inputs, then per K group an fp32 A tile times the
+    group's dequantized B tile, added into an fp32 C buffer in group order,
+    then the fp32 bias."""
+    packing = validate_canonical_w4g64_inputs(
+        x, qweight, scales, zeros, bias, out_features=out_features, in_features=in_features,
+        group_size=group_size, packing=packing,
+    )
+    groups = in_features // group_size
+    codes = unpack_int4(qweight, packing=packing).reshape(out_features, groups, group_size).to(torch.float32)
+    zero_points = unpack_int4(zeros, packing=packing, elements=out_features * groups).reshape(
+        out_features, groups).to(torch.float32)
+    a = x.reshape(-1, in_features).to(torch.float32)
+    c = torch.zeros((a.shape[0], out_features), dtype=torch.float32, device=x.device)
+    for g in range(groups):
+        b_tile = (codes[:, g, :] - zero_points[:, g:g + 1]) * scales[:, g:g + 1].to(torch.float32)
+        c.add_(torch.matmul(a[:, g * group_size:(g + 1) * group_size], b_tile.t()))
+    if bias is not None:
+        c.add_(bias.to(torch.float32))
+    return c.reshape(*x.shape[:-1], out_features).to(x.dtype)
+
+
+def triton_w4g64_linear(x, qweight, scales, zeros, bias, **kwargs) -> torch.Tensor:
+    """Registry arm of the reference's Triton operator (backends.py:153-181).
+    This build carries no Triton: the arm raises, as the reference's does
+    without a Triton installation (backends.py:166-167)."""
+    raise RuntimeError("Triton backend requires CUDA and a Triton installation; this build provides the 'hip' backend")
+
+
+BACKEND_IMPLEMENTATIONS = {
+    "torch": torch_w4g64_linear,
+    "lpu": lpu_w4g64_linear,
+    "triton": triton_w4g64_linear,
+    "hip": hip_w4g64_linear,
+}

@@ -1,7 +1,9 @@
 """Backend-dispatched quantized linear module (src/qwen_int4/linear.py:17-72).
 
 Same constructor, buffers, shapes and defaults as the reference's
-``QuantLinear``; the dispatch table holds the HIP backend.
+``QuantLinear``, except the default backend: ``"hip"`` here (the reference's
+default is ``"torch"``, linear.py:25).  The dispatch table is the reference's
+(torch, lpu, triton) plus ``"hip"``.
 """
 
 from __future__ import annotations
@@ -9,7 +11,7 @@ from __future__ import annotations
 import torch
 from torch import nn
 
-from .backends import SUPPORTED_BACKENDS, hip_w4g64_linear
+from .backends import BACKEND_IMPLEMENTATIONS, SUPPORTED_BACKENDS
 from .quantization import PackingFormat
 
 
@@ -51,7 +53,7 @@ class QuantLinear(nn.Module):
         self.backend = backend
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        implementation = {"hip": hip_w4g64_linear}[self.backend]
+        implementation = BACKEND_IMPLEMENTATIONS[self.backend]
         return implementation(
             x,
             self.qweight,

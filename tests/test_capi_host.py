@@ -416,7 +416,8 @@ def test_unknown_backend_is_rejected_and_registry_is_explicit():
     layer = QuantLinear(8, 4, group_size=4)
     with pytest.raises(ValueError):
         layer.set_backend("environment-variable-magic")
-    assert SUPPORTED_BACKENDS == ("hip",)
+    assert SUPPORTED_BACKENDS == ("torch", "lpu", "triton", "hip")
+    assert layer.backend == "hip"  # this package's default (the reference's is "torch")
     assert layer.qweight.shape == (16, 1) and layer.scales.shape == (4, 2) and layer.zeros.shape == (4, 1)
     assert QuantLinear(128, 6, group_size=64, bias=True).bias.dtype == torch.bfloat16
 
