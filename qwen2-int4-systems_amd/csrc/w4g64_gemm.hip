@@ -40,15 +40,12 @@
 //     Every 1 KB a wave instruction writes holds 8 tile rows; the 16 B
 //     chunks of a row are XOR-swizzled by a_swizzle(row), which the fragment
 //     reads undo, so fragment reads are conflict-free.
-//   * Stage s holds the activation tile of step s and each wave's packed
-//     weights of step s + 1.  A step walks 32 slots (row block, column
-//     block): the block's 2-MFMA chain over the group (lane group q of 4
-//     takes K values [16 q, 16 q + 16) of the group, MFMA h uses [16 q +
-//     8 h, + 8)), acc += scale * D of the previous slot's block, and an
-//     eighth of the decode of one column block of the NEXT step's (code -
-//     zero) -- an even mix of matrix and vector work in every slot.  The
-//     decoded B alternates between two register sets (two steps unrolled);
-//     the B of step 0 is loaded from global memory in the prologue.
+//   * Per step, a wave decodes its own 64 columns' (code - zero) for the
+//     whole group (4 column blocks x 2 MFMAs), then walks its 8 row blocks:
+//     for each, the four column blocks' 2-MFMA chains over the group (lane
+//     group q of 4 takes K values [16 q, 16 q + 16) of the group, MFMA h
+//     uses [16 q + 8 h, + 8)), then acc += scale * D, issued after the next
+//     row block's MFMAs so the matrix cores and the FMAs overlap.
 //   * Waits are explicit: every step issues the same number of vector memory
 //     operations, so "step s has landed" is a vmcnt bound known at compile
 //     time (steps past the end are not issued; the last waits tighten).
@@ -230,16 +227,14 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
     // cost no vector instructions.  The host keeps the staged rows and the
     // packed weights below 2^31 elements, so the byte offsets fit 32 bits.
     // activations: instruction d writes tile rows [8 (wave kDma + d), +8), 16 B per lane
-    // The staged rows are padded to whole tiles (rows past M hold whatever the
-    // workspace held; their outputs are never stored), so no row is clamped.
-    // Instructions d and d + 2 write rows 16 apart with the same swizzle: two
-    // per-lane offsets, and d / 2 * 16 rows go into the scalar offset.
-    uint32_t a_off[2];
+    uint32_t a_off[kDma];
 #pragma unroll
-    for (int d = 0; d < 2; ++d) {
+    for (int d = 0; d < kDma; ++d) {
         const int r = 8 * (wave * kDma + d) + (lane >> 3);
         const int chunk = (lane & 7) ^ a_swizzle(r);
-        a_off[d] = 2u * ((uint32_t)(m0 + r) * (uint32_t)a.K + 8u * (uint32_t)chunk);
+        int m = (int)m0 + r;
+        m = m < a.M ? m : a.M - 1;  // rows past M load a valid row; their outputs are not stored
+        a_off[d] = 2u * ((uint32_t)m * (uint32_t)a.K + 8u * (uint32_t)chunk);
     }
     // weights: DMA instruction b, lane L -> column nw + 32 b + L % 32, bytes [16 (L / 32), +16)
     const int c = lane & 15;   // this lane's column within a 16-column block / row within a 16-row block
@@ -268,26 +263,21 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
     // sizes): a load's address is the per-lane offset plus a per-step scalar
     // offset, and a step's issue costs scalar instructions only.
     const __amdgpu_buffer_rsrc_t x_rsrc =
-        __builtin_amdgcn_make_buffer_rsrc((void*)a.x, 0, (int)(2u * (uint32_t)(a.tiles_m * kBM) * (uint32_t)a.K), kRsrcWord3);
+        __builtin_amdgcn_make_buffer_rsrc((void*)a.x, 0, (int)(2u * (uint32_t)a.M * (uint32_t)a.K), kRsrcWord3);
     const __amdgpu_buffer_rsrc_t w_rsrc =
         __builtin_amdgcn_make_buffer_rsrc((void*)a.qweight, 0, (int)((uint32_t)a.N * (uint32_t)a.wg * 32u), kRsrcWord3);
     const __amdgpu_buffer_rsrc_t s_rsrc =
         __builtin_amdgcn_make_buffer_rsrc((void*)a.scales, 0, (int)((uint32_t)a.N * (uint32_t)a.wg * 2u), kRsrcWord3);
     const __amdgpu_buffer_rsrc_t z_rsrc =
         __builtin_amdgcn_make_buffer_rsrc((void*)a.zeros, 0, (int)(((uint32_t)a.N * (uint32_t)a.wg + 1u) >> 1), kRsrcWord3);
-    // Stage s holds the activation tile of step s and this wave's packed
-    // weights, scales and zero bytes of step s + 1: each step decodes the next
-    // step's B while it multiplies its own.  Past the last step the weight
-    // loads read an in-range group (or zero-fill past the buffer end); they
-    // are never used.
     auto issue = [&](int gg) {  // callers pass gg < G only
         unsigned char* st = smem[gg % kStages];
-        const int gw = wgroup(gg + 1);
+        const int gw = wgroup(gg);
         const uint32_t z_off = (gw & 1) ? z_off_odd : z_off_even;
 #pragma unroll
         for (int d = 0; d < kDma; ++d)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(x_rsrc, (lds_ptr_t)(st + 1024 * (wave * kDma + d)), 16,
-                                                     a_off[d & 1], 128 * (gbeg + gg) + (d >> 1) * 32 * a.K, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(x_rsrc, (lds_ptr_t)(st + 1024 * (wave * kDma + d)), 16, a_off[d],
+                                                     128 * (gbeg + gg), 0, 0);
 #pragma unroll
         for (int bj = 0; bj < 2; ++bj)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rsrc, (lds_ptr_t)(st + kABytes + 2048 * wave + 1024 * bj), 16,
@@ -311,15 +301,15 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
     const int cpar = c & a.wg & 1;
     const int zsh_even = 4 * cpar, zsh_odd = 4 * (cpar ^ 1);
 
-    // Packed B of column block bj: the 8 bytes = K values [16 kq, 16 kq + 16)
-    // of column nw + 16 bj + c; dword h holds the K slots of MFMA h (K values
-    // 16 kq + 8 h + [0, 8)).
+    // Packed weights of step g for column block bj, read back from the stage:
+    // the 8 bytes = K values [16 kq, 16 kq + 16) of column nw + 16 bj + c;
+    // dword h holds the K slots of MFMA h (K values 16 kq + 8 h + [0, 8)).
     struct BRaw {
         u32x2 w;
         uint32_t sbits;
         uint32_t zb;
     };
-    auto read_b = [&](int g, int bj) {  // from stage g, i.e. the B of step g + 1
+    auto read_b = [&](int g, int bj) {
         const unsigned char* st = smem[g % kStages];
         const int col = 16 * bj + c;  // column within the wave
         BRaw r;
@@ -329,44 +319,23 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
         r.zb = st[kABytes + kWBytes + kSBytes + 256 * wave + 4 * col];
         return r;
     };
-    auto load_b_global = [&](int gw, int bj) {  // the B of step 0, straight from global memory
-        int n = (int)nw + 16 * bj + c;
-        n = n < a.N ? n : a.N - 1;
-        const uint32_t e = (uint32_t)n * (uint32_t)a.wg + (uint32_t)gw;
-        BRaw r;
-        r.w = *(const u32x2*)(a.qweight + (size_t)e * 32 + 8 * kq);
-        r.sbits = a.scales[e];
-        r.zb = a.zeros[e >> 1];
-        return r;
-    };
-    // The zero point's magic offsets for both halves of a pair at once: fp16
-    // bits (1032 + z, 1032 + z) and (72 + z, 72 + z), z in [-8, 7] (no borrow
-    // crosses the halves).
+    // Per-group constants of one column: the zero point's magic offsets and
+    // the scale.  zsh = bit position of the column's zero nibble in its byte.
     struct BConst {
-        half2v zlo;
-        half2v zhi;
+        half2v zlo;  // (1032 + z, 1032 + z)
+        half2v zhi;  // (72 + z, 72 + z)
+        float s;
     };
     auto group_const = [&](int zsh, const BRaw& r) {
         const int zn = __builtin_amdgcn_sbfe((int)r.zb, zsh, 4);  // signed zero point
+        // fp16 bits of 1032 + z (mantissa unit 1) and of 72 + z (mantissa unit 1/16)
+        const _Float16 zl = __builtin_bit_cast(_Float16, (uint16_t)(0x6408 + zn));
+        const _Float16 zh = __builtin_bit_cast(_Float16, (uint16_t)(0x5480 + 16 * zn));
         BConst k;
-        k.zlo = __builtin_bit_cast(half2v, (uint32_t)(zn * 0x00010001) + 0x64086408u);
-        k.zhi = __builtin_bit_cast(half2v, (uint32_t)(zn * 0x00100010) + 0x54805480u);
+        k.zlo = half2v{zl, zl};
+        k.zhi = half2v{zh, zh};
+        k.s = half_bits_to_float((uint16_t)r.sbits);
         return k;
-    };
-    // The group scale as fp32 bits, converted once per group (the FMAs then
-    // take it as a plain fp32 operand).
-    auto scale_bits = [](uint32_t sbits) {
-        uint32_t r = __builtin_bit_cast(uint32_t, half_bits_to_float((uint16_t)sbits));
-        asm volatile("" : "+v"(r));
-        return r;
-    };
-    auto sc_f = [](uint32_t b) { return __builtin_bit_cast(float, b); };
-    // Pair p of a packed dword as (code - zero) fp16: p = 0 (k0, k4), 1 (k1,
-    // k5), 2 (k2, k6), 3 (k3, k7).
-    auto nib_pair = [](uint32_t w, int p, half2v zlo, half2v zhi) {
-        const uint32_t x = (p >= 2) ? (w >> 8) : w;
-        const uint32_t sel = (p & 1) ? nib_select<kSelHi, kMaskHi>(x) : nib_select<kSelLo, kMaskLo>(x);
-        return __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2v, sel) - ((p & 1) ? zhi : zlo));
     };
     // A fragment of row block bi for MFMA h: row 16 bi + c, K values 16 kq +
     // 8 h + [0, 8) = logical chunk 2 kq + h of the swizzled stage row.  The
@@ -382,67 +351,82 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
     };
 
     // ---- software pipeline ----
-    // A step walks 32 slots (row block rb, column block bj): the two MFMAs of
-    // the group's (rb, bj) block, the scaled accumulation of the previous
-    // slot's block, and 1/8 of the decode of one column block of the next
-    // step's B -- so every slot carries a similar mix of matrix and vector
-    // work.  The decoded B alternates between two register sets (the loop is
-    // unrolled by two steps).  Before the last row block: wait for this
-    // wave's loads of step g + 1, workgroup barrier (every wave has finished
-    // reading stage g, and all of step g + 1 has landed), refill of stage g
-    // with step g + 3.  "Step s has landed" for this wave = its vector memory
-    // counter is at most the number of operations issued after step s's
-    // (in-order completion).
+    // Step g: per row block the four column blocks' two-MFMA group chains and
+    // the scaled accumulation of the previous row block, with the A fragments
+    // of the row block two ahead read as soon as the current ones have been
+    // issued; in row block 0 each column block's B (read at the end of step
+    // g - 1) is decoded right before its first MFMA.  Before the last row
+    // block: wait for this wave's loads of step g + 1, workgroup barrier
+    // (every wave has finished reading stage g, and all of step g + 1 has
+    // landed), refill of stage g with step g + 3; after it, the packed B of
+    // step g + 1.
+    // "Step s has landed" for this wave = its vector memory counter is at most
+    // the number of operations issued after step s's (in-order completion).
     const int G = gcnt;  // steps of this workgroup's K range
-    // B of step 0 from global memory, issued ahead of the stage loads (the
-    // wait for it then leaves those in flight)
-    u32x4 fA[4][2], fB[4][2];
-    uint32_t scA[4], scB[4] = {0u, 0u, 0u, 0u};
-    const int gw0 = wgroup(0);
-    BRaw r0[4];
-#pragma unroll
-    for (int bj = 0; bj < 4; ++bj) r0[bj] = load_b_global(gw0, bj);
-    asm volatile("" ::: "memory");
     issue(0);
     if (G > 1) issue(1);
     if (G > 2) issue(2);
-    {
-        const int zsh0 = (gw0 & 1) ? zsh_odd : zsh_even;
-#pragma unroll
-        for (int bj = 0; bj < 4; ++bj) {
-            const BConst k = group_const(zsh0, r0[bj]);
-#pragma unroll
-            for (int h = 0; h < 2; ++h)
-#pragma unroll
-                for (int p = 0; p < 4; ++p) fA[bj][h][p] = nib_pair(r0[bj].w[h], p, k.zlo, k.zhi);
-            scA[bj] = scale_bits(r0[bj].sbits);
-        }
-    }
     if (G > 2) wait_vmcnt<2 * kOpsPerStep>();
     else if (G > 1) wait_vmcnt<kOpsPerStep>();
     else wait_vmcnt<0>();
     block_barrier();
 
-    u32x4 ab[2][2];  // A fragments of row blocks rb (ab[rb & 1]), read one row block ahead
-    ab[0][0] = read_a(smem[0], 0, 0);
-    ab[0][1] = read_a(smem[0], 0, 1);
-    BRaw rbn = read_b(0, 0);  // packed B of step 1, column block 0
-    float4v dd[2];            // group products of the last two slots
-    dd[1] = float4v{0.f, 0.f, 0.f, 0.f};
-
-    // Step g: A(g) times f (the decoded B of step g) with scales sc; decodes
-    // B(g + 1) into fn / scn.  Slot 0's FMA is the previous step's last, whose
-    // scale is still in scn[3] (overwritten only in slot 24).  Past the last
-    // step the decode and the next step's reads work on stale, in-range LDS
-    // data and are never used (no branches in the slots).
-    auto step = [&](const int g, u32x4(&f)[4][2], uint32_t(&sc)[4], u32x4(&fn)[4][2], uint32_t(&scn)[4]) {
-        const unsigned char* st = smem[g % kStages];
-        const int zshn = (wgroup(g + 1) & 1) ? zsh_odd : zsh_even;
-        BConst kn;
-        BRaw rbx;
+    // Packed B of step 0 (every load of the first steps has landed and the
+    // barrier above made them visible).  Stage g is refilled only after step
+    // g's own barrier, so the B of step g + 1 can be read at the end of step
+    // g, after that step's barrier.
+    BRaw rb[4];
 #pragma unroll
-        for (int rb = 0; rb < RB; ++rb) {
-            if (rb + 1 == RB) {
+    for (int bj = 0; bj < 4; ++bj) rb[bj] = read_b(0, bj);
+
+    for (int g = 0; g < G; ++g) {
+        const unsigned char* st = smem[g % kStages];
+        u32x4 f[4][2];  // (code - zero) of the four column blocks, both MFMAs of the group
+        float sc[4];    // the four column scales
+        const int zsh = (wgroup(g) & 1) ? zsh_odd : zsh_even;
+        // A fragments of row blocks bi (ab[bi & 1]), read two row blocks ahead
+        u32x4 ab[2][2];
+        ab[0][0] = read_a(st, 0, 0);
+        ab[0][1] = read_a(st, 0, 1);
+        ab[1][0] = read_a(st, 1, 0);
+        ab[1][1] = read_a(st, 1, 1);
+        // Row block bi's group products D go to dd[bi & 1]; its scaled
+        // accumulation runs after row block bi + 1's MFMAs have been issued,
+        // so the matrix cores and the FMAs of one wave overlap.
+        float4v dd[2][4];
+        auto scale_add = [&](int bi) {
+#pragma unroll
+            for (int bj = 0; bj < 4; ++bj)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    acc[bi][bj][i] = __builtin_fmaf(sc[bj], dd[bi & 1][bj][i], acc[bi][bj][i]);
+            // the empty asm pins the accumulation here (sunk to the end of the
+            // step, it would keep every block's products live)
+#pragma unroll
+            for (int bj = 0; bj < 4; ++bj) asm volatile("" : "+v"(acc[bi][bj]));
+        };
+        // Row block 0: each column block's B is decoded right before its first
+        // MFMA, so the decode of the next column blocks overlaps the products.
+#pragma unroll
+        for (int bj = 0; bj < 4; ++bj) {
+            const BConst k = group_const(zsh, rb[bj]);
+#pragma unroll
+            for (int h = 0; h < 2; ++h) f[bj][h] = decode_codes(rb[bj].w[h], k.zlo, k.zhi);
+            sc[bj] = k.s;
+            dd[0][bj] = mfma(ab[0][0], f[bj][0], float4v{0.f, 0.f, 0.f, 0.f});
+            __builtin_amdgcn_sched_barrier(0);  // keeps the next decode behind this product
+        }
+        ab[0][0] = read_a(st, 2, 0);
+#pragma unroll
+        for (int bj = 0; bj < 4; ++bj) dd[0][bj] = mfma(ab[0][1], f[bj][1], dd[0][bj]);
+        ab[0][1] = read_a(st, 2, 1);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int bi = 1; bi < RB; ++bi) {
+            if (bi + 1 == RB) {
+                // every A read of stage g has been issued; this wave's loads
+                // of step g + 1 have landed once at most those of step g + 2
+                // are outstanding
                 if (g + 2 < G) wait_vmcnt<kOpsPerStep>();
                 else wait_vmcnt<0>();
                 if (g + 1 < G) {
@@ -450,70 +434,26 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
                     block_barrier();
                     if (g + 3 < G) issue(g + 3);
                 }
-            } else {
-                ab[(rb + 1) & 1][0] = read_a(st, rb + 1, 0);
-                ab[(rb + 1) & 1][1] = read_a(st, rb + 1, 1);
             }
+            float4v(&d)[4] = dd[bi & 1];
 #pragma unroll
-            for (int bj = 0; bj < 4; ++bj) {
-                const int t = 4 * rb + bj;
-                if (rb + 1 == RB && bj == 1) {
-                    // the next step's row block 0 and its packed B of column
-                    // block 0 (stage g + 1, visible since the barrier)
-                    ab[0][0] = read_a(smem[(g + 1) % kStages], 0, 0);
-                    ab[0][1] = read_a(smem[(g + 1) % kStages], 0, 1);
-                    rbn = read_b(g + 1, 0);
-                }
-                float4v d = mfma(ab[rb & 1][0], f[bj][0], float4v{0.f, 0.f, 0.f, 0.f});
-                d = mfma(ab[rb & 1][1], f[bj][1], d);
-                dd[t & 1] = d;
-                // scaled accumulation of the previous slot; the empty asm pins
-                // it here (sunk to the end of the step, it would keep every
-                // block's products live)
-                if (t == 0) {
+            for (int bj = 0; bj < 4; ++bj) d[bj] = mfma(ab[bi & 1][0], f[bj][0], float4v{0.f, 0.f, 0.f, 0.f});
+            if (bi + 2 < RB) ab[bi & 1][0] = read_a(st, bi + 2, 0);
 #pragma unroll
-                    for (int i = 0; i < 4; ++i)
-                        acc[RB - 1][3][i] = __builtin_fmaf(sc_f(scn[3]), dd[1][i], acc[RB - 1][3][i]);
-                    asm volatile("" : "+v"(acc[RB - 1][3]));
-                } else {
-                    const int tp = t - 1;
-#pragma unroll
-                    for (int i = 0; i < 4; ++i)
-                        acc[tp >> 2][tp & 3][i] = __builtin_fmaf(sc_f(sc[tp & 3]), dd[tp & 1][i], acc[tp >> 2][tp & 3][i]);
-                    asm volatile("" : "+v"(acc[tp >> 2][tp & 3]));
-                }
-                // decode part t of the next step's B: column block t / 8, part t % 8
-                {
-                    const int bn = t >> 3, p = t & 7;
-                    if (p == 0) {
-                        kn = group_const(zshn, rbn);
-                        scn[bn] = scale_bits(rbn.sbits);
-                        asm volatile("" : "+v"(kn.zlo), "+v"(kn.zhi));
-                        rbx = rbn;
-                        if (bn < 3) rbn = read_b(g, bn + 1);
-                    } else if (p <= 4) {
-                        const int h = (p - 1) >> 1;
-                        const int q = ((p - 1) & 1) * 2;
-                        fn[bn][h][q] = nib_pair(rbx.w[h], q, kn.zlo, kn.zhi);
-                        fn[bn][h][q + 1] = nib_pair(rbx.w[h], q + 1, kn.zlo, kn.zhi);
-                        asm volatile("" : "+v"(fn[bn][h][q]), "+v"(fn[bn][h][q + 1]));
-                    }
-                }
-                __builtin_amdgcn_sched_barrier(0);
-            }
+            for (int bj = 0; bj < 4; ++bj) d[bj] = mfma(ab[bi & 1][1], f[bj][1], d[bj]);
+            if (bi + 2 < RB) ab[bi & 1][1] = read_a(st, bi + 2, 1);
+            scale_add(bi - 1);
+            // the scheduling barrier stops later blocks' reads and products
+            // from being hoisted (registers the accumulators need)
+            __builtin_amdgcn_sched_barrier(0);
         }
-    };
-    int g = 0;
-    for (; g + 1 < G; g += 2) {
-        step(g, fA, scA, fB, scB);
-        step(g + 1, fB, scB, fA, scA);
-    }
-    if (g < G) step(g, fA, scA, fB, scB);
-    {
-        // the last slot's accumulation (scales of the last step)
-        const uint32_t s_last = (G & 1) ? scA[3] : scB[3];
+        // packed B of step g + 1 (visible since this step's barrier); its LDS
+        // reads are in flight during the last row block's accumulation
+        if (g + 1 < G) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[RB - 1][3][i] = __builtin_fmaf(sc_f(s_last), dd[1][i], acc[RB - 1][3][i]);
+            for (int bj = 0; bj < 4; ++bj) rb[bj] = read_b(g + 1, bj);
+        }
+        scale_add(RB - 1);
     }
     wait_vmcnt<0>();  // no DMA may still target this workgroup's LDS at exit
 
@@ -895,8 +835,7 @@ GemmPlan plan_gemm(int64_t rows, int64_t out_features, int64_t k_staged) {
 bool two_planes(int x_kind) { return x_kind == kF32 || x_kind == kSwiGLU; }
 
 // Workspace: [split-tile partials][staged fp16 rows][row factors], each part
-// 256-byte aligned; the staged rows and row factors cover tiles_m * kBM rows
-// (the GEMM reads whole tiles of staged rows; rows past M are never stored).
+// 256-byte aligned; the staged rows and row factors cover tiles_m * kBM rows.
 struct GemmLayout {
     GemmPlan plan;
     int64_t staged_offset, rowscale_offset, bytes;
@@ -908,7 +847,7 @@ GemmLayout gemm_layout(int64_t rows, int64_t out_features, int64_t in_features, 
     const int64_t padded_rows = (int64_t)l.plan.tiles_m * kBM;
     auto up256 = [](int64_t v) { return (v + 255) / 256 * 256; };
     l.staged_offset = up256(l.plan.partial_bytes);
-    l.rowscale_offset = l.staged_offset + up256(padded_rows * k_staged * 2);
+    l.rowscale_offset = l.staged_offset + up256(rows * k_staged * 2);
     l.bytes = l.rowscale_offset + padded_rows * 4;
     return l;
 }
