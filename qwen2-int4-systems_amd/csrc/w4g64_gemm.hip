@@ -790,8 +790,10 @@ int gemm_slots() {
 // Choose data-parallel tiles and K splits.  Measured on MI355X: a K step
 // costs ~1.0 us with one workgroup per CU and ~1.54 us for the two that
 // share a CU; a round of workgroups costs ~6 us fixed (launch, pipeline
-// fill, epilogue); the reduction kernel ~2 us plus its partial-sum reads at
-// ~5 TB/s.  Full rounds of tiles stay data-parallel; the tiles of a last,
+// fill, epilogue); the reduction kernel ~2 us plus the partial sums at ~2.5
+// bytes per ns (written by the GEMM, read back by the reduction: at 5 the
+// model split gate 8960x1536 at 128 rows into 6 K ranges, which measured
+// 29.1 us against 27.2 us for 4).  Full rounds of tiles stay data-parallel; the tiles of a last,
 // less than half full round -- or all tiles, when there are fewer than the
 // workgroup slots -- are split into the K-range count with the lowest
 // modelled time.
@@ -815,7 +817,7 @@ GemmPlan plan_gemm(int64_t rows, int64_t out_features, int64_t k_staged) {
         for (int sp = 2; sp <= G && rem * sp <= slots; ++sp) {
             const int gps = (G + sp - 1) / sp;
             const int used = (G + gps - 1) / gps;
-            const double t = 6.0 + gps * step_us(rem * used) + 2.0 + (double)rem * used * kBM * kBN * 4 / 5e6;
+            const double t = 6.0 + gps * step_us(rem * used) + 2.0 + (double)rem * used * kBM * kBN * 4 / 2.5e6;
             if (t < best) {
                 best = t;
                 pl.splits = used;
