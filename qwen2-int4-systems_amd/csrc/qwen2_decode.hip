@@ -430,17 +430,18 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
     }
     W4G64_STAMP(5);
     // After the acquire, plain loads see every other workgroup's partials.
-    // The merge issues them all in one round trip: per thread t < group * 32
-    // the weighted sums of head t / 32, dimensions 4 (t % 32) .. + 3, of up to
-    // kMergeBatch chunks as 16-byte loads, then the statistics (whose copy
-    // into LDS waits for its loads -- and, returning in issue order, for the
-    // weighted sums').  Loads of chunks past `used` (or threads past the
+    // The merge issues them all at once: the statistics first (their loads
+    // return first), then per thread t < group * 32 the weighted sums of head
+    // t / 32, dimensions 4 (t % 32) .. + 3, of up to kMergeBatch chunks as
+    // 16-byte loads.  Loads of chunks past `used` (or threads past the
     // group's heads) re-read a valid partial; their scale is zero (or their
     // result is not stored), so the accumulation needs no branches.
     const int used = pos / kChunk + 1;  // chunks that hold positions 0..pos (all wrote partials)
     const float* base = a.partials + (int64_t)slot * a.chunks * kPartFloats;
     float* stats = (float*)&ks[0][0];    // [used][2 * kMaxGroup]: m, l per head
     float* scale_c = (float*)&vt[0][0];  // [kMaxChunks][kMaxGroup]: exp(m_c - m) / l, zero past `used`
+    for (int e = tid; e < used * 2 * kMaxGroup; e += kAttnThreads)
+        stats[e] = base[(e / (2 * kMaxGroup)) * kPartFloats + e % (2 * kMaxGroup)];
     const int f = min(tid, group * (kHeadDim / 4) - 1);
     const int gh = f / (kHeadDim / 4);     // head within the group
     const int d4 = 4 * (f % (kHeadDim / 4));  // first of its four dimensions
@@ -451,8 +452,6 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
             v[u] = *(const float4v*)(base + min(c0 + u, used - 1) * kPartFloats + 2 * kMaxGroup + gh * kHeadDim + d4);
     };
     load_batch(0);
-    for (int e = tid; e < used * 2 * kMaxGroup; e += kAttnThreads)
-        stats[e] = base[(e / (2 * kMaxGroup)) * kPartFloats + e % (2 * kMaxGroup)];
     __syncthreads();
     // per head g (wave w takes heads w, w + 4): lanes walk the chunks; the
     // head's maximum and rescaled sum are wave reductions.  Heads past
