@@ -290,12 +290,12 @@ def test_workspace_and_kernel_plan_queries():
     assert lib.w4g64_linear_workspace_bytes(16, 1536, 1536, _lib.DTYPE_F16) == 0
     assert lib.w4g64_linear_workspace_bytes(16, 40, 9280, _lib.DTYPE_BF16) == 6 * 16 * 40 * 4
     # prefill: 560 tiles of 128x256 on 512 workgroup slots (256 CUs, the default
-    # when no device answers): 512 data-parallel tiles, the other 48 split in 4
+    # when no device answers): 512 data-parallel tiles, the other 48 split in 3
     # K ranges with fp32 partials; whole rounds need none
     # and every GEMM stages its activations as fp16 rows (rows x in_features x 2 B)
     # plus one fp32 row factor per tile row
     staged = 2048 * 1536 * 2 + 16 * 128 * 4
-    assert lib.w4g64_linear_workspace_bytes(2048, 8960, 1536, _lib.DTYPE_BF16) == 48 * 4 * 128 * 256 * 4 + staged
+    assert lib.w4g64_linear_workspace_bytes(2048, 8960, 1536, _lib.DTYPE_BF16) == 48 * 3 * 128 * 256 * 4 + staged
     assert lib.w4g64_linear_workspace_bytes(2048, 8192, 1536, _lib.DTYPE_BF16) == staged
     # fp32 GEMM activations: two fp16 planes (rows x 2 in_features x 2 B) after the partials
     ws32 = lib.w4g64_linear_workspace_bytes(512, 1536, 8960, _lib.DTYPE_F32)
