@@ -87,6 +87,23 @@ int qwen2_decode_attention(const void* qkv, const void* cos, const void* sin, vo
                            int64_t num_kv_heads, int64_t head_dim, int64_t max_length, float scale,
                            void* workspace, int64_t workspace_bytes, void* stream);
 
+/* qwen2_decode_attention without its merge: the same rotary step and cache
+ * write, and every 64-position chunk's workgroup leaves its partial result
+ * (per query head: score maximum m_c, sum l_c of exp(score - m_c), and the
+ * exp-weighted value sums acc_c[128], fp32) in the workspace; chunks past the
+ * position leave m_c = -inf, l_c = 0 and zero sums.  No output row is
+ * written: w4g64_linear_attention_merge merges the chunks in the staging of
+ * the o_proj linear, with the result qwen2_decode_attention would have
+ * written.  Same arguments and workspace as qwen2_decode_attention, minus
+ * `out`; the counter area is left untouched.
+ * Replaces: with w4g64_linear_attention_merge, the rotary step, attention and
+ *           o_proj of QwenAttention.forward for one cached token
+ *           (src/qwen_int4/model.py:17-31, :61-122). */
+int qwen2_decode_attention_partials(const void* qkv, const void* cos, const void* sin, void* k_cache,
+                                    void* v_cache, const int64_t* position, int64_t batch, int64_t num_heads,
+                                    int64_t num_kv_heads, int64_t head_dim, int64_t max_length, float scale,
+                                    void* workspace, int64_t workspace_bytes, void* stream);
+
 /* Bytes of workspace qwen2_prefill_attention needs: the rotated queries,
  * bf16 [batch, num_heads, length, head_dim]. */
 int64_t qwen2_prefill_attention_workspace_bytes(int64_t batch, int64_t num_heads, int64_t length);

@@ -207,6 +207,26 @@ int w4g64_linear_rmsnorm(const void* residual, const void* delta, int delta_dtyp
                          int64_t out_features, int64_t in_features, void* workspace, int64_t workspace_bytes,
                          void* stream);
 
+/* Decode linear (one row, bf16: batch-1 decode) whose activation is the
+ * decode attention's output, merged in its staging from the per-chunk partial
+ * results that qwen2_decode_attention_partials leaves in its workspace:
+ *   x[h * 128 + d] = bf16( sum_c exp(m_c - m) acc_c[d] / sum_c exp(m_c - m) l_c ),
+ *       m = max_c m_c, over the chunks c of query head h's key/value head
+ *   y = x @ dequant(W)^T (+ bias), bf16 [rows, out_features]
+ * -- bit for bit qwen2_decode_attention's output followed by w4g64_linear.
+ * attention_workspace / attention_workspace_bytes, max_length, num_heads and
+ * num_kv_heads are those of the qwen2_decode_attention_partials call (batch
+ * = rows = 1); in_features = num_heads * 128.  Takes max_length <= 1024
+ * (every chunk's partial is loaded), num_heads <= 12 and in_features a
+ * multiple of 256; W4G64_STATUS_UNSUPPORTED otherwise (then use
+ * qwen2_decode_attention and w4g64_linear).  qweight 16-byte aligned.
+ * Replaces: the softmax-weighted sum of QwenAttention.forward and the o_proj
+ *           linear that follows it (src/qwen_int4/model.py:101-122). */
+int w4g64_linear_attention_merge(const void* attention_workspace, int64_t attention_workspace_bytes,
+                                 int64_t max_length, int64_t num_heads, int64_t num_kv_heads, const uint8_t* qweight,
+                                 const uint16_t* scales, const uint8_t* zeros, const void* bias, int bias_dtype,
+                                 void* y, int64_t rows, int64_t out_features, void* stream);
+
 /* Number of fp32 partial sums per output w4g64_linear_partials writes for this
  * problem (its K splits; 1 = unsplit), or 0 when the problem does not take
  * that form: x_dtype W4G64_DTYPE_BF16_PLANES or W4G64_DTYPE_F32, 1..16 rows. */

@@ -46,6 +46,9 @@ constexpr int kMaxGroup = 8;      // query heads per key/value head
 constexpr int kAttnThreads = 256;
 constexpr int kRowStride = kHeadDim + 8;  // bf16 elements per staged row (272 B)
 constexpr int kPartFloats = 2 * kMaxGroup + kMaxGroup * kHeadDim;  // m[8], l[8], acc[8][128]
+static_assert(kPartFloats == kAttnPartFloats && kChunk == kAttnChunk && kMaxGroup == kAttnMaxGroup &&
+                  kHeadDim == kAttnHeadDim,
+              "the partial-result layout the attention-merge GEMV reads");
 constexpr int kMergeBatch = 16;   // chunks whose partial sums one merge pass loads together
 // The merge keeps per-chunk statistics in the staging rows' LDS.
 constexpr int kMaxChunks = (kChunk * kRowStride * 2) / (2 * kMaxGroup * 4);
@@ -165,6 +168,10 @@ struct AttnArgs {
     float scale;
     unsigned* counters;  // [batch * kv_heads]
     float* partials;     // [batch * kv_heads][chunks][kPartFloats]
+    // nonzero: no merge -- every chunk's workgroup stores its partial result
+    // (a chunk past the position an empty one: m = -inf, l = 0, sums 0) and
+    // the next launch merges them (w4g64_linear_attention_merge)
+    int unmerged;
     W4G64_TIMELINE_FIELDS
 };
 
@@ -419,10 +426,20 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
         }
     }
 
+    W4G64_STAMP(4);
+    if (a.unmerged) {
+        // An empty chunk's partial adds exactly nothing to the merge:
+        // exp(-inf - m) = 0 scales its zero sums and its zero l.
+        if (nk <= 0)
+            for (int e = tid; e < 2 * kMaxGroup + group * kHeadDim; e += kAttnThreads)
+                part[e] = e < kMaxGroup ? -INFINITY : 0.0f;
+        W4G64_STAMP(5);
+        W4G64_TIMELINE_STORE(a);
+        return;
+    }
     // ---- arrival: the last workgroup of this (sequence, head) merges ----
     // The partial stores are published by the arrival's agent-scope release
     // and acquired by the last arriver (arrive_last).
-    W4G64_STAMP(4);
     if (!arrive_last(a.counters + slot, (unsigned)a.chunks, &s_last)) {
         W4G64_STAMP(5);
         W4G64_TIMELINE_STORE(a);
@@ -786,10 +803,6 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* gate_up, 
     out[i] = (g / (1.0f + expf(-g))) * u;
 }
 
-int64_t attention_counter_bytes(int64_t batch, int64_t kv_heads) {
-    return (batch * kv_heads * (int64_t)sizeof(unsigned) + 255) / 256 * 256;
-}
-
 bool aligned16(const void* p) { return (((uintptr_t)p) & 15) == 0; }
 
 int launch_status(hipError_t err, const char* what) {
@@ -835,10 +848,10 @@ int64_t qwen2_decode_attention_workspace_bytes(int64_t batch, int64_t num_kv_hea
            batch * num_kv_heads * chunks * kPartFloats * (int64_t)sizeof(float);
 }
 
-int qwen2_decode_attention(const void* qkv, const void* cos, const void* sin, void* k_cache, void* v_cache,
-                           const int64_t* position, void* out, int64_t batch, int64_t num_heads,
-                           int64_t num_kv_heads, int64_t head_dim, int64_t max_length, float scale,
-                           void* workspace, int64_t workspace_bytes, void* stream) {
+static int decode_attention(const void* qkv, const void* cos, const void* sin, void* k_cache, void* v_cache,
+                            const int64_t* position, void* out, bool unmerged, int64_t batch, int64_t num_heads,
+                            int64_t num_kv_heads, int64_t head_dim, int64_t max_length, float scale,
+                            void* workspace, int64_t workspace_bytes, void* stream) {
     if (batch < 0) return set_error(W4G64_STATUS_INVALID_VALUE, "batch must be non-negative");
     if (head_dim != kHeadDim)
         return set_error(W4G64_STATUS_UNSUPPORTED, "head_dim must be %d, got %lld", kHeadDim, (long long)head_dim);
@@ -851,7 +864,7 @@ int qwen2_decode_attention(const void* qkv, const void* cos, const void* sin, vo
         return set_error(W4G64_STATUS_INVALID_VALUE, "max_length must be in [1, %d], got %lld", kMaxLength,
                          (long long)max_length);
     if (batch == 0) return clear_error();
-    if (!qkv || !cos || !sin || !k_cache || !v_cache || !position || !out)
+    if (!qkv || !cos || !sin || !k_cache || !v_cache || !position || (!out && !unmerged))
         return set_error(W4G64_STATUS_INVALID_VALUE, "all tensors must be non-null device pointers");
     if (!aligned16(qkv) || !aligned16(k_cache) || !aligned16(v_cache))
         return set_error(W4G64_STATUS_INVALID_VALUE, "qkv, k_cache and v_cache must be 16-byte aligned");
@@ -880,9 +893,26 @@ int qwen2_decode_attention(const void* qkv, const void* cos, const void* sin, vo
     args.scale = scale;
     args.counters = (unsigned*)workspace;
     args.partials = (float*)((char*)workspace + attention_counter_bytes(batch, num_kv_heads));
+    args.unmerged = unmerged ? 1 : 0;
     W4G64_TIMELINE_SET(args);
     hipLaunchKernelGGL(attention_kernel, dim3((unsigned)blocks), dim3(kAttnThreads), 0, (hipStream_t)stream, args);
     return launch_status(hipGetLastError(), "decode_attention");
+}
+
+int qwen2_decode_attention(const void* qkv, const void* cos, const void* sin, void* k_cache, void* v_cache,
+                           const int64_t* position, void* out, int64_t batch, int64_t num_heads,
+                           int64_t num_kv_heads, int64_t head_dim, int64_t max_length, float scale,
+                           void* workspace, int64_t workspace_bytes, void* stream) {
+    return decode_attention(qkv, cos, sin, k_cache, v_cache, position, out, false, batch, num_heads, num_kv_heads,
+                            head_dim, max_length, scale, workspace, workspace_bytes, stream);
+}
+
+int qwen2_decode_attention_partials(const void* qkv, const void* cos, const void* sin, void* k_cache,
+                                    void* v_cache, const int64_t* position, int64_t batch, int64_t num_heads,
+                                    int64_t num_kv_heads, int64_t head_dim, int64_t max_length, float scale,
+                                    void* workspace, int64_t workspace_bytes, void* stream) {
+    return decode_attention(qkv, cos, sin, k_cache, v_cache, position, nullptr, true, batch, num_heads,
+                            num_kv_heads, head_dim, max_length, scale, workspace, workspace_bytes, stream);
 }
 
 int64_t qwen2_prefill_attention_workspace_bytes(int64_t batch, int64_t num_heads, int64_t length) {

@@ -419,6 +419,47 @@ int w4g64_linear_rmsnorm(const void* residual, const void* delta, int delta_dtyp
     return hip_status(w4g64::launch_gemv(p, plan, workspace, (hipStream_t)stream), "gemv");
 }
 
+int w4g64_linear_attention_merge(const void* attention_workspace, int64_t attention_workspace_bytes,
+                                 int64_t max_length, int64_t num_heads, int64_t num_kv_heads, const uint8_t* qweight,
+                                 const uint16_t* scales, const uint8_t* zeros, const void* bias, int bias_dtype,
+                                 void* y, int64_t rows, int64_t out_features, void* stream) {
+    if (num_kv_heads <= 0 || num_heads <= 0 || num_heads % num_kv_heads != 0 ||
+        num_heads / num_kv_heads > w4g64::kAttnMaxGroup)
+        return fail(W4G64_STATUS_INVALID_VALUE,
+                    "num_heads (%lld) must be a positive multiple of num_kv_heads (%lld), at most %d times",
+                    (long long)num_heads, (long long)num_kv_heads, w4g64::kAttnMaxGroup);
+    if (num_heads > (1 << 16)) return fail(W4G64_STATUS_INVALID_VALUE, "num_heads too large");
+    const int64_t in_features = num_heads * w4g64::kAttnHeadDim;
+    if (int st = fused_common_checks(qweight, scales, zeros, bias, bias_dtype, y, 2, rows, out_features, in_features))
+        return st;
+    if (rows != 1)
+        return fail(W4G64_STATUS_INVALID_VALUE, "the attention-merge linear takes one row, got %lld", (long long)rows);
+    if (max_length <= 0) return fail(W4G64_STATUS_INVALID_VALUE, "max_length must be positive");
+    const int64_t chunks = (max_length + w4g64::kAttnChunk - 1) / w4g64::kAttnChunk;
+    if (!attention_workspace || !aligned(attention_workspace, 16))
+        return fail(W4G64_STATUS_WORKSPACE, "the attention workspace must be a 16-byte aligned device pointer");
+    const int64_t counters = w4g64::attention_counter_bytes(rows, num_kv_heads);
+    const int64_t need = counters + rows * num_kv_heads * chunks * w4g64::kAttnPartFloats * (int64_t)sizeof(float);
+    if (attention_workspace_bytes < need)
+        return fail(W4G64_STATUS_WORKSPACE, "attention workspace of %lld bytes required, got %lld", (long long)need,
+                    (long long)attention_workspace_bytes);
+    w4g64::LinearProblem p{(const char*)attention_workspace + counters, w4g64::kAttnM, qweight, scales, zeros, bias,
+                           bias_dtype, y, rows, out_features, in_features};
+    p.att_chunks = (int)chunks;
+    p.att_group = (int)(num_heads / num_kv_heads);
+    p.att_kv_heads = (int)num_kv_heads;
+    w4g64::GemvPlan plan;
+    if (chunks > w4g64::kAttnMergeMaxChunks ||
+        !w4g64::plan_pipe_fused(w4g64::kAttnMerge, false, rows, out_features, in_features, plan) ||
+        !w4g64::pipe_supported(p))
+        return fail(W4G64_STATUS_UNSUPPORTED,
+                    "the attention-merge linear takes max_length <= %d, in_features a multiple of 256 up to 1536 "
+                    "and 16-byte aligned weights (max_length %lld, in_features %lld): use qwen2_decode_attention "
+                    "and w4g64_linear",
+                    w4g64::kAttnMergeMaxChunks * w4g64::kAttnChunk, (long long)max_length, (long long)in_features);
+    return hip_status(w4g64::launch_gemv_pipe(p, plan, nullptr, (hipStream_t)stream), "gemv");
+}
+
 int64_t w4g64_linear_partial_count(int64_t rows, int64_t out_features, int64_t in_features, int x_dtype) {
     if (rows < 1 || rows > w4g64::kGemvMaxRows || out_features <= 0 || out_features > w4g64::kGemvMaxOutFeatures ||
         in_features <= 0 || in_features % 64 || in_features > (1ll << 24))

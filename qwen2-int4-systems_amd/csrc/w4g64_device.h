@@ -36,7 +36,10 @@ enum XKind : int {
     // + delta), delta bf16 (kNormB), fp32 (kNormF) or the sum of up to
     // kMaxDeltaParts fp32 split-K partial sums of the previous projection
     // (kNormP); internal kinds
-    kNormB = 7, kNormF = 8, kNormP = 9
+    kNormB = 7, kNormF = 8, kNormP = 9,
+    // bf16 activations merged in the decode GEMV's staging from the decode
+    // attention's per-chunk partial results (internal kind)
+    kAttnM = 10
 };
 constexpr int kMaxDeltaParts = 8;
 
@@ -161,6 +164,24 @@ __device__ __forceinline__ float wave_sum64(float v) {
     // lanes outside a broadcast's row mask receive the `old` operand, 0
     v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x142, 0xA, 0xF, false));
     v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x143, 0xC, 0xF, false));
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
+// Wave-wide maximum over the wave sum's steps (quad swaps, half-row and row
+// mirrors, row broadcasts 15 and 31; lanes outside a broadcast's row mask
+// keep their own value); the result is lane 63's.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_keep(float x) {
+    const int b = __builtin_bit_cast(int, x);
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(b, b, CTRL, ROW_MASK, 0xF, false));
+}
+__device__ __forceinline__ float wave_max64(float v) {
+    v = fmaxf(v, dpp_keep<0xB1, 0xF>(v));
+    v = fmaxf(v, dpp_keep<0x4E, 0xF>(v));
+    v = fmaxf(v, dpp_keep<0x141, 0xF>(v));
+    v = fmaxf(v, dpp_keep<0x140, 0xF>(v));
+    v = fmaxf(v, dpp_keep<0x142, 0xA>(v));
+    v = fmaxf(v, dpp_keep<0x143, 0xC>(v));
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 

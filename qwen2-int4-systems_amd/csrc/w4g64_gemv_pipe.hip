@@ -74,6 +74,12 @@ struct PipeArgs {
     const uint16_t* norm_w;
     float eps;
     uint16_t* out_sum;
+    // attention-merge form: x is the decode attention's partial results
+    // (kAttnPartFloats per chunk, `att_chunks` chunks per (row, key/value
+    // head)); query head h of row m reads key/value head h / att_group
+    int att_chunks;
+    int att_group;
+    int att_kv_heads;
     W4G64_TIMELINE_FIELDS
 };
 
@@ -179,6 +185,8 @@ __global__ __launch_bounds__(WR * WK * 64) void gemv_pipe_kernel(PipeArgs a) {
     const int M = a.M, N = a.N, K = a.K, G = a.G, P = a.P;
     constexpr int PL = FORM == kPlanes3 ? 3 : 1;  // staged rows per output row
     constexpr bool kNorm = FORM == kNormBf16 || FORM == kNormParts;
+    constexpr bool kMerge = FORM == kAttnMerge;
+    static_assert(!kMerge || (!PAIRED && WK == 1), "attention merge: plain rows, the whole K range per workgroup");
     static_assert(!PAIRED || (RBW == 2 && WK == 1), "paired: gate rows in row block 0, up rows in row block 1");
     static_assert(XK == kBF16 || FORM == kPlain, "the fused forms are bf16");
     const int p0 = blockIdx.y * a.PS;        // first pair of the workgroup's K range
@@ -247,7 +255,7 @@ __global__ __launch_bounds__(WR * WK * 64) void gemv_pipe_kernel(PipeArgs a) {
         xit[u] = it;
         const int m = it / per_row;
         const int k8 = it - m * per_row;
-        xv[u] = *(const u32x4*)((const uint16_t*)a.x + (int64_t)m * K + (int64_t)p0 * 128 + 8 * k8);
+        if constexpr (!kMerge) xv[u] = *(const u32x4*)((const uint16_t*)a.x + (int64_t)m * K + (int64_t)p0 * 128 + 8 * k8);
         if constexpr (FORM == kNormBf16) {
             dv[u][0] = *(const u32x4*)((const uint16_t*)a.delta + 8 * k8);
         } else if constexpr (FORM == kNormParts) {
@@ -259,6 +267,47 @@ __global__ __launch_bounds__(WR * WK * 64) void gemv_pipe_kernel(PipeArgs a) {
             }
         }
         if constexpr (kNorm) nwv[u] = *(const u32x4*)(a.norm_w + 8 * k8);
+    }
+    // attention-merge form: the 8 exp-weighted value sums of item it's head in
+    // every chunk (threads past the items load nothing), and for the (row,
+    // head) pairs hm = wave + W j each lane c < att_chunks loads chunk c's m
+    // and l
+    constexpr int kMC = kMerge ? kAttnMergeMaxChunks : 1;
+    constexpr int kMJ = kMerge ? 4 : 1;
+    // (held as float vectors: a bit cast of one element of an integer vector
+    // compiles to element 0 of that vector with this compiler)
+    float4v mv[kMerge ? STG : 1][kMC][2];
+    float mstat[kMJ], lstat[kMJ];
+    if constexpr (kMerge) {
+        const float* parts = (const float*)a.x;
+        const int heads = K / kAttnHeadDim;
+#pragma unroll
+        for (int u = 0; u < STG; ++u) {
+            const int it = xit[u];
+            const int m = it / per_row;
+            const int k = 8 * (it - m * per_row);  // one K range: p0 = 0
+            const int h = k / kAttnHeadDim;
+            const float* src = parts + (int64_t)(m * a.att_kv_heads + h / a.att_group) * a.att_chunks * kAttnPartFloats +
+                               2 * kAttnMaxGroup + (h % a.att_group) * kAttnHeadDim + k % kAttnHeadDim;
+            if (kThreads * u + tid < items) {
+#pragma unroll
+                for (int c = 0; c < kMC; ++c)
+                    if (c < a.att_chunks) {
+                        mv[u][c][0] = *(const float4v*)(src + c * kAttnPartFloats);
+                        mv[u][c][1] = *(const float4v*)(src + c * kAttnPartFloats + 4);
+                    }
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < kMJ; ++j) {
+            const int hm = min(wave + W * j, M * heads - 1);
+            const int m = hm / heads, h = hm % heads;
+            const int cl = min(lane, a.att_chunks - 1);
+            const float* st = parts + ((int64_t)(m * a.att_kv_heads + h / a.att_group) * a.att_chunks + cl) * kAttnPartFloats +
+                              h % a.att_group;
+            mstat[j] = st[0];
+            lstat[j] = st[kAttnMaxGroup];
+        }
     }
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();  // every wave's staging loads issue before any weight load
@@ -293,12 +342,61 @@ __global__ __launch_bounds__(WR * WK * 64) void gemv_pipe_kernel(PipeArgs a) {
     for (int i = 0; i < PF; ++i) issue(i);
 #pragma unroll
     for (int u = 0; u < STG; ++u) {
-        asm volatile("" : "+v"(xv[u]));
+        if constexpr (kMerge) {
+#pragma unroll
+            for (int c = 0; c < kMC; ++c) asm volatile("" : "+v"(mv[u][c][0]), "+v"(mv[u][c][1]));
+        } else {
+            asm volatile("" : "+v"(xv[u]));
+        }
         if constexpr (kNorm) asm volatile("" : "+v"(nwv[u]));
 #pragma unroll
         for (int k = 0; k < kDeltaVecs; ++k) asm volatile("" : "+v"(dv[u][k]));
     }
+#pragma unroll
+    for (int j = 0; j < kMJ; ++j) asm volatile("" : "+v"(mstat[j]), "+v"(lstat[j]));
     W4G64_STAMP(1);
+
+    // ---- 2a. attention merge (model.py:101-104: softmax over all positions, then P V) ----
+    // The decode attention's own merge, operation for operation: per (row,
+    // head) m = max_c m_c, l = sum_c l_c exp(m_c - m) (lane c, then a wave
+    // sum), scale_c = exp(m_c - m) / l; then per value the sum over chunks in
+    // order of fmaf(sum_c, scale_c, .), rounded to bf16.  Chunks past the
+    // position hold m = -inf, l = 0 and zero sums, so they add exactly
+    // nothing, as the chunks past the position do in that merge.
+    if constexpr (kMerge) {
+        const int heads = K / kAttnHeadDim;
+        float* scl = (float*)(smem + L.total);  // [M heads][kMC]
+#pragma unroll
+        for (int j = 0; j < kMJ; ++j) {
+            const int hm = wave + W * j;
+            if (hm < M * heads) {
+                const bool live = lane < a.att_chunks;
+                const float mx = wave_max64(live ? fmaxf(-INFINITY, mstat[j]) : -INFINITY);
+                const float l = wave_sum64(live ? fmaf(lstat[j], expf(mstat[j] - mx), 0.0f) : 0.0f);
+                if (lane < kMC) scl[hm * kMC + lane] = live ? expf(mstat[j] - mx) / l : 0.0f;
+            }
+        }
+        lds_barrier();
+#pragma unroll
+        for (int u = 0; u < STG; ++u) {
+            const int it = xit[u];
+            const int m = it / per_row;
+            const int hm = m * heads + 8 * (it - m * per_row) / kAttnHeadDim;
+            float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            if (kThreads * u + tid < items) {
+#pragma unroll
+                for (int c = 0; c < kMC; ++c)
+                    if (c < a.att_chunks) {
+                        const float sc = scl[hm * kMC + c];
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) o[e] = fmaf(mv[u][c][e / 4][e % 4], sc, o[e]);
+                    }
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                xv[u][e] = float_to_bf16_bits(o[2 * e]) | ((uint32_t)float_to_bf16_bits(o[2 * e + 1]) << 16);
+        }
+    }
 
     // ---- 2b. RMSNorm prologue (model.py:40-44, residual adds :149-154) ----
     // s = bf16(x + bf16(delta)) (the partial sums added in order from 0, then
@@ -375,7 +473,9 @@ __global__ __launch_bounds__(WR * WK * 64) void gemv_pipe_kernel(PipeArgs a) {
             const int it = xit[u];
             const int m = it / per_row;
             const int k8 = it - m * per_row;
-            *(u32x4*)(smem + 2 * (m * L.xw + 8 * k8)) = permute_slots(xv[u]);
+            // (threads past the items repeat the last one; in the merge form
+            // they hold no value and leave its slot to the thread that has it)
+            if (!kMerge || kThreads * u + tid < items) *(u32x4*)(smem + 2 * (m * L.xw + 8 * k8)) = permute_slots(xv[u]);
             if constexpr (XK == kBF16) {
                 float sum = 0.0f;
 #pragma unroll
@@ -628,7 +728,8 @@ __global__ __launch_bounds__(WR * WK * 64) void gemv_pipe_kernel(PipeArgs a) {
     X(kNormBf16, true, 4, 1, 4, 1, 2, 3, 1, 1)       \
     X(kPlain, true, 4, 1, 4, 1, 2, 3, 3, 1)          \
     X(kNormParts, false, 4, 1, 4, 1, 1, 3, 3, 1)     \
-    X(kPlanes3, false, 2, 1, 4, 1, 1, 7, 4, 3)
+    X(kPlanes3, false, 2, 1, 4, 1, 1, 7, 4, 3)       \
+    X(kAttnMerge, false, 4, 1, 4, 1, 1, 3, 3, 1)
 
 typedef void (*PipeKernel)(PipeArgs);
 struct PipeEntry {
@@ -680,11 +781,12 @@ bool finish_pipe_plan(int64_t rows, int64_t out_features, int64_t in_features, G
     const int64_t staged = rows * (plan.form == kPlanes3 ? 3 : 1);
     if (2 * staged * sw > 16 * plan.tiles) return false;
     const bool norm = plan.form == kNormBf16 || plan.form == kNormParts;
-    if (norm && rows != 1) return false;
+    const bool merge = plan.form == kAttnMerge;
+    if ((norm || merge) && rows != 1) return false;
     if (plan.pair && (rbw != 2 || wk != 1 || out_features % 2)) return false;
     const int64_t span = (int64_t)wk * sw * t;  // pairs per workgroup K range
     const int64_t splits = (P + span - 1) / span;
-    if ((norm || plan.pair) && splits != 1) return false;  // the whole row, the whole (gate, up) pair
+    if ((norm || merge || plan.pair) && splits != 1) return false;  // the whole row, the whole (gate, up) pair
     plan.splits = (int)splits;
     plan.groups_per_split = (int)span;  // pairs per split (PS)
     const int64_t rows_per_block = (int64_t)wr * (16 / sw);
@@ -695,6 +797,10 @@ bool finish_pipe_plan(int64_t rows, int64_t out_features, int64_t in_features, G
     if (items > (int64_t)plan.stage * threads) return false;
     const int red = pipe_red_floats((int)staged, sw, wr, wk, rbw, sw == 1 && plan.form != kPlanes3 && !plan.pair);
     plan.lds_bytes = pipe_layout((int)staged, (int)span, red).total;
+    if (merge) {  // the chunk scales [rows heads][kAttnMergeMaxChunks] after the layout
+        if (in_features % kAttnHeadDim) return false;
+        plan.lds_bytes += (int)(rows * (in_features / kAttnHeadDim) * kAttnMergeMaxChunks * 4);
+    }
     if (plan.lds_bytes > kPipeMaxLds) return false;
     plan.workspace_bytes = splits > 1 ? splits * rows * out_features * 4 : 0;
     plan.kind = 4;
@@ -788,6 +894,7 @@ const PipeFusedShape kPipeFusedShapes[] = {
     {kPlain, true, 1, 1, 12, 4, 1, 4, 1, 2, 3, 3},
     {kNormParts, false, 1, 1, 12, 4, 1, 4, 1, 1, 3, 3},
     {kPlanes3, false, 1, 1, 1 << 20, 2, 1, 4, 1, 1, 7, 4},
+    {kAttnMerge, false, 1, 1, 12, 4, 1, 4, 1, 1, 3, 3},
 };
 
 bool plan_pipe_fused(int form, bool paired, int64_t rows, int64_t out_features, int64_t in_features,
@@ -828,7 +935,11 @@ bool pipe_supported(const LinearProblem& p) {
     // even pair count per row (in_features a multiple of 256) every row's
     // bytes start at an even index, and no word reaches past its row
     const bool norm = p.x_kind == kNormB || p.x_kind == kNormP || p.x_kind == kNormF;
-    if (!(p.x_kind == kF16 || p.x_kind == kBF16 || p.x_kind == kPlanes || norm)) return false;
+    if (!(p.x_kind == kF16 || p.x_kind == kBF16 || p.x_kind == kPlanes || p.x_kind == kAttnM || norm)) return false;
+    if (p.x_kind == kAttnM && (p.att_chunks < 1 || p.att_chunks > kAttnMergeMaxChunks || p.att_group < 1 ||
+                               p.att_group > kAttnMaxGroup || p.att_kv_heads < 1 ||
+                               p.in_features != (int64_t)p.att_group * p.att_kv_heads * kAttnHeadDim))
+        return false;
     if (p.paired && p.x_kind == kF16) return false;  // the fused forms are bf16
     if (norm &&
         (((uintptr_t)p.norm_delta % 16) || ((uintptr_t)p.norm_weight % 16) || ((uintptr_t)p.norm_out_sum % 16)))
@@ -860,6 +971,9 @@ hipError_t launch_gemv_pipe(const LinearProblem& p, const GemvPlan& plan, void* 
     a.norm_w = p.norm_weight;
     a.eps = p.norm_eps;
     a.out_sum = (uint16_t*)p.norm_out_sum;
+    a.att_chunks = p.att_chunks;
+    a.att_group = p.att_group;
+    a.att_kv_heads = p.att_kv_heads;
     a.K = (int)p.in_features;
     a.G = a.K / 64;
     a.P = a.G / 2;
@@ -873,6 +987,7 @@ hipError_t launch_gemv_pipe(const LinearProblem& p, const GemvPlan& plan, void* 
     if (!k || (plan.pair != 0) != (p.paired != 0)) return hipErrorInvalidValue;
     // an fp32 delta is the one-part case of the partial-sums form
     const int want_form = p.x_kind == kPlanes                       ? kPlanes3
+                          : p.x_kind == kAttnM                      ? kAttnMerge
                           : p.x_kind == kNormB                      ? kNormBf16
                           : (p.x_kind == kNormP || p.x_kind == kNormF) ? kNormParts
                                                                       : kPlain;

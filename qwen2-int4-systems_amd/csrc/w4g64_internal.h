@@ -32,6 +32,12 @@ struct LinearProblem {
     // decode GEMV: write the fp32 split-K partial sums [splits][rows][out_features]
     // here (no bias, no reduction launch; one split: the fp32 result)
     float* partials_out = nullptr;
+    // decode GEMV, x_kind kAttnM: x is the decode attention's partial results
+    // (att_chunks chunks per (row, key/value head), att_group query heads per
+    // key/value head, att_kv_heads key/value heads)
+    int att_chunks = 0;
+    int att_group = 0;
+    int att_kv_heads = 0;
 };
 
 // Decode GEMV (rows <= kGemvMaxRows).
@@ -111,11 +117,28 @@ bool plan_pipe(int64_t rows, int64_t out_features, int64_t in_features, int x_ki
 // Activation forms of the pipelined kernel (GemvPlan::form); each may be
 // paired (gate rows then up rows, SiLU-product planes out).
 enum PipeForm : int {
-    kPlain = 0,      // fp16 / bf16 rows
-    kPlanes3 = 1,    // three bf16 planes [3][Mo][K] (hi + mid + lo), staged as 3 Mo rows, summed; fp32 out
-    kNormBf16 = 2,   // RMSNorm(residual + bf16 delta), one row
-    kNormParts = 3,  // RMSNorm(residual + sum of fp32 partial sums), one row
+    kPlain = 0,       // fp16 / bf16 rows
+    kPlanes3 = 1,     // three bf16 planes [3][Mo][K] (hi + mid + lo), staged as 3 Mo rows, summed; fp32 out
+    kNormBf16 = 2,    // RMSNorm(residual + bf16 delta), one row
+    kNormParts = 3,   // RMSNorm(residual + sum of fp32 partial sums), one row
+    kAttnMerge = 4,   // the decode attention's per-chunk partial results, merged; one row
 };
+
+// The decode attention's workspace: arrival counters (256-byte aligned
+// area), then fp32 partial results [batch * kv_heads][chunks][kAttnPartFloats],
+// chunk c of a (sequence, key/value head) covering positions 64 c .. 64 c +
+// 63: m[8] (score maximum per query head of the group), l[8] (sum of
+// exp(score - m)), then the 8 heads' exp-weighted value sums [8][128].
+constexpr int kAttnChunk = 64;
+constexpr int kAttnMaxGroup = 8;
+constexpr int kAttnHeadDim = 128;
+constexpr int kAttnPartFloats = 2 * kAttnMaxGroup + kAttnMaxGroup * kAttnHeadDim;
+inline int64_t attention_counter_bytes(int64_t batch, int64_t kv_heads) {
+    return (batch * kv_heads * (int64_t)sizeof(unsigned) + 255) / 256 * 256;
+}
+// Chunks the attention-merge form of the pipelined GEMV takes (the cache's
+// max_length up to 1024 positions): it loads every chunk's partial result.
+constexpr int kAttnMergeMaxChunks = 16;
 bool plan_pipe_fused(int form, bool paired, int64_t rows, int64_t out_features, int64_t in_features,
                      GemvPlan& plan);
 bool pipe_supported(const LinearProblem& p);

@@ -57,11 +57,13 @@ SIGNATURES = {
     "w4g64_linear_gate_up_planes": (_int, [_p, _p, _p, _p, _p, _int, _p, _i64, _i64, _i64, _p, _i64, _p]),
     "w4g64_linear_rmsnorm": (_int, [_p, _p, _int, _p, ctypes.c_float, _p, _p, _p, _p, _p, _int, _p, _int, _i64, _i64,
                                     _i64, _p, _i64, _p]),
+    "w4g64_linear_attention_merge": (_int, [_p, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _int, _p, _i64, _i64, _p]),
     # include/qwen2_decode.h
     "qwen2_decode_prologue": (_int, [_p] * 8 + [ctypes.c_float, _p] + [_i64] * 4 + [_p]),
     "qwen2_add_rmsnorm": (_int, [_p, _p, _int, _p, ctypes.c_float, _p, _p, _i64, _i64, _p]),
     "qwen2_decode_attention_workspace_bytes": (_i64, [_i64, _i64, _i64]),
     "qwen2_decode_attention": (_int, [_p] * 7 + [_i64] * 5 + [ctypes.c_float, _p, _i64, _p]),
+    "qwen2_decode_attention_partials": (_int, [_p] * 6 + [_i64] * 5 + [ctypes.c_float, _p, _i64, _p]),
     "qwen2_prefill_attention_workspace_bytes": (_i64, [_i64, _i64, _i64]),
     "qwen2_prefill_attention": (_int, [_p] * 6 + [_i64] * 6 + [ctypes.c_float, _p, _i64, _p]),
     "qwen2_silu_mul": (_int, [_p, _p, _i64, _i64, _p]),

@@ -10,7 +10,11 @@ stream alternates between two buffers):
                          first, model.py:136) + input RMSNorm
     W4G64 q|k|v          one GEMV over the three projections' rows, with bias
     decode_attention     rotary on q and the new k, cache write, GQA attention
-    W4G64 o_proj
+                         over 64-position chunks, merged by the last chunk
+    W4G64 o_proj         (batch 1, caches up to 1024 positions: the attention
+                         leaves every chunk's partial result and the o_proj
+                         GEMV merges them in its staging,
+                         ``w4g64_linear_attention_merge``)
     add_rmsnorm          residual add of the attention output + RMSNorm
     W4G64 gate|up        one GEMV over both projections' rows; its epilogue
                          pairs gate row i with up row I + i and stores
@@ -145,9 +149,11 @@ def fuse_projections(model) -> list[dict]:
 class FusedDecodeStep:
     """Preallocated buffers and launch sequence of one decode step for
     ``batch`` sequences at a common position, over static caches
-    [batch, kv_heads, max_length, head_dim] (``model.new_static_cache``)."""
+    [batch, kv_heads, max_length, head_dim] (``model.new_static_cache``).
+    ``merge_attention_in_o_proj=False`` keeps the attention's own merge where
+    the o_proj GEMV would take it (the results are the same bit for bit)."""
 
-    def __init__(self, model, batch: int, max_length: int) -> None:
+    def __init__(self, model, batch: int, max_length: int, merge_attention_in_o_proj: bool = True) -> None:
         if not torch.cuda.is_available():
             raise RuntimeError("the fused decode step requires a ROCm GPU")
         self.lib = _lib.load()
@@ -207,6 +213,13 @@ class FusedDecodeStep:
         self.workspace = torch.zeros(max(ws, 1), dtype=torch.uint8, device=device)
         aws = self.lib.qwen2_decode_attention_workspace_bytes(batch, self.kv_heads, max_length)
         self.attn_workspace = torch.zeros(max(aws, 1), dtype=torch.uint8, device=device)
+        # batch 1, caches up to 1024 positions, up to 12 heads: the attention
+        # leaves its per-chunk partial results and the o_proj linear merges
+        # them in its staging (the same output; one cross-workgroup merge
+        # fewer per layer)
+        width = self.heads * self.head_dim
+        self.merge_in_o_proj = (merge_attention_in_o_proj and batch == 1 and max_length <= 1024
+                                and width % 256 == 0 and width <= 1536)
         head = model.lm_head.weight
         self.vocab = head.shape[0]
         # the HIP LM head (with fused greedy argmax) covers up to 16 rows
@@ -269,14 +282,24 @@ class FusedDecodeStep:
                 if delta is not None:  # the first layer's norm came with the prologue
                     self._norm_at(cur, delta, delta_code, layer.input_layernorm.weight, stream)
                 self._linear(self.normed, _lib.DTYPE_BF16, fused["qkv"], self.qkv, stream)
-            _lib.check(self.lib.qwen2_decode_attention(
-                _ptr(self.qkv), _ptr(cos), _ptr(sin), _ptr(k_cache), _ptr(v_cache), _ptr(position),
-                _ptr(self.attended), self.batch, self.heads, self.kv_heads, self.head_dim, k_cache.shape[2],
-                ctypes.c_float(self.scale), _ptr(self.attn_workspace), self.attn_workspace.numel(), stream))
             o_proj = layer.self_attn.o_proj
-            self._linear(self.attended, _lib.DTYPE_BF16,
-                         {"qweight": o_proj.qweight, "scales": o_proj.scales, "zeros": o_proj.zeros, "bias": None},
-                         self.o, stream)
+            if self.merge_in_o_proj:
+                _lib.check(self.lib.qwen2_decode_attention_partials(
+                    _ptr(self.qkv), _ptr(cos), _ptr(sin), _ptr(k_cache), _ptr(v_cache), _ptr(position), self.batch,
+                    self.heads, self.kv_heads, self.head_dim, k_cache.shape[2], ctypes.c_float(self.scale),
+                    _ptr(self.attn_workspace), self.attn_workspace.numel(), stream))
+                _lib.check(self.lib.w4g64_linear_attention_merge(
+                    _ptr(self.attn_workspace), self.attn_workspace.numel(), k_cache.shape[2], self.heads,
+                    self.kv_heads, _ptr(o_proj.qweight), _ptr(o_proj.scales), _ptr(o_proj.zeros), None,
+                    _lib.DTYPE_NONE, _ptr(self.o), self.batch, self.o.shape[1], stream))
+            else:
+                _lib.check(self.lib.qwen2_decode_attention(
+                    _ptr(self.qkv), _ptr(cos), _ptr(sin), _ptr(k_cache), _ptr(v_cache), _ptr(position),
+                    _ptr(self.attended), self.batch, self.heads, self.kv_heads, self.head_dim, k_cache.shape[2],
+                    ctypes.c_float(self.scale), _ptr(self.attn_workspace), self.attn_workspace.numel(), stream))
+                self._linear(self.attended, _lib.DTYPE_BF16,
+                             {"qweight": o_proj.qweight, "scales": o_proj.scales, "zeros": o_proj.zeros,
+                              "bias": None}, self.o, stream)
             down = layer.mlp.down_proj
             if self.fused_norm:
                 self._norm_linear(cur, self.o, _lib.DTYPE_BF16, layer.post_attention_layernorm.weight,

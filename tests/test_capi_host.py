@@ -277,6 +277,42 @@ def test_partial_sum_forms_reject_before_launch():
                                     64, null, 0, null) == _lib.STATUS_INVALID_DTYPE
 
 
+def test_attention_merge_forms_reject_before_launch():
+    lib = _lib.load()
+    null = None
+    buf = ctypes.create_string_buffer(1 << 16)
+    base = (ctypes.addressof(buf) + 255) & ~255
+    p = ctypes.c_void_p(base)
+    f = ctypes.c_float(128 ** -0.5)
+    big = 1 << 40  # workspace bytes claimed, so that the checks after the size one are reached
+    need = lib.qwen2_decode_attention_workspace_bytes(1, 2, 640)
+
+    def merge(ws=p, ws_bytes=big, max_length=640, heads=12, kv=2, rows=1, n=1536):
+        return lib.w4g64_linear_attention_merge(ws, ws_bytes, max_length, heads, kv, p, p, p, null, 0, p, rows, n,
+                                                null)
+
+    assert merge(rows=2) == _lib.STATUS_INVALID_VALUE and b"one row" in lib.w4g64_last_error()
+    assert merge(heads=12, kv=5) == _lib.STATUS_INVALID_VALUE
+    assert merge(heads=18, kv=2) == _lib.STATUS_INVALID_VALUE  # 9 query heads per key/value head
+    assert merge(max_length=0) == _lib.STATUS_INVALID_VALUE
+    assert merge(ws_bytes=need - 4) == _lib.STATUS_WORKSPACE
+    assert merge(ws=ctypes.c_void_p(base + 8)) == _lib.STATUS_WORKSPACE
+    assert merge(ws=null) == _lib.STATUS_WORKSPACE
+    # 17 chunks, 14 heads (1792 features), 3 heads (384: not a multiple of 256)
+    for kwargs in ({"max_length": 1025}, {"heads": 14, "kv": 2}, {"heads": 3, "kv": 3}):
+        assert merge(**kwargs) == _lib.STATUS_UNSUPPORTED, kwargs
+        assert b"qwen2_decode_attention and w4g64_linear" in lib.w4g64_last_error()
+    # the unmerged attention: qwen2_decode_attention's checks, without `out`
+    assert lib.qwen2_decode_attention_partials(p, p, p, p, p, p, 1, 12, 2, 128, 20000, f, p, big,
+                                               null) == _lib.STATUS_INVALID_VALUE
+    assert lib.qwen2_decode_attention_partials(p, p, p, p, p, p, 1, 12, 2, 64, 640, f, p, big,
+                                               null) == _lib.STATUS_UNSUPPORTED
+    assert lib.qwen2_decode_attention_partials(p, p, p, p, p, p, 1, 12, 2, 128, 640, f, null, 0,
+                                               null) == _lib.STATUS_WORKSPACE
+    assert lib.qwen2_decode_attention_partials(p, p, p, p, p, p, 1, 12, 2, 128, 640, f, p, need - 16,
+                                               null) == _lib.STATUS_WORKSPACE
+
+
 def test_workspace_and_kernel_plan_queries():
     lib = _lib.load()
     # decode shapes that split K across workgroups need a workspace for their

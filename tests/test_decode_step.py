@@ -172,6 +172,88 @@ def test_decode_attention_matches_torch(batch, heads, kv_heads, max_length, posi
             assert cos_sim.item() >= 0.99999, (pos, cos_sim.item())
 
 
+@pytest.mark.parametrize("heads,kv_heads,max_length,positions,n,with_bias", [
+    (12, 2, 640, (0, 1, 63, 64, 65, 511, 639), 1536, False),
+    (12, 2, 1024, (0, 700, 1023), 1536, True),  # 16 chunks: the most the merge form takes
+    (8, 1, 100, (3, 99), 200, False),            # 8 query heads per key/value head, a partial last chunk
+    (2, 2, 64, (0, 63), 96, False),              # one query head per key/value head, one chunk
+    (4, 2, 200, (130,), 1536, True),
+])
+def test_attention_merged_in_o_proj_equals_attention_then_o_proj(heads, kv_heads, max_length, positions, n,
+                                                                 with_bias):
+    """qwen2_decode_attention_partials + w4g64_linear_attention_merge against
+    qwen2_decode_attention + w4g64_linear on the same inputs: the same cache
+    writes and, bit for bit, the same o_proj output (the merge in the GEMV's
+    staging repeats the attention's own merge operation for operation).  The
+    unmerged path's workspace starts as NaN, so chunks past the position must
+    be written (as empty partials), not assumed."""
+    lib = _lib.load()
+    g = _gen(heads * 100 + kv_heads + max_length)
+    d = 128
+    k = heads * d
+    rot = RotaryEmbedding(d, 1_000_000.0).cuda()
+    k_cache = torch.randn((1, kv_heads, max_length, d), generator=g, device="cuda").to(torch.bfloat16)
+    v_cache = torch.randn((1, kv_heads, max_length, d), generator=g, device="cuda").to(torch.bfloat16)
+    k_part, v_part = k_cache.clone(), v_cache.clone()
+    qw, sc, z = _weights(n, k, heads + n, asymmetric=True)
+    bias = (torch.randn(n, generator=g, device="cuda") * 0.1).to(torch.bfloat16) if with_bias else None
+    bias_code = _lib.DTYPE_BF16 if with_bias else _lib.DTYPE_NONE
+    wbytes = lib.qwen2_decode_attention_workspace_bytes(1, kv_heads, max_length)
+    ws = torch.zeros(wbytes, dtype=torch.uint8, device="cuda")
+    ws_part = torch.full((wbytes,), 0xFF, dtype=torch.uint8, device="cuda")  # NaN partials
+    lws = torch.zeros(max(lib.w4g64_linear_workspace_bytes(1, n, k, _lib.DTYPE_BF16), 1), dtype=torch.uint8,
+                      device="cuda")
+    attended = torch.empty((1, k), dtype=torch.bfloat16, device="cuda")
+    want = torch.empty((1, n), dtype=torch.bfloat16, device="cuda")
+    got = torch.empty((1, n), dtype=torch.bfloat16, device="cuda")
+    for pos in positions:
+        qkv = (torch.randn((1, (heads + 2 * kv_heads) * d), generator=g, device="cuda") * 2).to(torch.bfloat16)
+        position = torch.tensor([pos], dtype=torch.long, device="cuda")
+        cos, sin = rot(position.view(1, 1), torch.bfloat16)
+        cos, sin = cos.reshape(1, d).contiguous(), sin.reshape(1, d).contiguous()
+        _lib.check(lib.qwen2_decode_attention(
+            _p(qkv), _p(cos), _p(sin), _p(k_cache), _p(v_cache), _p(position), _p(attended), 1, heads, kv_heads, d,
+            max_length, ctypes.c_float(d ** -0.5), _p(ws), ws.numel(), _stream()))
+        _lib.check(lib.w4g64_linear(_p(attended), _lib.DTYPE_BF16, _p(qw), _p(sc), _p(z), _p(bias), bias_code,
+                                    _p(want), 1, n, k, _p(lws), lws.numel(), _stream()))
+        _lib.check(lib.qwen2_decode_attention_partials(
+            _p(qkv), _p(cos), _p(sin), _p(k_part), _p(v_part), _p(position), 1, heads, kv_heads, d, max_length,
+            ctypes.c_float(d ** -0.5), _p(ws_part), ws_part.numel(), _stream()))
+        _lib.check(lib.w4g64_linear_attention_merge(_p(ws_part), ws_part.numel(), max_length, heads, kv_heads,
+                                                    _p(qw), _p(sc), _p(z), _p(bias), bias_code, _p(got), 1, n,
+                                                    _stream()))
+        torch.cuda.synchronize()
+        assert torch.equal(k_part, k_cache) and torch.equal(v_part, v_cache), pos
+        assert torch.isfinite(want.float()).all(), pos
+        assert torch.equal(got, want), (pos, (got.float() - want.float()).abs().max().item())
+
+
+def test_fused_decode_step_merged_in_o_proj_is_bit_identical():
+    """The batch-1 decode step with the attention merged in the o_proj GEMV
+    against the same step with the attention's own merge: identical logits,
+    greedy tokens and caches over 70 steps (across a 64-position chunk
+    boundary)."""
+    from qwen_int4_hip.decode import FusedDecodeStep
+    from qwen_int4_hip.generation import StaticGreedyDecoder
+
+    model = _build(SMALL128, 21)
+    prompt = torch.randint(0, SMALL128.vocab_size, (1, 13), generator=torch.Generator().manual_seed(7)).cuda()
+    merged = StaticGreedyDecoder(model, 1, 96, use_graph=False, fused=True)
+    plain = StaticGreedyDecoder(model, 1, 96, use_graph=False, fused=True)
+    plain.fused = FusedDecodeStep(model, 1, 96, merge_attention_in_o_proj=False)
+    assert merged.fused.merge_in_o_proj and not plain.fused.merge_in_o_proj
+    merged.prefill(prompt)
+    plain.prefill(prompt)
+    for step in range(70):
+        token = plain.token.clone()
+        want = plain.step(token).clone()
+        got = merged.step(token).clone()
+        assert torch.equal(got, want), step
+        assert torch.equal(merged.token, plain.token), step
+    for (k0, v0), (k1, v1) in zip(plain.caches, merged.caches):
+        assert torch.equal(k0, k1) and torch.equal(v0, v1)
+
+
 @pytest.mark.parametrize("batch,hidden,vocab", [(1, 1536, 151936), (3, 256, 512)])
 def test_decode_prologue_matches_embedding_and_rotary(batch, hidden, vocab):
     """qwen2_decode_prologue = the embedding lookup and RotaryEmbedding.forward
