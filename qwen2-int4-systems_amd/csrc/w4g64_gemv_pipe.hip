@@ -713,7 +713,8 @@ __global__ __launch_bounds__(WR * WK * 64) void gemv_pipe_kernel(PipeArgs a) {
     X(4, 1, 4, 1, 2, 3, 3, 1)  \
     X(4, 1, 1, 3, 1, 1, 1, 1)  \
     X(4, 1, 4, 1, 1, 3, 3, 1)  \
-    X(2, 1, 2, 7, 1, 1, 1, 1)  \
+    X(4, 1, 2, 4, 1, 5, 3, 5)  \
+    X(4, 2, 2, 6, 1, 3, 3, 6)  \
     X(2, 1, 4, 1, 2, 6, 3, 3)  \
     X(2, 1, 2, 2, 1, 3, 3, 3)  \
     X(1, 1, 1, 7, 1, 2, 2, 4)  \
@@ -813,8 +814,10 @@ bool finish_pipe_plan(int64_t rows, int64_t out_features, int64_t in_features, G
 // over cold weights, graph-replayed (decode calls) and one launch over a
 // 28-layer stack (steady state): one row, gate 8960x1536 4.3 us, down
 // 1536x8960 4.6 us, the stacked gate|up 5.7 TB/s and down 4.5 TB/s; 16
-// rows, gate 6.4 us, down 8.5 us (five K splits and the reduction).  A K
-// range longer than a shape's span is split across workgroups.
+// rows, gate 6.4 us, down 8.5 us (five K splits and the reduction; shapes
+// with 64-128 rows and 4-10 pairs per workgroup, 10-18 K splits, measured
+// 9.2-10.9 us).  A K range longer than a shape's span is split across
+// workgroups.
 struct PipeShape {
     int min_rows, max_rows;
     int64_t min_pairs, max_pairs;
@@ -830,8 +833,10 @@ const PipeShape kPipeShapes[] = {
     {1, 1, 1, 47, 32768, kAnyN, 4, 1, 4, 1, 2, 3, 3},
     {1, 1, 1, 47, 1, 512, 4, 1, 1, 3, 1, 1, 1},
     {1, 1, 1, 47, 1, kAnyN, 4, 1, 4, 1, 1, 3, 3},
-    // 2..4 rows
-    {2, 4, 48, 1 << 20, 1, kAnyN, 2, 1, 2, 7, 1, 1, 1},
+    // 2..4 rows: long K in one workgroup (72 or 80 pairs), no split-K
+    // reduction launch (down 1536x8960: 2 rows 7.3 -> 5.0 us, 4 rows 7.3 -> 6.2)
+    {2, 2, 48, 1 << 20, 1, kAnyN, 4, 1, 2, 4, 1, 5, 3},
+    {3, 4, 48, 1 << 20, 1, kAnyN, 4, 2, 2, 6, 1, 3, 3},
     {2, 4, 1, 47, 32768, kAnyN, 2, 1, 4, 1, 2, 6, 3},
     {2, 4, 1, 47, 1, kAnyN, 2, 1, 2, 2, 1, 3, 3},
     // 5..8 rows

@@ -362,12 +362,14 @@ def test_lean_kernel_with_an_empty_k_part_ignores_lds_leftovers(dtype):
 
 
 @pytest.mark.parametrize("dtype", ["fp16", "bf16"])
-@pytest.mark.parametrize("rows", [1, 3, 6, 12])
-@pytest.mark.parametrize("n,k", [(264, 4096), (1000, 3328), (40, 256)])
+@pytest.mark.parametrize("rows", [1, 2, 3, 4, 6, 12])
+@pytest.mark.parametrize("n,k", [(264, 4096), (1000, 3328), (40, 256), (264, 13824), (100, 6144)])
 def test_pipe_kernel_k_splits_and_pairs_past_the_range(n, k, rows, dtype):
     """The pipelined GEMV with K split across workgroups whose last split is
     mostly pairs past the range (K = 4096: spans of 12 pairs over 32 pairs;
-    K = 3328: 26 pairs, the last split 2 real pairs), a partial last row
+    K = 3328: 26 pairs, the last split 2 real pairs; at 2..4 rows the long-K
+    spans of 72 and 80 pairs: K = 13824 in two splits, K = 6144 in one span
+    a third past the range), a partial last row
     block (n = 264, 1000, 40), and LDS left full of NaN by a GEMM over NaN
     activations: steps past the range must add exactly nothing (their scales,
     activations and, bf16, group sums are never taken from stale LDS)."""
