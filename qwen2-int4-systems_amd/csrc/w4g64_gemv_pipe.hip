@@ -65,6 +65,14 @@ struct PipeArgs {
     int G;   // groups
     int P;   // group pairs
     int PS;  // pairs per K split
+    // attention-merge form: x is the decode attention's partial results
+    // (kAttnPartFloats per chunk, `att_chunks` chunks per key/value head,
+    // att_bytes in all); query head h reads key/value head h / att_group
+    // (att_ginv = 1 / att_group)
+    int att_chunks;
+    int att_group;
+    int att_bytes;
+    float att_ginv;
     // RMSNorm prologue (one row): x is the bf16 residual; the activation is
     // RMSNorm(x + delta) with `norm_w` and `eps`; workgroup (0, 0) stores
     // x + delta (bf16) to out_sum.  delta: bf16 [K] (FORM kNormBf16) or
@@ -74,12 +82,6 @@ struct PipeArgs {
     const uint16_t* norm_w;
     float eps;
     uint16_t* out_sum;
-    // attention-merge form: x is the decode attention's partial results
-    // (kAttnPartFloats per chunk, `att_chunks` chunks per (row, key/value
-    // head)); query head h of row m reads key/value head h / att_group
-    int att_chunks;
-    int att_group;
-    int att_kv_heads;
     W4G64_TIMELINE_FIELDS
 };
 
@@ -268,45 +270,44 @@ __global__ __launch_bounds__(WR * WK * 64) void gemv_pipe_kernel(PipeArgs a) {
         }
         if constexpr (kNorm) nwv[u] = *(const u32x4*)(a.norm_w + 8 * k8);
     }
-    // attention-merge form: the 8 exp-weighted value sums of item it's head in
-    // every chunk (threads past the items load nothing), and for the (row,
-    // head) pairs hm = wave + W j each lane c < att_chunks loads chunk c's m
-    // and l
+    // attention-merge form (one row): item it (values 8 it .. 8 it + 7 of
+    // head h = 8 it / 128) reads the 8 exp-weighted value sums of every chunk
+    // c < att_chunks (threads past the items load nothing), and for the
+    // heads h = wave + W j each lane c < att_chunks loads chunk c's m and l
+    static_assert(!kMerge || STG == 1, "attention merge: one staged item per thread");
     constexpr int kMC = kMerge ? kAttnMergeMaxChunks : 1;
     constexpr int kMJ = kMerge ? 4 : 1;
     // (held as float vectors: a bit cast of one element of an integer vector
     // compiles to element 0 of that vector with this compiler)
-    float4v mv[kMerge ? STG : 1][kMC][2];
+    float4v mv[kMC][2];
     float mstat[kMJ], lstat[kMJ];
     if constexpr (kMerge) {
-        const float* parts = (const float*)a.x;
+        // buffer loads: the chunk's offset is a scalar operand, so a chunk's
+        // loads need no per-lane address arithmetic (0x00020000: the gfx9
+        // raw-buffer descriptor word; offsets past att_bytes read zeros)
+        const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, 0, a.att_bytes, 0x00020000);
         const int heads = K / kAttnHeadDim;
+        const int it = xit[0];  // one row, one K range: values 8 it .. 8 it + 7 of head it / 16
+        const int h = it >> 4;
+        const int kvh = (int)(((float)h + 0.5f) * a.att_ginv);  // exact for h < 2^20
+        const int voff = 4 * (kvh * a.att_chunks * kAttnPartFloats + 2 * kAttnMaxGroup +
+                              (h - kvh * a.att_group) * kAttnHeadDim + 8 * (it & 15));
+        if (tid < items) {
 #pragma unroll
-        for (int u = 0; u < STG; ++u) {
-            const int it = xit[u];
-            const int m = it / per_row;
-            const int k = 8 * (it - m * per_row);  // one K range: p0 = 0
-            const int h = k / kAttnHeadDim;
-            const float* src = parts + (int64_t)(m * a.att_kv_heads + h / a.att_group) * a.att_chunks * kAttnPartFloats +
-                               2 * kAttnMaxGroup + (h % a.att_group) * kAttnHeadDim + k % kAttnHeadDim;
-            if (kThreads * u + tid < items) {
-#pragma unroll
-                for (int c = 0; c < kMC; ++c)
-                    if (c < a.att_chunks) {
-                        mv[u][c][0] = *(const float4v*)(src + c * kAttnPartFloats);
-                        mv[u][c][1] = *(const float4v*)(src + c * kAttnPartFloats + 4);
-                    }
-            }
+            for (int c = 0; c < kMC; ++c)
+                if (c < a.att_chunks) {
+                    mv[c][0] = __builtin_bit_cast(float4v, __builtin_amdgcn_raw_buffer_load_b128(prs, voff, c * 4 * kAttnPartFloats, 0));
+                    mv[c][1] = __builtin_bit_cast(float4v, __builtin_amdgcn_raw_buffer_load_b128(prs, voff + 16, c * 4 * kAttnPartFloats, 0));
+                }
         }
+        const int soff_lane = 4 * kAttnPartFloats * min(lane, a.att_chunks - 1);
 #pragma unroll
         for (int j = 0; j < kMJ; ++j) {
-            const int hm = min(wave + W * j, M * heads - 1);
-            const int m = hm / heads, h = hm % heads;
-            const int cl = min(lane, a.att_chunks - 1);
-            const float* st = parts + ((int64_t)(m * a.att_kv_heads + h / a.att_group) * a.att_chunks + cl) * kAttnPartFloats +
-                              h % a.att_group;
-            mstat[j] = st[0];
-            lstat[j] = st[kAttnMaxGroup];
+            const int hj = min(wave + W * j, heads - 1);
+            const int kj = (int)(((float)hj + 0.5f) * a.att_ginv);
+            const int soff = 4 * (kj * a.att_chunks * kAttnPartFloats + hj - kj * a.att_group);
+            mstat[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(prs, soff_lane, soff, 0));
+            lstat[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(prs, soff_lane + 4 * kAttnMaxGroup, soff, 0));
         }
     }
     asm volatile("" ::: "memory");
@@ -344,7 +345,7 @@ __global__ __launch_bounds__(WR * WK * 64) void gemv_pipe_kernel(PipeArgs a) {
     for (int u = 0; u < STG; ++u) {
         if constexpr (kMerge) {
 #pragma unroll
-            for (int c = 0; c < kMC; ++c) asm volatile("" : "+v"(mv[u][c][0]), "+v"(mv[u][c][1]));
+            for (int c = 0; c < kMC; ++c) asm volatile("" : "+v"(mv[c][0]), "+v"(mv[c][1]));
         } else {
             asm volatile("" : "+v"(xv[u]));
         }
@@ -366,36 +367,45 @@ __global__ __launch_bounds__(WR * WK * 64) void gemv_pipe_kernel(PipeArgs a) {
     if constexpr (kMerge) {
         const int heads = K / kAttnHeadDim;
         float* scl = (float*)(smem + L.total);  // [M heads][kMC]
+        // the kMJ pairs of a wave side by side (independent chains; pairs
+        // past the heads repeat the last one and are not stored)
+        const bool live = lane < a.att_chunks;
+        float mx[kMJ], ex[kMJ], lsum[kMJ];
+#pragma unroll
+        for (int j = 0; j < kMJ; ++j) mx[j] = wave_max64(live ? fmaxf(-INFINITY, mstat[j]) : -INFINITY);
+#pragma unroll
+        for (int j = 0; j < kMJ; ++j) ex[j] = live ? expf(mstat[j] - mx[j]) : 0.0f;
+#pragma unroll
+        for (int j = 0; j < kMJ; ++j) lsum[j] = wave_sum64(live ? fmaf(lstat[j], ex[j], 0.0f) : 0.0f);
 #pragma unroll
         for (int j = 0; j < kMJ; ++j) {
             const int hm = wave + W * j;
-            if (hm < M * heads) {
-                const bool live = lane < a.att_chunks;
-                const float mx = wave_max64(live ? fmaxf(-INFINITY, mstat[j]) : -INFINITY);
-                const float l = wave_sum64(live ? fmaf(lstat[j], expf(mstat[j] - mx), 0.0f) : 0.0f);
-                if (lane < kMC) scl[hm * kMC + lane] = live ? expf(mstat[j] - mx) / l : 0.0f;
-            }
+            if (hm < M * heads && lane < kMC) scl[hm * kMC + lane] = live ? ex[j] / lsum[j] : 0.0f;
         }
         lds_barrier();
+        W4G64_STAMP(5);
+        {
+            const int hm = 8 * xit[0] / kAttnHeadDim;
+            float scv[kMC];
 #pragma unroll
-        for (int u = 0; u < STG; ++u) {
-            const int it = xit[u];
-            const int m = it / per_row;
-            const int hm = m * heads + 8 * (it - m * per_row) / kAttnHeadDim;
+            for (int c = 0; c < kMC; ++c) scv[c] = scl[hm * kMC + c];  // all read before the sums
+            // the chunks that were loaded (a uniform branch each; threads
+            // past the items hold no value and store none)
             float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-            if (kThreads * u + tid < items) {
 #pragma unroll
-                for (int c = 0; c < kMC; ++c)
-                    if (c < a.att_chunks) {
-                        const float sc = scl[hm * kMC + c];
+            for (int c = 0; c < kMC; ++c)
+                if (c < a.att_chunks) {
 #pragma unroll
-                        for (int e = 0; e < 8; ++e) o[e] = fmaf(mv[u][c][e / 4][e % 4], sc, o[e]);
+                    for (int e = 0; e < 4; ++e) {
+                        o[e] = fmaf(mv[c][0][e], scv[c], o[e]);
+                        o[4 + e] = fmaf(mv[c][1][e], scv[c], o[4 + e]);
                     }
-            }
+                }
 #pragma unroll
             for (int e = 0; e < 4; ++e)
-                xv[u][e] = float_to_bf16_bits(o[2 * e]) | ((uint32_t)float_to_bf16_bits(o[2 * e + 1]) << 16);
+                xv[0][e] = float_to_bf16_bits(o[2 * e]) | ((uint32_t)float_to_bf16_bits(o[2 * e + 1]) << 16);
         }
+        W4G64_STAMP(6);
     }
 
     // ---- 2b. RMSNorm prologue (model.py:40-44, residual adds :149-154) ----
@@ -978,7 +988,8 @@ hipError_t launch_gemv_pipe(const LinearProblem& p, const GemvPlan& plan, void* 
     a.out_sum = (uint16_t*)p.norm_out_sum;
     a.att_chunks = p.att_chunks;
     a.att_group = p.att_group;
-    a.att_kv_heads = p.att_kv_heads;
+    a.att_bytes = (int)((int64_t)p.att_kv_heads * p.att_chunks * kAttnPartFloats * 4);
+    a.att_ginv = p.att_group > 0 ? 1.0f / (float)p.att_group : 0.0f;
     a.K = (int)p.in_features;
     a.G = a.K / 64;
     a.P = a.G / 2;
