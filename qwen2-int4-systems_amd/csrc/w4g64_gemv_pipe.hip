@@ -242,7 +242,7 @@ __global__ __launch_bounds__(WR * WK * 64) void gemv_pipe_kernel(PipeArgs a) {
 
     // ---- 1. staging loads: item it = 8 activation values of row m ----
     // (norm forms: the residual's 8 values, the delta's and the norm
-    // weight's; parts past delta_parts re-read the last one)
+    // weight's; parts past delta_parts are not read)
     const int per_row = ps * 16;
     const int items = M * per_row;
     constexpr int kDeltaVecs = FORM == kNormParts ? 2 * kMaxDeltaParts : (FORM == kNormBf16 ? 1 : 0);
@@ -261,12 +261,15 @@ __global__ __launch_bounds__(WR * WK * 64) void gemv_pipe_kernel(PipeArgs a) {
         if constexpr (FORM == kNormBf16) {
             dv[u][0] = *(const u32x4*)((const uint16_t*)a.delta + 8 * k8);
         } else if constexpr (FORM == kNormParts) {
+            // the delta_parts parts alone (a uniform branch each; the sums
+            // below read only these)
 #pragma unroll
-            for (int pt = 0; pt < kMaxDeltaParts; ++pt) {
-                const float* dsrc = (const float*)a.delta + (int64_t)min(pt, a.delta_parts - 1) * K + 8 * k8;
-                dv[u][2 * pt] = *(const u32x4*)dsrc;
-                dv[u][2 * pt + 1] = *(const u32x4*)(dsrc + 4);
-            }
+            for (int pt = 0; pt < kMaxDeltaParts; ++pt)
+                if (pt < a.delta_parts) {
+                    const float* dsrc = (const float*)a.delta + (int64_t)pt * K + 8 * k8;
+                    dv[u][2 * pt] = *(const u32x4*)dsrc;
+                    dv[u][2 * pt + 1] = *(const u32x4*)(dsrc + 4);
+                }
         }
         if constexpr (kNorm) nwv[u] = *(const u32x4*)(a.norm_w + 8 * k8);
     }
@@ -436,10 +439,11 @@ __global__ __launch_bounds__(WR * WK * 64) void gemv_pipe_kernel(PipeArgs a) {
                     } else {
                         float t = 0.0f;
 #pragma unroll
-                        for (int pt2 = 0; pt2 < kMaxDeltaParts; ++pt2) {
-                            const uint32_t bits = dv[u][2 * pt2 + (e + h) / 4][(e + h) % 4];
-                            t = pt2 < a.delta_parts ? t + __builtin_bit_cast(float, bits) : t;
-                        }
+                        for (int pt2 = 0; pt2 < kMaxDeltaParts; ++pt2)
+                            if (pt2 < a.delta_parts) {
+                                const uint32_t bits = dv[u][2 * pt2 + (e + h) / 4][(e + h) % 4];
+                                t = t + __builtin_bit_cast(float, bits);
+                            }
                         df = bf16_round(t + 0.0f);
                     }
                     sv[h] = bf16_round(xf + df);
