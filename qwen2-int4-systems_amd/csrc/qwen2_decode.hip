@@ -254,24 +254,37 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
     W4G64_STAMP(0);
 
     // ---- loads that do not depend on the position: queries, rotary factors, new key/value ----
-    constexpr int kQItems = kMaxGroup * kHeadDim / kAttnThreads;
-    uint16_t qx[kQItems], qp[kQItems], qc[kQItems], qn[kQItems];
-#pragma unroll
-    for (int i = 0; i < kQItems; ++i) {
-        const int e = tid + kAttnThreads * i;
-        const int g = min(e / kHeadDim, group - 1);
-        const int dd = e % kHeadDim;
-        const uint16_t* vec = qkv + (kvh * group + g) * kHeadDim;
-        qx[i] = vec[dd];
-        qp[i] = vec[dd ^ (kHeadDim / 2)];  // rotate_half partner
-        qc[i] = cs[dd];
-        qn[i] = sn[dd];
-    }
+    // Thread t: dimensions qd = 8 (t % 16) .. qd + 7 (and their rotate_half
+    // partners qd ^ 64 ..) of query head t / 16 of the group (threads past the
+    // group re-read its last head), the rotary factors of those dimensions,
+    // and -- used by threads t < 16 -- the same dimensions of the new key and
+    // value: 16-byte loads.
+    const int qg = tid / 16;
+    const int qd = 8 * (tid % 16);
+    const u32x4 qcv = *(const u32x4*)(cs + qd);
+    const u32x4 qnv = *(const u32x4*)(sn + qd);
+    const uint16_t* qvec = qkv + (kvh * group + min(qg, group - 1)) * kHeadDim;
+    const u32x4 qxv = *(const u32x4*)(qvec + qd);
+    const u32x4 qpv = *(const u32x4*)(qvec + (qd ^ (kHeadDim / 2)));
     const uint16_t* kvec = qkv + (a.heads + kvh) * kHeadDim;
-    const int dk = tid % kHeadDim;
-    const uint16_t kx = kvec[dk];
-    const uint16_t kp = kvec[dk ^ (kHeadDim / 2)];
-    const uint16_t vx = qkv[(a.heads + a.kv_heads + kvh) * kHeadDim + dk];
+    const u32x4 kxv = *(const u32x4*)(kvec + qd);
+    const u32x4 kpv = *(const u32x4*)(kvec + (qd ^ (kHeadDim / 2)));
+    const u32x4 vxv = *(const u32x4*)(qkv + (a.heads + a.kv_heads + kvh) * kHeadDim + qd);
+    // 8 rotated dimensions qd .. qd + 7 of a head vector (rope_elem per element)
+    auto rope8 = [&](const u32x4& x, const u32x4& partner) {
+        u32x4 r;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint16_t lo = float_to_bf16_bits(rope_elem((uint16_t)(x[e] & 0xFFFFu), (uint16_t)(partner[e] & 0xFFFFu),
+                                                             (uint16_t)(qcv[e] & 0xFFFFu), (uint16_t)(qnv[e] & 0xFFFFu),
+                                                             qd + 2 * e));
+            const uint16_t hi = float_to_bf16_bits(rope_elem((uint16_t)(x[e] >> 16), (uint16_t)(partner[e] >> 16),
+                                                             (uint16_t)(qcv[e] >> 16), (uint16_t)(qnv[e] >> 16),
+                                                             qd + 2 * e + 1));
+            r[e] = (uint32_t)lo | ((uint32_t)hi << 16);
+        }
+        return r;
+    };
     // The position is read first (its load returns before the chunk's), then
     // the chunk's 64 cache rows are loaded without waiting for it: rows past
     // the cache end re-read its last row, and rows at or past the position
@@ -307,18 +320,12 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
     if (nk > 0) {
         // cached rows t0 .. t0 + cached - 1 are used as loaded
         const int cached = min(nk, pos - t0);
-#pragma unroll
-        for (int i = 0; i < kQItems; ++i) {
-            const int e = tid + kAttnThreads * i;
-            if (e / kHeadDim < group)
-                qsb[e / kHeadDim][e % kHeadDim] = float_to_bf16_bits(rope_elem(qx[i], qp[i], qc[i], qn[i], e % kHeadDim));
-        }
-        if (pos - t0 < kChunk && tid < kHeadDim) {  // this chunk holds the new position
-            // qc[0] / qn[0] hold cos / sin of dimension (tid + 0) % 128 = tid
-            const uint16_t kb = float_to_bf16_bits(rope_elem(kx, kp, qc[0], qn[0], tid));
-            a.k_cache[cache_base + (int64_t)pos * kHeadDim + tid] = kb;
-            a.v_cache[cache_base + (int64_t)pos * kHeadDim + tid] = vx;
-            ks[pos - t0][tid] = kb;
+        if (qg < group) *(u32x4*)&qsb[qg][qd] = rope8(qxv, qpv);
+        if (pos - t0 < kChunk && tid < kHeadDim / 8) {  // this chunk holds the new position
+            const u32x4 kb = rope8(kxv, kpv);
+            *(u32x4*)(a.k_cache + cache_base + (int64_t)pos * kHeadDim + qd) = kb;
+            *(u32x4*)(a.v_cache + cache_base + (int64_t)pos * kHeadDim + qd) = vxv;
+            *(u32x4*)&ks[pos - t0][qd] = kb;
         }
 #pragma unroll
         for (int i = 0; i < kPieces; ++i) {
@@ -368,16 +375,29 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
         __syncthreads();
         W4G64_STAMP(2);
 
-        // ---- chunk softmax statistics: wave w takes heads w, w + 4; lane = position ----
-        for (int g = wave; g < group; g += kAttnThreads / 64) {
-            const float sv = pr[g][lane];
-            const float m = wave_max(sv);
-            const float e = lane < nk ? expf(sv - m) : 0.0f;
-            pr[g][lane] = e;
-            const float l = wave_sum(e);
+        // ---- chunk softmax statistics: wave w takes heads w and w + 4 side by
+        // side (two independent chains); lane = position ----
+        {
+            static_assert(kMaxGroup <= 2 * (kAttnThreads / 64), "two heads per wave");
+            const int g0 = wave, g1 = wave + kAttnThreads / 64;
+            const bool has0 = g0 < group, has1 = g1 < group;  // uniform
+            const float sv0 = pr[min(g0, group - 1)][lane];
+            const float sv1 = pr[min(g1, group - 1)][lane];
+            const float m0 = wave_max(sv0), m1 = wave_max(sv1);
+            const float e0 = lane < nk ? expf(sv0 - m0) : 0.0f;
+            const float e1 = lane < nk ? expf(sv1 - m1) : 0.0f;
+            const float l0 = wave_sum(e0), l1 = wave_sum(e1);
+            if (has0) pr[g0][lane] = e0;
+            if (has1) pr[g1][lane] = e1;
             if (lane == 0) {
-                stat_m[g] = m;
-                stat_l[g] = l;
+                if (has0) {
+                    stat_m[g0] = m0;
+                    stat_l[g0] = l0;
+                }
+                if (has1) {
+                    stat_m[g1] = m1;
+                    stat_l[g1] = l1;
+                }
             }
         }
         __syncthreads();
