@@ -796,6 +796,10 @@ GEMV_PHASES = ("entry", "staging landed", "staged in LDS", "LDS barrier", "MFMA 
                "partial sums combined", "stores issued", "stores complete")
 PIPE_PHASES = ("entry", "staging landed, first loads issued", "LDS barrier", "steps done", "stores issued", "-", "-",
                "stores complete")
+UNMERGED_ATTENTION_PHASES = ("entry", "chunk staged in LDS", "scores", "softmax statistics", "partials stored",
+                             "exit", "-", "stores complete")
+MERGE_PHASES = ("entry", "staging landed, first loads issued", "LDS barrier", "steps done", "stores issued",
+                "merge statistics in LDS", "merged row formed", "stores complete")
 ATTENTION_PHASES = ("entry", "chunk staged in LDS", "scores", "softmax statistics", "partials stored",
                     "arrival counted", "merge statistics (last arrival)", "stores complete")
 
@@ -970,6 +974,26 @@ def timeline_pass() -> int:
            lambda: _lib.check(lib.qwen2_decode_attention(p_(qkv), p_(cos), p_(sin), p_(kc), p_(vc), p_(position), p_(out),
                                                          1, heads, kvh, hd, max_len, hd ** -0.5, p_(aws), aws.numel(),
                                                          stream)),
+           scrubbed=False)
+    # the batch-1 decode step's form: the attention leaves its per-chunk partials and the o_proj GEMV merges them
+    # in its staging; the plain o_proj over the attention's output beside it
+    report(f"decode attention without its merge, position {pos} (partials only)", UNMERGED_ATTENTION_PHASES,
+           lambda: _lib.check(lib.qwen2_decode_attention_partials(p_(qkv), p_(cos), p_(sin), p_(kc), p_(vc),
+                                                                  p_(position), 1, heads, kvh, hd, max_len,
+                                                                  hd ** -0.5, p_(aws), aws.numel(), stream)),
+           scrubbed=False)
+    qo, so, zo = gen_weights(heads * hd, heads * hd, BASE_SEED + 23, torch)
+    yo = torch.empty((1, heads * hd), dtype=torch.bfloat16, device="cuda")
+    ows = _workspace(torch.device("cuda"), 1 << 20)
+    report(f"o_proj {heads * hd}x{heads * hd} merging the {-(-max_len // 64)} chunks' partials in its staging",
+           MERGE_PHASES,
+           lambda: _lib.check(lib.w4g64_linear_attention_merge(p_(aws), aws.numel(), max_len, heads, kvh, p_(qo), p_(so),
+                                                               p_(zo), None, _lib.DTYPE_NONE, p_(yo), 1, heads * hd,
+                                                               stream)),
+           scrubbed=False)
+    report(f"o_proj {heads * hd}x{heads * hd} over the attention's bf16 output (plain form)", PIPE_PHASES,
+           lambda: _lib.check(lib.w4g64_linear(p_(out), _lib.DTYPE_BF16, p_(qo), p_(so), p_(zo), None, _lib.DTYPE_NONE,
+                                               p_(yo), 1, heads * hd, heads * hd, p_(ows), ows.numel(), stream)),
            scrubbed=False)
     lib.w4g64_timeline_register(None, 0)
 
