@@ -220,15 +220,15 @@ def test_lean_decode_kernel(n, k, kind, rows, dtype):
 
 
 @pytest.mark.parametrize("dtype", ["fp16", "bf16"])
-@pytest.mark.parametrize("rows", [1, 3])
-def test_pipe_kernel_two_row_blocks_per_wave(rows, dtype):
-    """32768+ output features at 1..4 rows: each wave of the pipelined kernel
-    owns two row blocks, so the codes of one block are formed right before
-    their MFMAs -- the schedule in which an operand written without the
-    MFMA's wait states once corrupted every second block of bf16 rows."""
+@pytest.mark.parametrize("rows,n,k", [(1, 32768, 1536), (3, 32768, 1536), (1, 33032, 6144)])
+def test_pipe_kernel_two_row_blocks_per_wave(rows, n, k, dtype):
+    """32768+ output features at 1..4 rows (and at one row over a long K, with
+    a last row block that is only partly filled): each wave of the pipelined
+    kernel owns two row blocks, so the codes of one block are formed right
+    before their MFMAs -- the schedule in which an operand written without
+    the MFMA's wait states once corrupted every second block of bf16 rows."""
     from qwen_int4_hip import linear_kernel_name
 
-    n, k = 32768, 1536
     torch_dtype = torch.float16 if dtype == "fp16" else torch.bfloat16
     name = linear_kernel_name(rows, n, k, torch_dtype)
     assert name.startswith("gemv_pipe_kernel") and name.split(",")[5] == "2", name  # RBW = 2
