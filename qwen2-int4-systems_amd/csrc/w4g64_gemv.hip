@@ -848,8 +848,8 @@ const char* gemv_kernel_name(const GemvPlan& plan, int x_kind) {
         // the pipelined kernel's activation form comes from the plan
         static const char* forms[] = {"", "planes_bf16", "rmsnorm_bf16", "rmsnorm_partials"};
         const char* form = plan.form >= 1 && plan.form <= 3 ? forms[plan.form] : kinds[x_kind >= 1 && x_kind <= 8 ? x_kind : 0];
-        snprintf(name, sizeof(name), "gemv_pipe_kernel<%s%s,%d,%d,%d,%d,%d,%d,%d>", form, plan.pair ? "_gate_up" : "",
-                 plan.segments, plan.tiles, plan.fblocks, plan.kparts, plan.rbw, plan.steps, plan.depth);
+        snprintf(name, sizeof(name), "gemv_pipe_kernel<%s%s%s,%d,%d,%d,%d,%d,%d,%d>", form, plan.pair ? "_gate_up" : "",
+                 plan.form == kGrouped ? "_grouped" : "", plan.segments, plan.tiles, plan.fblocks, plan.kparts, plan.rbw, plan.steps, plan.depth);
         return name;
     }
     if (plan.kind == 2) {

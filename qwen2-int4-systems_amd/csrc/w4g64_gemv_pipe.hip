@@ -24,6 +24,12 @@
 //     bf16: B = 136 + code exactly, and the group result is corrected by
 //     -(136 + zero) * sum_g x[m] (group sums formed once at staging).  The
 //     group scale then multiplies in fp32.
+//   * Grouped form (up to 16 rows, one segment): the four dwords of a
+//     column's four lanes are transposed across the lanes (two
+//     v_permlane32_swap and two v_permlane16_swap), so dword u of lane q
+//     holds K values 32 u + 8 q + 0..7 and MFMAs 0, 1 see group 0 alone and
+//     2, 3 group 1 alone: A row i is activation row i itself, one A tile
+//     for all rows, and each group's D is scaled on its own.
 //   * The activation range of the workgroup is staged once in LDS in MFMA
 //     slot order.  Every wave first issues its share of the staging loads;
 //     a barrier that waits for no memory keeps every weight load behind
@@ -188,9 +194,11 @@ __global__ __launch_bounds__(WR * WK * 64) void gemv_pipe_kernel(PipeArgs a) {
     constexpr int PL = FORM == kPlanes3 ? 3 : 1;  // staged rows per output row
     constexpr bool kNorm = FORM == kNormBf16 || FORM == kNormParts;
     constexpr bool kMerge = FORM == kAttnMerge;
+    constexpr bool kGrp = FORM == kGrouped;
     static_assert(!kMerge || (!PAIRED && WK == 1), "attention merge: plain rows, the whole K range per workgroup");
+    static_assert(!kGrp || (SW == 1 && MT == 1 && !PAIRED), "grouped: one segment, one A tile of up to 16 rows");
     static_assert(!PAIRED || (RBW == 2 && WK == 1), "paired: gate rows in row block 0, up rows in row block 1");
-    static_assert(XK == kBF16 || FORM == kPlain, "the fused forms are bf16");
+    static_assert(XK == kBF16 || FORM == kPlain || kGrp, "the fused forms are bf16");
     const int p0 = blockIdx.y * a.PS;        // first pair of the workgroup's K range
     const int pe = min(p0 + a.PS, P);        // end of its range
     const int ps = pe - p0;                  // pairs staged (>= 1)
@@ -506,7 +514,9 @@ __global__ __launch_bounds__(WR * WK * 64) void gemv_pipe_kernel(PipeArgs a) {
 
     // ---- 4. steps ----
     // A row of this lane in tile mt: i = lane % 16 -> v = 8 mt + i / 2, half
-    // p = i % 2; it reads x only for m < M and q / 2 == p.
+    // p = i % 2; it reads x only for m < M and q / 2 == p.  Grouped: A row i
+    // is activation row i (rows past M repeat row M - 1; their D rows are
+    // not stored).
     const int ai = lane & 15;
     const int ap = ai & 1;
     int am[MT], as_[MT];
@@ -521,9 +531,11 @@ __global__ __launch_bounds__(WR * WK * 64) void gemv_pipe_kernel(PipeArgs a) {
     // D rows of this lane: i = 4 q + r' -> v = 8 mt + 2 q + r' / 2, p = r' % 2
     const float* sxl = (const float*)(smem + L.sx);
     const unsigned char* xs = smem;
-    float4v acc[MT][RBW];
+    // (grouped: acc[g] sums group g of every pair, D row i = 4 q + r')
+    constexpr int NA = kGrp ? 2 : MT;
+    float4v acc[NA][RBW];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+    for (int mt = 0; mt < NA; ++mt)
 #pragma unroll
         for (int b = 0; b < RBW; ++b) acc[mt][b] = float4v{0.f, 0.f, 0.f, 0.f};
 
@@ -531,19 +543,35 @@ __global__ __launch_bounds__(WR * WK * 64) void gemv_pipe_kernel(PipeArgs a) {
     for (int t = 0; t < T; ++t) {
         // this step's A fragments (shared by the RBW row blocks)
         u16x8 av[MT][4];
+        if constexpr (kGrp) {
+            // MFMA u: K values 32 u + 8 q + 0..7 of the pair (a pair past
+            // the range reads the zero bytes, the same 16 for every u)
+            const int ja = pb + t;
+            const bool in = ja < pe;
+            const unsigned char* asrc = in ? xs + 2 * (min(ai, M - 1) * L.xw + (ja - p0) * 128 + 8 * q) : smem + L.zero;
+            const int ust = in ? 64 : 0;
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-            const int ja = pb + as_[mt] + SW * t;
-            const bool alive = alive0[mt] && ja < pe;
-            // (dead lanes read the 64 zero bytes)
-            const unsigned char* asrc =
-                alive ? xs + 2 * (am[mt] * L.xw + (ja - p0) * 128 + 32 * q) : smem + L.zero;
+            for (int u = 0; u < 4; ++u) av[0][u] = *(const u16x8*)(asrc + ust * u);
+        } else {
 #pragma unroll
-            for (int u = 0; u < 4; ++u) av[mt][u] = *(const u16x8*)(asrc + 16 * u);
+            for (int mt = 0; mt < MT; ++mt) {
+                const int ja = pb + as_[mt] + SW * t;
+                const bool alive = alive0[mt] && ja < pe;
+                // (dead lanes read the 64 zero bytes)
+                const unsigned char* asrc =
+                    alive ? xs + 2 * (am[mt] * L.xw + (ja - p0) * 128 + 32 * q) : smem + L.zero;
+#pragma unroll
+                for (int u = 0; u < 4; ++u) av[mt][u] = *(const u16x8*)(asrc + 16 * u);
+            }
         }
         // bf16 group sums of the D rows' (m, pair) (clamped into the staged range)
-        float2v gsum[MT][2];
-        if constexpr (XK == kBF16) {
+        float2v gsum[MT][kGrp ? 4 : 2];
+        if constexpr (XK == kBF16 && kGrp) {
+            // D rows 4 q + r' (clamped), the step's pair
+            const int jp = min(pb + t - p0, ps - 1);
+#pragma unroll
+            for (int h = 0; h < 4; ++h) gsum[0][h] = *(const float2v*)(sxl + min(4 * q + h, M - 1) * 2 * a.PS + 2 * jp);
+        } else if constexpr (XK == kBF16) {
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -561,6 +589,15 @@ __global__ __launch_bounds__(WR * WK * 64) void gemv_pipe_kernel(PipeArgs a) {
             u32x4 w = wbuf[i % PF];
             uint32_t sw2 = sbuf[i % PF];
             asm volatile("" : "+v"(w), "+v"(sw2));  // this chunk's loads land here
+            if constexpr (kGrp) {
+                // 4 x 4 transpose of (lane row q, dword u) over the column's
+                // lanes c, c + 16, c + 32, c + 48
+                const auto t02 = __builtin_amdgcn_permlane32_swap(w[0], w[2], false, false);
+                const auto t13 = __builtin_amdgcn_permlane32_swap(w[1], w[3], false, false);
+                const auto t01 = __builtin_amdgcn_permlane16_swap(t02[0], t13[0], false, false);
+                const auto t23 = __builtin_amdgcn_permlane16_swap(t02[1], t13[1], false, false);
+                w = u32x4{t01[0], t01[1], t23[0], t23[1]};
+            }
             const uint32_t zb = take_u16(zbuf[i % PF]);
             const int zoff = 8 * ((jj < pe ? jj : p0) & 1);  // the zero byte's half
             // a pair past the range re-reads an in-range pair and has zero A
@@ -569,8 +606,45 @@ __global__ __launch_bounds__(WR * WK * 64) void gemv_pipe_kernel(PipeArgs a) {
             const bool live = XK == kF16 || jj < pe;
             const float s0 = live ? half_bits_to_float((uint16_t)(sw2 & 0xFFFFu)) : 0.0f;
             const float s1 = live ? half_bits_to_float((uint16_t)(sw2 >> 16)) : 0.0f;
-            float4v d[MT];
-            if constexpr (XK == kF16) {
+            float4v d[NA];
+            if constexpr (kGrp) {
+                // MFMAs 0, 1: group 0 of the pair; 2, 3: group 1
+                const int z0 = (int)__builtin_amdgcn_sbfe((int)zb, zoff, 4);
+                const int z1 = (int)__builtin_amdgcn_sbfe((int)zb, zoff + 4, 4);
+                if constexpr (XK == kF16) {
+                    half8 bv[4];
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        const int zl = u < 2 ? z0 : z1;
+                        bv[u] = codes8_f16(w[u], (uint32_t)(0x6408 + zl) * 0x00010001u,
+                                           (uint32_t)(0x5480 + 16 * zl) * 0x00010001u);
+                    }
+#pragma unroll
+                    for (int g = 0; g < 2; ++g) {
+                        d[g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, av[0][2 * g]), bv[2 * g],
+                                                                      float4v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                        d[g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, av[0][2 * g + 1]),
+                                                                      bv[2 * g + 1], d[g], 0, 0, 0);
+                    }
+                } else {
+                    bf16x8 bv[4];
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) bv[u] = codes8_bf16_biased(w[u]);
+#pragma unroll
+                    for (int g = 0; g < 2; ++g) {
+                        d[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, av[0][2 * g]), bv[2 * g],
+                                                                       float4v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                        d[g] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, av[0][2 * g + 1]),
+                                                                       bv[2 * g + 1], d[g], 0, 0, 0);
+                    }
+                    const float c0 = 136.0f + (float)z0, c1 = 136.0f + (float)z1;
+#pragma unroll
+                    for (int h = 0; h < 4; ++h) {
+                        d[0][h] = fmaf(-c0, gsum[0][h][0], d[0][h]);
+                        d[1][h] = fmaf(-c1, gsum[0][h][1], d[1][h]);
+                    }
+                }
+            } else if constexpr (XK == kF16) {
                 // the zero point of this lane's own group (q / 2)
                 const int zl = (int)__builtin_amdgcn_sbfe((int)zb, zoff + 4 * (q >> 1), 4);
                 const uint32_t clo = (uint32_t)(0x6408 + zl) * 0x00010001u;
@@ -608,13 +682,21 @@ __global__ __launch_bounds__(WR * WK * 64) void gemv_pipe_kernel(PipeArgs a) {
                         d[mt][2 * h + 1] = fmaf(-c1, gsum[mt][h][1], d[mt][2 * h + 1]);
                     }
             }
+            if constexpr (kGrp) {
 #pragma unroll
-            for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    acc[mt][b][2 * h] = fmaf(s0, d[mt][2 * h], acc[mt][b][2 * h]);
-                    acc[mt][b][2 * h + 1] = fmaf(s1, d[mt][2 * h + 1], acc[mt][b][2 * h + 1]);
+                for (int h = 0; h < 4; ++h) {
+                    acc[0][b][h] = fmaf(s0, d[0][h], acc[0][b][h]);
+                    acc[1][b][h] = fmaf(s1, d[1][h], acc[1][b][h]);
                 }
+            } else {
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        acc[mt][b][2 * h] = fmaf(s0, d[mt][2 * h], acc[mt][b][2 * h]);
+                        acc[mt][b][2 * h + 1] = fmaf(s1, d[mt][2 * h + 1], acc[mt][b][2 * h + 1]);
+                    }
+            }
             asm volatile("" ::: "memory");
             if (i + PF < C) issue(i + PF);
         }
@@ -631,7 +713,37 @@ __global__ __launch_bounds__(WR * WK * 64) void gemv_pipe_kernel(PipeArgs a) {
         if (split_out) a.partials[((int64_t)blockIdx.y * Mo + m) * N + n] = v;
         else store_out<FORM == kPlanes3 ? kF32 : XK>(a.y, (int64_t)m * N + n, v + bias_of(b));
     };
-    if constexpr (kWaveLocal && SW == 1 && PL == 1 && !PAIRED) {
+    if constexpr (kGrp && kWaveLocal) {
+        // lane (q, c): D rows 4 q + h are activation rows, column c is row r
+#pragma unroll
+        for (int b = 0; b < RBW; ++b)
+#pragma unroll
+            for (int h = 0; h < 4; ++h) {
+                const int m = 4 * q + h;
+                const int n = rowof(b, r);
+                if (m < M && n < N) emit(m, n, acc[0][b][h] + acc[1][b][h], b);
+            }
+    } else if constexpr (kGrp) {
+        float* red = (float*)(smem + L.red);  // [WK][M][RWG]
+#pragma unroll
+        for (int b = 0; b < RBW; ++b)
+#pragma unroll
+            for (int h = 0; h < 4; ++h) {
+                const int m = 4 * q + h;
+                if (m < M) red[(wk * M + m) * RWG + (b * WR + wr) * R + r] = acc[0][b][h] + acc[1][b][h];
+            }
+        lds_barrier();
+        for (int o = tid; o < Mo * RWG; o += kThreads) {
+            const int m = o / RWG, wrow = o % RWG;
+            const int n = row0 + wrow;
+            if (n < N) {
+                float v = 0.0f;
+#pragma unroll
+                for (int k2 = 0; k2 < WK; ++k2) v += red[(k2 * M + m) * RWG + wrow];
+                emit(m, n, v, 0);
+            }
+        }
+    } else if constexpr (kWaveLocal && SW == 1 && PL == 1 && !PAIRED) {
         // lane (q, c): rows v = 8 mt + 2 q + h of D are activation rows m = v
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
@@ -746,6 +858,12 @@ __global__ __launch_bounds__(WR * WK * 64) void gemv_pipe_kernel(PipeArgs a) {
     X(kPlanes3, false, 2, 1, 4, 1, 1, 7, 4, 3)       \
     X(kAttnMerge, false, 4, 1, 4, 1, 1, 3, 3, 1)
 
+// The grouped form (9..16 rows): (SW, MT, WR, WK, RBW, T, DP, STG).
+#define W4G64_PIPE_GROUPED_SHAPES(X) \
+    X(1, 1, 2, 7, 1, 2, 2, 4)        \
+    X(1, 1, 4, 2, 1, 6, 3, 6)        \
+    X(1, 1, 1, 12, 1, 1, 1, 4)
+
 typedef void (*PipeKernel)(PipeArgs);
 struct PipeEntry {
     int form, paired, sw, mt, wr, wk, rbw, t, dp, stg;
@@ -756,6 +874,10 @@ struct PipeEntry {
     {kPlain, 0, SW, MT, WR, WK, RBW, T, DP, STG,                                                       \
      gemv_pipe_kernel<kF16, kPlain, false, SW, MT, WR, WK, RBW, T, DP, STG>,                           \
      gemv_pipe_kernel<kBF16, kPlain, false, SW, MT, WR, WK, RBW, T, DP, STG>},
+#define W4G64_PIPE_GROUPED_ENTRY(SW, MT, WR, WK, RBW, T, DP, STG)                                      \
+    {kGrouped, 0, SW, MT, WR, WK, RBW, T, DP, STG,                                                     \
+     gemv_pipe_kernel<kF16, kGrouped, false, SW, MT, WR, WK, RBW, T, DP, STG>,                         \
+     gemv_pipe_kernel<kBF16, kGrouped, false, SW, MT, WR, WK, RBW, T, DP, STG>},
 #define W4G64_PIPE_FUSED_ENTRY(FORM, PAIRED, SW, MT, WR, WK, RBW, T, DP, STG)                          \
     {FORM, PAIRED ? 1 : 0, SW, MT, WR, WK, RBW, T, DP, STG, nullptr,                                   \
      gemv_pipe_kernel<kBF16, FORM, PAIRED, SW, MT, WR, WK, RBW, T, DP, STG>},
@@ -763,6 +885,7 @@ struct PipeEntry {
 const PipeEntry kPipeTable[] = {
     W4G64_PIPE_SHAPES(W4G64_PIPE_ENTRY)
     W4G64_PIPE_FUSED_SHAPES(W4G64_PIPE_FUSED_ENTRY)
+    W4G64_PIPE_GROUPED_SHAPES(W4G64_PIPE_GROUPED_ENTRY)
 #ifdef W4G64_PIPE_EXTRA_SHAPES  // tuning builds: more shapes, fp16 only
 #define W4G64_PIPE_ENTRY_F16(SW, MT, WR, WK, RBW, T, DP, STG) \
     {kPlain, 0, SW, MT, WR, WK, RBW, T, DP, STG, gemv_pipe_kernel<kF16, kPlain, false, SW, MT, WR, WK, RBW, T, DP, STG>, nullptr},
@@ -770,6 +893,11 @@ const PipeEntry kPipeTable[] = {
 #endif
 #ifdef W4G64_PIPE_EXTRA_FUSED_SHAPES  // tuning builds: more fused shapes
     W4G64_PIPE_EXTRA_FUSED_SHAPES(W4G64_PIPE_FUSED_ENTRY)
+#endif
+#ifdef W4G64_PIPE_EXTRA_GROUPED_SHAPES  // tuning builds: more grouped shapes, fp16 only
+#define W4G64_PIPE_GROUPED_ENTRY_F16(SW, MT, WR, WK, RBW, T, DP, STG) \
+    {kGrouped, 0, SW, MT, WR, WK, RBW, T, DP, STG, gemv_pipe_kernel<kF16, kGrouped, false, SW, MT, WR, WK, RBW, T, DP, STG>, nullptr},
+    W4G64_PIPE_EXTRA_GROUPED_SHAPES(W4G64_PIPE_GROUPED_ENTRY_F16)
 #endif
 };
 
@@ -794,7 +922,9 @@ bool finish_pipe_plan(int64_t rows, int64_t out_features, int64_t in_features, G
     const int sw = plan.segments, wr = plan.fblocks, wk = plan.kparts, rbw = plan.rbw, t = plan.steps;
     if (rows < 1 || rows > kGemvMaxRows || in_features % 128 || sw < 1 || 16 % sw) return false;
     const int64_t staged = rows * (plan.form == kPlanes3 ? 3 : 1);
-    if (2 * staged * sw > 16 * plan.tiles) return false;
+    if (plan.form == kGrouped ? (sw != 1 || plan.tiles != 1 || plan.pair || staged > 16)
+                              : 2 * staged * sw > 16 * plan.tiles)
+        return false;
     const bool norm = plan.form == kNormBf16 || plan.form == kNormParts;
     const bool merge = plan.form == kAttnMerge;
     if ((norm || merge) && rows != 1) return false;
@@ -837,6 +967,7 @@ struct PipeShape {
     int64_t min_pairs, max_pairs;
     int64_t min_n, max_n;
     int sw, mt, wr, wk, rbw, t, dp;
+    int form = kPlain;
 };
 constexpr int64_t kAnyN = int64_t(1) << 40;
 const PipeShape kPipeShapes[] = {
@@ -857,10 +988,10 @@ const PipeShape kPipeShapes[] = {
     // 5..8 rows
     {5, 8, 48, 1 << 20, 1, kAnyN, 1, 1, 1, 7, 1, 2, 2},
     {5, 8, 1, 47, 1, kAnyN, 1, 1, 1, 4, 1, 3, 3},
-    // 9..16 rows
-    {9, 16, 48, 1 << 20, 1, kAnyN, 1, 2, 2, 7, 1, 2, 2},
-    {9, 16, 1, 47, 4096, kAnyN, 1, 2, 4, 2, 1, 6, 3},
-    {9, 16, 1, 47, 1, kAnyN, 1, 2, 1, 12, 1, 1, 1},
+    // 9..16 rows: one group per MFMA
+    {9, 16, 48, 1 << 20, 1, kAnyN, 1, 1, 2, 7, 1, 2, 2, kGrouped},
+    {9, 16, 1, 47, 4096, kAnyN, 1, 1, 4, 2, 1, 6, 3, kGrouped},
+    {9, 16, 1, 47, 1, kAnyN, 1, 1, 1, 12, 1, 1, 1, kGrouped},
 };
 
 bool plan_pipe(int64_t rows, int64_t out_features, int64_t in_features, int x_kind, GemvPlan& plan) {
@@ -872,10 +1003,11 @@ bool plan_pipe(int64_t rows, int64_t out_features, int64_t in_features, int x_ki
             continue;
         const PipeEntry* best = nullptr;
         for (const PipeEntry& e : kPipeTable) {
-            if (e.form != kPlain || e.paired || e.sw != sh.sw || e.mt != sh.mt || e.wr != sh.wr || e.wk != sh.wk ||
+            if (e.form != sh.form || e.paired || e.sw != sh.sw || e.mt != sh.mt || e.wr != sh.wr || e.wk != sh.wk ||
                 e.rbw != sh.rbw || e.t != sh.t || e.dp != sh.dp || !e.bf16 || !e.f16)
                 continue;
             GemvPlan cand{};
+            cand.form = e.form;
             cand.segments = e.sw;
             cand.tiles = e.mt;
             cand.fblocks = e.wr;
@@ -1012,7 +1144,8 @@ hipError_t launch_gemv_pipe(const LinearProblem& p, const GemvPlan& plan, void* 
                           : p.x_kind == kNormB                      ? kNormBf16
                           : (p.x_kind == kNormP || p.x_kind == kNormF) ? kNormParts
                                                                       : kPlain;
-    if (want_form != plan.form || (plan.pair && (split || unreduced))) return hipErrorInvalidValue;
+    const bool form_ok = want_form == plan.form || (want_form == kPlain && plan.form == kGrouped);
+    if (!form_ok || (plan.pair && (split || unreduced))) return hipErrorInvalidValue;
     const dim3 grid(plan.n_blocks, plan.splits), block(plan.fblocks * plan.kparts * 64);
     hipError_t err = launch_kernel(k, grid, block, (size_t)plan.lds_bytes, stream, start, split ? nullptr : stop, a);
     if (err != hipSuccess || !split) return err;

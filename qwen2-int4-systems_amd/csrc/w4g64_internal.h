@@ -122,6 +122,7 @@ enum PipeForm : int {
     kNormBf16 = 2,    // RMSNorm(residual + bf16 delta), one row
     kNormParts = 3,   // RMSNorm(residual + sum of fp32 partial sums), one row
     kAttnMerge = 4,   // the decode attention's per-chunk partial results, merged; one row
+    kGrouped = 5,     // fp16 / bf16 rows (up to 16), one quantization group per MFMA: all rows in one A tile
 };
 
 // The decode attention's workspace: arrival counters (256-byte aligned
