@@ -755,6 +755,44 @@ __global__ __launch_bounds__(WR * WK * 64) void gemv_pipe_kernel(PipeArgs a) {
                     const int n = rowof(b, r);
                     if (m < M && n < N) emit(m, n, acc[mt][b][2 * h] + acc[mt][b][2 * h + 1], b);
                 }
+    } else if (kWaveLocal && PL == 1 && (SW == 4 || SW == 8) && Mo == 1) {
+        // one row: the value of row r, segment s sits in lane (r SW + s,
+        // q = s / 2), D row 2 s + (0, 1); the four lane rows are added by
+        // two row swaps, then the SW lanes of the segment group by DPP
+        // (quad swaps, half-row mirror), so every lane of the group holds
+        // the row's sum.  Lane r SW + r stores row r: its bias is row r's.
+        // (the swapped pair is bit cast as a whole: a bit cast of one
+        // element of an integer vector compiles to element 0 with this
+        // compiler)
+        auto swap_sum = [](float v, auto swap) {
+            const uint32_t a = __builtin_bit_cast(uint32_t, v);
+            const float2v r = __builtin_bit_cast(float2v, swap(a, a));
+            return r[0] + r[1];
+        };
+        auto rowsum = [&](int b) {
+            const int h = s & 1;
+            float v = q == (s >> 1) ? acc[0][b][2 * h] + acc[0][b][2 * h + 1] : 0.0f;
+            v = swap_sum(v, [](uint32_t x, uint32_t y) { return __builtin_amdgcn_permlane16_swap(x, y, false, false); });
+            v = swap_sum(v, [](uint32_t x, uint32_t y) { return __builtin_amdgcn_permlane32_swap(x, y, false, false); });
+            v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+            v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+            if constexpr (SW == 8)
+                v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
+            return v;
+        };
+        const bool storer = q == 0 && s == r;
+        if constexpr (PAIRED) {
+            const float g = rowsum(0), u = rowsum(1);
+            const int i = blockIdx.x * (WR * R) + wr * R + r;
+            if (storer && i < a.I) store_silu_planes(a.y, 0, i, Mo, a.I, g + bias_of(0), u + bias_of(1));
+        } else {
+#pragma unroll
+            for (int b = 0; b < RBW; ++b) {
+                const float v = rowsum(b);
+                const int n = rowof(b, r);
+                if (storer && n < N) emit(0, n, v, b);
+            }
+        }
     } else if constexpr (kWaveLocal) {
         // the segments of a row meet in a private area of the wave: no
         // workgroup barrier, only the wave's own LDS order
