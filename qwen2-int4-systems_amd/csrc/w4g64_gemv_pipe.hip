@@ -878,7 +878,7 @@ __global__ __launch_bounds__(WR * WK * 64) void gemv_pipe_kernel(PipeArgs a) {
     X(4, 1, 1, 3, 1, 1, 1, 1)  \
     X(4, 1, 4, 1, 1, 3, 3, 1)  \
     X(4, 1, 2, 4, 1, 5, 3, 5)  \
-    X(4, 2, 2, 6, 1, 3, 3, 6)  \
+    X(2, 1, 1, 12, 1, 3, 2, 6) \
     X(2, 1, 4, 1, 2, 6, 3, 3)  \
     X(2, 1, 2, 2, 1, 3, 3, 3)  \
     X(1, 1, 1, 7, 1, 2, 2, 4)  \
@@ -898,8 +898,8 @@ __global__ __launch_bounds__(WR * WK * 64) void gemv_pipe_kernel(PipeArgs a) {
 
 // The grouped form (9..16 rows): (SW, MT, WR, WK, RBW, T, DP, STG).
 #define W4G64_PIPE_GROUPED_SHAPES(X) \
-    X(1, 1, 2, 7, 1, 2, 2, 4)        \
-    X(1, 1, 4, 2, 1, 6, 3, 6)        \
+    X(1, 1, 2, 7, 1, 2, 1, 4)        \
+    X(1, 1, 4, 2, 1, 6, 2, 6)        \
     X(1, 1, 1, 12, 1, 1, 1, 4)
 
 typedef void (*PipeKernel)(PipeArgs);
@@ -1018,17 +1018,20 @@ const PipeShape kPipeShapes[] = {
     {1, 1, 1, 47, 1, 512, 4, 1, 1, 3, 1, 1, 1},
     {1, 1, 1, 47, 1, kAnyN, 4, 1, 4, 1, 1, 3, 3},
     // 2..4 rows: long K in one workgroup (72 or 80 pairs), no split-K
-    // reduction launch (down 1536x8960: 2 rows 7.3 -> 5.0 us, 4 rows 7.3 -> 6.2)
+    // reduction launch (down 1536x8960: 2 rows 7.3 -> 5.0 us, 4 rows 7.3 ->
+    // 6.2; two segments, one A tile and two chunks in flight: 4 rows 6.4 ->
+    // 5.6 us)
     {2, 2, 48, 1 << 20, 1, kAnyN, 4, 1, 2, 4, 1, 5, 3},
-    {3, 4, 48, 1 << 20, 1, kAnyN, 4, 2, 2, 6, 1, 3, 3},
+    {3, 4, 48, 1 << 20, 1, kAnyN, 2, 1, 1, 12, 1, 3, 2},
     {2, 4, 1, 47, 32768, kAnyN, 2, 1, 4, 1, 2, 6, 3},
     {2, 4, 1, 47, 1, kAnyN, 2, 1, 2, 2, 1, 3, 3},
     // 5..8 rows
     {5, 8, 48, 1 << 20, 1, kAnyN, 1, 1, 1, 7, 1, 2, 2},
     {5, 8, 1, 47, 1, kAnyN, 1, 1, 1, 4, 1, 3, 3},
-    // 9..16 rows: one group per MFMA
-    {9, 16, 48, 1 << 20, 1, kAnyN, 1, 1, 2, 7, 1, 2, 2, kGrouped},
-    {9, 16, 1, 47, 4096, kAnyN, 1, 1, 4, 2, 1, 6, 3, kGrouped},
+    // 9..16 rows: one group per MFMA (fewer chunks in flight: down 8.5 ->
+    // 8.15 us, gate 6.54 -> 6.43)
+    {9, 16, 48, 1 << 20, 1, kAnyN, 1, 1, 2, 7, 1, 2, 1, kGrouped},
+    {9, 16, 1, 47, 4096, kAnyN, 1, 1, 4, 2, 1, 6, 2, kGrouped},
     {9, 16, 1, 47, 1, kAnyN, 1, 1, 1, 12, 1, 1, 1, kGrouped},
 };
 

@@ -349,8 +349,8 @@ def test_workspace_and_kernel_plan_queries():
     assert lib.w4g64_linear_kernel_name(1, 1536, 8960, _lib.DTYPE_F16) == b"gemv_pipe_kernel<f16,8,1,4,1,1,9,5>"
     assert lib.w4g64_linear_kernel_name(4, 1536, 1536, _lib.DTYPE_BF16) == b"gemv_pipe_kernel<bf16,2,1,2,2,1,3,3>"
     assert lib.w4g64_linear_kernel_name(8, 1536, 8960, _lib.DTYPE_F16) == b"gemv_pipe_kernel<f16,1,1,1,7,1,2,2>"
-    assert lib.w4g64_linear_kernel_name(16, 1536, 8960, _lib.DTYPE_BF16) == b"gemv_pipe_kernel<bf16_grouped,1,1,2,7,1,2,2>"
-    assert lib.w4g64_linear_kernel_name(16, 8960, 1536, _lib.DTYPE_F16) == b"gemv_pipe_kernel<f16_grouped,1,1,4,2,1,6,3>"
+    assert lib.w4g64_linear_kernel_name(16, 1536, 8960, _lib.DTYPE_BF16) == b"gemv_pipe_kernel<bf16_grouped,1,1,2,7,1,2,1>"
+    assert lib.w4g64_linear_kernel_name(16, 8960, 1536, _lib.DTYPE_F16) == b"gemv_pipe_kernel<f16_grouped,1,1,4,2,1,6,2>"
     assert lib.w4g64_linear_kernel_name(16, 1536, 1536, _lib.DTYPE_F16) == b"gemv_pipe_kernel<f16_grouped,1,1,1,12,1,1,1>"
     # the down projection at 16 rows splits K in 5 (span 14 pairs): fp32 partial sums
     assert lib.w4g64_linear_workspace_bytes(16, 1536, 8960, _lib.DTYPE_F16) >= 5 * 16 * 1536 * 4
