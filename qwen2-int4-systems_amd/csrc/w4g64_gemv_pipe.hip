@@ -877,6 +877,7 @@ __global__ __launch_bounds__(WR * WK * 64) void gemv_pipe_kernel(PipeArgs a) {
     X(4, 1, 4, 1, 2, 3, 3, 1)  \
     X(4, 1, 1, 3, 1, 1, 1, 1)  \
     X(4, 1, 4, 1, 1, 3, 3, 1)  \
+    X(8, 1, 4, 1, 1, 2, 2, 1)  \
     X(4, 1, 2, 4, 1, 5, 3, 5)  \
     X(2, 1, 1, 12, 1, 3, 2, 6) \
     X(2, 1, 4, 1, 2, 6, 3, 3)  \
@@ -892,9 +893,9 @@ __global__ __launch_bounds__(WR * WK * 64) void gemv_pipe_kernel(PipeArgs a) {
 #define W4G64_PIPE_FUSED_SHAPES(X)                   \
     X(kNormBf16, true, 4, 1, 4, 1, 2, 3, 1, 1)       \
     X(kPlain, true, 4, 1, 4, 1, 2, 3, 3, 1)          \
-    X(kNormParts, false, 4, 1, 4, 1, 1, 3, 3, 1)     \
+    X(kNormParts, false, 8, 1, 4, 1, 1, 2, 2, 1)     \
     X(kPlanes3, false, 2, 1, 4, 1, 1, 7, 4, 3)       \
-    X(kAttnMerge, false, 4, 1, 4, 1, 1, 3, 3, 1)
+    X(kAttnMerge, false, 8, 1, 4, 1, 1, 2, 2, 1)
 
 // The grouped form (9..16 rows): (SW, MT, WR, WK, RBW, T, DP, STG).
 #define W4G64_PIPE_GROUPED_SHAPES(X) \
@@ -1016,6 +1017,7 @@ const PipeShape kPipeShapes[] = {
     // one row: span 12
     {1, 1, 1, 47, 32768, kAnyN, 4, 1, 4, 1, 2, 3, 3},
     {1, 1, 1, 47, 1, 512, 4, 1, 1, 3, 1, 1, 1},
+    {1, 1, 1, 47, 1, 2048, 8, 1, 4, 1, 1, 2, 2},  // q/o 1536x1536 3.11 -> 2.99 us
     {1, 1, 1, 47, 1, kAnyN, 4, 1, 4, 1, 1, 3, 3},
     // 2..4 rows: long K in one workgroup (72 or 80 pairs), no split-K
     // reduction launch (down 1536x8960: 2 rows 7.3 -> 5.0 us, 4 rows 7.3 ->
@@ -1073,7 +1075,10 @@ bool plan_pipe(int64_t rows, int64_t out_features, int64_t in_features, int x_ki
 // 17920x1536 6.8 us (7.3 with three chunks in flight per row block), the
 // planes down projection 1536x8960 into five partial sums 4.4 us (5.3 with
 // seven K parts per workgroup), RMSNorm over five partial sums + q|k|v
-// 2048x1536 4.1 us (4.6 with three K parts).  The RMSNorm and paired forms
+// 2048x1536 4.1 us (4.6 with three K parts).  RMSNorm + q|k|v and the
+// attention-merge o_proj take 8 segments and two steps per wave, whose
+// segment sums stay in registers (decode 0.849 -> 0.841 ms per token; the
+// paired forms at 8 segments: 0.855-0.861).  The RMSNorm and paired forms
 // need the whole K range in one workgroup.
 struct PipeFusedShape {
     int form;
@@ -1085,9 +1090,9 @@ struct PipeFusedShape {
 const PipeFusedShape kPipeFusedShapes[] = {
     {kNormBf16, true, 1, 1, 12, 4, 1, 4, 1, 2, 3, 1},
     {kPlain, true, 1, 1, 12, 4, 1, 4, 1, 2, 3, 3},
-    {kNormParts, false, 1, 1, 12, 4, 1, 4, 1, 1, 3, 3},
+    {kNormParts, false, 1, 1, 12, 8, 1, 4, 1, 1, 2, 2},
     {kPlanes3, false, 1, 1, 1 << 20, 2, 1, 4, 1, 1, 7, 4},
-    {kAttnMerge, false, 1, 1, 12, 4, 1, 4, 1, 1, 3, 3},
+    {kAttnMerge, false, 1, 1, 12, 8, 1, 4, 1, 1, 2, 2},
 };
 
 bool plan_pipe_fused(int form, bool paired, int64_t rows, int64_t out_features, int64_t in_features,

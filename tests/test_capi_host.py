@@ -342,7 +342,7 @@ def test_workspace_and_kernel_plan_queries():
     # GEMV, its launch shape by rows, K and out_features (no workspace unless
     # K is split across workgroups)
     assert lib.w4g64_linear_kernel_name(1, 8960, 1536, _lib.DTYPE_F16) == b"gemv_pipe_kernel<f16,4,1,4,1,1,3,3>"
-    assert lib.w4g64_linear_kernel_name(1, 1536, 1536, _lib.DTYPE_BF16) == b"gemv_pipe_kernel<bf16,4,1,4,1,1,3,3>"
+    assert lib.w4g64_linear_kernel_name(1, 1536, 1536, _lib.DTYPE_BF16) == b"gemv_pipe_kernel<bf16,8,1,4,1,1,2,2>"
     assert lib.w4g64_linear_kernel_name(1, 256, 1536, _lib.DTYPE_F16) == b"gemv_pipe_kernel<f16,4,1,1,3,1,1,1>"
     assert lib.w4g64_linear_kernel_name(1, 501760, 1536, _lib.DTYPE_F16) == b"gemv_pipe_kernel<f16,4,1,4,1,2,3,3>"
     assert lib.w4g64_linear_workspace_bytes(1, 8960, 1536, _lib.DTYPE_F16) == 0
