@@ -891,7 +891,7 @@ __global__ __launch_bounds__(WR * WK * 64) void gemv_pipe_kernel(PipeArgs a) {
 // The fused forms of the decode step (bf16): (FORM, PAIRED, SW, MT, WR, WK,
 // RBW, T, DP, STG).
 #define W4G64_PIPE_FUSED_SHAPES(X)                   \
-    X(kNormBf16, true, 4, 1, 4, 1, 2, 3, 1, 1)       \
+    X(kNormBf16, true, 4, 1, 4, 1, 2, 3, 2, 1)       \
     X(kPlain, true, 4, 1, 4, 1, 2, 3, 3, 1)          \
     X(kNormParts, false, 8, 1, 4, 1, 1, 2, 2, 1)     \
     X(kPlanes3, false, 2, 1, 4, 1, 1, 7, 4, 3)       \
@@ -1072,7 +1072,9 @@ bool plan_pipe(int64_t rows, int64_t out_features, int64_t in_features, int x_ki
 // The decode step's fused forms (bf16, out_features rows; paired: gate rows
 // then up rows): one shape each, from forced-shape sweeps of the Qwen2-1.5B
 // decode step at one row over cold weights, graph-replayed: RMSNorm + gate|up
-// 17920x1536 6.8 us (7.3 with three chunks in flight per row block), the
+// 17920x1536 6.8 us (7.3 with three chunks in flight per row block; two,
+// since the segment sums moved into registers: decode 0.840 -> 0.833 ms per
+// token), the
 // planes down projection 1536x8960 into five partial sums 4.4 us (5.3 with
 // seven K parts per workgroup), RMSNorm over five partial sums + q|k|v
 // 2048x1536 4.1 us (4.6 with three K parts).  RMSNorm + q|k|v and the
@@ -1088,7 +1090,7 @@ struct PipeFusedShape {
     int sw, mt, wr, wk, rbw, t, dp;
 };
 const PipeFusedShape kPipeFusedShapes[] = {
-    {kNormBf16, true, 1, 1, 12, 4, 1, 4, 1, 2, 3, 1},
+    {kNormBf16, true, 1, 1, 12, 4, 1, 4, 1, 2, 3, 2},
     {kPlain, true, 1, 1, 12, 4, 1, 4, 1, 2, 3, 3},
     {kNormParts, false, 1, 1, 12, 8, 1, 4, 1, 1, 2, 2},
     {kPlanes3, false, 1, 1, 1 << 20, 2, 1, 4, 1, 1, 7, 4},
