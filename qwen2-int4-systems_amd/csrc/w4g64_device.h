@@ -153,6 +153,15 @@ __device__ __forceinline__ void store_out(void* y, int64_t idx, float v) {
 
 __device__ __forceinline__ float bf16_round(float v) { return bf16_bits_to_float(float_to_bf16_bits(v)); }
 
+// Two values rounded to bf16 (round to nearest even, as float_to_bf16_bits)
+// by one conversion instruction: a in the low half, b in the high half.
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(float2v{a, b}, bf16x2v));
+}
+// The low and high bf16 halves of a word as fp32.
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __builtin_bit_cast(float, w & 0xFFFF0000u); }
+
 // Sum over the 64 lanes of a wave (quad swaps, half-row and row mirrors give
 // every lane its row's sum; row broadcasts 15 and 31 add the rows up in
 // lane 63), read from lane 63: one fixed order of additions.

@@ -435,29 +435,33 @@ __global__ __launch_bounds__(WR * WK * 64) void gemv_pipe_kernel(PipeArgs a) {
             u32x4 sb;
 #pragma unroll
             for (int e = 0; e < 8; e += 2) {
-                float sv[2];
+                // (each pair rounded to bf16 by one conversion instruction)
+                const uint32_t xw = xv[u][e / 2];
+                float df[2];
+                if constexpr (FORM == kNormBf16) {
+                    const uint32_t dw = dv[u][0][e / 2];
+                    df[0] = bf16_lo(dw);
+                    df[1] = bf16_hi(dw);
+                } else {
+                    float t[2] = {0.0f, 0.0f};
 #pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    const uint32_t xw = xv[u][e / 2];
-                    const float xf = bf16_bits_to_float(h ? xw >> 16 : xw & 0xFFFFu);
-                    float df;
-                    if constexpr (FORM == kNormBf16) {
-                        const uint32_t dw = dv[u][0][e / 2];
-                        df = bf16_bits_to_float(h ? dw >> 16 : dw & 0xFFFFu);
-                    } else {
-                        float t = 0.0f;
+                    for (int pt2 = 0; pt2 < kMaxDeltaParts; ++pt2)
+                        if (pt2 < a.delta_parts) {
 #pragma unroll
-                        for (int pt2 = 0; pt2 < kMaxDeltaParts; ++pt2)
-                            if (pt2 < a.delta_parts) {
+                            for (int h = 0; h < 2; ++h) {
                                 const uint32_t bits = dv[u][2 * pt2 + (e + h) / 4][(e + h) % 4];
-                                t = t + __builtin_bit_cast(float, bits);
+                                t[h] = t[h] + __builtin_bit_cast(float, bits);
                             }
-                        df = bf16_round(t + 0.0f);
-                    }
-                    sv[h] = bf16_round(xf + df);
-                    ps_ += __fmul_rn(sv[h], sv[h]);
+                        }
+                    const uint32_t dp = pack_bf16x2(t[0] + 0.0f, t[1] + 0.0f);
+                    df[0] = bf16_lo(dp);
+                    df[1] = bf16_hi(dp);
                 }
-                sb[e / 2] = float_to_bf16_bits(sv[0]) | ((uint32_t)float_to_bf16_bits(sv[1]) << 16);
+                const uint32_t sp = pack_bf16x2(bf16_lo(xw) + df[0], bf16_hi(xw) + df[1]);
+                const float sv0 = bf16_lo(sp), sv1 = bf16_hi(sp);
+                ps_ += __fmul_rn(sv0, sv0);
+                ps_ += __fmul_rn(sv1, sv1);
+                sb[e / 2] = sp;
             }
             xv[u] = sb;
             pt += it < items ? ps_ : 0.0f;  // clamped items repeat a real one
@@ -476,10 +480,8 @@ __global__ __launch_bounds__(WR * WK * 64) void gemv_pipe_kernel(PipeArgs a) {
             u32x4 xb;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const float n0 = bf16_round(bf16_bits_to_float(xv[u][e] & 0xFFFFu) * rinv) *
-                                 bf16_bits_to_float(nwv[u][e] & 0xFFFFu);
-                const float n1 = bf16_round(bf16_bits_to_float(xv[u][e] >> 16) * rinv) * bf16_bits_to_float(nwv[u][e] >> 16);
-                xb[e] = float_to_bf16_bits(n0) | ((uint32_t)float_to_bf16_bits(n1) << 16);
+                const uint32_t r = pack_bf16x2(bf16_lo(xv[u][e]) * rinv, bf16_hi(xv[u][e]) * rinv);
+                xb[e] = pack_bf16x2(bf16_lo(r) * bf16_lo(nwv[u][e]), bf16_hi(r) * bf16_hi(nwv[u][e]));
             }
             xv[u] = xb;
         }
