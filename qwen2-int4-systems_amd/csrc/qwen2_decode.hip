@@ -270,18 +270,18 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(AttnArgs a) {
     const u32x4 kxv = *(const u32x4*)(kvec + qd);
     const u32x4 kpv = *(const u32x4*)(kvec + (qd ^ (kHeadDim / 2)));
     const u32x4 vxv = *(const u32x4*)(qkv + (a.heads + a.kv_heads + kvh) * kHeadDim + qd);
-    // 8 rotated dimensions qd .. qd + 7 of a head vector (rope_elem per element)
+    // 8 rotated dimensions qd .. qd + 7 of a head vector: rope_elem's
+    // operations, two dimensions per bf16 conversion instruction (the 8
+    // dimensions lie in one half of the head, so rotate_half's sign is one)
+    const float rsign = qd < kHeadDim / 2 ? -1.0f : 1.0f;
     auto rope8 = [&](const u32x4& x, const u32x4& partner) {
         u32x4 r;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            const uint16_t lo = float_to_bf16_bits(rope_elem((uint16_t)(x[e] & 0xFFFFu), (uint16_t)(partner[e] & 0xFFFFu),
-                                                             (uint16_t)(qcv[e] & 0xFFFFu), (uint16_t)(qnv[e] & 0xFFFFu),
-                                                             qd + 2 * e));
-            const uint16_t hi = float_to_bf16_bits(rope_elem((uint16_t)(x[e] >> 16), (uint16_t)(partner[e] >> 16),
-                                                             (uint16_t)(qcv[e] >> 16), (uint16_t)(qnv[e] >> 16),
-                                                             qd + 2 * e + 1));
-            r[e] = (uint32_t)lo | ((uint32_t)hi << 16);
+            const uint32_t pa = pack_bf16x2(bf16_lo(x[e]) * bf16_lo(qcv[e]), bf16_hi(x[e]) * bf16_hi(qcv[e]));
+            const uint32_t pb = pack_bf16x2((rsign * bf16_lo(partner[e])) * bf16_lo(qnv[e]),
+                                            (rsign * bf16_hi(partner[e])) * bf16_hi(qnv[e]));
+            r[e] = pack_bf16x2(bf16_lo(pa) + bf16_lo(pb), bf16_hi(pa) + bf16_hi(pb));
         }
         return r;
     };
