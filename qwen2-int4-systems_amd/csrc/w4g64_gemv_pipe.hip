@@ -225,6 +225,10 @@ __global__ __launch_bounds__(WR * WK * 64) void gemv_pipe_kernel(PipeArgs a) {
     // the workgroup (kThreads % RWG == 0)
     constexpr bool kWaveLocal = WK == 1;
     constexpr int NB = kWaveLocal ? RBW : 1;
+    // one K part, one A tile, 2-8 segments: the segment sums stay in
+    // registers (the epilogue below), and the storing lane of row r is lane
+    // r SW of a lane row, so each lane's bias is that of row c / SW
+    constexpr bool kRegSum = kWaveLocal && PL == 1 && MT == 1 && !kGrp && (SW == 2 || SW == 4 || SW == 8);
     static_assert(kWaveLocal || kThreads % RWG == 0, "a thread's outputs share its row");
 
     // ---- 0. bias of the stored outputs (raw bits, decoded at the stores) ----
@@ -233,7 +237,7 @@ __global__ __launch_bounds__(WR * WK * 64) void gemv_pipe_kernel(PipeArgs a) {
     _Float16 bias_lo[NB], bias_hi[NB];
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
-        int brow = kWaveLocal ? rowof(b, lane % R) : row0 + tid % RWG;
+        int brow = kWaveLocal ? rowof(b, kRegSum ? r : lane % R) : row0 + tid % RWG;
         brow = min(brow, N - 1);
         const _Float16* bp = (const _Float16*)(a.bias_kind == 0 ? (const void*)a.scales : a.bias);
         const int e = a.bias_kind == kF32 ? 2 * brow : (a.bias_kind == 0 ? 0 : brow);
@@ -757,42 +761,49 @@ __global__ __launch_bounds__(WR * WK * 64) void gemv_pipe_kernel(PipeArgs a) {
                     const int n = rowof(b, r);
                     if (m < M && n < N) emit(m, n, acc[mt][b][2 * h] + acc[mt][b][2 * h + 1], b);
                 }
-    } else if (kWaveLocal && PL == 1 && (SW == 4 || SW == 8) && Mo == 1) {
-        // one row: the value of row r, segment s sits in lane (r SW + s,
-        // q = s / 2), D row 2 s + (0, 1); the four lane rows are added by
-        // two row swaps, then the SW lanes of the segment group by DPP
-        // (quad swaps, half-row mirror), so every lane of the group holds
-        // the row's sum.  Lane r SW + r stores row r: its bias is row r's.
-        // (the swapped pair is bit cast as a whole: a bit cast of one
-        // element of an integer vector compiles to element 0 with this
-        // compiler)
+    } else if constexpr (kRegSum) {
+        // Row m, row r, segment s: D row v = m SW + s of lane (r SW + s, q =
+        // v / 2) (one A tile: v < 8), both halves of the pair added.  The lane
+        // rows holding one activation row's segments are added by row swaps
+        // (v_permlane16_swap: rows 2m, 2m + 1 at SW 4; v_permlane32_swap as
+        // well at SW 8, one row), then the SW lanes of the segment group by
+        // DPP (quad swaps, half-row mirror), so every lane of the group holds
+        // the row's sum; lane r SW of the row's first lane row stores it.
+        // (the swapped pair is bit cast as a whole: a bit cast of one element
+        // of an integer vector compiles to element 0 with this compiler)
         auto swap_sum = [](float v, auto swap) {
             const uint32_t a = __builtin_bit_cast(uint32_t, v);
             const float2v r = __builtin_bit_cast(float2v, swap(a, a));
             return r[0] + r[1];
         };
+        const int h = s & 1;
+        const int vr = 2 * q + h;  // this lane's D row pair: virtual row vr
+        const bool own = vr % SW == s && vr / SW < Mo;
         auto rowsum = [&](int b) {
-            const int h = s & 1;
-            float v = q == (s >> 1) ? acc[0][b][2 * h] + acc[0][b][2 * h + 1] : 0.0f;
-            v = swap_sum(v, [](uint32_t x, uint32_t y) { return __builtin_amdgcn_permlane16_swap(x, y, false, false); });
-            v = swap_sum(v, [](uint32_t x, uint32_t y) { return __builtin_amdgcn_permlane32_swap(x, y, false, false); });
+            float v = own ? acc[0][b][2 * h] + acc[0][b][2 * h + 1] : 0.0f;
+            if constexpr (SW >= 4)
+                v = swap_sum(v, [](uint32_t x, uint32_t y) { return __builtin_amdgcn_permlane16_swap(x, y, false, false); });
+            if constexpr (SW == 8)
+                v = swap_sum(v, [](uint32_t x, uint32_t y) { return __builtin_amdgcn_permlane32_swap(x, y, false, false); });
             v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
-            v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+            if constexpr (SW >= 4)
+                v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
             if constexpr (SW == 8)
                 v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
             return v;
         };
-        const bool storer = q == 0 && s == r;
+        const int m = SW == 2 ? q : (SW == 4 ? q >> 1 : 0);
+        const bool storer = s == 0 && (SW == 2 || (SW == 4 ? (q & 1) == 0 : q == 0)) && m < Mo;
         if constexpr (PAIRED) {
             const float g = rowsum(0), u = rowsum(1);
             const int i = blockIdx.x * (WR * R) + wr * R + r;
-            if (storer && i < a.I) store_silu_planes(a.y, 0, i, Mo, a.I, g + bias_of(0), u + bias_of(1));
+            if (storer && i < a.I) store_silu_planes(a.y, m, i, Mo, a.I, g + bias_of(0), u + bias_of(1));
         } else {
 #pragma unroll
             for (int b = 0; b < RBW; ++b) {
                 const float v = rowsum(b);
                 const int n = rowof(b, r);
-                if (storer && n < N) emit(0, n, v, b);
+                if (storer && n < N) emit(m, n, v, b);
             }
         }
     } else if constexpr (kWaveLocal) {
