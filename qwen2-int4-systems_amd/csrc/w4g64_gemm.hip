@@ -162,17 +162,27 @@ __device__ __forceinline__ void tile_coords(int t, int tiles_m, int tiles_n, int
     }
 }
 
-template <int OUTK>
-__global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
+// NWV waves per workgroup, each owning CW = 256 / NWV output features: 4
+// waves (two workgroups per CU, gemm_kernel) or 8 (one workgroup per CU, two
+// waves per SIMD on the same tile, gemm_kernel8, for launches with at most
+// one workgroup per CU).  The body is a device function: kernels whose own
+// template parameters decide the wave count were given no host-side launch
+// handle by this compiler.
+template <int OUTK, int NWV>
+__device__ __forceinline__ void gemm_body(const GemmArgs& a) {
+    static_assert(NWV == 4 || NWV == 8, "4 or 8 waves");
+    constexpr int CW = kBN / NWV;               // output features per wave (64 or 32)
+    constexpr int CB = CW / 16;                 // 16-column MFMA blocks per wave
+    constexpr int WB = CW / 32;                 // 1 KB weight DMA instructions per wave (32 columns each)
     constexpr int RB = kBM / 16;                // 16-row MFMA blocks per wave
     constexpr int kABytes = kBM * 128;          // kBM rows x 64 fp16 values
-    constexpr int kWBytes = 4 * 2 * 1024;       // 4 waves x 2 column blocks x (32 columns x 32 B)
+    constexpr int kWBytes = NWV * WB * 1024;    // per wave WB x (32 columns x 32 B)
     // Sub-dword global->LDS loads write one zero-extended dword per lane.
-    constexpr int kSBytes = 4 * 64 * 4;         // one fp16 scale per column (in a dword)
-    constexpr int kZBytes = 4 * 64 * 4;         // the byte holding each column's zero nibble (in a dword)
+    constexpr int kSBytes = NWV * 64 * 4;       // one fp16 scale per column (in a dword; lanes past CW unused)
+    constexpr int kZBytes = NWV * 64 * 4;       // the byte holding each column's zero nibble (in a dword)
     constexpr int kStageBytes = kABytes + kWBytes + kSBytes + kZBytes;
-    constexpr int kDma = kBM / 32;              // 1 KB activation DMA instructions per wave
-    constexpr int kOpsPerStep = kDma + 2 + 1 + 1;  // + weight blocks, scales, zeros
+    constexpr int kDma = kABytes / 1024 / NWV;  // 1 KB activation DMA instructions per wave
+    constexpr int kOpsPerStep = kDma + WB + 1 + 1;  // + weight blocks, scales, zeros
     __shared__ __attribute__((aligned(1024))) unsigned char smem[kStages][kStageBytes];
 
     const int tid = threadIdx.x;
@@ -219,7 +229,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
     int tile_m, tile_n;
     tile_coords(t, a.tiles_m, a.tiles_n, a.band_group, tile_m, tile_n);
     const int64_t m0 = (int64_t)tile_m * kBM;
-    const int64_t nw = (int64_t)tile_n * kBN + 64 * wave;  // this wave's first output feature
+    const int64_t nw = (int64_t)tile_n * kBN + CW * wave;  // this wave's first output feature
 
     // ---- per-lane DMA sources ----
     // Each load address is a uniform base advanced per step (scalar
@@ -239,9 +249,9 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
     // weights: DMA instruction b, lane L -> column nw + 32 b + L % 32, bytes [16 (L / 32), +16)
     const int c = lane & 15;   // this lane's column within a 16-column block / row within a 16-row block
     const int kq = lane >> 4;  // this lane's K slot group
-    uint32_t w_off[2];
+    uint32_t w_off[WB];
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
+    for (int b = 0; b < WB; ++b) {
         int n = (int)nw + 32 * b + (lane & 31);
         n = n < a.N ? n : a.N - 1;
         w_off[b] = (uint32_t)n * (uint32_t)a.wg * 32u + 16u * (uint32_t)(lane >> 5);
@@ -279,8 +289,8 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
             __builtin_amdgcn_raw_ptr_buffer_load_lds(x_rsrc, (lds_ptr_t)(st + 1024 * (wave * kDma + d)), 16, a_off[d],
                                                      128 * (gbeg + gg), 0, 0);
 #pragma unroll
-        for (int bj = 0; bj < 2; ++bj)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rsrc, (lds_ptr_t)(st + kABytes + 2048 * wave + 1024 * bj), 16,
+        for (int bj = 0; bj < WB; ++bj)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(w_rsrc, (lds_ptr_t)(st + kABytes + 1024 * (WB * wave + bj)), 16,
                                                      w_off[bj], 32 * gw, 0, 0);
         __builtin_amdgcn_raw_ptr_buffer_load_lds(s_rsrc, (lds_ptr_t)(st + kABytes + kWBytes + 256 * wave), 2, s_off,
                                                  2 * gw, 0, 0);
@@ -288,11 +298,11 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
                                                  z_off, gw >> 1, 0, 0);
     };
 
-    float4v acc[RB][4];
+    float4v acc[RB][CB];
 #pragma unroll
     for (int i = 0; i < RB; ++i)
 #pragma unroll
-        for (int bj = 0; bj < 4; ++bj) acc[i][bj] = float4v{0.f, 0.f, 0.f, 0.f};
+        for (int bj = 0; bj < CB; ++bj) acc[i][bj] = float4v{0.f, 0.f, 0.f, 0.f};
 
     // Bit position of the zero nibble of this lane's columns nw + 16 bj + c in
     // its byte: the parity of the element index n wg + gw, i.e. of c wg + gw
@@ -313,7 +323,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
         const unsigned char* st = smem[g % kStages];
         const int col = 16 * bj + c;  // column within the wave
         BRaw r;
-        r.w = *(const u32x2*)(st + kABytes + 2048 * wave + 1024 * (col >> 5) + 16 * ((col & 31) + 32 * (kq >> 1)) +
+        r.w = *(const u32x2*)(st + kABytes + 1024 * (WB * wave + (col >> 5)) + 16 * ((col & 31) + 32 * (kq >> 1)) +
                               8 * (kq & 1));
         r.sbits = *(const uint16_t*)(st + kABytes + kWBytes + 256 * wave + 4 * col);
         r.zb = st[kABytes + kWBytes + kSBytes + 256 * wave + 4 * col];
@@ -375,14 +385,14 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
     // barrier above made them visible).  Stage g is refilled only after step
     // g's own barrier, so the B of step g + 1 can be read at the end of step
     // g, after that step's barrier.
-    BRaw rb[4];
+    BRaw rb[CB];
 #pragma unroll
-    for (int bj = 0; bj < 4; ++bj) rb[bj] = read_b(0, bj);
+    for (int bj = 0; bj < CB; ++bj) rb[bj] = read_b(0, bj);
 
     for (int g = 0; g < G; ++g) {
         const unsigned char* st = smem[g % kStages];
-        u32x4 f[4][2];  // (code - zero) of the four column blocks, both MFMAs of the group
-        float sc[4];    // the four column scales
+        u32x4 f[CB][2];  // (code - zero) of the column blocks, both MFMAs of the group
+        float sc[CB];    // the column scales
         const int zsh = (wgroup(g) & 1) ? zsh_odd : zsh_even;
         // A fragments of row blocks bi (ab[bi & 1]), read two row blocks ahead
         u32x4 ab[2][2];
@@ -393,22 +403,22 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
         // Row block bi's group products D go to dd[bi & 1]; its scaled
         // accumulation runs after row block bi + 1's MFMAs have been issued,
         // so the matrix cores and the FMAs of one wave overlap.
-        float4v dd[2][4];
+        float4v dd[2][CB];
         auto scale_add = [&](int bi) {
 #pragma unroll
-            for (int bj = 0; bj < 4; ++bj)
+            for (int bj = 0; bj < CB; ++bj)
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
                     acc[bi][bj][i] = __builtin_fmaf(sc[bj], dd[bi & 1][bj][i], acc[bi][bj][i]);
             // the empty asm pins the accumulation here (sunk to the end of the
             // step, it would keep every block's products live)
 #pragma unroll
-            for (int bj = 0; bj < 4; ++bj) asm volatile("" : "+v"(acc[bi][bj]));
+            for (int bj = 0; bj < CB; ++bj) asm volatile("" : "+v"(acc[bi][bj]));
         };
         // Row block 0: each column block's B is decoded right before its first
         // MFMA, so the decode of the next column blocks overlaps the products.
 #pragma unroll
-        for (int bj = 0; bj < 4; ++bj) {
+        for (int bj = 0; bj < CB; ++bj) {
             const BConst k = group_const(zsh, rb[bj]);
 #pragma unroll
             for (int h = 0; h < 2; ++h) f[bj][h] = decode_codes(rb[bj].w[h], k.zlo, k.zhi);
@@ -418,7 +428,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
         }
         ab[0][0] = read_a(st, 2, 0);
 #pragma unroll
-        for (int bj = 0; bj < 4; ++bj) dd[0][bj] = mfma(ab[0][1], f[bj][1], dd[0][bj]);
+        for (int bj = 0; bj < CB; ++bj) dd[0][bj] = mfma(ab[0][1], f[bj][1], dd[0][bj]);
         ab[0][1] = read_a(st, 2, 1);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -435,12 +445,12 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
                     if (g + 3 < G) issue(g + 3);
                 }
             }
-            float4v(&d)[4] = dd[bi & 1];
+            float4v(&d)[CB] = dd[bi & 1];
 #pragma unroll
-            for (int bj = 0; bj < 4; ++bj) d[bj] = mfma(ab[bi & 1][0], f[bj][0], float4v{0.f, 0.f, 0.f, 0.f});
+            for (int bj = 0; bj < CB; ++bj) d[bj] = mfma(ab[bi & 1][0], f[bj][0], float4v{0.f, 0.f, 0.f, 0.f});
             if (bi + 2 < RB) ab[bi & 1][0] = read_a(st, bi + 2, 0);
 #pragma unroll
-            for (int bj = 0; bj < 4; ++bj) d[bj] = mfma(ab[bi & 1][1], f[bj][1], d[bj]);
+            for (int bj = 0; bj < CB; ++bj) d[bj] = mfma(ab[bi & 1][1], f[bj][1], d[bj]);
             if (bi + 2 < RB) ab[bi & 1][1] = read_a(st, bi + 2, 1);
             scale_add(bi - 1);
             // the scheduling barrier stops later blocks' reads and products
@@ -451,7 +461,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
         // reads are in flight during the last row block's accumulation
         if (g + 1 < G) {
 #pragma unroll
-            for (int bj = 0; bj < 4; ++bj) rb[bj] = read_b(g + 1, bj);
+            for (int bj = 0; bj < CB; ++bj) rb[bj] = read_b(g + 1, bj);
         }
         scale_add(RB - 1);
     }
@@ -465,7 +475,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
         for (int bi = 0; bi < RB; ++bi) {
             const float4v rs = *(const float4v*)(a.rowscale + m0 + 16 * bi + 4 * kq);
 #pragma unroll
-            for (int bj = 0; bj < 4; ++bj)
+            for (int bj = 0; bj < CB; ++bj)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) acc[bi][bj][i] *= rs[i];
         }
@@ -473,31 +483,33 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
 
     // ---- split tile: fp32 partial sums, added up by gemm_reduce_kernel ----
     if (slot >= 0) {
-        float* part = a.partials + (int64_t)slot * (kBM * kBN) + 64 * wave + c;
+        float* part = a.partials + (int64_t)slot * (kBM * kBN) + CW * wave + c;
 #pragma unroll
         for (int bi = 0; bi < RB; ++bi)
 #pragma unroll
-            for (int bj = 0; bj < 4; ++bj)
+            for (int bj = 0; bj < CB; ++bj)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) part[(16 * bi + 4 * kq + i) * kBN + 16 * bj] = acc[bi][bj][i];
         return;
     }
 
     // ---- epilogue ----
-    // Each wave stages its 64 output columns through LDS, half of its rows at
-    // a time, and writes 16 B per lane: full 128-byte row segments.  Row
-    // stride 144 B (fp32: 272 B) keeps the 16-byte reads aligned.
+    // Each wave stages its CW output columns through LDS, half of its rows
+    // at a time, and writes 16 B per lane: full row segments of the wave's
+    // columns.  Row stride 2 CW + 16 B (fp32: 4 CW + 16) keeps the 16-byte
+    // reads aligned.
     block_barrier();  // every wave has finished reading the pipeline stages
-    float bias_v[4];
+    float bias_v[CB];
 #pragma unroll
-    for (int bj = 0; bj < 4; ++bj) {
+    for (int bj = 0; bj < CB; ++bj) {
         const int64_t n = nw + 16 * bj + c;
         bias_v[bj] = n < a.N ? load_bias(a.bias, a.bias_kind, n) : 0.0f;
     }
     constexpr int kHalfRows = kBM / 2;
     if constexpr (OUTK == kF32) {
-        constexpr int kOutStride32 = 272;
-        static_assert(4 * kHalfRows * kOutStride32 <= kStages * kStageBytes, "output staging exceeds LDS");
+        constexpr int kOutStride32 = 4 * CW + 16;
+        constexpr int kLanesPerRow = CW / 4;  // 16 B per lane
+        static_assert(NWV * kHalfRows * kOutStride32 <= kStages * kStageBytes, "output staging exceeds LDS");
         unsigned char* ost = &smem[0][0] + wave * kHalfRows * kOutStride32;
         float* y = (float*)a.y;
 #pragma unroll
@@ -505,16 +517,16 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
 #pragma unroll
             for (int bi = 0; bi < RB / 2; ++bi)
 #pragma unroll
-                for (int bj = 0; bj < 4; ++bj)
+                for (int bj = 0; bj < CB; ++bj)
 #pragma unroll
                     for (int i = 0; i < 4; ++i)
                         *(float*)(ost + (16 * bi + 4 * kq + i) * kOutStride32 + 4 * (16 * bj + c)) =
                             acc[hh * (RB / 2) + bi][bj][i] + bias_v[bj];
             asm volatile("" ::: "memory");
 #pragma unroll
-            for (int it = 0; it < kHalfRows / 4; ++it) {
-                const int row = 4 * it + (lane >> 4);
-                const int c4 = lane & 15;
+            for (int it = 0; it < kHalfRows * kLanesPerRow / 64; ++it) {
+                const int row = (64 / kLanesPerRow) * it + lane / kLanesPerRow;
+                const int c4 = lane % kLanesPerRow;
                 const u32x4 v = *(const u32x4*)(ost + row * kOutStride32 + 16 * c4);
                 const int64_t m = m0 + hh * kHalfRows + row;
                 const int64_t n = nw + 4 * c4;
@@ -532,8 +544,9 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
         }
         return;
     }
-    constexpr int kOutStride = 144;
-    static_assert(4 * kHalfRows * kOutStride <= kStages * kStageBytes, "output staging exceeds LDS");
+    constexpr int kOutStride = 2 * CW + 16;
+    constexpr int kLanesPerRow = CW / 8;  // 16 B per lane
+    static_assert(NWV * kHalfRows * kOutStride <= kStages * kStageBytes, "output staging exceeds LDS");
     unsigned char* ost = &smem[0][0] + wave * kHalfRows * kOutStride;
     uint16_t* y = (uint16_t*)a.y;
 #pragma unroll
@@ -541,7 +554,7 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
 #pragma unroll
         for (int bi = 0; bi < RB / 2; ++bi)
 #pragma unroll
-            for (int bj = 0; bj < 4; ++bj)
+            for (int bj = 0; bj < CB; ++bj)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const float v = acc[hh * (RB / 2) + bi][bj][i] + bias_v[bj];
@@ -552,9 +565,9 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
         // compiler from reordering the staging writes and reads.
         asm volatile("" ::: "memory");
 #pragma unroll
-        for (int it = 0; it < kHalfRows / 8; ++it) {
-            const int row = 8 * it + (lane >> 3);
-            const int c8 = lane & 7;
+        for (int it = 0; it < kHalfRows * kLanesPerRow / 64; ++it) {
+            const int row = (64 / kLanesPerRow) * it + lane / kLanesPerRow;
+            const int c8 = lane % kLanesPerRow;
             const u32x4 v = *(const u32x4*)(ost + row * kOutStride + 16 * c8);
             const int64_t m = m0 + hh * kHalfRows + row;
             const int64_t n = nw + 8 * c8;
@@ -570,6 +583,15 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
         }
         asm volatile("" ::: "memory");
     }
+}
+
+template <int OUTK>
+__global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs a) {
+    gemm_body<OUTK, 4>(a);
+}
+template <int OUTK>
+__global__ __launch_bounds__(512, 1) void gemm_kernel8(GemmArgs a) {
+    gemm_body<OUTK, 8>(a);
 }
 
 // Sum of the K-range partials of every split tile, in range order
@@ -836,6 +858,16 @@ GemmPlan plan_gemm(int64_t rows, int64_t out_features, int64_t k_staged) {
 
 bool two_planes(int x_kind) { return x_kind == kF32 || x_kind == kSwiGLU; }
 
+// 8-wave workgroups for launches of at most one workgroup per CU with no K
+// split.  Measured (bf16 rows, same process, bit-identical outputs): gate
+// 8960x1536 at 512 rows (140 tiles) 40.1 -> 38.2 us; split launches gain
+// nothing or lose (gate at 128 rows, 35 tiles in 4 K ranges, 28.0 -> 26.5
+// us, but down 1536x8960 at 512 rows, 24 tiles in 10 ranges, 40.3 -> 40.9,
+// and the end-to-end prefill, whose small GEMMs all split, 6.16 -> 6.26 ms).
+bool gemm_eight_waves(const GemmPlan& pl) {
+    return pl.split_tiles == 0 && pl.dp_tiles <= gemm_slots() / 2;
+}
+
 // Workspace: [split-tile partials][staged fp16 rows][row factors], each part
 // 256-byte aligned; the staged rows and row factors cover tiles_m * kBM rows.
 struct GemmLayout {
@@ -867,11 +899,19 @@ bool gemm_supported(const LinearProblem& p) {
     return p.rows * k_staged < (int64_t(1) << 31) && p.out_features * (p.in_features / 2) < (int64_t(1) << 31);
 }
 
-const char* gemm_kernel_name(int64_t, int64_t, int64_t, int x_kind) {
-    if (x_kind == kF16) return "gemm_kernel<f16 a x int b,128x256> (fp16 rows staged)";
-    if (x_kind == kBF16) return "gemm_kernel<f16 a x int b,128x256> (bf16 rows staged as scaled fp16)";
-    if (x_kind == kSwiGLU) return "gemm_kernel<f16 a x int b,128x256> (silu(gate)*up staged as scaled fp16 hi|lo)";
-    return "gemm_kernel<f16 a x int b,128x256> (f32 rows staged as scaled fp16 hi|lo)";
+const char* gemm_kernel_name(int64_t rows, int64_t out_features, int64_t in_features, int x_kind) {
+    const bool eight = gemm_eight_waves(gemm_layout(rows, out_features, in_features, x_kind).plan);
+    if (x_kind == kF16)
+        return eight ? "gemm_kernel<f16 a x int b,128x256,8 waves> (fp16 rows staged)"
+                     : "gemm_kernel<f16 a x int b,128x256> (fp16 rows staged)";
+    if (x_kind == kBF16)
+        return eight ? "gemm_kernel<f16 a x int b,128x256,8 waves> (bf16 rows staged as scaled fp16)"
+                     : "gemm_kernel<f16 a x int b,128x256> (bf16 rows staged as scaled fp16)";
+    if (x_kind == kSwiGLU)
+        return eight ? "gemm_kernel<f16 a x int b,128x256,8 waves> (silu(gate)*up staged as scaled fp16 hi|lo)"
+                     : "gemm_kernel<f16 a x int b,128x256> (silu(gate)*up staged as scaled fp16 hi|lo)";
+    return eight ? "gemm_kernel<f16 a x int b,128x256,8 waves> (f32 rows staged as scaled fp16 hi|lo)"
+                 : "gemm_kernel<f16 a x int b,128x256> (f32 rows staged as scaled fp16 hi|lo)";
 }
 
 hipError_t launch_gemm(const LinearProblem& p, void* workspace, hipStream_t stream, hipEvent_t start,
@@ -929,16 +969,22 @@ hipError_t launch_gemm(const LinearProblem& p, void* workspace, hipStream_t stre
             break;
     }
     if (err != hipSuccess) return err;
+    // at most one workgroup per CU: 8 waves each (two per SIMD on one tile)
+    const bool eight = gemm_eight_waves(pl);
+    hipEvent_t gstop = reduce ? nullptr : stop;
     if (p.x_kind == kF16) {
-        err = launch_kernel(gemm_kernel<kF16>, grid, dim3(256), 0, stream, nullptr, reduce ? nullptr : stop, args);
+        err = eight ? launch_kernel(gemm_kernel8<kF16>, grid, dim3(512), 0, stream, nullptr, gstop, args)
+                    : launch_kernel(gemm_kernel<kF16>, grid, dim3(256), 0, stream, nullptr, gstop, args);
         if (err == hipSuccess && reduce)
             err = launch_kernel(gemm_reduce_kernel<kF16>, rgrid, dim3(256), 0, stream, nullptr, stop, args);
     } else if (p.x_kind == kBF16) {
-        err = launch_kernel(gemm_kernel<kBF16>, grid, dim3(256), 0, stream, nullptr, reduce ? nullptr : stop, args);
+        err = eight ? launch_kernel(gemm_kernel8<kBF16>, grid, dim3(512), 0, stream, nullptr, gstop, args)
+                    : launch_kernel(gemm_kernel<kBF16>, grid, dim3(256), 0, stream, nullptr, gstop, args);
         if (err == hipSuccess && reduce)
             err = launch_kernel(gemm_reduce_kernel<kBF16>, rgrid, dim3(256), 0, stream, nullptr, stop, args);
     } else {
-        err = launch_kernel(gemm_kernel<kF32>, grid, dim3(256), 0, stream, nullptr, reduce ? nullptr : stop, args);
+        err = eight ? launch_kernel(gemm_kernel8<kF32>, grid, dim3(512), 0, stream, nullptr, gstop, args)
+                    : launch_kernel(gemm_kernel<kF32>, grid, dim3(256), 0, stream, nullptr, gstop, args);
         if (err == hipSuccess && reduce)
             err = launch_kernel(gemm_reduce_kernel<kF32>, rgrid, dim3(256), 0, stream, nullptr, stop, args);
     }
