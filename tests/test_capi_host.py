@@ -362,6 +362,12 @@ def test_workspace_and_kernel_plan_queries():
     assert lib.w4g64_linear_kernel_name(16, 40, 9280, _lib.DTYPE_BF16).startswith(b"gemv16_kernel<bf16")
     assert lib.w4g64_linear_kernel_name(16, 1536, 8960, _lib.DTYPE_F32).startswith(b"gemv_kernel<f32")
     assert lib.w4g64_linear_kernel_name(2048, 8960, 1536, _lib.DTYPE_BF16).startswith(b"gemm_kernel<")
+    # 8-wave workgroups only for unsplit launches of at most one workgroup per CU (256 CUs)
+    assert b"8 waves" in lib.w4g64_linear_kernel_name(512, 8960, 1536, _lib.DTYPE_BF16)  # 140 tiles
+    assert b"8 waves" in lib.w4g64_linear_kernel_name(512, 8960, 1536, _lib.DTYPE_F32)
+    assert b"8 waves" not in lib.w4g64_linear_kernel_name(2048, 8960, 1536, _lib.DTYPE_BF16)  # 560 tiles
+    assert b"8 waves" not in lib.w4g64_linear_kernel_name(128, 8960, 1536, _lib.DTYPE_BF16)  # K split
+    assert b"8 waves" not in lib.w4g64_linear_kernel_name(512, 1536, 8960, _lib.DTYPE_BF16)  # K split
     assert lib.w4g64_linear_kernel_name(1, 8960, 1536, 8) == b"none"
 
 

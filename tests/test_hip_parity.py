@@ -300,6 +300,27 @@ def test_prefill_mlp_shapes_bf16(name, rows):
     check_linear(x, q, s, z, None, n, k, "bf16")
 
 
+@pytest.mark.parametrize("dtype", ["fp16", "bf16", "fp32"])
+def test_gemm_eight_wave_workgroups(dtype):
+    """gate_proj 8960x1536 at 512 rows: 140 unsplit tiles, at most one
+    workgroup per CU, so each workgroup runs 8 waves of 32 output features
+    (two per SIMD on one tile); fp32 rows take the two-plane staging and the
+    fp32-output epilogue."""
+    from qwen_int4_hip import linear_kernel_name
+
+    n, k = SHAPES["gate_proj"]
+    torch_dtype = {"fp16": torch.float16, "bf16": torch.bfloat16, "fp32": torch.float32}[dtype]
+    assert "8 waves" in linear_kernel_name(512, n, k, torch_dtype)
+    q, s, z = weights("asym", n, k, O.BASE_SEED + 41)
+    x = O.activations(512, k, seed=O.BASE_SEED + 43, dtype=dtype)
+    if dtype == "fp32":
+        bias = np.linspace(-1, 1, n, dtype=np.float32)
+        check_linear(x, q, s, z, bias, n, k, "fp32", bias_dtype="fp32", normwise=1e-5, tol=(1e-4, 1e-4))
+    else:
+        bias = O.f32_to_bf16_bits(np.linspace(-1, 1, n, dtype=np.float32))
+        check_linear(x, q, s, z, bias, n, k, dtype)
+
+
 @pytest.mark.parametrize("rows", [1, 2048])
 @pytest.mark.parametrize("name", list(SHAPES))
 def test_asymmetric_awq_shapes_fp16_with_outliers(name, rows):
