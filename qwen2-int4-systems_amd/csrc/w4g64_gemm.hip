@@ -813,7 +813,7 @@ int gemm_slots() {
 // costs ~1.0 us with one workgroup per CU and ~1.54 us for the two that
 // share a CU; a round of workgroups costs ~6 us fixed (launch, pipeline
 // fill, epilogue); the reduction kernel ~2 us plus the partial sums at ~2.5
-// bytes per ns (written by the GEMM, read back by the reduction: at 5 the
+// TB/s (written by the GEMM, read back by the reduction: at 5 TB/s the
 // model split gate 8960x1536 at 128 rows into 6 K ranges, which measured
 // 29.1 us against 27.2 us for 4).  Full rounds of tiles stay data-parallel; the tiles of a last,
 // less than half full round -- or all tiles, when there are fewer than the
