@@ -534,7 +534,7 @@ def cpu_model_name() -> str:
 
 
 def cpu_parity(decode, gemm, torch):
-    """The cpu_baseline leg's checker, run before any timed region: every
+    """The cpu_baseline leg's parity check, run before any timed region: every
     decode output and the rows-2048 GEMM outputs of this run against the
     CPU restatement of the reference's torch backend (backends.py:73-98),
     normwise relative error <= 1e-2 -- the reference harness checks parity
